@@ -1,0 +1,296 @@
+#!/usr/bin/env python
+"""QSA decode benchmark on one MI355X.
+
+Workload (the benchmark's headline shape, one GPU's TP2 share): decode batch 64,
+context lengths uniform in [8192, 32768], 16 q / 2 kv heads x 128, bf16 paged KV
+with 16-token pages, compress ratio 16, indexer 32 heads x 128, top-k 2048
+tokens (128 pages) per query. A step is one QSA layer's decode path on that
+batch: indexer scoring -> exact top-k + expansion to physical slots + counts ->
+sparse paged attention (+ split merge). Inputs are resident in HBM.
+
+Several query sets rotate across steps so successive steps select different
+pages (the selected KV of all sets exceeds the 256 MB Infinity Cache). Steps
+run from HIP graphs (one graph per block of steps) so host launch overhead is
+not timed; K steps are timed with HIP events between two synchronisations.
+
+The attention kernel's roofline figure comes from a separate timed loop of
+attention-only graphs on the same stream: achieved = algorithmic bytes per
+launch / mean launch time, against 8 TB/s. The CPU baseline times the eager
+PyTorch oracle of the same path on this host on a bounded sample.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+METRIC = "QSA decode tokens/s + sparse-attn HBM GB/s (% of peak), 32k ctx, 1 MI355X"
+HBM_PEAK_GBPS = 8000.0
+WORKLOAD = "decode_32k"
+
+
+def parse_args():
+    p = argparse.ArgumentParser(description=__doc__.split("\n\n")[0])
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=200)
+    p.add_argument("--warmup", type=int, default=20)
+    p.add_argument("--sets", type=int, default=4, help="query sets rotated across steps")
+    p.add_argument("--cpu-seconds", type=float, default=10.0,
+                   help="CPU work budget for the oracle baseline (0 disables it)")
+    p.add_argument("--cpu-threads", type=int, default=0, help="0: min(16, cpu_count)")
+    p.add_argument("--traffic", default=os.path.join(os.path.dirname(os.path.abspath(__file__)),
+                                                     "profiles", "sparse_attn_decode_32k_traffic.txt"),
+                   help="committed rocprofv3 PMC summary giving HBM bytes per attention launch")
+    return p.parse_args()
+
+
+def log(msg):
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def read_traffic(path):
+    """HBM bytes per attention launch from the committed PMC summary, if present."""
+    try:
+        with open(path) as fh:
+            for line in fh:
+                if line.startswith("traffic_bytes_per_launch:"):
+                    return float(line.split(":", 1)[1].split()[0])
+    except OSError:
+        pass
+    return None
+
+
+def main():
+    args = parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only (asked for --gpus {args.gpus}); the QSA path is "
+              "built and measured on a single MI355X.", file=sys.stderr)
+        return 2
+    if args.steps <= 0:
+        raise SystemExit("--steps must be positive")
+
+    import torch
+
+    from qsa_vllm_amd.ops import qsa_sparse_paged_attention, select_paged_tokens, topk_expand
+    from qsa_vllm_amd.workloads import (SHAPES, attention_bytes, fresh_queries, indexer_bytes,
+                                        make_workload)
+
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    t0 = time.time()
+    wl = make_workload(WORKLOAD, device=dev)
+    s = wl.shape
+    rows = wl.rows
+    sets = [(wl.q, wl.q_index)] + [fresh_queries(wl, 100 + i) for i in range(args.sets - 1)]
+    n_sets = len(sets)
+    idx = [torch.empty(rows, s.width, dtype=torch.int32, device=dev) for _ in sets]
+    counts = [torch.empty(rows, dtype=torch.int32, device=dev) for _ in sets]
+    outs = [torch.zeros_like(wl.q) for _ in sets]
+    cols = wl.index_table.shape[1] * wl.index_cache.shape[1]
+    from qsa_vllm_amd.graph_dispatch import decode_logits_columns
+    cols = decode_logits_columns(wl.max_seq_len, s.compress_ratio, cols)
+    logits = [torch.empty(rows, cols, dtype=torch.float32, device=dev) for _ in sets]
+    log(f"workload {WORKLOAD} built in {time.time() - t0:.1f}s: rows={rows} "
+        f"kv_cache={wl.kv_cache.numel() * 2 / 1e9:.2f} GB")
+
+    def select(i):
+        select_paged_tokens(sets[i][1], wl.index_cache, wl.index_table, wl.token_to_req,
+                            wl.positions, wl.seq_lens, s.token_topk, s.compress_ratio, idx[i],
+                            query_start_loc=wl.query_start_loc, max_query_len=1,
+                            max_seq_len=wl.max_seq_len, num_decodes=rows, num_decode_tokens=rows,
+                            visible_blocks=wl.visible, main_block_table=wl.block_table,
+                            main_page_size=s.page_size, valid_counts_out=counts[i])
+
+    def attend(i):
+        qsa_sparse_paged_attention(sets[i][0], wl.k_cache, wl.v_cache, idx[i], wl.block_table,
+                                   wl.token_to_req, outs[i], use_decode_kernel=True,
+                                   indices_are_physical=True, valid_counts=counts[i])
+
+    def index_only(i):
+        torch.ops.yulan_qsa_kernels.indexer_decode(sets[i][1], wl.index_cache, wl.index_table,
+                                                   wl.visible, logits[i], 1)
+
+    def topk_only(i):
+        topk_expand(logits[i], wl.visible, wl.positions, wl.seq_lens, wl.token_to_req, idx[i],
+                    s.compress_ratio, main_block_table=wl.block_table,
+                    main_page_size=s.page_size, valid_counts_out=counts[i])
+
+    def step(i):
+        select(i)
+        attend(i)
+
+    # Eager pass (also initialises allocator pools), then capture.
+    for i in range(n_sets):
+        step(i)
+        index_only(i)
+        topk_only(i)
+    torch.cuda.synchronize()
+
+    def capture(fn, indices):
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            for i in indices:
+                fn(i)
+        torch.cuda.current_stream().wait_stream(side)
+        torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            for i in indices:
+                fn(i)
+        return g
+
+    block_graph = capture(step, list(range(n_sets)))
+    single = [capture(step, [i]) for i in range(n_sets)]
+    reps = 8
+    attn_graph = capture(attend, list(range(n_sets)) * reps)
+    index_graph = capture(index_only, list(range(n_sets)) * reps)
+    topk_graph = capture(topk_only, list(range(n_sets)) * reps)
+
+    def run_steps(k):
+        full, rest = divmod(k, n_sets)
+        for _ in range(full):
+            block_graph.replay()
+        for i in range(rest):
+            single[i].replay()
+
+    run_steps(args.warmup)
+    torch.cuda.synchronize()
+
+    stream = torch.cuda.current_stream()
+    start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    start.record(stream)
+    run_steps(args.steps)
+    stop.record(stream)
+    torch.cuda.synchronize()
+    ms_step = start.elapsed_time(stop) / args.steps
+
+    def time_graph(graph, launches, rounds):
+        graph.replay()
+        torch.cuda.synchronize()
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record(stream)
+        for _ in range(rounds):
+            graph.replay()
+        b.record(stream)
+        torch.cuda.synchronize()
+        return a.elapsed_time(b) * 1e3 / (launches * rounds)  # us per launch
+
+    rounds = max(2, args.steps // (n_sets * reps))
+    attn_us = time_graph(attn_graph, n_sets * reps, rounds)
+    index_us = time_graph(index_graph, n_sets * reps, rounds)
+    topk_us = time_graph(topk_graph, n_sets * reps, rounds)
+
+    # Correctness gate on the timed data: counts follow the closed form.
+    want_counts = s.token_topk + wl.seq_lens % s.compress_ratio
+    for i in range(n_sets):
+        if not torch.equal(counts[i], want_counts):
+            raise SystemExit("valid counts differ from the closed form: results invalid")
+        if not torch.isfinite(outs[i].float()).all():
+            raise SystemExit("non-finite attention output: results invalid")
+
+    attn_bytes = sum(attention_bytes(wl, counts[i]) for i in range(n_sets)) / n_sets
+    attn_gbps = attn_bytes / (attn_us * 1e-6) / 1e9
+    idx_bytes = indexer_bytes(wl)
+    traffic = read_traffic(args.traffic)
+
+    result = {
+        "metric": METRIC,
+        "value": round(rows / (ms_step * 1e-3), 1),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_step, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic: seeded N(0,1) activations and caches, permuted block tables",
+        "config": {
+            "workload": f"{WORKLOAD}: decode batch {s.batch}, context U[{s.seq_len_min},"
+                        f"{s.seq_len_max}], {s.num_q_heads}q/{s.num_kv_heads}kv x {s.head_dim}, "
+                        f"page {s.page_size}, compress ratio {s.compress_ratio}, top-k "
+                        f"{s.token_topk} tokens, indexer {s.index_heads}x{s.index_dim}",
+            "batch": s.batch,
+            "query_sets": n_sets,
+            "kv_layout": s.kv_layout,
+            "graph": "HIP graph per block of steps",
+        },
+        "roofline": {
+            "kernel": "sparse_attn_kernel (+ split merge)",
+            "bound": "hbm",
+            "achieved": round(attn_gbps, 1),
+            "peak": HBM_PEAK_GBPS,
+            "unit": "GB/s",
+            "frac": round(attn_gbps / HBM_PEAK_GBPS, 4),
+            "traffic": traffic,
+            "algorithmic_bytes_per_launch": int(attn_bytes),
+            "us_per_launch": round(attn_us, 3),
+        },
+        "breakdown_us": {
+            "indexer_decode": round(index_us, 3),
+            "topk_expand": round(topk_us, 3),
+            "sparse_attention": round(attn_us, 3),
+            "step": round(ms_step * 1e3, 3),
+        },
+        "indexer_gbps": round(idx_bytes / (index_us * 1e-6) / 1e9, 1),
+    }
+    if args.cpu_seconds > 0:
+        result["cpu_baseline"] = cpu_baseline(wl, args)
+    print(json.dumps(result), flush=True)
+    return 0
+
+
+def cpu_baseline(wl, args):
+    """Eager-PyTorch oracle of the same decode step on this host's cores."""
+    import torch
+
+    import oracle
+
+    threads = args.cpu_threads or min(16, os.cpu_count() or 1)
+    torch.set_num_threads(threads)
+    cpu = {n: getattr(wl, n).cpu() for n in ("q", "q_index", "index_cache", "index_table",
+                                             "block_table", "positions", "seq_lens")}
+    kv = wl.kv_cache.cpu()
+    d = wl.shape.head_dim
+    k_cache, v_cache = kv[..., :d], kv[..., d:]
+    steps = 0
+    t0 = time.perf_counter()
+    while True:
+        oracle.decode_step(cpu["q_index"], cpu["index_cache"], cpu["index_table"], cpu["q"],
+                           k_cache, v_cache, cpu["block_table"], cpu["positions"],
+                           cpu["seq_lens"], wl.shape.token_topk, wl.shape.compress_ratio)
+        steps += 1
+        elapsed = time.perf_counter() - t0
+        if elapsed >= args.cpu_seconds:
+            break
+    return {
+        "value": round(steps * wl.rows / elapsed, 2),
+        "unit": "tokens/s",
+        "cores": threads,
+        "kind": "port",
+        "sample": f"{steps} full decode step(s) of the {WORKLOAD} batch ({wl.rows} rows) in "
+                  f"{elapsed:.1f}s: oracle indexer -> top-k/expand -> fp32 sparse attention",
+        "cpu": _cpu_model(),
+        "torch": torch.__version__,
+    }
+
+
+def _cpu_model():
+    try:
+        with open("/proc/cpuinfo") as fh:
+            for line in fh:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+if __name__ == "__main__":
+    sys.exit(main())

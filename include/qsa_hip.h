@@ -1,0 +1,183 @@
+/*
+ * qsa_hip.h - C ABI of the MI355X (gfx950) QSA sparse-attention path.
+ *
+ * Plain pointers, sizes and element strides only; every entry point enqueues
+ * its kernels on `stream` (a hipStream_t passed as void*) and never
+ * synchronises or reads device data on the host. Entry points return QSA_OK or
+ * a negative status; qsa_last_error() gives the message of the calling thread's
+ * last failure.
+ *
+ * Each entry point replaces one interface of the reference vLLM plugin
+ * (clotholza/qsa_vllm, package yulan_qsa_vllm); the citation names the file
+ * and lines whose behaviour it reproduces.
+ */
+#ifndef QSA_HIP_H
+#define QSA_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define QSA_OK 0
+#define QSA_ERR_INVALID (-1)     /* bad shape, stride, pointer or size */
+#define QSA_ERR_UNSUPPORTED (-2) /* valid input this build has no kernel for */
+#define QSA_ERR_HIP (-3)         /* a HIP runtime call failed */
+#define QSA_ERR_WORKSPACE (-4)   /* workspace missing or too small */
+
+/* Message of the calling thread's last failed call ("" if none). */
+const char* qsa_last_error(void);
+
+/* ABI version of this library (increments on any signature change). */
+int qsa_abi_version(void);
+
+/* ------------------------------------------------------------------------ */
+/* Kernel 2: exact top-k block selection                                     */
+/* ------------------------------------------------------------------------ */
+
+/* Bytes of device workspace qsa_topk / qsa_topk_expand need for this shape
+ * (0 when the row fits the single-pass kernel). */
+size_t qsa_topk_workspace_bytes(int rows, int cols, int topk);
+
+/*
+ * Replaces torch.ops.yulan_qsa_kernels.topk (ops/csrc/topk.cu:527-545,
+ * schema :549, Python wrapper ops/topk.py:25-26).
+ *
+ * scores [rows, cols] fp32 (row stride score_row_stride, unit column stride),
+ * lengths [rows] int32, output [rows, topk] int32 (unit column stride).
+ * Per row, L = lengths[r]: L <= topk writes ids 0..L-1 then -1; otherwise the
+ * topk ids whose scores have the largest raw fp32 bit patterns read as uint32
+ * (lowest id first among equal patterns), in ascending id order.
+ */
+int qsa_topk(const float* scores, int64_t score_row_stride, int rows, int cols,
+             const int32_t* lengths, int32_t* output, int64_t output_row_stride, int topk,
+             void* workspace, size_t workspace_bytes, void* stream);
+
+/*
+ * Replaces torch.ops.yulan_qsa_kernels.topk_expand (ops/csrc/topk.cu:470-525,
+ * schema :550-552, Python wrapper ops/topk.py:29-39).
+ *
+ * Selection as qsa_topk with topk = output_width / ratio, then each selected
+ * block b at rank i expands to tokens b*ratio + o at output columns
+ * i*ratio + o, followed by the visible incomplete causal tail, then -1.
+ * physical != 0 maps tokens through `table` [num_requests, table_width] to
+ * slots page*page_size + offset; store_counts != 0 writes counts[rows].
+ * positions are int64; all other index arrays int32 and contiguous.
+ */
+int qsa_topk_expand(const float* scores, int64_t score_row_stride, int rows, int cols,
+                    const int32_t* lengths, const int64_t* positions,
+                    const int32_t* sequence_lengths, int num_requests,
+                    const int32_t* token_to_req,
+                    const int32_t* table, int64_t table_row_stride, int table_width,
+                    int32_t* output, int64_t output_row_stride, int64_t output_col_stride,
+                    int output_width, int32_t* counts, int ratio, int page_size,
+                    int physical, int store_counts,
+                    void* workspace, size_t workspace_bytes, void* stream);
+
+/* ------------------------------------------------------------------------ */
+/* Kernel 1: indexer scoring                                                 */
+/* ------------------------------------------------------------------------ */
+
+/*
+ * Replaces the decode scoring launch of qsa_select_paged_decode
+ * (ops/indexer.py:24-114, launch :259-272).
+ *
+ * q [rows, num_heads, head_dim] bf16 (unit dim stride); k_cache
+ * [num_blocks, cache_page, (1,) head_dim] bf16 (unit dim stride);
+ * page_table [rows / decode_query_len, table_width] int32; visible [rows].
+ * Writes logits[r, c] = head_dim^-0.5 * sum_h relu(q[r,h,:] . K[c,:]) for
+ * c < min(visible[r], table_width * cache_page, logits_cols); other columns
+ * are left untouched.
+ */
+int qsa_indexer_decode(const void* q, int64_t q_row_stride, int64_t q_head_stride,
+                       int rows, int num_heads, int head_dim,
+                       const void* k_cache, int64_t cache_block_stride,
+                       int64_t cache_token_stride, int num_blocks, int cache_page,
+                       const int32_t* page_table, int64_t table_row_stride, int table_width,
+                       const int32_t* visible, int decode_query_len,
+                       float* logits, int64_t logits_row_stride, int logits_cols,
+                       void* stream);
+
+/*
+ * Replaces _prefill_logits (ops/indexer.py:117-223, launch :282-302).
+ *
+ * q / visible are indexed by the prefill-relative absolute row; logits rows by
+ * row - query_offset for the num_rows rows of this chunk. Request req covers
+ * rows [query_start_loc[req] - query_start_loc[0],
+ * query_start_loc[req+1] - query_start_loc[0]) and uses page_table[req].
+ */
+int qsa_indexer_prefill(const void* q, int64_t q_row_stride, int64_t q_head_stride,
+                        int num_heads, int head_dim,
+                        const void* k_cache, int64_t cache_block_stride,
+                        int64_t cache_token_stride, int num_blocks, int cache_page,
+                        const int32_t* page_table, int64_t table_row_stride, int table_width,
+                        int num_requests, const int32_t* query_start_loc,
+                        const int32_t* visible, int query_offset, int num_rows,
+                        int max_query_len,
+                        float* logits, int64_t logits_row_stride, int logits_cols,
+                        void* stream);
+
+/* ------------------------------------------------------------------------ */
+/* Kernel 3: bf16 paged sparse GQA attention                                 */
+/* ------------------------------------------------------------------------ */
+
+/* Split count the library picks for this shape (use_decode_kernel as in
+ * ops/qsa.py:620-645: decode rows iterate only their valid count). */
+int qsa_sparse_attention_splits(int rows, int num_q_heads, int num_kv_heads, int head_dim,
+                                int width, int use_decode_kernel);
+
+/* Bytes of fp32 split partials (output + log2-LSE) for num_splits > 1. */
+size_t qsa_sparse_attention_workspace_bytes(int rows, int num_q_heads, int head_dim,
+                                            int num_splits);
+
+/*
+ * Replaces qsa_sparse_paged_attention (ops/qsa.py:594-688) and its kernels
+ * _qsa_sparse_paged_gqa_splitk_kernel (:109-303) and _qsa_merge_splitk_kernel
+ * (:306-362).
+ *
+ * q [rows, Hq, D] bf16; k_cache / v_cache [num_blocks, page_size, Hkv, D] bf16
+ * views with arbitrary block/token/head strides and unit dim stride;
+ * indices [rows, width] int32 (unit column stride): physical slots
+ * (page*page_size + offset) when indices_are_physical, else logical token ids
+ * mapped through block_table[token_to_req[r]]. valid_counts (may be NULL)
+ * limits row r to its first valid_counts[r] entries. Head h attends with kv
+ * head h / (Hq / Hkv). out [rows, Hq, D] bf16 (unit dim stride); gate (may be
+ * NULL) multiplies bf16(out) by sigmoid(gate). num_splits > 1 needs a workspace
+ * of qsa_sparse_attention_workspace_bytes(). Strides are in elements.
+ */
+int qsa_sparse_attention(const void* q, int64_t q_row_stride, int64_t q_head_stride,
+                         int rows, int num_q_heads, int head_dim,
+                         const void* k_cache, int64_t k_block_stride, int64_t k_token_stride,
+                         int64_t k_head_stride,
+                         const void* v_cache, int64_t v_block_stride, int64_t v_token_stride,
+                         int64_t v_head_stride,
+                         int num_blocks, int page_size, int num_kv_heads,
+                         const int32_t* indices, int64_t indices_row_stride, int width,
+                         const int32_t* block_table, int64_t table_row_stride,
+                         int table_width, int num_requests,
+                         const int32_t* token_to_req, const int32_t* valid_counts,
+                         void* out, int64_t out_row_stride, int64_t out_head_stride,
+                         const void* gate, int64_t gate_row_stride, int64_t gate_head_stride,
+                         int64_t gate_dim_stride,
+                         int indices_are_physical, int num_splits,
+                         void* workspace, size_t workspace_bytes, void* stream);
+
+/*
+ * Replaces _qsa_merge_splitk_kernel (ops/qsa.py:306-362) as a standalone call:
+ * partial_out [num_splits, rows, Hq, D] fp32, partial_lse [num_splits, rows, Hq]
+ * fp32 (log2 domain, -inf for empty splits) -> out bf16 (+ optional gate).
+ */
+int qsa_sparse_attention_merge(const float* partial_out, const float* partial_lse,
+                               int num_splits, int rows, int num_q_heads, int head_dim,
+                               void* out, int64_t out_row_stride, int64_t out_head_stride,
+                               const void* gate, int64_t gate_row_stride,
+                               int64_t gate_head_stride, int64_t gate_dim_stride,
+                               void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* QSA_HIP_H */

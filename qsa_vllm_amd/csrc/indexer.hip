@@ -1,0 +1,345 @@
+// Kernel 1: QSA indexer scoring, gfx950.
+//
+// logits[r, c] = D^-0.5 * sum_h relu(q[r, h, :] . K[c, :]) over the visible
+// compressed keys of row r (ops/indexer.py:24-114 decode, :117-223 prefill),
+// bf16 inputs, fp32 accumulation, written only for c < visible[r].
+//
+// Both kernels use v_mfma_f32_32x32x16_bf16 with the index heads on M and 32
+// keys on N: A = Q[32 heads][16 dims] stays in registers for the whole row,
+// B = K^T[16 dims][32 keys] is one 16 B load per lane per K step. The 32x32
+// accumulator holds 16 heads of one key per lane, so the ReLU head-sum is 16
+// in-lane adds plus one cross-half shuffle, and lanes 0..31 then hold the 32
+// logits of the tile for one coalesced 128 B store.
+//
+// Decode: a row's keys are only read once, so each wave streams key tiles of
+// one row straight from HBM (GEMV-like, bandwidth bound).
+// Prefill: consecutive query rows of a request see nearly the same keys, so a
+// 4-wave workgroup owns 16 rows (4 per wave, their Q in registers) and stages
+// each 32-key tile once in LDS, where all 16 rows reuse it (MFMA bound).
+#include "qsa_common.h"
+#include "../../include/qsa_hip.h"
+
+namespace qsa {
+namespace {
+
+struct IndexerParams {
+  const uint16_t* q;
+  int64_t q_row, q_head;  // elements
+  const char* k;
+  int64_t kb, kt;  // bytes
+  int num_blocks;
+  int cache_page;
+  FastDiv page_div;
+  const int32_t* table;
+  int64_t table_row;
+  int table_width;
+  const int32_t* visible;
+  int num_heads;
+  int decode_query_len;
+  float* logits;
+  int64_t logits_row;
+  int logits_cols;
+  float scale;
+  // prefill only
+  const int32_t* query_start_loc;
+  int num_requests;
+  int query_offset;
+  int num_rows;
+  int key_tiles_per_wg;
+};
+
+// Byte address of compressed key c of a request, or the zero block.
+__device__ __forceinline__ const char* key_ptr(const IndexerParams& p, const int32_t* trow, int c,
+                                               bool live) {
+  const char* zero = reinterpret_cast<const char*>(g_qsa_zero_rows);
+  if (!live) return zero;
+  const int lp = p.page_div.div(c);
+  const int off = c - lp * p.cache_page;
+  const int page = trow[lp];
+  if (page < 0 || page >= p.num_blocks) return zero;
+  return p.k + (int64_t)page * p.kb + (int64_t)off * p.kt;
+}
+
+__device__ __forceinline__ float relu_head_sum(const f32x16& acc) {
+  float s = 0.0f;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) s += fmaxf(acc[i], 0.0f);
+  return s;
+}
+
+// ---------------------------------------------------------------------------
+// Decode: grid (programs, rows), one wave per workgroup.
+// ---------------------------------------------------------------------------
+template <int D, int MB>
+__global__ __launch_bounds__(64) void indexer_decode_kernel(const IndexerParams p) {
+  constexpr int KS = D / 16;
+  const int lane = threadIdx.x;
+  const int kk = lane & 31;
+  const int half = lane >> 5;
+  const int row = blockIdx.y;
+  const int prog = blockIdx.x;
+  const int num_columns = p.table_width * p.cache_page;
+  const int vis = min(min(p.visible[row], num_columns), p.logits_cols);
+  if (prog * 32 >= vis) return;
+  const int req = row / p.decode_query_len;
+  const int32_t* trow = p.table + (int64_t)req * p.table_row;
+
+  // A operand: lane holds Q[head 32 mb + kk][16 s + 8 half .. +7].
+  bf16x8 qa[MB][KS];
+#pragma unroll
+  for (int mb = 0; mb < MB; ++mb) {
+    const int h = 32 * mb + kk;
+    const uint16_t* qrow = p.q + (int64_t)row * p.q_row + (int64_t)(h < p.num_heads ? h : 0) * p.q_head;
+#pragma unroll
+    for (int s = 0; s < KS; ++s) {
+      u32x4 raw = {0u, 0u, 0u, 0u};
+      if (h < p.num_heads) raw = load_u32x4(qrow + 16 * s + 8 * half);
+      qa[mb][s] = __builtin_bit_cast(bf16x8, raw);
+    }
+  }
+
+  float* lrow = p.logits + (int64_t)row * p.logits_row;
+  for (int tile = prog; tile * 32 < vis; tile += gridDim.x) {
+    const int c = tile * 32 + kk;
+    const bool live = c < vis;
+    const char* kp = key_ptr(p, trow, c, live);
+    bf16x8 kb[KS];
+#pragma unroll
+    for (int s = 0; s < KS; ++s) kb[s] = __builtin_bit_cast(bf16x8, load_u32x4(kp + (16 * s + 8 * half) * 2));
+    float sum = 0.0f;
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb) {
+      f32x16 acc = {};
+#pragma unroll
+      for (int s = 0; s < KS; ++s)
+        acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(qa[mb][s], kb[s], acc, 0, 0, 0);
+      sum += relu_head_sum(acc);
+    }
+    sum += shfl_xor_f(sum, 32);
+    if (half == 0 && live) lrow[c] = sum * p.scale;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Prefill: grid (requests, row tiles of 16, key-tile chunks), 4 waves.
+// ---------------------------------------------------------------------------
+constexpr int kPrefillRowsPerWave = 4;
+constexpr int kPrefillWaves = 4;
+constexpr int kPrefillRows = kPrefillRowsPerWave * kPrefillWaves;
+
+template <int D>
+__global__ __launch_bounds__(256) void indexer_prefill_kernel(const IndexerParams p) {
+  constexpr int KS = D / 16;
+  constexpr int ROW_BYTES = D * 2 + 16;  // padded LDS row: conflict-free 16 B reads
+  __shared__ __attribute__((aligned(16))) char s_keys[32 * ROW_BYTES];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int kk = lane & 31;
+  const int half = lane >> 5;
+  const int req = blockIdx.x;
+  const int base = p.query_start_loc[0];
+  const int query_end = p.query_offset + p.num_rows;
+  const int req_start = max(p.query_start_loc[req] - base, p.query_offset);
+  const int req_end = min(p.query_start_loc[req + 1] - base, query_end);
+  const int tile_row0 = req_start + blockIdx.y * kPrefillRows;
+  if (tile_row0 >= req_end) return;
+
+  const int num_columns = p.table_width * p.cache_page;
+  const int32_t* trow = p.table + (int64_t)req * p.table_row;
+
+  // This wave's rows and their visible counts.
+  int rvis[kPrefillRowsPerWave];
+  int wave_vis = 0;
+#pragma unroll
+  for (int i = 0; i < kPrefillRowsPerWave; ++i) {
+    const int r = tile_row0 + wave * kPrefillRowsPerWave + i;
+    rvis[i] = r < req_end ? min(min(p.visible[r], num_columns), p.logits_cols) : 0;
+    wave_vis = max(wave_vis, rvis[i]);
+  }
+  // Key range of the workgroup (all 16 rows).
+  int wg_vis = 0;
+  for (int i = 0; i < kPrefillRows; ++i) {
+    const int r = tile_row0 + i;
+    if (r < req_end) wg_vis = max(wg_vis, min(min(p.visible[r], num_columns), p.logits_cols));
+  }
+  const int t_begin = blockIdx.z * p.key_tiles_per_wg;
+  const int t_end = min(t_begin + p.key_tiles_per_wg, (wg_vis + 31) / 32);
+  if (t_begin >= t_end) return;
+
+  bf16x8 qa[kPrefillRowsPerWave][KS];
+#pragma unroll
+  for (int i = 0; i < kPrefillRowsPerWave; ++i) {
+    const int r = tile_row0 + wave * kPrefillRowsPerWave + i;
+    const bool ok = r < req_end && kk < p.num_heads;
+    const uint16_t* qrow = p.q + (int64_t)(ok ? r : 0) * p.q_row + (int64_t)(ok ? kk : 0) * p.q_head;
+#pragma unroll
+    for (int s = 0; s < KS; ++s) {
+      u32x4 raw = {0u, 0u, 0u, 0u};
+      if (ok) raw = load_u32x4(qrow + 16 * s + 8 * half);
+      qa[i][s] = __builtin_bit_cast(bf16x8, raw);
+    }
+  }
+
+  // Cooperative tile load: thread t copies 16 B chunks of key (t / CH).
+  constexpr int CH = D * 2 / 16;  // 16 B chunks per key row
+  for (int tile = t_begin; tile < t_end; ++tile) {
+    __syncthreads();
+    for (int e = tid; e < 32 * CH; e += 256) {
+      const int key = e / CH, ch = e % CH;
+      const int c = tile * 32 + key;
+      const char* kp = key_ptr(p, trow, c, c < wg_vis);
+      *reinterpret_cast<u32x4*>(s_keys + key * ROW_BYTES + ch * 16) = load_u32x4(kp + ch * 16);
+    }
+    __syncthreads();
+    if (tile * 32 >= wave_vis) continue;
+    bf16x8 kb[KS];
+#pragma unroll
+    for (int s = 0; s < KS; ++s)
+      kb[s] = __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4*>(
+                                             s_keys + kk * ROW_BYTES + (16 * s + 8 * half) * 2));
+    const int c = tile * 32 + kk;
+#pragma unroll
+    for (int i = 0; i < kPrefillRowsPerWave; ++i) {
+      f32x16 acc = {};
+#pragma unroll
+      for (int s = 0; s < KS; ++s)
+        acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(qa[i][s], kb[s], acc, 0, 0, 0);
+      float sum = relu_head_sum(acc);
+      sum += shfl_xor_f(sum, 32);
+      const int r = tile_row0 + wave * kPrefillRowsPerWave + i;
+      if (half == 0 && c < rvis[i])
+        p.logits[(int64_t)(r - p.query_offset) * p.logits_row + c] = sum * p.scale;
+    }
+  }
+}
+
+int check_indexer(const void* q, int num_heads, int head_dim, const void* k_cache,
+                  int cache_page, const int32_t* page_table, const int32_t* visible,
+                  const float* logits, int64_t q_head_stride, int64_t q_row_stride,
+                  int64_t cb, int64_t ct, const char* name) {
+  if (!q || !k_cache || !page_table || !visible || !logits)
+    return fail(QSA_ERR_INVALID, std::string(name) + ": null tensor pointer");
+  if (head_dim != 64 && head_dim != 128)
+    return fail(QSA_ERR_UNSUPPORTED, std::string(name) + ": head_dim must be 64 or 128");
+  if (num_heads <= 0 || num_heads > 64)
+    return fail(QSA_ERR_UNSUPPORTED, std::string(name) + ": num_heads must be in 1..64");
+  if (cache_page <= 0) return fail(QSA_ERR_INVALID, std::string(name) + ": bad cache page size");
+  if (((uintptr_t)q | (uintptr_t)k_cache) & 15u || (q_head_stride | q_row_stride | cb | ct) & 7)
+    return fail(QSA_ERR_INVALID, std::string(name) +
+                                     ": q/k_cache must be 16-byte aligned with strides that are "
+                                     "multiples of 8 elements");
+  return QSA_OK;
+}
+
+}  // namespace
+}  // namespace qsa
+
+using namespace qsa;
+
+extern "C" int qsa_indexer_decode(const void* q, int64_t q_row_stride, int64_t q_head_stride,
+                                  int rows, int num_heads, int head_dim, const void* k_cache,
+                                  int64_t cache_block_stride, int64_t cache_token_stride,
+                                  int num_blocks, int cache_page, const int32_t* page_table,
+                                  int64_t table_row_stride, int table_width,
+                                  const int32_t* visible, int decode_query_len, float* logits,
+                                  int64_t logits_row_stride, int logits_cols, void* stream) {
+  if (rows < 0) return fail(QSA_ERR_INVALID, "qsa_indexer_decode: rows < 0");
+  if (rows == 0 || logits_cols <= 0 || table_width <= 0) return QSA_OK;
+  int st = check_indexer(q, num_heads, head_dim, k_cache, cache_page, page_table, visible, logits,
+                         q_head_stride, q_row_stride, cache_block_stride, cache_token_stride,
+                         "qsa_indexer_decode");
+  if (st != QSA_OK) return st;
+  if (decode_query_len <= 0) return fail(QSA_ERR_INVALID, "qsa_indexer_decode: decode_query_len");
+  IndexerParams p = {};
+  p.q = static_cast<const uint16_t*>(q);
+  p.q_row = q_row_stride;
+  p.q_head = q_head_stride;
+  p.k = static_cast<const char*>(k_cache);
+  p.kb = cache_block_stride * 2;
+  p.kt = cache_token_stride * 2;
+  p.num_blocks = num_blocks;
+  p.cache_page = cache_page;
+  p.page_div = FastDiv::make(cache_page);
+  p.table = page_table;
+  p.table_row = table_row_stride;
+  p.table_width = table_width;
+  p.visible = visible;
+  p.num_heads = num_heads;
+  p.decode_query_len = decode_query_len;
+  p.logits = logits;
+  p.logits_row = logits_row_stride;
+  p.logits_cols = logits_cols;
+  p.scale = (float)(1.0 / __builtin_sqrt((double)head_dim));
+  const int max_tiles = (std::min(logits_cols, table_width * cache_page) + 31) / 32;
+  int programs = (1024 + rows - 1) / rows;
+  programs = std::max(1, std::min(programs, max_tiles));
+  const dim3 grid(programs, rows);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (rows > 65535) return fail(QSA_ERR_UNSUPPORTED, "qsa_indexer_decode: more than 65535 rows");
+  if (head_dim == 128) {
+    if (num_heads <= 32) hipLaunchKernelGGL((indexer_decode_kernel<128, 1>), grid, dim3(64), 0, s, p);
+    else hipLaunchKernelGGL((indexer_decode_kernel<128, 2>), grid, dim3(64), 0, s, p);
+  } else {
+    if (num_heads <= 32) hipLaunchKernelGGL((indexer_decode_kernel<64, 1>), grid, dim3(64), 0, s, p);
+    else hipLaunchKernelGGL((indexer_decode_kernel<64, 2>), grid, dim3(64), 0, s, p);
+  }
+  return check_launch("qsa_indexer_decode launch");
+}
+
+extern "C" int qsa_indexer_prefill(const void* q, int64_t q_row_stride, int64_t q_head_stride,
+                                   int num_heads, int head_dim, const void* k_cache,
+                                   int64_t cache_block_stride, int64_t cache_token_stride,
+                                   int num_blocks, int cache_page, const int32_t* page_table,
+                                   int64_t table_row_stride, int table_width, int num_requests,
+                                   const int32_t* query_start_loc, const int32_t* visible,
+                                   int query_offset, int num_rows, int max_query_len,
+                                   float* logits, int64_t logits_row_stride, int logits_cols,
+                                   void* stream) {
+  if (num_rows < 0 || num_requests < 0) return fail(QSA_ERR_INVALID, "qsa_indexer_prefill: negative shape");
+  if (num_rows == 0 || num_requests == 0 || logits_cols <= 0 || table_width <= 0) return QSA_OK;
+  int st = check_indexer(q, num_heads, head_dim, k_cache, cache_page, page_table, visible, logits,
+                         q_head_stride, q_row_stride, cache_block_stride, cache_token_stride,
+                         "qsa_indexer_prefill");
+  if (st != QSA_OK) return st;
+  if (num_heads > 32)
+    return fail(QSA_ERR_UNSUPPORTED, "qsa_indexer_prefill: more than 32 index heads");
+  if (!query_start_loc) return fail(QSA_ERR_INVALID, "qsa_indexer_prefill: null query_start_loc");
+  IndexerParams p = {};
+  p.q = static_cast<const uint16_t*>(q);
+  p.q_row = q_row_stride;
+  p.q_head = q_head_stride;
+  p.k = static_cast<const char*>(k_cache);
+  p.kb = cache_block_stride * 2;
+  p.kt = cache_token_stride * 2;
+  p.num_blocks = num_blocks;
+  p.cache_page = cache_page;
+  p.page_div = FastDiv::make(cache_page);
+  p.table = page_table;
+  p.table_row = table_row_stride;
+  p.table_width = table_width;
+  p.visible = visible;
+  p.num_heads = num_heads;
+  p.decode_query_len = 1;
+  p.logits = logits;
+  p.logits_row = logits_row_stride;
+  p.logits_cols = logits_cols;
+  p.scale = (float)(1.0 / __builtin_sqrt((double)head_dim));
+  p.query_start_loc = query_start_loc;
+  p.num_requests = num_requests;
+  p.query_offset = query_offset;
+  p.num_rows = num_rows;
+  p.key_tiles_per_wg = 8;
+  const int row_span = std::max(1, std::min(num_rows, max_query_len > 0 ? max_query_len : num_rows));
+  const int row_tiles = (row_span + kPrefillRows - 1) / kPrefillRows;
+  const int max_tiles = (std::min(logits_cols, table_width * cache_page) + 31) / 32;
+  const int key_chunks = (max_tiles + p.key_tiles_per_wg - 1) / p.key_tiles_per_wg;
+  if (row_tiles > 65535 || key_chunks > 65535)
+    return fail(QSA_ERR_UNSUPPORTED, "qsa_indexer_prefill: grid too large");
+  const dim3 grid(num_requests, row_tiles, key_chunks);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (head_dim == 128) hipLaunchKernelGGL((indexer_prefill_kernel<128>), grid, dim3(256), 0, s, p);
+  else hipLaunchKernelGGL((indexer_prefill_kernel<64>), grid, dim3(256), 0, s, p);
+  return check_launch("qsa_indexer_prefill launch");
+}

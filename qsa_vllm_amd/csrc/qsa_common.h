@@ -1,0 +1,66 @@
+// Shared device and host helpers for the gfx950 QSA kernels.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+#include <string>
+
+#include "fastdiv.h"
+
+namespace qsa {
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+// ---------------------------------------------------------------------------
+// Host-side error reporting shared by every entry point (qsa_errors.hip).
+// ---------------------------------------------------------------------------
+void set_error(const std::string& message);
+int fail(int status, const std::string& message);
+int check_launch(const char* what);
+
+// ---------------------------------------------------------------------------
+// Device helpers.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ uint32_t perm_b32(uint32_t hi_src, uint32_t lo_src, uint32_t sel) {
+  // v_perm_b32: byte i of the result is byte sel.byte[i] of the 8 bytes
+  // (hi_src:lo_src), lo_src supplying bytes 0-3.
+  return __builtin_amdgcn_perm(hi_src, lo_src, sel);
+}
+
+__device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
+  const __bf16 a = (__bf16)lo;  // round to nearest even
+  const __bf16 b = (__bf16)hi;
+  return (uint32_t)__builtin_bit_cast(uint16_t, a) |
+         ((uint32_t)__builtin_bit_cast(uint16_t, b) << 16);
+}
+
+__device__ __forceinline__ float bf16_lo(uint32_t pair) {
+  return __builtin_bit_cast(float, pair << 16);
+}
+__device__ __forceinline__ float bf16_hi(uint32_t pair) {
+  return __builtin_bit_cast(float, pair & 0xffff0000u);
+}
+
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+__device__ __forceinline__ float shfl_xor_f(float v, int mask) { return __shfl_xor(v, mask, 64); }
+__device__ __forceinline__ int shfl_xor_i(int v, int mask) { return __shfl_xor(v, mask, 64); }
+
+__device__ __forceinline__ u32x4 load_u32x4(const void* p) {
+  return *reinterpret_cast<const u32x4*>(p);
+}
+__device__ __forceinline__ u32x2 load_u32x2(const void* p) {
+  return *reinterpret_cast<const u32x2*>(p);
+}
+
+}  // namespace qsa
+
+// A block of zeros in device memory (one copy per translation unit). Gathers of
+// invalid slots are redirected here so masked K/V rows read as exact zeros.
+static __device__ __attribute__((aligned(256))) uint32_t g_qsa_zero_rows[256];

@@ -1,0 +1,577 @@
+// Kernel 3: bf16 paged sparse GQA attention over selected KV slots, gfx950.
+//
+// Behaviour follows ops/qsa.py:109-362 and :594-688 of the reference plugin
+// (split-K online softmax in the log2 domain, P rounded to bf16 before P.V,
+// normalised fp32 partials + log2-LSE merge, optional bf16(o)*sigmoid(gate)).
+//
+// Work decomposition. One workgroup = 4 waves handles (row, split, head
+// group). A head group is 16 query-head slots sharing NKV kv heads (GQA group
+// G, NKV*G <= 16). Each wave walks 32-token tiles of the row's index list:
+//
+//   S^T[tok][head] = K_tile (A, 16 tokens x 32 dims) * Q^T (B, 32 dims x 16 heads)
+//       v_mfma_f32_16x16x32_bf16, K read straight from HBM into the A operand
+//       (16 B per lane, 64 B contiguous per token per instruction);
+//       the NKV kv heads accumulate into one S because each lane's Q column
+//       is zero for the kv heads it does not belong to.
+//   O^T[dim][head] += V_tile^T (A, 16 dims x 32 tokens) * P^T (B, 32 tok x 16 heads)
+//       each lane loads an 8 token x DPL dim block of V (one 16 B row load per
+//       token) and transposes it in registers with v_perm_b32; P^T is exactly
+//       the lane's own softmax numerators, so P never leaves registers and the
+//       per-head rescale factor lives in the lane that owns that head.
+//
+// The 4 waves merge their (max, sum, O) through LDS; with one split the
+// workgroup writes bf16 output (and gate), otherwise fp32 partials that
+// qsa_sparse_attention_merge reduces.
+#include "qsa_common.h"
+#include "../../include/qsa_hip.h"
+
+#include <algorithm>
+
+namespace qsa {
+namespace {
+
+constexpr int kWaves = 4;
+constexpr int kThreads = 64 * kWaves;
+constexpr int kTile = 32;
+constexpr float kInitMax = -1.0e20f;  // finite running-max seed (ops/qsa.py:173)
+
+struct AttnParams {
+  const uint16_t* q;
+  int64_t q_row, q_head;  // elements
+  const char* k;
+  const char* v;
+  int64_t kb, kt, kh;  // bytes
+  int64_t vb, vt, vh;  // bytes
+  int num_blocks;
+  int page_size;
+  FastDiv page_div;
+  const int32_t* indices;
+  int64_t idx_row;
+  int width;
+  const int32_t* table;
+  int64_t table_row;
+  int table_width;
+  int num_requests;
+  const int32_t* token_to_req;
+  const int32_t* valid_counts;
+  uint16_t* out;
+  int64_t out_row, out_head;  // elements
+  const uint16_t* gate;
+  int64_t g_row, g_head, g_dim;  // elements
+  float* part_out;
+  float* part_lse;
+  int rows;
+  int num_q_heads;
+  int group;
+  int heads_per_wave;
+  int num_splits;
+  int physical;
+  float scale_log2;
+};
+
+__device__ __forceinline__ float sigmoidf_(float x) { return 1.0f / (1.0f + __expf(-x)); }
+
+// Byte offsets of one token's row (without head offset) in K and V, or -1.
+struct SlotInfo {
+  int64_t koff;
+  int64_t voff;
+  bool valid;
+};
+
+__device__ __forceinline__ SlotInfo resolve_slot(const AttnParams& p, const int32_t* irow,
+                                                 const int32_t* trow, bool req_ok, int col,
+                                                 int n_valid) {
+  SlotInfo s;
+  const int tok = col < n_valid ? irow[col] : -1;
+  bool valid = tok >= 0;
+  int page = 0, off = 0;
+  if (valid) {
+    const int lp = p.page_div.div(tok);
+    off = tok - lp * p.page_size;
+    if (p.physical) {
+      page = lp;
+      valid = page < p.num_blocks;
+    } else {
+      valid = req_ok && lp < p.table_width;
+      page = valid ? trow[lp] : -1;
+      valid = valid && page >= 0 && page < p.num_blocks;
+    }
+  }
+  s.valid = valid;
+  s.koff = valid ? (int64_t)page * p.kb + (int64_t)off * p.kt : 0;
+  s.voff = valid ? (int64_t)page * p.vb + (int64_t)off * p.vt : 0;
+  return s;
+}
+
+template <int D>
+struct VRow;
+template <>
+struct VRow<128> {
+  typedef u32x4 type;
+  static __device__ __forceinline__ type load(const char* ptr) { return load_u32x4(ptr); }
+};
+template <>
+struct VRow<64> {
+  typedef u32x2 type;
+  static __device__ __forceinline__ type load(const char* ptr) { return load_u32x2(ptr); }
+};
+
+template <int D, int NKV>
+__global__ __launch_bounds__(kThreads) void sparse_attn_kernel(const AttnParams p) {
+  constexpr int DPL = D / 16;  // V dims per lane = P.V MFMAs per kv slot
+  constexpr int KS = D / 32;   // K steps of the Q.K MFMA
+  typedef typename VRow<D>::type vrow_t;
+
+  __shared__ float s_m[kWaves][16];
+  __shared__ float s_l[kWaves][16];
+  __shared__ float s_o[kWaves][16][D + 4];
+
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int g = lane >> 4;
+  const int n = lane & 15;
+  const int row = blockIdx.x;
+  const int split = blockIdx.y;
+  const int hg = blockIdx.z;
+
+  const int head0 = hg * p.heads_per_wave;
+  const int kv0 = head0 / p.group;
+  const bool head_ok = n < p.heads_per_wave;
+  const int qh = head0 + n;
+  const int vslot = head_ok ? qh / p.group - kv0 : -1;
+
+  // Q^T as the B operand: lane holds Q[qh][32 s + 8 g .. +7], zero for the
+  // kv slots this head does not attend with.
+  bf16x8 bq[NKV][KS];
+  {
+    const uint16_t* qrow = p.q + (int64_t)row * p.q_row + (int64_t)(head_ok ? qh : 0) * p.q_head;
+#pragma unroll
+    for (int s = 0; s < KS; ++s) {
+      u32x4 raw = {0u, 0u, 0u, 0u};
+      if (head_ok) raw = load_u32x4(qrow + 32 * s + 8 * g);
+#pragma unroll
+      for (int v = 0; v < NKV; ++v) {
+        const u32x4 sel = (vslot == v) ? raw : u32x4{0u, 0u, 0u, 0u};
+        bq[v][s] = __builtin_bit_cast(bf16x8, sel);
+      }
+    }
+  }
+
+  int n_valid = p.width;
+  if (p.valid_counts) n_valid = max(0, min(p.valid_counts[row], p.width));
+  const int req = p.token_to_req[row];
+  const bool req_ok = req >= 0 && req < p.num_requests;
+  const int32_t* trow = p.table + (int64_t)(req_ok ? req : 0) * p.table_row;
+  const int32_t* irow = p.indices + (int64_t)row * p.idx_row;
+  const int tiles = (n_valid + kTile - 1) / kTile;
+  const int t_begin = (int)((int64_t)split * tiles / p.num_splits);
+  const int t_end = (int)((int64_t)(split + 1) * tiles / p.num_splits);
+
+  const char* zero = reinterpret_cast<const char*>(g_qsa_zero_rows);
+  int64_t khead[NKV], vhead[NKV];
+#pragma unroll
+  for (int v = 0; v < NKV; ++v) {
+    khead[v] = (int64_t)(kv0 + v) * p.kh;
+    vhead[v] = (int64_t)(kv0 + v) * p.vh;
+  }
+
+  float m_run = kInitMax;
+  float l_run = 0.0f;
+  f32x4 oacc[DPL];
+#pragma unroll
+  for (int j = 0; j < DPL; ++j) oacc[j] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  for (int tile = t_begin + wave; tile < t_end; tile += kWaves) {
+    const int c0 = tile * kTile;
+
+    // K rows: tokens c0 + 16 u + n (A-operand row = token).
+    u32x4 kr[NKV][2][KS];
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      const SlotInfo si = resolve_slot(p, irow, trow, req_ok, c0 + 16 * u + n, n_valid);
+#pragma unroll
+      for (int v = 0; v < NKV; ++v) {
+        const char* base = si.valid ? p.k + si.koff + khead[v] : zero;
+#pragma unroll
+        for (int s = 0; s < KS; ++s) kr[v][u][s] = load_u32x4(base + (32 * s + 8 * g) * 2);
+      }
+    }
+    // V rows: tokens tok(i) = 16 (i / 4) + 4 g + i % 4, dims DPL n .. +DPL-1.
+    vrow_t vr[NKV][8];
+    uint32_t vmask = 0;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const SlotInfo si =
+          resolve_slot(p, irow, trow, req_ok, c0 + 16 * (i >> 2) + 4 * g + (i & 3), n_valid);
+      vmask |= si.valid ? (1u << i) : 0u;
+#pragma unroll
+      for (int v = 0; v < NKV; ++v) {
+        const char* base = si.valid ? p.v + si.voff + vhead[v] : zero;
+        vr[v][i] = VRow<D>::load(base + DPL * n * 2);
+      }
+    }
+
+    // S^T for the two 16-token halves; lane holds S[tok 16u + 4g + r][head n].
+    f32x4 sacc[2];
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int v = 0; v < NKV; ++v)
+#pragma unroll
+        for (int s = 0; s < KS; ++s)
+          acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+              __builtin_bit_cast(bf16x8, kr[v][u][s]), bq[v][s], acc, 0, 0, 0);
+      sacc[u] = acc;
+    }
+
+    // Online softmax (log2 domain) for head n over this tile's 32 tokens.
+    float sc[8];
+    float tmax = -INFINITY;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const float x = sacc[i >> 2][i & 3] * p.scale_log2;
+      sc[i] = (vmask >> i) & 1u ? x : -INFINITY;
+      tmax = fmaxf(tmax, sc[i]);
+    }
+    tmax = fmaxf(tmax, shfl_xor_f(tmax, 16));
+    tmax = fmaxf(tmax, shfl_xor_f(tmax, 32));
+    const float m_new = fmaxf(m_run, tmax);
+    const float alpha = fast_exp2(m_run - m_new);
+    float lsum = 0.0f;
+    float pv[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      pv[i] = fast_exp2(sc[i] - m_new);
+      lsum += pv[i];
+    }
+    l_run = l_run * alpha + lsum;
+    m_run = m_new;
+#pragma unroll
+    for (int j = 0; j < DPL; ++j) oacc[j] *= alpha;
+
+    u32x4 praw;
+    praw[0] = pack_bf16x2(pv[0], pv[1]);
+    praw[1] = pack_bf16x2(pv[2], pv[3]);
+    praw[2] = pack_bf16x2(pv[4], pv[5]);
+    praw[3] = pack_bf16x2(pv[6], pv[7]);
+
+#pragma unroll
+    for (int v = 0; v < NKV; ++v) {
+      const u32x4 pm = (vslot == v) ? praw : u32x4{0u, 0u, 0u, 0u};
+      const bf16x8 bp = __builtin_bit_cast(bf16x8, pm);
+#pragma unroll
+      for (int j = 0; j < DPL; ++j) {
+        const uint32_t sel = (j & 1) ? 0x07060302u : 0x05040100u;
+        u32x4 a;
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+          a[q] = perm_b32(vr[v][2 * q + 1][j >> 1], vr[v][2 * q][j >> 1], sel);
+        oacc[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a), bp,
+                                                          oacc[j], 0, 0, 0);
+      }
+    }
+  }
+
+  // Row sums are lane-partial (each lane summed its own tokens).
+  l_run += shfl_xor_f(l_run, 16);
+  l_run += shfl_xor_f(l_run, 32);
+
+  // oacc[j][r] = O[head n][DPL * (4 g + r) + j].
+#pragma unroll
+  for (int j = 0; j < DPL; ++j)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) s_o[wave][n][DPL * (4 * g + r) + j] = oacc[j][r];
+  if (g == 0) {
+    s_m[wave][n] = m_run;
+    s_l[wave][n] = l_run;
+  }
+  __syncthreads();
+
+  // Thread t finalises head t / 16, dims [(t % 16) * DPL, +DPL).
+  const int h = threadIdx.x >> 4;
+  const int d0 = (threadIdx.x & 15) * DPL;
+  if (h >= p.heads_per_wave) return;
+  float mw[kWaves];
+  float mx = kInitMax;
+#pragma unroll
+  for (int w = 0; w < kWaves; ++w) {
+    mw[w] = s_m[w][h];
+    mx = fmaxf(mx, mw[w]);
+  }
+  float lsum = 0.0f;
+  float o[DPL];
+#pragma unroll
+  for (int d = 0; d < DPL; ++d) o[d] = 0.0f;
+#pragma unroll
+  for (int w = 0; w < kWaves; ++w) {
+    const float wt = fast_exp2(mw[w] - mx);
+    lsum += wt * s_l[w][h];
+#pragma unroll
+    for (int d = 0; d < DPL; ++d) o[d] += wt * s_o[w][h][d0 + d];
+  }
+  const bool has = lsum > 0.0f;
+  const float inv = has ? 1.0f / fmaxf(lsum, 1.0e-20f) : 0.0f;
+  const int head = head0 + h;
+
+  if (p.num_splits == 1) {
+    uint16_t* optr = p.out + (int64_t)row * p.out_row + (int64_t)head * p.out_head + d0;
+    const uint16_t* gptr =
+        p.gate ? p.gate + (int64_t)row * p.g_row + (int64_t)head * p.g_head : nullptr;
+#pragma unroll
+    for (int d = 0; d < DPL; d += 2) {
+      float a = o[d] * inv, b = o[d + 1] * inv;
+      if (gptr) {
+        // bf16(o) * sigmoid(gate) (ops/qsa.py:257-269).
+        const uint32_t ob = pack_bf16x2(a, b);
+        const float ga = bf16_lo((uint32_t)gptr[(int64_t)(d0 + d) * p.g_dim]);
+        const float gb = bf16_lo((uint32_t)gptr[(int64_t)(d0 + d + 1) * p.g_dim]);
+        a = bf16_lo(ob) * sigmoidf_(ga);
+        b = bf16_hi(ob) * sigmoidf_(gb);
+      }
+      *reinterpret_cast<uint32_t*>(optr + d) = pack_bf16x2(a, b);
+    }
+  } else {
+    const int64_t prow = ((int64_t)split * p.rows + row) * p.num_q_heads + head;
+    float* po = p.part_out + prow * D + d0;
+#pragma unroll
+    for (int d = 0; d < DPL; ++d) po[d] = o[d] * inv;
+    if ((threadIdx.x & 15) == 0)
+      p.part_lse[prow] = has ? mx + __log2f(fmaxf(lsum, 1.0e-20f)) : -INFINITY;
+  }
+}
+
+// LSE merge of split partials (ops/qsa.py:306-362): one workgroup per row,
+// each thread owns 4 consecutive dims of one head.
+__global__ __launch_bounds__(256) void merge_kernel(const float* __restrict__ part_out,
+                                                    const float* __restrict__ part_lse,
+                                                    int num_splits, int rows, int num_q_heads,
+                                                    int head_dim, uint16_t* out, int64_t out_row,
+                                                    int64_t out_head, const uint16_t* gate,
+                                                    int64_t g_row, int64_t g_head, int64_t g_dim) {
+  const int row = blockIdx.x;
+  const int chunks = head_dim / 4;
+  for (int item = threadIdx.x; item < num_q_heads * chunks; item += blockDim.x) {
+    const int head = item / chunks;
+    const int d0 = (item % chunks) * 4;
+    float lmax = -INFINITY;
+    for (int s = 0; s < num_splits; ++s)
+      lmax = fmaxf(lmax, part_lse[((int64_t)s * rows + row) * num_q_heads + head]);
+    float acc[4] = {0.f, 0.f, 0.f, 0.f};
+    float den = 0.0f;
+    if (lmax > -INFINITY) {
+      for (int s = 0; s < num_splits; ++s) {
+        const int64_t prow = ((int64_t)s * rows + row) * num_q_heads + head;
+        const float w = fast_exp2(part_lse[prow] - lmax);
+        den += w;
+        const float4 v = *reinterpret_cast<const float4*>(part_out + prow * head_dim + d0);
+        acc[0] += w * v.x;
+        acc[1] += w * v.y;
+        acc[2] += w * v.z;
+        acc[3] += w * v.w;
+      }
+    }
+    float o[4];
+    for (int d = 0; d < 4; ++d) o[d] = den > 0.0f ? acc[d] / den : 0.0f;
+    uint16_t* optr = out + (int64_t)row * out_row + (int64_t)head * out_head + d0;
+    if (gate) {
+      const uint16_t* gptr = gate + (int64_t)row * g_row + (int64_t)head * g_head;
+      for (int d = 0; d < 4; d += 2) {
+        const uint32_t ob = pack_bf16x2(o[d], o[d + 1]);
+        o[d] = bf16_lo(ob) * sigmoidf_(bf16_lo((uint32_t)gptr[(int64_t)(d0 + d) * g_dim]));
+        o[d + 1] = bf16_hi(ob) * sigmoidf_(bf16_lo((uint32_t)gptr[(int64_t)(d0 + d + 1) * g_dim]));
+      }
+    }
+    *reinterpret_cast<uint32_t*>(optr) = pack_bf16x2(o[0], o[1]);
+    *reinterpret_cast<uint32_t*>(optr + 2) = pack_bf16x2(o[2], o[3]);
+  }
+}
+
+struct HeadPlan {
+  int nkv;             // kv heads per head group
+  int heads_per_wave;  // query-head slots used (<= 16)
+  int groups;          // head groups per row
+};
+
+bool plan_heads(int num_q_heads, int num_kv_heads, HeadPlan* plan) {
+  if (num_kv_heads <= 0 || num_q_heads <= 0 || num_q_heads % num_kv_heads) return false;
+  const int group = num_q_heads / num_kv_heads;
+  if (group > 16) {
+    if (group % 16) return false;
+    plan->nkv = 1;
+    plan->heads_per_wave = 16;
+  } else {
+    int nkv = 1;
+    for (int cand : {4, 2, 1}) {
+      if (cand * group <= 16 && num_kv_heads % cand == 0) {
+        nkv = cand;
+        break;
+      }
+    }
+    plan->nkv = nkv;
+    plan->heads_per_wave = nkv * group;
+  }
+  plan->groups = num_q_heads / plan->heads_per_wave;
+  return true;
+}
+
+template <int D, int NKV>
+hipError_t launch_attn(const AttnParams& p, dim3 grid, hipStream_t stream) {
+  hipLaunchKernelGGL((sparse_attn_kernel<D, NKV>), grid, dim3(kThreads), 0, stream, p);
+  return hipGetLastError();
+}
+
+}  // namespace
+}  // namespace qsa
+
+using namespace qsa;
+
+extern "C" int qsa_sparse_attention_splits(int rows, int num_q_heads, int num_kv_heads,
+                                           int head_dim, int width, int use_decode_kernel) {
+  (void)head_dim;
+  HeadPlan plan;
+  if (rows <= 0 || !plan_heads(num_q_heads, num_kv_heads, &plan)) return 1;
+  const int tiles = (width + kTile - 1) / kTile;
+  const int base = rows * plan.groups;
+  const int target = use_decode_kernel ? 512 : 256;  // workgroups in flight on 256 CUs
+  int splits = 1;
+  while (splits * 2 * base <= target && splits * 2 <= std::max(1, tiles / 2) && splits < 64)
+    splits *= 2;
+  return splits;
+}
+
+extern "C" size_t qsa_sparse_attention_workspace_bytes(int rows, int num_q_heads, int head_dim,
+                                                       int num_splits) {
+  if (num_splits <= 1 || rows <= 0) return 0;
+  const size_t n = (size_t)num_splits * rows * num_q_heads;
+  return n * head_dim * sizeof(float) + n * sizeof(float);
+}
+
+extern "C" int qsa_sparse_attention(
+    const void* q, int64_t q_row_stride, int64_t q_head_stride, int rows, int num_q_heads,
+    int head_dim, const void* k_cache, int64_t k_block_stride, int64_t k_token_stride,
+    int64_t k_head_stride, const void* v_cache, int64_t v_block_stride, int64_t v_token_stride,
+    int64_t v_head_stride, int num_blocks, int page_size, int num_kv_heads,
+    const int32_t* indices, int64_t indices_row_stride, int width, const int32_t* block_table,
+    int64_t table_row_stride, int table_width, int num_requests, const int32_t* token_to_req,
+    const int32_t* valid_counts, void* out, int64_t out_row_stride, int64_t out_head_stride,
+    const void* gate, int64_t gate_row_stride, int64_t gate_head_stride, int64_t gate_dim_stride,
+    int indices_are_physical, int num_splits, void* workspace, size_t workspace_bytes,
+    void* stream) {
+  if (rows < 0) return fail(QSA_ERR_INVALID, "qsa_sparse_attention: rows < 0");
+  if (rows == 0) return QSA_OK;
+  if (head_dim != 64 && head_dim != 128)
+    return fail(QSA_ERR_UNSUPPORTED, "qsa_sparse_attention: head_dim must be 64 or 128");
+  HeadPlan plan;
+  if (!plan_heads(num_q_heads, num_kv_heads, &plan))
+    return fail(QSA_ERR_UNSUPPORTED,
+                "qsa_sparse_attention: query heads must be a multiple of kv heads with a GQA "
+                "group that divides 16 or is a multiple of 16");
+  if (!q || !k_cache || !v_cache || !indices || !token_to_req || !out)
+    return fail(QSA_ERR_INVALID, "qsa_sparse_attention: null tensor pointer");
+  if (!indices_are_physical && (!block_table || table_width <= 0 || num_requests <= 0))
+    return fail(QSA_ERR_INVALID, "qsa_sparse_attention: logical indices need a block table");
+  if (page_size <= 0 || num_blocks < 0 || width < 0)
+    return fail(QSA_ERR_INVALID, "qsa_sparse_attention: bad page_size/num_blocks/width");
+  if (num_splits < 1 || num_splits > 1024)
+    return fail(QSA_ERR_INVALID, "qsa_sparse_attention: num_splits out of range");
+  const size_t need = qsa_sparse_attention_workspace_bytes(rows, num_q_heads, head_dim, num_splits);
+  if (need && (!workspace || workspace_bytes < need))
+    return fail(QSA_ERR_WORKSPACE, "qsa_sparse_attention: workspace too small for split partials");
+  if (((uintptr_t)q | (uintptr_t)k_cache | (uintptr_t)v_cache) & 15u ||
+      (q_row_stride | q_head_stride | k_block_stride | k_token_stride | k_head_stride |
+       v_block_stride | v_token_stride | v_head_stride) & 7)
+    return fail(QSA_ERR_INVALID,
+                "qsa_sparse_attention: q/k/v must be 16-byte aligned with strides that are "
+                "multiples of 8 elements");
+  if (((uintptr_t)out & 3u) || (out_row_stride | out_head_stride) & 1)
+    return fail(QSA_ERR_INVALID, "qsa_sparse_attention: out must be 4-byte aligned with even strides");
+
+  AttnParams p;
+  p.q = static_cast<const uint16_t*>(q);
+  p.q_row = q_row_stride;
+  p.q_head = q_head_stride;
+  p.k = static_cast<const char*>(k_cache);
+  p.v = static_cast<const char*>(v_cache);
+  p.kb = k_block_stride * 2;
+  p.kt = k_token_stride * 2;
+  p.kh = k_head_stride * 2;
+  p.vb = v_block_stride * 2;
+  p.vt = v_token_stride * 2;
+  p.vh = v_head_stride * 2;
+  p.num_blocks = num_blocks;
+  p.page_size = page_size;
+  p.page_div = FastDiv::make(page_size);
+  p.indices = indices;
+  p.idx_row = indices_row_stride;
+  p.width = width;
+  p.table = block_table ? block_table : indices;
+  p.table_row = table_row_stride;
+  p.table_width = table_width;
+  p.num_requests = num_requests;
+  p.token_to_req = token_to_req;
+  p.valid_counts = valid_counts;
+  p.out = static_cast<uint16_t*>(out);
+  p.out_row = out_row_stride;
+  p.out_head = out_head_stride;
+  p.gate = static_cast<const uint16_t*>(gate);
+  p.g_row = gate_row_stride;
+  p.g_head = gate_head_stride;
+  p.g_dim = gate_dim_stride;
+  const size_t n_part = (size_t)num_splits * rows * num_q_heads;
+  p.part_out = need ? static_cast<float*>(workspace) : nullptr;
+  p.part_lse = need ? static_cast<float*>(workspace) + n_part * head_dim : nullptr;
+  p.rows = rows;
+  p.num_q_heads = num_q_heads;
+  p.group = num_q_heads / num_kv_heads;
+  p.heads_per_wave = plan.heads_per_wave;
+  p.num_splits = num_splits;
+  p.physical = indices_are_physical ? 1 : 0;
+  p.scale_log2 = (float)(1.0 / __builtin_sqrt((double)head_dim) * 1.4426950408889634);
+
+  if (plan.groups > 65535 || num_splits > 65535)
+    return fail(QSA_ERR_UNSUPPORTED, "qsa_sparse_attention: grid too large");
+  const dim3 grid(rows, num_splits, plan.groups);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  hipError_t err = hipSuccess;
+  if (head_dim == 128) {
+    if (plan.nkv == 1) err = launch_attn<128, 1>(p, grid, s);
+    else if (plan.nkv == 2) err = launch_attn<128, 2>(p, grid, s);
+    else err = launch_attn<128, 4>(p, grid, s);
+  } else {
+    if (plan.nkv == 1) err = launch_attn<64, 1>(p, grid, s);
+    else if (plan.nkv == 2) err = launch_attn<64, 2>(p, grid, s);
+    else err = launch_attn<64, 4>(p, grid, s);
+  }
+  if (err != hipSuccess)
+    return fail(QSA_ERR_HIP, std::string("qsa_sparse_attention launch: ") + hipGetErrorString(err));
+  if (num_splits > 1) {
+    hipLaunchKernelGGL(merge_kernel, dim3(rows), dim3(256), 0, s, p.part_out, p.part_lse,
+                       num_splits, rows, num_q_heads, head_dim, p.out, out_row_stride,
+                       out_head_stride, p.gate, gate_row_stride, gate_head_stride,
+                       gate_dim_stride);
+    return check_launch("qsa_sparse_attention merge launch");
+  }
+  return QSA_OK;
+}
+
+extern "C" int qsa_sparse_attention_merge(const float* partial_out, const float* partial_lse,
+                                          int num_splits, int rows, int num_q_heads, int head_dim,
+                                          void* out, int64_t out_row_stride,
+                                          int64_t out_head_stride, const void* gate,
+                                          int64_t gate_row_stride, int64_t gate_head_stride,
+                                          int64_t gate_dim_stride, void* stream) {
+  if (rows < 0 || num_splits < 1 || num_q_heads <= 0 || head_dim <= 0 || head_dim % 4)
+    return fail(QSA_ERR_INVALID, "qsa_sparse_attention_merge: bad shape");
+  if (rows == 0) return QSA_OK;
+  if (!partial_out || !partial_lse || !out)
+    return fail(QSA_ERR_INVALID, "qsa_sparse_attention_merge: null tensor pointer");
+  if (((uintptr_t)partial_out & 15u) || ((uintptr_t)out & 3u) || (out_row_stride | out_head_stride) & 1)
+    return fail(QSA_ERR_INVALID, "qsa_sparse_attention_merge: misaligned partials or output");
+  hipLaunchKernelGGL(merge_kernel, dim3(rows), dim3(256), 0, static_cast<hipStream_t>(stream),
+                     partial_out, partial_lse, num_splits, rows, num_q_heads, head_dim,
+                     static_cast<uint16_t*>(out), out_row_stride, out_head_stride,
+                     static_cast<const uint16_t*>(gate), gate_row_stride, gate_head_stride,
+                     gate_dim_stride);
+  return check_launch("qsa_sparse_attention_merge launch");
+}

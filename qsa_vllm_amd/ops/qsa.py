@@ -1,0 +1,95 @@
+"""BF16 paged sparse GQA attention on gfx950.
+
+Same entry points and signatures as the reference ``yulan_qsa_vllm/ops/qsa.py``:
+``qsa_sparse_paged_attention`` (:594-688) and ``qsa_select_paged_tokens``
+(:753-782). The split-K kernel and the LSE merge run in ``libqsa_hip.so``
+behind ``torch.ops.yulan_qsa_kernels.sparse_attention``.
+
+``decode_config`` keeps the reference's ``(block_n, target_splits, warps)``
+tuple; only ``target_splits`` is meaningful here (the HIP kernel walks fixed
+32-token tiles with 4 waves), and it caps the split count exactly as the
+reference caps its own (``num_splits = min(pow2floor(tiles), target)``).
+"""
+
+from __future__ import annotations
+
+import torch
+
+from .. import _lib
+from .topk import _torch_ops  # noqa: F401  (registers torch.ops.yulan_qsa_kernels)
+
+_TILE = 32
+
+
+def _pow2floor(x: int) -> int:
+    return 1 << (max(1, x).bit_length() - 1)
+
+
+def choose_num_splits(q, k_cache, logical_indices, use_decode_kernel, decode_config=None):
+    """Split count for a call: the library heuristic, or the reference-style cap."""
+    rows, hq, dim = q.shape
+    width = logical_indices.shape[1]
+    if decode_config is not None:
+        target = int(decode_config[1])
+        return max(1, min(_pow2floor(-(-width // _TILE)), target))
+    return _lib.load().qsa_sparse_attention_splits(
+        rows, hq, k_cache.shape[2], dim, width, int(bool(use_decode_kernel)))
+
+
+def qsa_sparse_paged_attention(
+    q: torch.Tensor,
+    k_cache: torch.Tensor,
+    v_cache: torch.Tensor,
+    logical_indices: torch.Tensor,
+    block_table: torch.Tensor,
+    token_to_req: torch.Tensor,
+    out: torch.Tensor | None = None,
+    *,
+    output_gate: torch.Tensor | None = None,
+    use_decode_kernel: bool = False,
+    indices_are_physical: bool = False,
+    valid_counts: torch.Tensor | None = None,
+    decode_config: tuple[int, int, int] | None = None,
+) -> torch.Tensor:
+    """BF16 paged GQA over the selected slots (physical decode or logical prefill)."""
+    if out is None:
+        out = torch.empty_like(q)
+    if not q.shape[0]:
+        return out
+    num_splits = choose_num_splits(q, k_cache, logical_indices, use_decode_kernel, decode_config)
+    torch.ops.yulan_qsa_kernels.sparse_attention(
+        q, k_cache, v_cache, logical_indices, block_table, token_to_req, out,
+        output_gate, valid_counts, bool(indices_are_physical), int(num_splits))
+    return out
+
+
+def qsa_select_paged_tokens(
+    q: torch.Tensor,
+    k_cache: torch.Tensor,
+    page_table: torch.Tensor,
+    token_to_req: torch.Tensor,
+    query_positions: torch.Tensor,
+    sequence_lengths: torch.Tensor,
+    token_topk: int,
+    compress_ratio: int,
+    out: torch.Tensor | None = None,
+    *,
+    query_start_loc: torch.Tensor,
+    max_query_len: int,
+    max_seq_len: int,
+    num_decodes: int = 0,
+    num_decode_tokens: int = 0,
+    decode_query_len: int = 1,
+    visible_blocks: torch.Tensor | None = None,
+) -> torch.Tensor:
+    """Select with the fused HIP top-k and the HIP prefill/decode scoring."""
+    from .indexer import select_paged_tokens
+
+    return select_paged_tokens(
+        q, k_cache, page_table, token_to_req, query_positions, sequence_lengths,
+        token_topk, compress_ratio, out,
+        query_start_loc=query_start_loc, max_query_len=max_query_len,
+        max_seq_len=max_seq_len, num_decodes=num_decodes,
+        num_decode_tokens=num_decode_tokens, decode_query_len=decode_query_len,
+        visible_blocks=visible_blocks,
+    )

@@ -1,0 +1,253 @@
+"""Seeded synthetic QSA workloads: paged caches, block tables and row metadata.
+
+Builds the tensors the QSA path consumes in serving, in the layouts the
+reference plugin uses:
+
+* main KV cache: one bf16 allocation whose per-page rows hold K|V interleaved
+  per (token, kv head) (``backend.py:148-153`` splits the last dim into K and
+  V views ``[blocks, page, kv_heads, head_dim]``); ``token_major`` stores
+  ``[blocks, page, kv_heads, 2*D]``, ``head_major`` ``[blocks, kv_heads, page, 2*D]``;
+* compressed index-key cache ``[blocks, cache_page, 1, D_idx]`` with its own
+  page table (one key per ``compress_ratio`` tokens, complete blocks only);
+* block tables drawn from a seeded random permutation of the page pool,
+  ``-1`` past each sequence's last page;
+* decode rows: position = seq_len - 1, visible = seq_len // compress_ratio;
+  chunked prefill rows: positions prefix .. prefix + chunk - 1.
+
+Activations are N(0, 1) * ``act_scale`` rounded to bf16. Everything is
+generated on ``device`` from one ``torch.Generator`` seed.
+"""
+
+from __future__ import annotations
+
+import math
+from dataclasses import dataclass, field, replace
+
+import torch
+
+
+@dataclass(frozen=True)
+class QSAShape:
+    name: str
+    batch: int
+    num_q_heads: int
+    num_kv_heads: int
+    head_dim: int
+    page_size: int
+    compress_ratio: int
+    index_heads: int
+    index_dim: int
+    token_topk: int
+    seq_len_min: int
+    seq_len_max: int
+    seq_len_dist: str = "uniform"      # "uniform", "fixed" or "lognormal"
+    lognormal_median: float = 65536.0
+    lognormal_sigma: float = 0.5
+    index_cache_page: int = 16
+    pool_pages: int = 0                # 0: exactly the pages the batch needs
+    act_scale: float = 1.0
+    gate: bool = False
+    kv_layout: str = "token_major"
+    chunk: int = 0                     # > 0: chunked prefill of `chunk` new tokens per sequence
+    prefix: int = 0
+    seed: int = 0
+
+    @property
+    def width(self) -> int:
+        return self.token_topk + self.compress_ratio - 1
+
+
+# Shapes named in the benchmark plan (one GPU's TP2 share of the serving model).
+SHAPES = {
+    # Eager CPU decode step: batch 4, GQA 8:1, 4096 tokens, pages from a 2048-page pool.
+    "cpu_decode_4k": QSAShape(
+        "cpu_decode_4k", batch=4, num_q_heads=8, num_kv_heads=1, head_dim=128, page_size=16,
+        compress_ratio=16, index_heads=8, index_dim=64, token_topk=1024,
+        seq_len_min=4096, seq_len_max=4096, seq_len_dist="fixed", pool_pages=2048,
+        act_scale=0.5, seed=1),
+    # Decode at 8k-32k context, batch 64, 16 q / 2 kv heads, top-k 2048 tokens.
+    "decode_32k": QSAShape(
+        "decode_32k", batch=64, num_q_heads=16, num_kv_heads=2, head_dim=128, page_size=16,
+        compress_ratio=16, index_heads=32, index_dim=128, token_topk=2048,
+        seq_len_min=8192, seq_len_max=32768, seed=2),
+    # Chunked prefill: 4 sequences x 8192 new tokens on a 16384-token prefix.
+    "prefill_8k_on_16k": QSAShape(
+        "prefill_8k_on_16k", batch=4, num_q_heads=16, num_kv_heads=2, head_dim=128,
+        page_size=16, compress_ratio=16, index_heads=32, index_dim=128, token_topk=2048,
+        seq_len_min=24576, seq_len_max=24576, seq_len_dist="fixed", chunk=8192,
+        prefix=16384, seed=3),
+    # Long-context skewed decode: batch 8, lognormal(median 64k, sigma 0.5) in [16k, 128k].
+    "decode_long_skew": QSAShape(
+        "decode_long_skew", batch=8, num_q_heads=16, num_kv_heads=2, head_dim=128,
+        page_size=16, compress_ratio=16, index_heads=32, index_dim=128, token_topk=2048,
+        seq_len_min=16384, seq_len_max=131072, seq_len_dist="lognormal", seed=4),
+}
+
+
+@dataclass
+class QSAWorkload:
+    shape: QSAShape
+    device: torch.device
+    seq_lens: torch.Tensor            # [requests] int32
+    positions: torch.Tensor           # [rows] int64
+    token_to_req: torch.Tensor        # [rows] int32
+    query_start_loc: torch.Tensor     # [requests + 1] int32
+    visible: torch.Tensor             # [rows] int32
+    kv_cache: torch.Tensor            # physical allocation
+    k_cache: torch.Tensor             # [blocks, page, kv_heads, D] view
+    v_cache: torch.Tensor             # [blocks, page, kv_heads, D] view
+    block_table: torch.Tensor         # [requests, pages] int32
+    index_cache: torch.Tensor         # [blocks, cache_page, 1, D_idx]
+    index_table: torch.Tensor         # [requests, pages] int32
+    q: torch.Tensor                   # [rows, Hq, D]
+    q_index: torch.Tensor             # [rows, H_idx, D_idx]
+    gate: torch.Tensor | None = None
+    max_seq_len: int = 0
+    max_query_len: int = 1
+    extra: dict = field(default_factory=dict)
+
+    @property
+    def rows(self) -> int:
+        return self.q.shape[0]
+
+    @property
+    def is_decode(self) -> bool:
+        return self.shape.chunk == 0
+
+
+def _seq_lens(shape: QSAShape, gen: torch.Generator) -> torch.Tensor:
+    b = shape.batch
+    if shape.seq_len_dist == "fixed":
+        return torch.full((b,), shape.seq_len_min, dtype=torch.int64)
+    if shape.seq_len_dist == "uniform":
+        return torch.randint(shape.seq_len_min, shape.seq_len_max + 1, (b,), generator=gen)
+    if shape.seq_len_dist == "lognormal":
+        z = torch.randn(b, generator=gen, dtype=torch.float64)
+        v = torch.exp(math.log(shape.lognormal_median) + shape.lognormal_sigma * z)
+        return v.round().clamp(shape.seq_len_min, shape.seq_len_max).to(torch.int64)
+    raise ValueError(f"unknown seq_len_dist {shape.seq_len_dist}")
+
+
+def _paged_table(lengths: torch.Tensor, page: int, pool: int, gen: torch.Generator):
+    """Permuted page assignment: returns (table [B, max_pages] int32, num_blocks)."""
+    pages = [(int(n) + page - 1) // page for n in lengths]
+    need = sum(pages)
+    num_blocks = max(need, pool, 1)
+    perm = torch.randperm(num_blocks, generator=gen)
+    width = max(max(pages, default=1), 1)
+    table = torch.full((len(pages), width), -1, dtype=torch.int32)
+    at = 0
+    for i, n in enumerate(pages):
+        table[i, :n] = perm[at:at + n].to(torch.int32)
+        at += n
+    return table, num_blocks
+
+
+def _randn_bf16(shape, gen, device, scale):
+    # Chunked so large caches never hold a full fp32 copy.
+    out = torch.empty(shape, dtype=torch.bfloat16, device=device)
+    flat = out.view(-1)
+    step = 1 << 26
+    for i in range(0, flat.numel(), step):
+        n = min(step, flat.numel() - i)
+        flat[i:i + n] = (torch.randn(n, generator=gen, device=device) * scale).to(torch.bfloat16)
+    return out
+
+
+def make_workload(shape: QSAShape | str, device="cpu", **overrides) -> QSAWorkload:
+    """Generate a seeded workload for ``shape`` (a QSAShape or a SHAPES key)."""
+    if isinstance(shape, str):
+        shape = SHAPES[shape]
+    if overrides:
+        shape = replace(shape, **overrides)
+    device = torch.device(device)
+    cpu_gen = torch.Generator().manual_seed(shape.seed)
+    dev_gen = torch.Generator(device=device).manual_seed(shape.seed + 1000)
+
+    seq_lens = _seq_lens(shape, cpu_gen)
+    b = shape.batch
+    if shape.chunk:
+        n_new = shape.chunk
+        positions = torch.cat([torch.arange(int(s) - n_new, int(s)) for s in seq_lens])
+        token_to_req = torch.arange(b, dtype=torch.int32).repeat_interleave(n_new)
+        query_start_loc = torch.arange(0, (b + 1) * n_new, n_new, dtype=torch.int32)
+        max_query_len = n_new
+    else:
+        positions = seq_lens - 1
+        token_to_req = torch.arange(b, dtype=torch.int32)
+        query_start_loc = torch.arange(b + 1, dtype=torch.int32)
+        max_query_len = 1
+    rows = positions.numel()
+    r = shape.compress_ratio
+    visible = torch.minimum((positions + 1) // r, seq_lens[token_to_req.long()] // r).to(torch.int32)
+
+    block_table, num_blocks = _paged_table(seq_lens, shape.page_size, shape.pool_pages, cpu_gen)
+    index_keys = seq_lens // r
+    index_table, index_blocks = _paged_table(index_keys, shape.index_cache_page, 0, cpu_gen)
+
+    d, hkv = shape.head_dim, shape.num_kv_heads
+    if shape.kv_layout == "token_major":
+        kv = _randn_bf16((num_blocks, shape.page_size, hkv, 2 * d), dev_gen, device, shape.act_scale)
+        k_cache, v_cache = kv[..., :d], kv[..., d:]
+    elif shape.kv_layout == "head_major":
+        kv = _randn_bf16((num_blocks, hkv, shape.page_size, 2 * d), dev_gen, device, shape.act_scale)
+        k_cache, v_cache = kv.transpose(1, 2).split(d, dim=-1)
+    else:
+        raise ValueError(f"unknown kv_layout {shape.kv_layout}")
+    index_cache = _randn_bf16((index_blocks, shape.index_cache_page, 1, shape.index_dim),
+                              dev_gen, device, shape.act_scale)
+    q = _randn_bf16((rows, shape.num_q_heads, d), dev_gen, device, shape.act_scale)
+    q_index = _randn_bf16((rows, shape.index_heads, shape.index_dim), dev_gen, device,
+                          shape.act_scale)
+    gate = (_randn_bf16((rows, shape.num_q_heads, d), dev_gen, device, 1.0)
+            if shape.gate else None)
+    to = dict(device=device)
+    return QSAWorkload(
+        shape=shape, device=device,
+        seq_lens=seq_lens.to(torch.int32).to(**to),
+        positions=positions.to(torch.int64).to(**to),
+        token_to_req=token_to_req.to(**to),
+        query_start_loc=query_start_loc.to(**to),
+        visible=visible.to(**to),
+        kv_cache=kv, k_cache=k_cache, v_cache=v_cache,
+        block_table=block_table.to(**to),
+        index_cache=index_cache,
+        index_table=index_table.to(**to),
+        q=q, q_index=q_index, gate=gate,
+        max_seq_len=int(seq_lens.max()),
+        max_query_len=max_query_len,
+    )
+
+
+def fresh_queries(wl: QSAWorkload, seed: int):
+    """New (q, q_index) of the workload's shapes, e.g. to rotate decode steps."""
+    gen = torch.Generator(device=wl.device).manual_seed(seed)
+    q = _randn_bf16(tuple(wl.q.shape), gen, wl.device, wl.shape.act_scale)
+    qi = _randn_bf16(tuple(wl.q_index.shape), gen, wl.device, wl.shape.act_scale)
+    return q, qi
+
+
+def attention_bytes(wl: QSAWorkload, counts: torch.Tensor) -> int:
+    """Algorithmic HBM bytes of one sparse-attention launch (decode rows).
+
+    Per row: count * Hkv * 2 (K,V) * D * 2 B gathered + q and out (bf16)
+    + gate if present + the W int32 indices + its count.
+    """
+    s = wl.shape
+    gathered = int(counts.clamp_min(0).to(torch.int64).sum()) * s.num_kv_heads * 2 * s.head_dim * 2
+    per_row = 2 * s.num_q_heads * s.head_dim * 2 + s.width * 4 + 4
+    if wl.gate is not None:
+        per_row += s.num_q_heads * s.head_dim * 2
+    return gathered + wl.rows * per_row
+
+
+def indexer_bytes(wl: QSAWorkload) -> int:
+    """Algorithmic bytes of the decode indexer: keys + queries + logits."""
+    s = wl.shape
+    vis = int(wl.visible.to(torch.int64).sum())
+    return vis * s.index_dim * 2 + wl.rows * s.index_heads * s.index_dim * 2 + vis * 4
+
+
+def indexer_flops(wl: QSAWorkload) -> int:
+    s = wl.shape
+    return 2 * s.index_heads * s.index_dim * int(wl.visible.to(torch.int64).sum())

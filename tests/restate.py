@@ -1,0 +1,92 @@
+"""Independent pure-Python statements used to pin the oracle (tests only).
+
+Each function is written from a different angle than ``oracle/qsa_oracle.py``
+(rank counting instead of sorting, column-wise instead of rank-wise expansion,
+scalar loops instead of tensor ops) so that a slip in one does not hide in the
+other. Sizes must stay tiny.
+"""
+
+from __future__ import annotations
+
+import math
+
+
+def c_div(a, b):
+    q = abs(a) // abs(b)
+    return q if (a >= 0) == (b >= 0) else -q
+
+
+def u32_keys(float32_tensor):
+    import torch
+    return [(v & 0xFFFFFFFF) for v in float32_tensor.contiguous().view(torch.int32).tolist()]
+
+
+def topk_by_rank(keys, length, k):
+    """Selected ids by rank counting: rank(i) = #{key_j > key_i} + #{j < i : key_j == key_i}."""
+    if length <= k:
+        return [i if i < length else -1 for i in range(k)]
+    keys = keys[:length]
+    chosen = []
+    for i in range(length):
+        rank = 0
+        for j in range(length):
+            if keys[j] > keys[i] or (keys[j] == keys[i] and j < i):
+                rank += 1
+        if rank < k:
+            chosen.append(i)
+    assert len(chosen) == k
+    return chosen
+
+
+def expand_columns(block_ids, pos, req, seq_lens, ratio, width, physical, table, page):
+    """Column-wise expansion following the reference's second statement of the
+    rule (the Triton kernel ``ops/qsa.py:44-106``). Returns (row, count)."""
+    k = len(block_ids)
+    num_requests = len(seq_lens)
+    mapped = 0 <= req < num_requests
+    seq_len = seq_lens[req] if mapped else 0
+    safe_req = min(max(req, 0), num_requests - 1)
+    complete = min(min(c_div(pos + 1, ratio), c_div(seq_len, ratio)), k)
+    expanded_count = complete * ratio
+    tail_start = c_div(pos + 1, ratio) * ratio
+    tail_count = pos + 1 - tail_start
+    row = []
+    for col in range(width):
+        is_exp = col < expanded_count
+        rank, off = col // ratio, col % ratio
+        block = block_ids[min(rank, k - 1)] if is_exp else -1
+        tail_off = col - expanded_count
+        is_tail = col >= expanded_count and tail_off < tail_count and tail_off < ratio - 1
+        token = block * ratio + off if is_exp else tail_start + tail_off
+        valid = (is_exp or is_tail) and 0 <= token < seq_len
+        if physical and valid:
+            lp = token // page
+            pp = table[safe_req][lp] if lp < len(table[safe_req]) else -1
+            valid = pp >= 0
+            token = pp * page + token % page
+        row.append(token if valid else -1)
+    count = min(expanded_count + tail_count, seq_len) if mapped else 0
+    return row, count
+
+
+def relu_head_scores(q_row, keys):
+    """q_row: [H][D] floats, keys: [n][D] floats -> n scores (double precision)."""
+    dim = len(q_row[0])
+    out = []
+    for key in keys:
+        total = 0.0
+        for qh in q_row:
+            dot = sum(a * b for a, b in zip(qh, key))
+            total += max(dot, 0.0)
+        out.append(total * dim ** -0.5)
+    return out
+
+
+def softmax_attend(q_vec, keys, values):
+    """Single-head attention in double precision with explicit loops."""
+    dim = len(q_vec)
+    scores = [sum(a * b for a, b in zip(q_vec, k)) * dim ** -0.5 for k in keys]
+    m = max(scores)
+    w = [math.exp(s - m) for s in scores]
+    z = sum(w)
+    return [sum(w[t] * values[t][d] for t in range(len(keys))) / z for d in range(dim)]

@@ -1,0 +1,122 @@
+"""C-ABI library checks that need no GPU: exports, signatures, argument errors."""
+
+import ctypes
+import re
+import subprocess
+import shutil
+from pathlib import Path
+
+import pytest
+
+from qsa_vllm_amd import _lib
+
+ROOT = Path(__file__).resolve().parents[1]
+HEADER = ROOT / "include" / "qsa_hip.h"
+
+
+def header_functions():
+    text = HEADER.read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(qsa_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_library_exports_every_declared_symbol():
+    lib = ctypes.CDLL(str(_lib.library_path()))
+    names = header_functions()
+    assert len(names) >= 10
+    missing = [n for n in names if not hasattr(lib, n)]
+    assert not missing, missing
+
+
+def test_binding_table_matches_header():
+    assert sorted(_lib.SIGNATURES) == header_functions()
+    text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
+    for name, (_, argtypes) in _lib.SIGNATURES.items():
+        decl = re.search(rf"\b{name}\s*\((.*?)\);", text, flags=re.S).group(1).strip()
+        nargs = 0 if decl in ("", "void") else len(decl.split(","))
+        assert nargs == len(argtypes), name
+
+
+def test_abi_version_and_clean_error():
+    lib = _lib.load()
+    assert lib.qsa_abi_version() == _lib.ABI_VERSION
+    assert lib.qsa_last_error() is not None
+
+
+def _attn_args(**over):
+    a = dict(q=1 << 20, qr=256, qh=128, rows=4, hq=16, d=128, k=1 << 21, kb=4096, kt=256, kh=128,
+             v=(1 << 21) + 256, vb=4096, vt=256, vh=128, nblk=8, page=16, hkv=2, idx=1 << 22,
+             idxr=64, width=64, table=1 << 23, tabr=4, tabw=4, nreq=4, t2r=1 << 24, counts=None,
+             out=1 << 25, outr=2048, outh=128, gate=None, gr=0, gh=0, gd=0, phys=1, splits=1,
+             ws=None, wsb=0, stream=None)
+    a.update(over)
+    return list(a.values())
+
+
+def test_attention_argument_errors_need_no_launch():
+    lib = _lib.load()
+    f = lib.qsa_sparse_attention
+    assert f(*_attn_args(rows=0)) == 0
+    assert f(*_attn_args(d=96)) == -2
+    assert b"head_dim" in lib.qsa_last_error()
+    assert f(*_attn_args(hq=12, hkv=8)) == -2          # 12 % 8 != 0
+    assert f(*_attn_args(hq=48, hkv=2)) == -2          # group 24 neither divides nor multiplies 16
+    assert f(*_attn_args(splits=4)) == -4              # split partials need a workspace
+    assert f(*_attn_args(q=(1 << 20) + 2)) == -1       # misaligned q
+    assert f(*_attn_args(phys=0, table=None)) == -1
+
+
+def test_topk_argument_errors_need_no_launch():
+    lib = _lib.load()
+    args = [1 << 20, 64, 0, 64, 1 << 21, 1 << 22, 64, 8, None, 0, None]
+    assert lib.qsa_topk(*args) == 0                     # zero rows
+    args[2] = 4
+    args[7] = 0
+    assert lib.qsa_topk(*args) == -1                    # topk must be positive
+    assert lib.qsa_topk_workspace_bytes(4, 16384, 128) == 0
+    assert lib.qsa_topk_workspace_bytes(4, 65536, 128) == 4 * 8 * 128 * 4
+    args = [1 << 20, 70000, 4, 70000, 1 << 21, 1 << 22, 64, 128, None, 0, None]
+    assert lib.qsa_topk(*args) == -4                    # long rows need the partition workspace
+
+
+def test_workspace_and_split_helpers():
+    lib = _lib.load()
+    assert lib.qsa_sparse_attention_workspace_bytes(64, 16, 128, 1) == 0
+    assert lib.qsa_sparse_attention_workspace_bytes(64, 16, 128, 4) == 4 * 64 * 16 * (128 + 1) * 4
+    s = lib.qsa_sparse_attention_splits(64, 16, 2, 128, 2063, 1)
+    assert s >= 1 and s & (s - 1) == 0
+    assert lib.qsa_sparse_attention_splits(32768, 16, 2, 128, 2063, 0) == 1
+
+
+@pytest.mark.skipif(shutil.which("g++") is None, reason="needs g++")
+def test_fastdiv_exhaustive_host(tmp_path):
+    src = tmp_path / "fd.cpp"
+    src.write_text(r'''
+#include "fastdiv.h"
+#include <cstdio>
+#include <cstdint>
+int main() {
+  const int32_t divisors[] = {1, 2, 3, 4, 5, 7, 15, 16, 17, 31, 64, 100, 255, 256, 272, 1000,
+                              4096, 65535, 65536, 1 << 20, 2147483647};
+  uint32_t x = 12345;
+  for (int32_t d : divisors) {
+    qsa::FastDiv f = qsa::FastDiv::make(d);
+    for (int32_t n = 0; n < 200000; ++n)
+      if (f.div(n) != n / d) { printf("FAIL d=%d n=%d\n", d, n); return 1; }
+    for (int i = 0; i < 200000; ++i) {
+      x = x * 1664525u + 1013904223u;
+      int32_t n = (int32_t)(x & 0x7fffffffu);
+      if (f.div(n) != n / d) { printf("FAIL d=%d n=%d\n", d, n); return 1; }
+    }
+    int32_t top = 2147483647;
+    if (f.div(top) != top / d) { printf("FAIL d=%d top\n", d); return 1; }
+  }
+  printf("OK\n");
+  return 0;
+}
+''')
+    exe = tmp_path / "fd"
+    subprocess.run(["g++", "-O2", "-std=c++17", "-I", str(ROOT / "qsa_vllm_amd" / "csrc"),
+                    str(src), "-o", str(exe)], check=True)
+    out = subprocess.run([str(exe)], capture_output=True, text=True)
+    assert out.returncode == 0 and "OK" in out.stdout, out.stdout

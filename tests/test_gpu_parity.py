@@ -1,0 +1,356 @@
+"""GPU parity: the HIP kernels (through the C ABI / torch ops) against the CPU oracle.
+
+Bars: top-k indices, expansion and counts bit-exact on identical fp32 scores;
+indexer scores within fp32 accumulation error (|err| <= 2e-5 * sum|q*k| * D^-0.5
++ 1e-6); attention within max-abs 2e-2 and mean-abs 2e-3 of the fp32 oracle.
+"""
+
+import math
+
+import pytest
+import torch
+
+import oracle
+from qsa_vllm_amd.ops import (qsa_sparse_paged_attention, select_paged_tokens, topk,
+                              topk_expand)
+from qsa_vllm_amd.workloads import make_workload
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda:0"
+MAX_ABS, MEAN_ABS = 2e-2, 2e-3
+
+
+def _note(msg):
+    print(f"[case] {msg}", flush=True)
+
+
+def _special_scores(rows, cols, g, mode):
+    if mode == "random":
+        return torch.randn(rows, cols, generator=g) * 10
+    if mode == "ties":
+        return torch.randint(0, 5, (rows, cols), generator=g).float()
+    if mode == "relu":  # nonnegative with exact zeros, like ReLU-summed scores
+        return (torch.randn(rows, cols, generator=g) * 4).clamp_min(0)
+    if mode == "specials":
+        pool = torch.tensor([0.0, -0.0, 1.0, -1.0, float("inf"), float("-inf"), 1e-40, 3.5],
+                            dtype=torch.float32)
+        s = pool[torch.randint(0, len(pool), (rows, cols), generator=g)]
+        nan_bits = torch.tensor([0x7FC00000, 0x7F800001, -4194304], dtype=torch.int32)
+        mask = torch.rand(rows, cols, generator=g) < 0.05
+        nans = nan_bits[torch.randint(0, 3, (rows, cols), generator=g)].view(torch.float32)
+        return torch.where(mask, nans, s)
+    raise ValueError(mode)
+
+
+@pytest.mark.parametrize("cols,k", [(64, 16), (1000, 128), (2048, 128), (4096, 128), (8192, 128),
+                                    (16384, 512), (40000, 128), (70000, 512)])
+@pytest.mark.parametrize("mode", ["random", "ties", "relu", "specials"])
+def test_topk_bit_exact(cols, k, mode):
+    _note(f"topk cols={cols} k={k} mode={mode}")
+    g = torch.Generator().manual_seed(cols * 7 + k + len(mode))
+    rows = 6 if cols > 16384 else 33
+    scores = _special_scores(rows, cols, g, mode)
+    lengths = torch.randint(0, cols + 1, (rows,), generator=g, dtype=torch.int32)
+    lengths[0], lengths[1], lengths[2] = cols, k, min(cols, k + 1)
+    want = oracle.topk_ids(scores, lengths, k)
+    out = torch.full((rows, k), -7, dtype=torch.int32, device=DEV)
+    topk(scores.to(DEV), lengths.to(DEV), out)
+    torch.cuda.synchronize()
+    assert torch.equal(out.cpu(), want)
+
+
+def _expand_case(g, rows, cols, ratio, page, k, physical, reqs=5):
+    seq = torch.randint(0, cols * ratio + 40, (reqs,), generator=g, dtype=torch.int32)
+    t2r = torch.randint(-1, reqs + 1, (rows,), generator=g, dtype=torch.int32)
+    t2r[:4] = torch.arange(4, dtype=torch.int32) % reqs
+    mapped = (t2r >= 0) & (t2r < reqs)
+    sl = torch.where(mapped, seq[t2r.clamp(0, reqs - 1).long()], torch.zeros_like(seq[:1]))
+    pos = (torch.rand(rows, generator=g) * (sl.float() + 20)).long()
+    # visible blocks of mapped rows; unmapped rows (padding or out-of-range request) see none
+    vis = torch.where(mapped, torch.minimum((pos + 1) // ratio, sl.long() // ratio),
+                      torch.zeros_like(pos)).to(torch.int32).clamp_max(cols)
+    vis[-1] = cols  # a row whose visible count exceeds the token budget
+    width = (max(int(seq.max()), 1) + page - 1) // page + 1
+    table = torch.randint(0, 1000, (reqs, width), generator=g, dtype=torch.int32)
+    table[torch.rand(reqs, width, generator=g) < 0.1] = -1
+    scores = (torch.randn(rows, cols, generator=g) * 3).clamp_min(0)
+    return seq, t2r, pos, vis, table, scores
+
+
+@pytest.mark.parametrize("ratio,page,physical", [(16, 16, True), (4, 272, True), (4, 6, True),
+                                                 (4, 16, False), (16, 16, False), (1, 16, True)])
+@pytest.mark.parametrize("cols,k", [(2048, 128), (9000, 64), (40000, 128)])
+def test_topk_expand_bit_exact(ratio, page, physical, cols, k):
+    _note(f"topk_expand ratio={ratio} page={page} physical={physical} cols={cols} k={k}")
+    g = torch.Generator().manual_seed(ratio * 1000 + page + cols + physical)
+    rows = 8 if cols > 16384 else 40
+    seq, t2r, pos, vis, table, scores = _expand_case(g, rows, cols, ratio, page, k, physical)
+    width = k * ratio + ratio - 1
+    want, want_counts = oracle.topk_expand(scores, vis, pos, seq, t2r, table, width, ratio, page,
+                                           physical)
+    # A strided output view checks that the column stride is honoured.
+    big = torch.full((rows, 2 * width), -9, dtype=torch.int32, device=DEV)
+    out = big[:, ::2]
+    counts = torch.full((rows,), -9, dtype=torch.int32, device=DEV)
+    topk_expand(scores.to(DEV), vis.to(DEV), pos.to(DEV), seq.to(DEV), t2r.to(DEV), out, ratio,
+                main_block_table=table.to(DEV) if physical else None, main_page_size=page,
+                valid_counts_out=counts)
+    torch.cuda.synchronize()
+    assert torch.equal(out.cpu(), want)
+    assert torch.equal(counts.cpu(), want_counts)
+    assert (big[:, 1::2] == -9).all()
+
+
+def _score_tol(q, keys, dim):
+    mag = (q.float().abs() @ keys.float().abs().T).sum(0) * dim ** -0.5
+    return 2e-5 * mag + 1e-6
+
+
+@pytest.mark.parametrize("heads,dim,dql", [(32, 128, 1), (8, 64, 1), (4, 128, 2), (48, 128, 1)])
+def test_indexer_decode_parity(heads, dim, dql):
+    _note(f"indexer_decode heads={heads} dim={dim} dql={dql}")
+    g = torch.Generator().manual_seed(heads + dim + dql)
+    reqs, cpage, width = 9, 16, 13
+    rows = reqs * dql
+    q = torch.randn(rows, heads, dim, generator=g).to(torch.bfloat16)
+    cache = torch.randn(150, cpage, 1, dim, generator=g).to(torch.bfloat16)
+    table = torch.randperm(150, generator=g)[:reqs * width].view(reqs, width).to(torch.int32)
+    vis = torch.randint(0, width * cpage + 1, (rows,), generator=g, dtype=torch.int32)
+    vis[0], vis[1] = width * cpage, 0
+    cols = width * cpage
+    want = oracle.indexer_scores_decode(q, cache, table, vis, dql, cols)
+    logits = torch.full((rows, cols), float("nan"), device=DEV)
+    torch.ops.yulan_qsa_kernels.indexer_decode(q.to(DEV), cache.to(DEV), table.to(DEV), vis.to(DEV),
+                                               logits, dql)
+    got = logits.cpu()
+    for r in range(rows):
+        n = int(vis[r])
+        keys = torch.stack([cache[int(table[r // dql, c // cpage]), c % cpage, 0]
+                            for c in range(n)]) if n else torch.zeros(0, dim)
+        if n:
+            tol = _score_tol(q[r], keys, dim)
+            assert ((got[r, :n] - want[r, :n]).abs() <= tol).all(), r
+        assert torch.isnan(got[r, n:]).all(), "columns beyond visible must stay untouched"
+
+
+def test_indexer_prefill_parity():
+    _note("indexer_prefill")
+    g = torch.Generator().manual_seed(21)
+    heads, dim, cpage = 32, 128, 16
+    lens = [37, 1, 70, 20]
+    qsl = torch.tensor([5] + [5 + sum(lens[:i + 1]) for i in range(len(lens))], dtype=torch.int32)
+    rows = sum(lens)
+    width = 6
+    q = torch.randn(rows, heads, dim, generator=g).to(torch.bfloat16)
+    cache = torch.randn(40, cpage, 1, dim, generator=g).to(torch.bfloat16)
+    table = torch.randperm(40, generator=g)[:len(lens) * width].view(len(lens), width).to(torch.int32)
+    vis = torch.randint(0, width * cpage + 1, (rows,), generator=g, dtype=torch.int32)
+    lw = width * cpage
+    for offset, n in [(0, rows), (30, 50)]:
+        want = oracle.indexer_scores_prefill(q, cache, table, qsl, vis, offset, n, lw)
+        logits = torch.full((n, lw), float("nan"), device=DEV)
+        torch.ops.yulan_qsa_kernels.indexer_prefill(q.to(DEV), cache.to(DEV), table.to(DEV),
+                                                    qsl.to(DEV), vis.to(DEV), logits, offset, n,
+                                                    max(lens))
+        got = logits.cpu()
+        written = ~torch.isnan(want)
+        assert torch.equal(written, ~torch.isnan(got))
+        assert torch.allclose(got[written], want[written], rtol=2e-5, atol=2e-4)
+
+
+def _attn_check(got, want, what):
+    err = (got.float().cpu() - want).abs()
+    _note(f"{what}: max_abs={err.max().item():.3e} mean_abs={err.mean().item():.3e}")
+    assert err.max().item() <= MAX_ABS and err.mean().item() <= MEAN_ABS, what
+
+
+def _random_physical_indices(g, rows, width, num_blocks, page, counts):
+    idx = torch.randint(0, num_blocks * page, (rows, width), generator=g, dtype=torch.int32)
+    idx[torch.rand(rows, width, generator=g) < 0.05] = -1
+    idx[:, -3:] = num_blocks * page + 5        # out-of-cache slots are invalid
+    for r in range(rows):
+        idx[r, int(counts[r]):] = -1
+    return idx
+
+
+@pytest.mark.parametrize("hq,hkv,dim", [(16, 2, 128), (8, 1, 128), (4, 4, 128), (32, 2, 128),
+                                         (64, 2, 128), (16, 2, 64), (8, 8, 64)])
+@pytest.mark.parametrize("splits", [1, 3, 8])
+@pytest.mark.parametrize("layout", ["token_major", "head_major"])
+def test_attention_physical_parity(hq, hkv, dim, splits, layout):
+    _note(f"attention physical hq={hq} hkv={hkv} dim={dim} splits={splits} layout={layout}")
+    g = torch.Generator().manual_seed(hq * 31 + hkv * 7 + dim + splits)
+    rows, page, num_blocks, width = 6, 16, 40, 200
+    if layout == "token_major":
+        kv = torch.randn(num_blocks, page, hkv, 2 * dim, generator=g).to(torch.bfloat16)
+        k, v = kv[..., :dim], kv[..., dim:]
+    else:
+        kv = torch.randn(num_blocks, hkv, page, 2 * dim, generator=g).to(torch.bfloat16)
+        k, v = kv.transpose(1, 2).split(dim, dim=-1)
+    q = torch.randn(rows, hq, dim, generator=g).to(torch.bfloat16)
+    gate = torch.randn(rows, hq, dim, generator=g).to(torch.bfloat16)
+    counts = torch.tensor([width, 0, 1, 33, 150, 199], dtype=torch.int32)
+    idx = _random_physical_indices(g, rows, width, num_blocks, page, counts)
+    table = torch.zeros(1, 1, dtype=torch.int32)
+    t2r = torch.zeros(rows, dtype=torch.int32)
+    kvd = kv.to(DEV)
+    if layout == "token_major":
+        kd, vd = kvd[..., :dim], kvd[..., dim:]
+    else:
+        kd, vd = kvd.transpose(1, 2).split(dim, dim=-1)
+    for use_gate in (False, True):
+        want = oracle.sparse_attention(q, k, v, idx, table, t2r, indices_are_physical=True,
+                                       valid_counts=counts, output_gate=gate if use_gate else None)
+        out = torch.full((rows, hq, dim), float("nan"), dtype=torch.bfloat16, device=DEV)
+        torch.ops.yulan_qsa_kernels.sparse_attention(
+            q.to(DEV), kd, vd, idx.to(DEV), table.to(DEV), t2r.to(DEV), out,
+            gate.to(DEV) if use_gate else None, counts.to(DEV), True, splits)
+        torch.cuda.synchronize()
+        _attn_check(out, want, f"gate={use_gate}")
+        assert (out[1].float() == 0).all(), "a row with no valid slot must be zero"
+
+
+@pytest.mark.parametrize("splits", [1, 4])
+def test_attention_logical_parity(splits):
+    _note(f"attention logical splits={splits}")
+    g = torch.Generator().manual_seed(40 + splits)
+    reqs, hq, hkv, dim, page, num_blocks = 3, 16, 2, 128, 16, 30
+    k = torch.randn(num_blocks, page, hkv, dim, generator=g).to(torch.bfloat16)
+    v = torch.randn(num_blocks, page, hkv, dim, generator=g).to(torch.bfloat16)
+    table = torch.randperm(num_blocks, generator=g)[:reqs * 8].view(reqs, 8).to(torch.int32)
+    table[1, 5:] = -1
+    table[2, 0] = num_blocks + 4             # an out-of-cache page is invalid
+    rows, width = 9, 100
+    t2r = torch.tensor([0, 0, 1, 1, 2, 2, -1, 3, 0], dtype=torch.int32)  # padding + bad request
+    idx = torch.randint(-2, 8 * page + 10, (rows, width), generator=g, dtype=torch.int32)
+    q = torch.randn(rows, hq, dim, generator=g).to(torch.bfloat16)
+    want = oracle.sparse_attention(q, k, v, idx, table, t2r)
+    out = qsa_sparse_paged_attention(q.to(DEV), k.to(DEV), v.to(DEV), idx.to(DEV), table.to(DEV),
+                                     t2r.to(DEV), decode_config=(32, splits, 4))
+    torch.cuda.synchronize()
+    _attn_check(out, want, "logical")
+    assert (out[6:8].float() == 0).all()
+
+
+def test_decode_select_then_attend_small():
+    _note("end-to-end small decode (cpu_decode_4k shape)")
+    wl = make_workload("cpu_decode_4k", device="cpu")
+    s = wl.shape
+    d = {n: getattr(wl, n).to(DEV) for n in ("q_index", "index_cache", "index_table", "token_to_req",
+                                              "positions", "seq_lens", "query_start_loc", "visible",
+                                              "block_table", "q")}
+    kv = wl.kv_cache.to(DEV)
+    kd, vd = kv[..., :s.head_dim], kv[..., s.head_dim:]
+    rows = wl.rows
+    out_idx = torch.empty(rows, s.width, dtype=torch.int32, device=DEV)
+    counts = torch.empty(rows, dtype=torch.int32, device=DEV)
+    select_paged_tokens(d["q_index"], d["index_cache"], d["index_table"], d["token_to_req"],
+                        d["positions"], d["seq_lens"], s.token_topk, s.compress_ratio, out_idx,
+                        query_start_loc=d["query_start_loc"], max_query_len=1,
+                        max_seq_len=wl.max_seq_len, num_decodes=rows, num_decode_tokens=rows,
+                        visible_blocks=d["visible"], main_block_table=d["block_table"],
+                        main_page_size=s.page_size, valid_counts_out=counts)
+    # Recompute the logits the kernel used, then check top-k bit-exact on them.
+    cols = oracle.decode_logits_columns(wl.max_seq_len, s.compress_ratio,
+                                        wl.index_table.shape[1] * wl.index_cache.shape[1])
+    logits = torch.full((rows, cols), float("nan"), device=DEV)
+    torch.ops.yulan_qsa_kernels.indexer_decode(d["q_index"], d["index_cache"], d["index_table"],
+                                               d["visible"], logits, 1)
+    want_logits = oracle.indexer_scores_decode(wl.q_index, wl.index_cache, wl.index_table,
+                                               wl.visible, 1, cols)
+    n = int(wl.visible.max())
+    assert torch.allclose(logits.cpu()[:, :n], want_logits[:, :n], rtol=2e-5, atol=1e-4)
+    want_idx, want_counts = oracle.topk_expand(logits.cpu(), wl.visible, wl.positions, wl.seq_lens,
+                                               wl.token_to_req, wl.block_table, s.width,
+                                               s.compress_ratio, s.page_size, True)
+    assert torch.equal(out_idx.cpu(), want_idx)
+    assert torch.equal(counts.cpu(), want_counts)
+    out = torch.zeros_like(d["q"])
+    qsa_sparse_paged_attention(d["q"], kd, vd, out_idx, d["block_table"], d["token_to_req"], out,
+                               use_decode_kernel=True, indices_are_physical=True,
+                               valid_counts=counts)
+    want = oracle.sparse_attention(wl.q, wl.k_cache, wl.v_cache, want_idx, wl.block_table,
+                                   wl.token_to_req, indices_are_physical=True,
+                                   valid_counts=want_counts)
+    _attn_check(out, want, "decode end-to-end")
+
+
+def test_decode_32k_full_size_properties():
+    """BASELINE decode shape at full size: exact checks on a row subset + global invariants."""
+    _note("decode_32k full size")
+    wl = make_workload("decode_32k", device=DEV)
+    s = wl.shape
+    rows = wl.rows
+    out_idx = torch.empty(rows, s.width, dtype=torch.int32, device=DEV)
+    counts = torch.empty(rows, dtype=torch.int32, device=DEV)
+    select_paged_tokens(wl.q_index, wl.index_cache, wl.index_table, wl.token_to_req, wl.positions,
+                        wl.seq_lens, s.token_topk, s.compress_ratio, out_idx,
+                        query_start_loc=wl.query_start_loc, max_query_len=1,
+                        max_seq_len=wl.max_seq_len, num_decodes=rows, num_decode_tokens=rows,
+                        visible_blocks=wl.visible, main_block_table=wl.block_table,
+                        main_page_size=s.page_size, valid_counts_out=counts)
+    out = torch.zeros_like(wl.q)
+    qsa_sparse_paged_attention(wl.q, wl.k_cache, wl.v_cache, out_idx, wl.block_table,
+                               wl.token_to_req, out, use_decode_kernel=True,
+                               indices_are_physical=True, valid_counts=counts)
+    torch.cuda.synchronize()
+    seq = wl.seq_lens.cpu()
+    assert torch.equal(counts.cpu(), s.token_topk + seq % s.compress_ratio)
+    assert torch.isfinite(out.float()).all()
+    idx = out_idx.cpu()
+    table = wl.block_table.cpu()
+    # every selected slot lies in a page of its own request and blocks are page-aligned runs
+    for r in range(0, rows, 9):
+        valid = idx[r, :int(counts[r])]
+        pages = set(table[r, :(int(seq[r]) + 15) // 16].tolist())
+        assert all(int(x) // 16 in pages for x in valid)
+        runs = valid[:s.token_topk].view(-1, 16)
+        assert torch.equal(runs - runs[:, :1], torch.arange(16).expand_as(runs))
+    # exact parity on a subset of rows (oracle on CPU, same indices)
+    sub = list(range(0, rows, 16))
+    kv_cpu = wl.kv_cache.cpu()
+    want = oracle.sparse_attention(
+        wl.q[sub].cpu(), kv_cpu[..., :s.head_dim], kv_cpu[..., s.head_dim:], idx[sub],
+        table, wl.token_to_req[sub].cpu(), indices_are_physical=True, valid_counts=counts[sub].cpu())
+    _attn_check(out[sub], want, "decode_32k rows subset")
+
+
+def test_graph_replay_matches_eager():
+    _note("hip graph replay of the decode step")
+    wl = make_workload("cpu_decode_4k", device=DEV, batch=16)
+    s = wl.shape
+    rows = wl.rows
+    out_idx = torch.empty(rows, s.width, dtype=torch.int32, device=DEV)
+    counts = torch.empty(rows, dtype=torch.int32, device=DEV)
+    out = torch.zeros_like(wl.q)
+
+    def step():
+        select_paged_tokens(wl.q_index, wl.index_cache, wl.index_table, wl.token_to_req,
+                            wl.positions, wl.seq_lens, s.token_topk, s.compress_ratio, out_idx,
+                            query_start_loc=wl.query_start_loc, max_query_len=1,
+                            max_seq_len=wl.max_seq_len, num_decodes=rows, num_decode_tokens=rows,
+                            visible_blocks=wl.visible, main_block_table=wl.block_table,
+                            main_page_size=s.page_size, valid_counts_out=counts)
+        qsa_sparse_paged_attention(wl.q, wl.k_cache, wl.v_cache, out_idx, wl.block_table,
+                                   wl.token_to_req, out, use_decode_kernel=True,
+                                   indices_are_physical=True, valid_counts=counts)
+
+    step()
+    torch.cuda.synchronize()
+    ref_out, ref_idx = out.clone(), out_idx.clone()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        step()
+    torch.cuda.current_stream().wait_stream(side)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        step()
+    for i in range(4):
+        out.fill_(float("nan"))
+        out_idx.fill_(-5)
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out_idx, ref_idx), i
+        assert torch.equal(out, ref_out), i
