@@ -19,9 +19,18 @@
 //       the lane's own softmax numerators, so P never leaves registers and the
 //       per-head rescale factor lives in the lane that owns that head.
 //
-// The 4 waves merge their (max, sum, O) through LDS; with one split the
-// workgroup writes bf16 output (and gate), otherwise fp32 partials that
-// qsa_sparse_attention_merge reduces.
+// While a tile's K/V loads are in flight the wave already resolves the next
+// tile's slots (index loads, and block-table lookups for logical indices), so
+// only the K/V latency is exposed per tile. Invalid slots read a block of
+// zeros in device memory instead of K/V, so no per-element masking is needed
+// beyond the -inf score.
+//
+// The 4 waves merge (max, sum, O) through LDS. With one split the workgroup
+// writes the bf16 output (and gate); with several it writes an fp32 partial +
+// log2-LSE and a second kernel merges them. (Merging in the last-arriving
+// workgroup needs device-scope release/acquire fences, which on gfx950 write
+// back and invalidate the XCD's whole L2 per wave; measured, that cost far
+// more than the separate launch.)
 #include "qsa_common.h"
 #include "../../include/qsa_hip.h"
 
@@ -34,6 +43,7 @@ constexpr int kWaves = 4;
 constexpr int kThreads = 64 * kWaves;
 constexpr int kTile = 32;
 constexpr float kInitMax = -1.0e20f;  // finite running-max seed (ops/qsa.py:173)
+constexpr int kMergeChunk = 8;        // split partials a merge thread loads at once
 
 struct AttnParams {
   const uint16_t* q;
@@ -64,6 +74,7 @@ struct AttnParams {
   int num_q_heads;
   int group;
   int heads_per_wave;
+  int head_groups;
   int num_splits;
   int physical;
   float scale_log2;
@@ -71,36 +82,25 @@ struct AttnParams {
 
 __device__ __forceinline__ float sigmoidf_(float x) { return 1.0f / (1.0f + __expf(-x)); }
 
-// Byte offsets of one token's row (without head offset) in K and V, or -1.
-struct SlotInfo {
-  int64_t koff;
-  int64_t voff;
-  bool valid;
-};
-
-__device__ __forceinline__ SlotInfo resolve_slot(const AttnParams& p, const int32_t* irow,
-                                                 const int32_t* trow, bool req_ok, int col,
-                                                 int n_valid) {
-  SlotInfo s;
+// Validated physical slot (page * page_size + offset) of index column `col`,
+// or -1 (ops/qsa.py:186-212).
+__device__ __forceinline__ int resolve_slot(const AttnParams& p, const int32_t* irow,
+                                            const int32_t* trow, bool req_ok, int col,
+                                            int n_valid) {
   const int tok = col < n_valid ? irow[col] : -1;
-  bool valid = tok >= 0;
-  int page = 0, off = 0;
-  if (valid) {
-    const int lp = p.page_div.div(tok);
-    off = tok - lp * p.page_size;
-    if (p.physical) {
-      page = lp;
-      valid = page < p.num_blocks;
-    } else {
-      valid = req_ok && lp < p.table_width;
-      page = valid ? trow[lp] : -1;
-      valid = valid && page >= 0 && page < p.num_blocks;
-    }
-  }
-  s.valid = valid;
-  s.koff = valid ? (int64_t)page * p.kb + (int64_t)off * p.kt : 0;
-  s.voff = valid ? (int64_t)page * p.vb + (int64_t)off * p.vt : 0;
-  return s;
+  if (tok < 0) return -1;
+  const int lp = p.page_div.div(tok);
+  if (p.physical) return lp < p.num_blocks ? tok : -1;
+  if (!req_ok || lp >= p.table_width) return -1;
+  const int page = trow[lp];
+  return (page >= 0 && page < p.num_blocks) ? page * p.page_size + (tok - lp * p.page_size) : -1;
+}
+
+// Byte offset of a validated slot's row in a cache with (block, token) strides.
+__device__ __forceinline__ int64_t slot_offset(const AttnParams& p, int slot, int64_t sb,
+                                               int64_t st) {
+  const int page = p.page_div.div(slot);
+  return (int64_t)page * sb + (int64_t)(slot - page * p.page_size) * st;
 }
 
 template <int D>
@@ -116,8 +116,15 @@ struct VRow<64> {
   static __device__ __forceinline__ type load(const char* ptr) { return load_u32x2(ptr); }
 };
 
+// Token of K-operand slot u (0,1) and V-operand slot i (0..7) inside a tile.
+__device__ __forceinline__ int k_col(int u, int n) { return 16 * u + n; }
+__device__ __forceinline__ int v_col(int i, int g) { return 16 * (i >> 2) + 4 * g + (i & 3); }
+
+// Two waves per SIMD wherever the registers allow it without spilling.
 template <int D, int NKV>
-__global__ __launch_bounds__(kThreads) void sparse_attn_kernel(const AttnParams p) {
+__global__ __launch_bounds__(kThreads)
+__attribute__((amdgpu_waves_per_eu(D == 128 && NKV == 4 ? 1 : 2)))
+void sparse_attn_kernel(const AttnParams p) {
   constexpr int DPL = D / 16;  // V dims per lane = P.V MFMAs per kv slot
   constexpr int KS = D / 32;   // K steps of the Q.K MFMA
   typedef typename VRow<D>::type vrow_t;
@@ -181,34 +188,49 @@ __global__ __launch_bounds__(kThreads) void sparse_attn_kernel(const AttnParams 
 #pragma unroll
   for (int j = 0; j < DPL; ++j) oacc[j] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-  for (int tile = t_begin + wave; tile < t_end; tile += kWaves) {
-    const int c0 = tile * kTile;
+  int tile = t_begin + wave;
+  int kslot[2], vsl[8];
+  if (tile < t_end) {
+#pragma unroll
+    for (int u = 0; u < 2; ++u) kslot[u] = resolve_slot(p, irow, trow, req_ok, tile * kTile + k_col(u, n), n_valid);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) vsl[i] = resolve_slot(p, irow, trow, req_ok, tile * kTile + v_col(i, g), n_valid);
+  }
 
-    // K rows: tokens c0 + 16 u + n (A-operand row = token).
+  for (; tile < t_end; tile += kWaves) {
+    // K rows: tokens 16 u + n (A-operand row = token).
     u32x4 kr[NKV][2][KS];
 #pragma unroll
     for (int u = 0; u < 2; ++u) {
-      const SlotInfo si = resolve_slot(p, irow, trow, req_ok, c0 + 16 * u + n, n_valid);
+      const int64_t off = kslot[u] >= 0 ? slot_offset(p, kslot[u], p.kb, p.kt) : 0;
 #pragma unroll
       for (int v = 0; v < NKV; ++v) {
-        const char* base = si.valid ? p.k + si.koff + khead[v] : zero;
+        const char* base = kslot[u] >= 0 ? p.k + off + khead[v] : zero;
 #pragma unroll
         for (int s = 0; s < KS; ++s) kr[v][u][s] = load_u32x4(base + (32 * s + 8 * g) * 2);
       }
     }
-    // V rows: tokens tok(i) = 16 (i / 4) + 4 g + i % 4, dims DPL n .. +DPL-1.
+    // V rows: tokens 16 (i / 4) + 4 g + i % 4, dims DPL n .. +DPL-1.
     vrow_t vr[NKV][8];
     uint32_t vmask = 0;
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
-      const SlotInfo si =
-          resolve_slot(p, irow, trow, req_ok, c0 + 16 * (i >> 2) + 4 * g + (i & 3), n_valid);
-      vmask |= si.valid ? (1u << i) : 0u;
+      vmask |= vsl[i] >= 0 ? (1u << i) : 0u;
+      const int64_t off = vsl[i] >= 0 ? slot_offset(p, vsl[i], p.vb, p.vt) : 0;
 #pragma unroll
       for (int v = 0; v < NKV; ++v) {
-        const char* base = si.valid ? p.v + si.voff + vhead[v] : zero;
+        const char* base = vsl[i] >= 0 ? p.v + off + vhead[v] : zero;
         vr[v][i] = VRow<D>::load(base + DPL * n * 2);
       }
+    }
+
+    // Resolve the next tile's slots while this tile's loads are in flight.
+    const int next = tile + kWaves;
+    if (next < t_end) {
+#pragma unroll
+      for (int u = 0; u < 2; ++u) kslot[u] = resolve_slot(p, irow, trow, req_ok, next * kTile + k_col(u, n), n_valid);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) vsl[i] = resolve_slot(p, irow, trow, req_ok, next * kTile + v_col(i, g), n_valid);
     }
 
     // S^T for the two 16-token halves; lane holds S[tok 16u + 4g + r][head n].
@@ -291,100 +313,121 @@ __global__ __launch_bounds__(kThreads) void sparse_attn_kernel(const AttnParams 
   // Thread t finalises head t / 16, dims [(t % 16) * DPL, +DPL).
   const int h = threadIdx.x >> 4;
   const int d0 = (threadIdx.x & 15) * DPL;
-  if (h >= p.heads_per_wave) return;
-  float mw[kWaves];
-  float mx = kInitMax;
-#pragma unroll
-  for (int w = 0; w < kWaves; ++w) {
-    mw[w] = s_m[w][h];
-    mx = fmaxf(mx, mw[w]);
-  }
-  float lsum = 0.0f;
-  float o[DPL];
-#pragma unroll
-  for (int d = 0; d < DPL; ++d) o[d] = 0.0f;
-#pragma unroll
-  for (int w = 0; w < kWaves; ++w) {
-    const float wt = fast_exp2(mw[w] - mx);
-    lsum += wt * s_l[w][h];
-#pragma unroll
-    for (int d = 0; d < DPL; ++d) o[d] += wt * s_o[w][h][d0 + d];
-  }
-  const bool has = lsum > 0.0f;
-  const float inv = has ? 1.0f / fmaxf(lsum, 1.0e-20f) : 0.0f;
+  const bool h_ok = h < p.heads_per_wave;
   const int head = head0 + h;
-
-  if (p.num_splits == 1) {
-    uint16_t* optr = p.out + (int64_t)row * p.out_row + (int64_t)head * p.out_head + d0;
-    const uint16_t* gptr =
-        p.gate ? p.gate + (int64_t)row * p.g_row + (int64_t)head * p.g_head : nullptr;
+  float o[DPL];
+  float mx = kInitMax, lsum = 0.0f;
+  if (h_ok) {
+    float mw[kWaves];
 #pragma unroll
-    for (int d = 0; d < DPL; d += 2) {
-      float a = o[d] * inv, b = o[d + 1] * inv;
-      if (gptr) {
-        // bf16(o) * sigmoid(gate) (ops/qsa.py:257-269).
-        const uint32_t ob = pack_bf16x2(a, b);
-        const float ga = bf16_lo((uint32_t)gptr[(int64_t)(d0 + d) * p.g_dim]);
-        const float gb = bf16_lo((uint32_t)gptr[(int64_t)(d0 + d + 1) * p.g_dim]);
-        a = bf16_lo(ob) * sigmoidf_(ga);
-        b = bf16_hi(ob) * sigmoidf_(gb);
-      }
-      *reinterpret_cast<uint32_t*>(optr + d) = pack_bf16x2(a, b);
+    for (int w = 0; w < kWaves; ++w) {
+      mw[w] = s_m[w][h];
+      mx = fmaxf(mx, mw[w]);
     }
-  } else {
+#pragma unroll
+    for (int d = 0; d < DPL; ++d) o[d] = 0.0f;
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) {
+      const float wt = fast_exp2(mw[w] - mx);
+      lsum += wt * s_l[w][h];
+#pragma unroll
+      for (int d = 0; d < DPL; ++d) o[d] += wt * s_o[w][h][d0 + d];
+    }
+    const float inv = lsum > 0.0f ? 1.0f / fmaxf(lsum, 1.0e-20f) : 0.0f;
+#pragma unroll
+    for (int d = 0; d < DPL; ++d) o[d] *= inv;
+  }
+
+  if (!h_ok) return;
+  if (p.num_splits > 1) {
+    // Normalised fp32 partial + log2-LSE for the merge kernel (ops/qsa.py:278-303).
     const int64_t prow = ((int64_t)split * p.rows + row) * p.num_q_heads + head;
     float* po = p.part_out + prow * D + d0;
 #pragma unroll
-    for (int d = 0; d < DPL; ++d) po[d] = o[d] * inv;
+    for (int d = 0; d < DPL; ++d) po[d] = o[d];
     if ((threadIdx.x & 15) == 0)
-      p.part_lse[prow] = has ? mx + __log2f(fmaxf(lsum, 1.0e-20f)) : -INFINITY;
+      p.part_lse[prow] = lsum > 0.0f ? mx + __log2f(fmaxf(lsum, 1.0e-20f)) : -INFINITY;
+    return;
+  }
+
+  uint16_t* optr = p.out + (int64_t)row * p.out_row + (int64_t)head * p.out_head + d0;
+  const uint16_t* gptr = p.gate ? p.gate + (int64_t)row * p.g_row + (int64_t)head * p.g_head : nullptr;
+#pragma unroll
+  for (int d = 0; d < DPL; d += 2) {
+    float a = o[d], b = o[d + 1];
+    if (gptr) {
+      // bf16(o) * sigmoid(gate) (ops/qsa.py:257-269).
+      const uint32_t ob = pack_bf16x2(a, b);
+      const float ga = bf16_lo((uint32_t)gptr[(int64_t)(d0 + d) * p.g_dim]);
+      const float gb = bf16_lo((uint32_t)gptr[(int64_t)(d0 + d + 1) * p.g_dim]);
+      a = bf16_lo(ob) * sigmoidf_(ga);
+      b = bf16_hi(ob) * sigmoidf_(gb);
+    }
+    *reinterpret_cast<uint32_t*>(optr + d) = pack_bf16x2(a, b);
   }
 }
 
-// LSE merge of split partials (ops/qsa.py:306-362): one workgroup per row,
-// each thread owns 4 consecutive dims of one head.
+// LSE merge of split partials (ops/qsa.py:306-362). One thread per (row, head,
+// 4 dims); a thread issues the loads of up to kMergeChunk splits at once so a
+// merge costs one memory round trip per chunk.
 __global__ __launch_bounds__(256) void merge_kernel(const float* __restrict__ part_out,
                                                     const float* __restrict__ part_lse,
                                                     int num_splits, int rows, int num_q_heads,
                                                     int head_dim, uint16_t* out, int64_t out_row,
                                                     int64_t out_head, const uint16_t* gate,
                                                     int64_t g_row, int64_t g_head, int64_t g_dim) {
-  const int row = blockIdx.x;
   const int chunks = head_dim / 4;
-  for (int item = threadIdx.x; item < num_q_heads * chunks; item += blockDim.x) {
-    const int head = item / chunks;
-    const int d0 = (item % chunks) * 4;
-    float lmax = -INFINITY;
-    for (int s = 0; s < num_splits; ++s)
-      lmax = fmaxf(lmax, part_lse[((int64_t)s * rows + row) * num_q_heads + head]);
-    float acc[4] = {0.f, 0.f, 0.f, 0.f};
-    float den = 0.0f;
-    if (lmax > -INFINITY) {
-      for (int s = 0; s < num_splits; ++s) {
-        const int64_t prow = ((int64_t)s * rows + row) * num_q_heads + head;
-        const float w = fast_exp2(part_lse[prow] - lmax);
-        den += w;
-        const float4 v = *reinterpret_cast<const float4*>(part_out + prow * head_dim + d0);
-        acc[0] += w * v.x;
-        acc[1] += w * v.y;
-        acc[2] += w * v.z;
-        acc[3] += w * v.w;
-      }
+  const int64_t item = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (item >= (int64_t)rows * num_q_heads * chunks) return;
+  const int d0 = (int)(item % chunks) * 4;
+  const int64_t rh = item / chunks;  // row * num_q_heads + head
+  const int row = (int)(rh / num_q_heads);
+  const int head = (int)(rh % num_q_heads);
+  const int64_t split_stride = (int64_t)rows * num_q_heads;
+  float lmax = -INFINITY, den = 0.0f;
+  float acc[4] = {0.f, 0.f, 0.f, 0.f};
+  for (int s0 = 0; s0 < num_splits; s0 += kMergeChunk) {
+    float lse[kMergeChunk];
+    float4 v[kMergeChunk];
+#pragma unroll
+    for (int c = 0; c < kMergeChunk; ++c) {
+      const int64_t pr = (int64_t)(s0 + c) * split_stride + rh;
+      const bool ok = s0 + c < num_splits;
+      lse[c] = ok ? part_lse[pr] : -INFINITY;
+      v[c] = ok ? *reinterpret_cast<const float4*>(part_out + pr * head_dim + d0)
+                : float4{0.f, 0.f, 0.f, 0.f};
     }
-    float o[4];
-    for (int d = 0; d < 4; ++d) o[d] = den > 0.0f ? acc[d] / den : 0.0f;
-    uint16_t* optr = out + (int64_t)row * out_row + (int64_t)head * out_head + d0;
-    if (gate) {
-      const uint16_t* gptr = gate + (int64_t)row * g_row + (int64_t)head * g_head;
-      for (int d = 0; d < 4; d += 2) {
-        const uint32_t ob = pack_bf16x2(o[d], o[d + 1]);
-        o[d] = bf16_lo(ob) * sigmoidf_(bf16_lo((uint32_t)gptr[(int64_t)(d0 + d) * g_dim]));
-        o[d + 1] = bf16_hi(ob) * sigmoidf_(bf16_lo((uint32_t)gptr[(int64_t)(d0 + d + 1) * g_dim]));
-      }
+    float cmax = lmax;
+#pragma unroll
+    for (int c = 0; c < kMergeChunk; ++c) cmax = fmaxf(cmax, lse[c]);
+    if (cmax == -INFINITY) continue;
+    const float rescale = fast_exp2(lmax - cmax);  // 0 while nothing has been merged
+    den *= rescale;
+    for (int d = 0; d < 4; ++d) acc[d] *= rescale;
+#pragma unroll
+    for (int c = 0; c < kMergeChunk; ++c) {
+      const float w = fast_exp2(lse[c] - cmax);
+      den += w;
+      acc[0] += w * v[c].x;
+      acc[1] += w * v[c].y;
+      acc[2] += w * v[c].z;
+      acc[3] += w * v[c].w;
     }
-    *reinterpret_cast<uint32_t*>(optr) = pack_bf16x2(o[0], o[1]);
-    *reinterpret_cast<uint32_t*>(optr + 2) = pack_bf16x2(o[2], o[3]);
+    lmax = cmax;
   }
+  float o[4];
+  for (int d = 0; d < 4; ++d) o[d] = den > 0.0f ? acc[d] / den : 0.0f;
+  uint16_t* optr = out + (int64_t)row * out_row + (int64_t)head * out_head + d0;
+  if (gate) {
+    const uint16_t* gptr = gate + (int64_t)row * g_row + (int64_t)head * g_head;
+    for (int d = 0; d < 4; d += 2) {
+      const uint32_t ob = pack_bf16x2(o[d], o[d + 1]);
+      o[d] = bf16_lo(ob) * sigmoidf_(bf16_lo((uint32_t)gptr[(int64_t)(d0 + d) * g_dim]));
+      o[d + 1] = bf16_hi(ob) * sigmoidf_(bf16_lo((uint32_t)gptr[(int64_t)(d0 + d + 1) * g_dim]));
+    }
+  }
+  *reinterpret_cast<uint32_t*>(optr) = pack_bf16x2(o[0], o[1]);
+  *reinterpret_cast<uint32_t*>(optr + 2) = pack_bf16x2(o[2], o[3]);
 }
 
 struct HeadPlan {
@@ -419,6 +462,17 @@ template <int D, int NKV>
 hipError_t launch_attn(const AttnParams& p, dim3 grid, hipStream_t stream) {
   hipLaunchKernelGGL((sparse_attn_kernel<D, NKV>), grid, dim3(kThreads), 0, stream, p);
   return hipGetLastError();
+}
+
+int launch_merge(const float* part_out, const float* part_lse, int num_splits, int rows,
+                 int num_q_heads, int head_dim, uint16_t* out, int64_t out_row, int64_t out_head,
+                 const uint16_t* gate, int64_t g_row, int64_t g_head, int64_t g_dim,
+                 hipStream_t s) {
+  const int64_t items = (int64_t)rows * num_q_heads * (head_dim / 4);
+  const dim3 grid((unsigned)((items + 255) / 256));
+  hipLaunchKernelGGL(merge_kernel, grid, dim3(256), 0, s, part_out, part_lse, num_splits, rows,
+                     num_q_heads, head_dim, out, out_row, out_head, gate, g_row, g_head, g_dim);
+  return check_launch("qsa_sparse_attention merge launch");
 }
 
 }  // namespace
@@ -473,6 +527,8 @@ extern "C" int qsa_sparse_attention(
     return fail(QSA_ERR_INVALID, "qsa_sparse_attention: logical indices need a block table");
   if (page_size <= 0 || num_blocks < 0 || width < 0)
     return fail(QSA_ERR_INVALID, "qsa_sparse_attention: bad page_size/num_blocks/width");
+  if ((int64_t)num_blocks * page_size > INT32_MAX)
+    return fail(QSA_ERR_UNSUPPORTED, "qsa_sparse_attention: more than 2^31 cache slots");
   if (num_splits < 1 || num_splits > 1024)
     return fail(QSA_ERR_INVALID, "qsa_sparse_attention: num_splits out of range");
   const size_t need = qsa_sparse_attention_workspace_bytes(rows, num_q_heads, head_dim, num_splits);
@@ -486,6 +542,8 @@ extern "C" int qsa_sparse_attention(
                 "multiples of 8 elements");
   if (((uintptr_t)out & 3u) || (out_row_stride | out_head_stride) & 1)
     return fail(QSA_ERR_INVALID, "qsa_sparse_attention: out must be 4-byte aligned with even strides");
+  if (need && ((uintptr_t)workspace & 15u))
+    return fail(QSA_ERR_INVALID, "qsa_sparse_attention: workspace must be 16-byte aligned");
 
   AttnParams p;
   p.q = static_cast<const uint16_t*>(q);
@@ -525,6 +583,7 @@ extern "C" int qsa_sparse_attention(
   p.num_q_heads = num_q_heads;
   p.group = num_q_heads / num_kv_heads;
   p.heads_per_wave = plan.heads_per_wave;
+  p.head_groups = plan.groups;
   p.num_splits = num_splits;
   p.physical = indices_are_physical ? 1 : 0;
   p.scale_log2 = (float)(1.0 / __builtin_sqrt((double)head_dim) * 1.4426950408889634);
@@ -545,13 +604,10 @@ extern "C" int qsa_sparse_attention(
   }
   if (err != hipSuccess)
     return fail(QSA_ERR_HIP, std::string("qsa_sparse_attention launch: ") + hipGetErrorString(err));
-  if (num_splits > 1) {
-    hipLaunchKernelGGL(merge_kernel, dim3(rows), dim3(256), 0, s, p.part_out, p.part_lse,
-                       num_splits, rows, num_q_heads, head_dim, p.out, out_row_stride,
-                       out_head_stride, p.gate, gate_row_stride, gate_head_stride,
-                       gate_dim_stride);
-    return check_launch("qsa_sparse_attention merge launch");
-  }
+  if (num_splits > 1)
+    return launch_merge(p.part_out, p.part_lse, num_splits, rows, num_q_heads, head_dim, p.out,
+                        out_row_stride, out_head_stride, p.gate, gate_row_stride,
+                        gate_head_stride, gate_dim_stride, s);
   return QSA_OK;
 }
 
@@ -568,10 +624,8 @@ extern "C" int qsa_sparse_attention_merge(const float* partial_out, const float*
     return fail(QSA_ERR_INVALID, "qsa_sparse_attention_merge: null tensor pointer");
   if (((uintptr_t)partial_out & 15u) || ((uintptr_t)out & 3u) || (out_row_stride | out_head_stride) & 1)
     return fail(QSA_ERR_INVALID, "qsa_sparse_attention_merge: misaligned partials or output");
-  hipLaunchKernelGGL(merge_kernel, dim3(rows), dim3(256), 0, static_cast<hipStream_t>(stream),
-                     partial_out, partial_lse, num_splits, rows, num_q_heads, head_dim,
-                     static_cast<uint16_t*>(out), out_row_stride, out_head_stride,
-                     static_cast<const uint16_t*>(gate), gate_row_stride, gate_head_stride,
-                     gate_dim_stride);
-  return check_launch("qsa_sparse_attention_merge launch");
+  return launch_merge(partial_out, partial_lse, num_splits, rows, num_q_heads, head_dim,
+                      static_cast<uint16_t*>(out), out_row_stride, out_head_stride,
+                      static_cast<const uint16_t*>(gate), gate_row_stride, gate_head_stride,
+                      gate_dim_stride, static_cast<hipStream_t>(stream));
 }

@@ -8,44 +8,57 @@
 //  * expansion, causal tail, physical slot mapping and counts as
 //    ExpandedWriter (topk.cu:97-180).
 //
-// Algorithm (own design for wave64 + LDS): one workgroup per row holds the
+// Algorithm (own design for wave64 + LDS). One workgroup per row holds the
 // row's keys in registers (blocked: thread t owns ids [t*ITEMS, t*ITEMS+ITEMS)).
-// A radix select narrows the candidate set 8 bits at a time, always starting
-// at the highest bit in which the remaining candidates still differ (found by a
-// block min/max), so clustered scores do not waste passes on a shared prefix.
-// Histograms use LDS atomics with a wave-uniform fast path. When the candidate
-// range collapses to one key T, the selected set is {key > T} plus the first
-// `remaining` ids with key == T, and a block-wide exclusive scan of
-// (count > T, count == T) in id order gives every selected id its output rank.
+// A radix select walks 8-bit digits downward from the highest bit in which the
+// row's keys differ (one block min/max). Each pass builds an LDS histogram
+// (atomics with a wave-uniform fast path) and one wave locates the bin holding
+// the k-th largest key with a DPP scan. The walk stops as soon as that bin
+// holds exactly the number of keys still needed - then the selection is every
+// key >= the bin's smallest possible key - or when all 32 bits are fixed, in
+// which case the remaining slots go to the lowest ids with that exact key.
+// A block-wide exclusive scan of (selected, tied) counts in id order gives
+// each selected id its output rank; ranks land in LDS and the whole output row
+// (expanded slots, causal tail, -1 padding) is written with coalesced stores.
+//
+// The kernel is a chain of short dependent steps, so latency is what counts:
+// every independent load (scores, row metadata, the page-table entry of every
+// block a thread holds, the causal tail's pages) is issued at entry, the
+// barriers order LDS only (so those loads stay in flight through the radix
+// passes), derived row metadata is computed only when the row is written, and
+// reductions and scans are DPP sequences.
+//
 // Rows longer than the register-resident capacity use two passes: exact top-k
 // per 8192-column partition, then exact top-k over the partition winners.
 #include "qsa_common.h"
 #include "../../include/qsa_hip.h"
+
+extern "C" __device__ unsigned int __ockl_wfred_min_u32(unsigned int);
+extern "C" __device__ unsigned int __ockl_wfred_max_u32(unsigned int);
+extern "C" __device__ int __ockl_wfscan_add_i32(int, bool);
 
 namespace qsa {
 namespace {
 
 constexpr int kPartitionColumns = 8192;
 constexpr int kMaxDirectColumns = 16384;  // register-resident capacity: 1024 threads x 16 keys
+constexpr int kMaxTopk = 8192;            // selected ids per row staged in LDS
+constexpr int kTailSlots = 64;            // causal-tail pages fetched ahead of time
 
 template <int THREADS>
-struct SelectShared {
+struct TopkShared {
   uint32_t hist[256];
   uint32_t wmin[THREADS / 64];
   uint32_t wmax[THREADS / 64];
-  int wgt[THREADS / 64];
-  int weq[THREADS / 64];
+  int wsel[THREADS / 64];
+  int wtie[THREADS / 64];
+  int tail_page[kTailSlots];
   int bin;
   int remaining;
+  int bin_count;
 };
 
-// --- writers ---------------------------------------------------------------
-
-struct CompressedWriter {  // topk.cu:90-95
-  int32_t* out;
-  __device__ __forceinline__ void operator()(int rank, int id) const { out[rank] = id; }
-  __device__ __forceinline__ void finish() const {}
-};
+// --- row metadata -------------------------------------------------------------
 
 struct ExpandMeta {
   const int64_t* positions;
@@ -60,82 +73,39 @@ struct ExpandMeta {
   int page_size;
   FastDiv page_div;
   int ratio;
+  FastDiv ratio_div;
   int out_width;
   int physical;
   int store_counts;
 };
 
-struct ExpandWriter {  // topk.cu:107-180
-  int32_t* out;
-  int32_t* count;
-  const int32_t* table_row;
-  int64_t col_stride;
-  int seq_len, complete, tail_start, tail_count;
-  int page_size, table_width, ratio, out_width;
-  FastDiv page_div;
-  bool physical;
-
-  __device__ __forceinline__ int map_token(int t) const {
-    if (t < 0 || t >= seq_len) return -1;
-    if (!physical) return t;
-    const int lp = page_div.div(t);
-    if (lp >= table_width) return -1;
-    const int pp = table_row[lp];
-    return pp >= 0 ? pp * page_size + (t - lp * page_size) : -1;
-  }
-
-  __device__ __forceinline__ void operator()(int rank, int block) const {
-    if (rank >= complete) return;
-    const int first = block * ratio;
-    int32_t* dst = out + (int64_t)rank * ratio * col_stride;
-    if (physical && page_size % ratio == 0) {
-      // The block lies inside one page: one table lookup serves all members.
-      int first_slot = -1;
-      if (first >= 0 && first < seq_len) {
-        const int lp = page_div.div(first);
-        const int pp = lp < table_width ? table_row[lp] : -1;
-        if (pp >= 0) first_slot = pp * page_size + (first - lp * page_size);
-      }
-      for (int o = 0; o < ratio; ++o)
-        dst[(int64_t)o * col_stride] = (first_slot >= 0 && first + o < seq_len) ? first_slot + o : -1;
-      return;
-    }
-    for (int o = 0; o < ratio; ++o) dst[(int64_t)o * col_stride] = map_token(first + o);
-  }
-
-  __device__ __forceinline__ void finish() const {
-    const int expanded = complete * ratio;
-    for (int column = expanded + (int)threadIdx.x; column < out_width; column += blockDim.x) {
-      const int off = column - expanded;
-      out[(int64_t)column * col_stride] =
-          (off < tail_count && off < ratio - 1) ? map_token(tail_start + off) : -1;
-    }
-    if (count && threadIdx.x == 0) *count = min(expanded + tail_count, seq_len);
-  }
+// Raw per-row inputs of the expansion (topk.cu:166-180); everything derived
+// from them is computed when the row is written.
+struct RowMeta {
+  int seq_len;
+  int pos;
+  const int32_t* table_row;  // null unless physical
 };
 
-__device__ __forceinline__ ExpandWriter make_expand_writer(const ExpandMeta& m, int row, int topk,
-                                                           int32_t* out_row) {
-  ExpandWriter w;
-  const int req = m.token_to_req[row];
-  const bool mapped = req >= 0 && req < m.num_requests;
-  w.seq_len = mapped ? m.sequence_lengths[req] : 0;
-  const int pos = (int)m.positions[row];
-  const int p1 = pos + 1;
-  w.complete = max(0, min(min(p1 / m.ratio, w.seq_len / m.ratio), topk));
-  w.tail_start = (p1 / m.ratio) * m.ratio;
-  w.tail_count = p1 - w.tail_start;
-  w.out = out_row;
-  w.count = m.store_counts ? m.counts + row : nullptr;
-  w.table_row = m.physical ? m.table + (int64_t)(mapped ? req : 0) * m.table_row_stride : nullptr;
-  w.col_stride = m.out_col_stride;
-  w.page_size = m.page_size;
-  w.table_width = m.table_width;
-  w.ratio = m.ratio;
-  w.out_width = m.out_width;
-  w.page_div = m.page_div;
-  w.physical = m.physical != 0;
-  return w;
+__device__ __forceinline__ int tail_start_of(int pos, int ratio) { return ((pos + 1) / ratio) * ratio; }
+
+// Logical page of token t, or -1 when t has no page-table entry to read.
+__device__ __forceinline__ int token_page(const ExpandMeta& m, int t) {
+  if (t < 0) return -1;
+  const int lp = m.page_div.div(t);
+  return lp < m.table_width ? lp : -1;
+}
+
+// Physical slot of token t given its prefetched physical page (topk.cu:116-125).
+__device__ __forceinline__ int slot_of(const ExpandMeta& m, const RowMeta& r, int t, int pp) {
+  if (t < 0 || t >= r.seq_len) return -1;
+  if (!m.physical) return t;
+  if (pp < 0) return -1;
+  return pp * m.page_size + (t - m.page_div.div(t) * m.page_size);
+}
+
+__device__ __forceinline__ int table_entry(const RowMeta& r, int lp) {
+  return (r.table_row && lp >= 0) ? r.table_row[lp] : -1;
 }
 
 // --- loaders ---------------------------------------------------------------
@@ -143,36 +113,51 @@ __device__ __forceinline__ ExpandWriter make_expand_writer(const ExpandMeta& m, 
 struct DirectLoader {  // ids start + i over a contiguous score row
   const float* scores;
   int start;
-  __device__ __forceinline__ uint32_t key(int i) const {
-    return __builtin_bit_cast(uint32_t, scores[start + i]);
-  }
   __device__ __forceinline__ int id(int i) const { return start + i; }
+  template <int ITEMS>
+  __device__ __forceinline__ void load(int base, int limit, uint32_t (&key)[ITEMS]) const {
+    const float* p = scores + start + base;
+    if (ITEMS % 4 == 0 && base + ITEMS <= limit && (((uintptr_t)p) & 15u) == 0) {
+#pragma unroll
+      for (int j = 0; j < ITEMS; j += 4) {
+        const u32x4 v = load_u32x4(p + j);
+        key[j] = v[0];
+        key[j + 1] = v[1];
+        key[j + 2] = v[2];
+        key[j + 3] = v[3];
+      }
+      return;
+    }
+#pragma unroll
+    for (int j = 0; j < ITEMS; ++j)
+      key[j] = base + j < limit ? __builtin_bit_cast(uint32_t, p[j]) : 0u;
+  }
 };
 
 struct IndirectLoader {  // candidate list of ids into a score row
   const float* scores;
   const int32_t* ids;
-  __device__ __forceinline__ uint32_t key(int i) const {
-    return __builtin_bit_cast(uint32_t, scores[ids[i]]);
-  }
   __device__ __forceinline__ int id(int i) const { return ids[i]; }
+  template <int ITEMS>
+  __device__ __forceinline__ void load(int base, int limit, uint32_t (&key)[ITEMS]) const {
+#pragma unroll
+    for (int j = 0; j < ITEMS; ++j)
+      key[j] = base + j < limit ? __builtin_bit_cast(uint32_t, scores[ids[base + j]]) : 0u;
+  }
 };
 
-// --- block primitives ------------------------------------------------------
+// --- block primitives (DPP wave reductions/scans + one LDS exchange) --------
 
 template <int THREADS>
-__device__ __forceinline__ void block_minmax(uint32_t& lo, uint32_t& hi, SelectShared<THREADS>& sh) {
+__device__ __forceinline__ void block_minmax(uint32_t& lo, uint32_t& hi, TopkShared<THREADS>& sh) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-#pragma unroll
-  for (int off = 32; off > 0; off >>= 1) {
-    lo = min(lo, (uint32_t)__shfl_xor((int)lo, off, 64));
-    hi = max(hi, (uint32_t)__shfl_xor((int)hi, off, 64));
-  }
+  lo = __ockl_wfred_min_u32(lo);
+  hi = __ockl_wfred_max_u32(hi);
   if (lane == 0) {
     sh.wmin[wave] = lo;
     sh.wmax[wave] = hi;
   }
-  __syncthreads();
+  lds_barrier();
   lo = 0xffffffffu;
   hi = 0u;
 #pragma unroll
@@ -180,154 +165,253 @@ __device__ __forceinline__ void block_minmax(uint32_t& lo, uint32_t& hi, SelectS
     lo = min(lo, sh.wmin[w]);
     hi = max(hi, sh.wmax[w]);
   }
-  __syncthreads();
 }
 
 // Exclusive scan of two counters over threads in thread order.
 template <int THREADS>
-__device__ __forceinline__ void block_scan2(int& a, int& b, SelectShared<THREADS>& sh) {
+__device__ __forceinline__ void block_scan2(int& a, int& b, TopkShared<THREADS>& sh) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  int ia = a, ib = b;
-#pragma unroll
-  for (int off = 1; off < 64; off <<= 1) {
-    const int ta = __shfl_up(ia, off, 64);
-    const int tb = __shfl_up(ib, off, 64);
-    if (lane >= off) {
-      ia += ta;
-      ib += tb;
-    }
-  }
+  const int ea = __ockl_wfscan_add_i32(a, false);
+  const int eb = __ockl_wfscan_add_i32(b, false);
   if (lane == 63) {
-    sh.wgt[wave] = ia;
-    sh.weq[wave] = ib;
+    sh.wsel[wave] = ea + a;
+    sh.wtie[wave] = eb + b;
   }
-  __syncthreads();
+  lds_barrier();
   int pa = 0, pb = 0;
 #pragma unroll
   for (int w = 0; w < THREADS / 64; ++w) {
     if (w < wave) {
-      pa += sh.wgt[w];
-      pb += sh.weq[w];
+      pa += sh.wsel[w];
+      pb += sh.wtie[w];
     }
   }
-  a = pa + ia - a;
-  b = pb + ib - b;
+  a = pa + ea;
+  b = pb + eb;
 }
 
-// Exact top-k of `length` keys delivered by `load`; emits (rank, id) pairs in
-// any order with ranks = position in ascending-id order. Requires
-// length <= THREADS * ITEMS when length > topk.
-template <int THREADS, int ITEMS, typename Loader, typename Writer>
-__device__ void select_topk(const Loader& load, int length, int topk, const Writer& write,
-                            SelectShared<THREADS>& sh) {
+// --- selection --------------------------------------------------------------
+
+// Exact top-k of `length` (> topk) keys in registers. Writes the selected ids
+// in ascending-id order to sel[0..topk) and the matching prefetched values of
+// aux to sel[topk..2 topk).
+template <int THREADS, int ITEMS, typename Loader>
+__device__ void select_long(const Loader& load, int length, int topk, const uint32_t (&key)[ITEMS],
+                            const int (&aux)[ITEMS], TopkShared<THREADS>& sh, int* sel) {
   const int tid = threadIdx.x;
-  if (length <= topk) {
-    for (int i = tid; i < topk; i += THREADS) write(i, i < length ? load.id(i) : -1);
-    return;
-  }
+  const int lane = tid & 63;
   const int base = tid * ITEMS;
-  uint32_t key[ITEMS];
   uint32_t active = 0;
   uint32_t lo = 0xffffffffu, hi = 0u;
 #pragma unroll
   for (int j = 0; j < ITEMS; ++j) {
-    const bool a = base + j < length;
-    key[j] = a ? load.key(base + j) : 0u;
-    if (a) {
+    if (base + j < length) {
       active |= 1u << j;
       lo = min(lo, key[j]);
       hi = max(hi, key[j]);
     }
   }
-  if (tid < 256) sh.hist[tid] = 0u;
-  for (int b = tid + THREADS; b < 256; b += THREADS) sh.hist[b] = 0u;
   block_minmax<THREADS>(lo, hi, sh);
 
-  const int lane = tid & 63;
+  // Result: selected = {key > thr} + first `remaining` ids with key == thr
+  // (tie mode), or {key >= thr} (ge mode).
+  uint32_t thr = lo;
+  bool ge = false;
   int remaining = topk;
-  uint32_t cand = active;
-  while (lo != hi) {
+  if (lo != hi) {
     const int high_bit = 31 - __builtin_clz(lo ^ hi);
-    const int shift = high_bit > 7 ? high_bit - 7 : 0;
+    int shift = high_bit > 7 ? high_bit - 7 : 0;
+    uint32_t prefix = shift + 8 >= 32 ? 0u : (lo & ~((1u << (shift + 8)) - 1u));
+    uint32_t cand = active;
+    for (;;) {
 #pragma unroll
-    for (int j = 0; j < ITEMS; ++j) {
-      const bool a = (cand >> j) & 1u;
-      const int d = (int)((key[j] >> shift) & 255u);
-      const uint64_t am = __ballot(a);
-      if (am == 0) continue;
-      const int first = __builtin_ctzll(am);
-      const int d_first = __shfl(d, first, 64);
-      const uint64_t same = __ballot(a && d == d_first);
-      if (same == am) {
-        if (lane == first) atomicAdd(&sh.hist[d], (uint32_t)__builtin_popcountll(am));
-      } else if (a) {
-        atomicAdd(&sh.hist[d], 1u);
-      }
-    }
-    __syncthreads();
-    if (tid < 64) {
-      // Suffix counts over 256 bins: lane owns bins 4*lane .. 4*lane+3.
-      uint32_t h[4];
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        h[i] = sh.hist[4 * lane + i];
-        sh.hist[4 * lane + i] = 0u;
-      }
-      const int tot = (int)(h[0] + h[1] + h[2] + h[3]);
-      int suf = tot;
-#pragma unroll
-      for (int off = 1; off < 64; off <<= 1) {
-        const int t = __shfl_down(suf, off, 64);
-        if (lane + off < 64) suf += t;
-      }
-      int above = suf - tot;  // candidates in bins above this lane's bins
-#pragma unroll
-      for (int i = 3; i >= 0; --i) {
-        if (above < remaining && above + (int)h[i] >= remaining) {
-          sh.bin = 4 * lane + i;
-          sh.remaining = remaining - above;
+      for (int j = 0; j < ITEMS; ++j) {
+        const bool a = (cand >> j) & 1u;
+        const int d = (int)((key[j] >> shift) & 255u);
+        const uint64_t am = __ballot(a);
+        if (am == 0) continue;
+        const int first = __builtin_ctzll(am);
+        const int d_first = __builtin_amdgcn_readlane(d, first);
+        const uint64_t same = __ballot(a && d == d_first);
+        if (same == am) {
+          if (lane == first) atomicAdd(&sh.hist[d], (uint32_t)__builtin_popcountll(am));
+        } else if (a) {
+          atomicAdd(&sh.hist[d], 1u);
         }
-        above += (int)h[i];
       }
-    }
-    __syncthreads();
-    const uint32_t bin = (uint32_t)sh.bin;
-    remaining = sh.remaining;
-    uint32_t next = 0;
-    lo = 0xffffffffu;
-    hi = 0u;
+      lds_barrier();
+      if (tid < 64) {
+        // Bin of the remaining-th largest candidate; lane owns bins 4*lane..+3.
+        uint32_t h[4];
 #pragma unroll
-    for (int j = 0; j < ITEMS; ++j) {
-      if (((cand >> j) & 1u) && ((key[j] >> shift) & 255u) == bin) {
-        next |= 1u << j;
-        lo = min(lo, key[j]);
-        hi = max(hi, key[j]);
+        for (int i = 0; i < 4; ++i) {
+          h[i] = sh.hist[4 * lane + i];
+          sh.hist[4 * lane + i] = 0u;
+        }
+        const int tot = (int)(h[0] + h[1] + h[2] + h[3]);
+        const int excl = __ockl_wfscan_add_i32(tot, false);
+        const int total = __builtin_amdgcn_readlane(excl + tot, 63);
+        int above = total - excl - tot;
+#pragma unroll
+        for (int i = 3; i >= 0; --i) {
+          if (above < remaining && above + (int)h[i] >= remaining) {
+            sh.bin = 4 * lane + i;
+            sh.remaining = remaining - above;
+            sh.bin_count = (int)h[i];
+          }
+          above += (int)h[i];
+        }
       }
+      lds_barrier();
+      const uint32_t bin = (uint32_t)sh.bin;
+      const int need = sh.remaining;
+      const int in_bin = sh.bin_count;
+      prefix |= bin << shift;
+      if (in_bin == need) {  // the whole bin is taken: every key >= its smallest key
+        thr = prefix;
+        ge = true;
+        break;
+      }
+      uint32_t next = 0;
+#pragma unroll
+      for (int j = 0; j < ITEMS; ++j)
+        if (((cand >> j) & 1u) && ((key[j] >> shift) & 255u) == bin) next |= 1u << j;
+      cand = next;
+      remaining = need;
+      if (shift == 0) {  // all 32 bits fixed: the bin holds one key value
+        thr = prefix;
+        break;
+      }
+      shift = shift >= 8 ? shift - 8 : 0;
     }
-    cand = next;
-    block_minmax<THREADS>(lo, hi, sh);
   }
 
-  const uint32_t threshold = lo;
-  int gt = 0, eq = 0;
+  int n_sel = 0, n_tie = 0;
 #pragma unroll
   for (int j = 0; j < ITEMS; ++j) {
     if ((active >> j) & 1u) {
-      gt += key[j] > threshold;
-      eq += key[j] == threshold;
+      n_sel += ge ? key[j] >= thr : key[j] > thr;
+      n_tie += !ge && key[j] == thr;
     }
   }
-  block_scan2<THREADS>(gt, eq, sh);
+  block_scan2<THREADS>(n_sel, n_tie, sh);
 #pragma unroll
   for (int j = 0; j < ITEMS; ++j) {
     if (!((active >> j) & 1u)) continue;
-    if (key[j] > threshold) {
-      write(gt + min(eq, remaining), load.id(base + j));
-      ++gt;
-    } else if (key[j] == threshold) {
-      if (eq < remaining) write(gt + eq, load.id(base + j));
-      ++eq;
+    const bool strict = ge ? key[j] >= thr : key[j] > thr;
+    int rank = -1;
+    if (strict) {
+      rank = n_sel + min(n_tie, remaining);
+      ++n_sel;
+    } else if (!ge && key[j] == thr) {
+      if (n_tie < remaining) rank = n_sel + n_tie;
+      ++n_tie;
     }
+    if (rank >= 0) {
+      sel[rank] = load.id(base + j);
+      sel[topk + rank] = aux[j];
+    }
+  }
+}
+
+// Writes one expanded output row (coalesced over columns) from ranked block
+// ids in sel[0..topk) and their first-token physical pages in sel[topk..).
+__device__ __forceinline__ void write_expanded(const ExpandMeta& m, const RowMeta& r, int row,
+                                               int topk, const int* sel, const int* tail_page,
+                                               int32_t* out) {
+  const int p1 = r.pos + 1;
+  const int complete = max(0, min(min(p1 / m.ratio, r.seq_len / m.ratio), topk));
+  const int tail_start = tail_start_of(r.pos, m.ratio);
+  const int tail_count = p1 - tail_start;
+  const int expanded = complete * m.ratio;
+  const bool block_in_page = m.physical && (m.page_size % m.ratio == 0);
+  for (int c = threadIdx.x; c < m.out_width; c += blockDim.x) {
+    int v = -1;
+    if (c < expanded) {
+      const int rank = m.ratio_div.div(c);
+      const int o = c - rank * m.ratio;
+      const int block = sel[rank];
+      if (block >= 0) {
+        const int first = block * m.ratio;
+        if (!m.physical) {
+          v = slot_of(m, r, first + o, 0);
+        } else if (block_in_page) {
+          // The block lies inside one page (topk.cu:134-146).
+          const int s0 = slot_of(m, r, first, sel[topk + rank]);
+          v = (s0 >= 0 && first + o < r.seq_len) ? s0 + o : -1;
+        } else {
+          const int t = first + o;
+          v = slot_of(m, r, t, table_entry(r, token_page(m, t)));
+        }
+      }
+    } else {
+      const int off = c - expanded;
+      if (off < tail_count && off < m.ratio - 1) {
+        const int t = tail_start + off;
+        const int pp = !m.physical ? 0
+                       : (off < kTailSlots ? tail_page[off] : table_entry(r, token_page(m, t)));
+        v = slot_of(m, r, t, pp);
+      }
+    }
+    out[(int64_t)c * m.out_col_stride] = v;
+  }
+  if (m.store_counts && threadIdx.x == 0) m.counts[row] = min(expanded + tail_count, r.seq_len);
+}
+
+// One row: issue every independent load first, select, then write the row.
+// `limit` bounds the speculative score loads; rows longer than topk must have
+// length <= min(limit, THREADS * ITEMS).
+template <int THREADS, int ITEMS, bool EXPAND, typename Loader>
+__device__ void process_row(const Loader& load, int limit, int length_raw, int clamp, int topk,
+                            const ExpandMeta& m, int row, int32_t* out,
+                            TopkShared<THREADS>& sh, int* sel) {
+  const int tid = threadIdx.x;
+  RowMeta r = {0, 0, nullptr};
+  int req = -1;
+  if (EXPAND) {
+    req = m.token_to_req[row];
+    r.pos = (int)m.positions[row];
+  }
+  uint32_t key[ITEMS];
+  load.template load<ITEMS>(tid * ITEMS, limit, key);
+  if (tid < 256) sh.hist[tid] = 0u;
+  for (int b = tid + THREADS; b < 256; b += THREADS) sh.hist[b] = 0u;
+
+  // Page-table entries this thread's blocks and the causal tail will need.
+  int aux[ITEMS];
+  int tail_pp = -1;
+  if (EXPAND) {
+    const bool mapped = req >= 0 && req < m.num_requests;
+    r.seq_len = mapped ? m.sequence_lengths[req] : 0;
+    r.table_row = m.physical ? m.table + (int64_t)(mapped ? req : 0) * m.table_row_stride : nullptr;
+#pragma unroll
+    for (int j = 0; j < ITEMS; ++j) {
+      const int i = tid * ITEMS + j;
+      aux[j] = (i < limit) ? table_entry(r, token_page(m, load.id(i) * m.ratio)) : -1;
+    }
+    if (tid < kTailSlots && tid < m.ratio - 1)
+      tail_pp = table_entry(r, token_page(m, tail_start_of(r.pos, m.ratio) + tid));
+  } else {
+#pragma unroll
+    for (int j = 0; j < ITEMS; ++j) aux[j] = 0;
+  }
+
+  const int length = length_raw > topk ? min(length_raw, clamp) : length_raw;
+  if (length > topk) {
+    select_long<THREADS, ITEMS>(load, length, topk, key, aux, sh, sel);
+  } else {
+    for (int i = tid; i < topk; i += THREADS) {
+      const int id = i < length ? load.id(i) : -1;
+      sel[i] = id;
+      sel[topk + i] = (EXPAND && id >= 0) ? table_entry(r, token_page(m, id * m.ratio)) : -1;
+    }
+  }
+  if (EXPAND && tid < kTailSlots && tid < m.ratio - 1) sh.tail_page[tid] = tail_pp;
+  lds_barrier();
+  if (EXPAND) {
+    write_expanded(m, r, row, topk, sel, sh.tail_page, out);
+  } else {
+    for (int c = tid; c < topk; c += THREADS) out[c] = sel[c];
   }
 }
 
@@ -343,7 +427,6 @@ struct TopkArgs {
   int parts;
   int topk;
   int cols;  // row width: lengths beyond it are clamped so no read leaves the row
-  int expand;
   ExpandMeta meta;
 };
 
@@ -355,89 +438,79 @@ __device__ __forceinline__ int row_length(const TopkArgs& a, int row) {
   return length > a.topk ? min(length, a.cols) : length;
 }
 
-template <int THREADS, int ITEMS>
+template <int THREADS, int ITEMS, bool EXPAND>
 __global__ __launch_bounds__(THREADS) void topk_direct_kernel(const TopkArgs a) {
-  __shared__ SelectShared<THREADS> sh;
+  __shared__ TopkShared<THREADS> sh;
+  extern __shared__ int sel[];
   const int row = blockIdx.x;
   const float* srow = a.scores + (int64_t)row * a.score_row_stride;
-  int32_t* orow = a.out + (int64_t)row * a.out_row_stride;
-  const DirectLoader load{srow, 0};
-  const int length = row_length(a, row);
-  if (a.expand) {
-    const ExpandWriter w = make_expand_writer(a.meta, row, a.topk, orow);
-    select_topk<THREADS, ITEMS>(load, length, a.topk, w, sh);
-    w.finish();
-  } else {
-    select_topk<THREADS, ITEMS>(load, length, a.topk, CompressedWriter{orow}, sh);
-  }
+  process_row<THREADS, ITEMS, EXPAND>(DirectLoader{srow, 0}, a.cols, a.lengths[row], a.cols,
+                                      a.topk, a.meta, row, a.out + (int64_t)row * a.out_row_stride,
+                                      sh, sel);
 }
 
 // Pass 1 of long rows: rows short enough for one pass finish in partition 0.
-template <int THREADS, int ITEMS>
+template <int THREADS, int ITEMS, bool EXPAND>
 __global__ __launch_bounds__(THREADS) void topk_partition_kernel(const TopkArgs a) {
-  __shared__ SelectShared<THREADS> sh;
+  __shared__ TopkShared<THREADS> sh;
+  extern __shared__ int sel[];
   const int row = blockIdx.x;
   const int part = blockIdx.y;
   const int length = row_length(a, row);
   const float* srow = a.scores + (int64_t)row * a.score_row_stride;
   if (length <= kPartitionColumns) {
-    if (part != 0) return;
-    int32_t* orow = a.out + (int64_t)row * a.out_row_stride;
-    const DirectLoader load{srow, 0};
-    if (a.expand) {
-      const ExpandWriter w = make_expand_writer(a.meta, row, a.topk, orow);
-      select_topk<THREADS, ITEMS>(load, length, a.topk, w, sh);
-      w.finish();
-    } else {
-      select_topk<THREADS, ITEMS>(load, length, a.topk, CompressedWriter{orow}, sh);
-    }
+    if (part == 0)
+      process_row<THREADS, ITEMS, EXPAND>(DirectLoader{srow, 0}, length, length, length, a.topk,
+                                          a.meta, row, a.out + (int64_t)row * a.out_row_stride,
+                                          sh, sel);
     return;
   }
   const int start = part * kPartitionColumns;
   if (start >= length) return;
   const int count = min(kPartitionColumns, length - start);
   int32_t* prow = a.partial + ((int64_t)row * a.parts + part) * a.topk;
-  select_topk<THREADS, ITEMS>(DirectLoader{srow, start}, count, a.topk, CompressedWriter{prow}, sh);
+  process_row<THREADS, ITEMS, false>(DirectLoader{srow, start}, count, count, count, a.topk,
+                                     a.meta, row, prow, sh, sel);
 }
 
 // Pass 2: exact top-k over the concatenated partition winners (ascending ids).
-template <int THREADS, int ITEMS>
+template <int THREADS, int ITEMS, bool EXPAND>
 __global__ __launch_bounds__(THREADS) void topk_merge_kernel(const TopkArgs a) {
-  __shared__ SelectShared<THREADS> sh;
+  __shared__ TopkShared<THREADS> sh;
+  extern __shared__ int sel[];
   const int row = blockIdx.x;
   const int length = row_length(a, row);
   if (length <= kPartitionColumns) return;
   const int count = (length / kPartitionColumns) * a.topk + min(length % kPartitionColumns, a.topk);
   const float* srow = a.scores + (int64_t)row * a.score_row_stride;
-  int32_t* orow = a.out + (int64_t)row * a.out_row_stride;
   const IndirectLoader load{srow, a.partial + (int64_t)row * a.parts * a.topk};
-  if (a.expand) {
-    const ExpandWriter w = make_expand_writer(a.meta, row, a.topk, orow);
-    select_topk<THREADS, ITEMS>(load, count, a.topk, w, sh);
-    w.finish();
-  } else {
-    select_topk<THREADS, ITEMS>(load, count, a.topk, CompressedWriter{orow}, sh);
-  }
+  process_row<THREADS, ITEMS, EXPAND>(load, count, count, count, a.topk, a.meta, row,
+                                      a.out + (int64_t)row * a.out_row_stride, sh, sel);
 }
 
-template <int THREADS, int ITEMS>
-hipError_t launch_direct(const TopkArgs& a, int rows, hipStream_t s) {
-  hipLaunchKernelGGL((topk_direct_kernel<THREADS, ITEMS>), dim3(rows), dim3(THREADS), 0, s, a);
+template <int THREADS, int ITEMS, bool EXPAND>
+hipError_t launch_direct(const TopkArgs& a, int rows, size_t lds, hipStream_t s) {
+  hipLaunchKernelGGL((topk_direct_kernel<THREADS, ITEMS, EXPAND>), dim3(rows), dim3(THREADS), lds,
+                     s, a);
   return hipGetLastError();
 }
 
 int partitions_for(int cols) { return (cols + kPartitionColumns - 1) / kPartitionColumns; }
 
+template <bool EXPAND>
 int launch_topk(TopkArgs a, int rows, int cols, void* workspace, size_t workspace_bytes,
                 hipStream_t s) {
   if (rows == 0) return QSA_OK;
+  if (a.topk > kMaxTopk)
+    return fail(QSA_ERR_UNSUPPORTED, "qsa_topk: more than 8192 selected blocks per row");
+  const size_t lds = (size_t)2 * a.topk * sizeof(int);
   hipError_t err;
   if (cols <= kMaxDirectColumns) {
-    if (cols <= 1024) err = launch_direct<256, 4>(a, rows, s);
-    else if (cols <= 2048) err = launch_direct<256, 8>(a, rows, s);
-    else if (cols <= 4096) err = launch_direct<512, 8>(a, rows, s);
-    else if (cols <= 8192) err = launch_direct<1024, 8>(a, rows, s);
-    else err = launch_direct<1024, 16>(a, rows, s);
+    if (cols <= 1024) err = launch_direct<256, 4, EXPAND>(a, rows, lds, s);
+    else if (cols <= 2048) err = launch_direct<256, 8, EXPAND>(a, rows, lds, s);
+    else if (cols <= 4096) err = launch_direct<512, 8, EXPAND>(a, rows, lds, s);
+    else if (cols <= 8192) err = launch_direct<1024, 8, EXPAND>(a, rows, lds, s);
+    else err = launch_direct<1024, 16, EXPAND>(a, rows, lds, s);
     if (err != hipSuccess) return fail(QSA_ERR_HIP, std::string("qsa_topk launch: ") + hipGetErrorString(err));
     return QSA_OK;
   }
@@ -445,16 +518,17 @@ int launch_topk(TopkArgs a, int rows, int cols, void* workspace, size_t workspac
   if ((int64_t)parts * a.topk > kMaxDirectColumns)
     return fail(QSA_ERR_UNSUPPORTED, "qsa_topk: partition winners exceed 16384 candidates");
   if (a.topk > kPartitionColumns)
-    return fail(QSA_ERR_UNSUPPORTED, "qsa_topk: topk above 8192 with rows above 32768 columns");
+    return fail(QSA_ERR_UNSUPPORTED, "qsa_topk: topk above 8192 with rows above 16384 columns");
   const size_t need = (size_t)rows * parts * a.topk * sizeof(int32_t);
   if (!workspace || workspace_bytes < need)
     return fail(QSA_ERR_WORKSPACE, "qsa_topk: workspace too small for partition winners");
   a.partial = static_cast<int32_t*>(workspace);
   a.parts = parts;
-  hipLaunchKernelGGL((topk_partition_kernel<1024, 8>), dim3(rows, parts), dim3(1024), 0, s, a);
+  hipLaunchKernelGGL((topk_partition_kernel<1024, 8, EXPAND>), dim3(rows, parts), dim3(1024), lds,
+                     s, a);
   if ((err = hipGetLastError()) != hipSuccess)
     return fail(QSA_ERR_HIP, std::string("qsa_topk partition launch: ") + hipGetErrorString(err));
-  hipLaunchKernelGGL((topk_merge_kernel<1024, 16>), dim3(rows), dim3(1024), 0, s, a);
+  hipLaunchKernelGGL((topk_merge_kernel<1024, 16, EXPAND>), dim3(rows), dim3(1024), lds, s, a);
   if ((err = hipGetLastError()) != hipSuccess)
     return fail(QSA_ERR_HIP, std::string("qsa_topk merge launch: ") + hipGetErrorString(err));
   return QSA_OK;
@@ -493,8 +567,12 @@ extern "C" int qsa_topk(const float* scores, int64_t score_row_stride, int rows,
   a.out_row_stride = output_row_stride;
   a.topk = topk;
   a.cols = cols;
-  a.expand = 0;
-  return launch_topk(a, rows, cols, workspace, workspace_bytes, static_cast<hipStream_t>(stream));
+  a.meta.ratio = 1;
+  a.meta.ratio_div = FastDiv::make(1);
+  a.meta.page_size = 1;
+  a.meta.page_div = FastDiv::make(1);
+  return launch_topk<false>(a, rows, cols, workspace, workspace_bytes,
+                            static_cast<hipStream_t>(stream));
 }
 
 extern "C" int qsa_topk_expand(const float* scores, int64_t score_row_stride, int rows, int cols,
@@ -523,7 +601,6 @@ extern "C" int qsa_topk_expand(const float* scores, int64_t score_row_stride, in
   a.out_row_stride = output_row_stride;
   a.topk = topk;
   a.cols = cols;
-  a.expand = 1;
   a.meta.positions = positions;
   a.meta.sequence_lengths = sequence_lengths;
   a.meta.token_to_req = token_to_req;
@@ -536,8 +613,10 @@ extern "C" int qsa_topk_expand(const float* scores, int64_t score_row_stride, in
   a.meta.page_size = page_size > 0 ? page_size : 1;
   a.meta.page_div = FastDiv::make(page_size > 0 ? page_size : 1);
   a.meta.ratio = ratio;
+  a.meta.ratio_div = FastDiv::make(ratio);
   a.meta.out_width = output_width;
   a.meta.physical = physical ? 1 : 0;
   a.meta.store_counts = store_counts ? 1 : 0;
-  return launch_topk(a, rows, cols, workspace, workspace_bytes, static_cast<hipStream_t>(stream));
+  return launch_topk<true>(a, rows, cols, workspace, workspace_bytes,
+                           static_cast<hipStream_t>(stream));
 }
