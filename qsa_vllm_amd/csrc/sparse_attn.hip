@@ -4,7 +4,7 @@
 // (split-K online softmax in the log2 domain, P rounded to bf16 before P.V,
 // normalised fp32 partials + log2-LSE merge, optional bf16(o)*sigmoid(gate)).
 //
-// Work decomposition. One workgroup = 4 waves handles (row, split, head
+// Work decomposition. One workgroup of WAVES waves handles (row, split, head
 // group). A head group is 16 query-head slots sharing NKV kv heads (GQA group
 // G, NKV*G <= 16). Each wave walks 32-token tiles of the row's index list:
 //
@@ -19,18 +19,26 @@
 //       the lane's own softmax numerators, so P never leaves registers and the
 //       per-head rescale factor lives in the lane that owns that head.
 //
-// While a tile's K/V loads are in flight the wave already resolves the next
-// tile's slots (index loads, and block-table lookups for logical indices), so
-// only the K/V latency is exposed per tile. Invalid slots read a block of
-// zeros in device memory instead of K/V, so no per-element masking is needed
-// beyond the -inf score.
+// Load schedule. A wave's global loads complete in issue order, so the tile
+// loop is a two-stage pipeline over the K and V halves of a tile:
 //
-// The 4 waves merge (max, sum, O) through LDS. With one split the workgroup
+//   Q.K + softmax (t) | resolve slots, issue K (t+W) | P.V (t) |
+//   issue index loads (t+2W), issue V (t+W)
+//
+// Every wait is for the oldest group in flight, and the next tile's K (V)
+// bytes stream in while P.V (the next Q.K) computes, so a wave never leaves
+// the memory system idle behind its own arithmetic. sched_barrier pins that
+// issue order against the scheduler. Invalid slots read a block of zeros in
+// device memory instead of K/V, so no per-element masking is needed beyond
+// the -inf score. Logical indices add a dependent block-table load per slot;
+// it waits behind the tile in flight, so the physical form is the fast one.
+//
+// The waves merge (max, sum, O) through LDS. With one split the workgroup
 // writes the bf16 output (and gate); with several it writes an fp32 partial +
-// log2-LSE and a second kernel merges them. (Merging in the last-arriving
-// workgroup needs device-scope release/acquire fences, which on gfx950 write
-// back and invalidate the XCD's whole L2 per wave; measured, that cost far
-// more than the separate launch.)
+// log2-LSE and a second kernel merges them. Merging in the last-arriving
+// workgroup instead was measured slower on gfx950: device-scope release
+// fences write back the XCD's L2, and write-through partial stores cost more
+// than the second launch.
 #include "qsa_common.h"
 #include "../../include/qsa_hip.h"
 
@@ -39,11 +47,10 @@
 namespace qsa {
 namespace {
 
-constexpr int kWaves = 4;
-constexpr int kThreads = 64 * kWaves;
 constexpr int kTile = 32;
 constexpr float kInitMax = -1.0e20f;  // finite running-max seed (ops/qsa.py:173)
 constexpr int kMergeChunk = 8;        // split partials a merge thread loads at once
+constexpr int kCUs = 256;             // compute units of an MI355X
 
 struct AttnParams {
   const uint16_t* q;
@@ -74,7 +81,6 @@ struct AttnParams {
   int num_q_heads;
   int group;
   int heads_per_wave;
-  int head_groups;
   int num_splits;
   int physical;
   float scale_log2;
@@ -82,12 +88,17 @@ struct AttnParams {
 
 __device__ __forceinline__ float sigmoidf_(float x) { return 1.0f / (1.0f + __expf(-x)); }
 
-// Validated physical slot (page * page_size + offset) of index column `col`,
+#define QSA_SCHED_FENCE() __builtin_amdgcn_sched_barrier(0)
+
+// Index-list entry of column `col`, -1 past the row's valid count.
+__device__ __forceinline__ int index_at(const int32_t* irow, int col, int n_valid) {
+  return col < n_valid ? irow[col] : -1;
+}
+
+// Validated physical slot (page * page_size + offset) of index value `tok`,
 // or -1 (ops/qsa.py:186-212).
-__device__ __forceinline__ int resolve_slot(const AttnParams& p, const int32_t* irow,
-                                            const int32_t* trow, bool req_ok, int col,
-                                            int n_valid) {
-  const int tok = col < n_valid ? irow[col] : -1;
+__device__ __forceinline__ int resolve_slot(const AttnParams& p, const int32_t* trow, bool req_ok,
+                                            int tok) {
   if (tok < 0) return -1;
   const int lp = p.page_div.div(tok);
   if (p.physical) return lp < p.num_blocks ? tok : -1;
@@ -116,22 +127,153 @@ struct VRow<64> {
   static __device__ __forceinline__ type load(const char* ptr) { return load_u32x2(ptr); }
 };
 
-// Token of K-operand slot u (0,1) and V-operand slot i (0..7) inside a tile.
-__device__ __forceinline__ int k_col(int u, int n) { return 16 * u + n; }
-__device__ __forceinline__ int v_col(int i, int g) { return 16 * (i >> 2) + 4 * g + (i & 3); }
+// One tile's operands in registers: K rows for tokens 16 u + n, V rows for
+// tokens 16 (i / 4) + 4 g + i % 4.
+template <int D, int NKV>
+struct TileK {
+  u32x4 r[NKV][2][D / 32];
+};
+template <int D, int NKV>
+struct TileV {
+  typename VRow<D>::type r[NKV][8];
+  uint32_t mask;  // bit i: token slot i is valid
+};
+
+__device__ __forceinline__ int k_col(int tile, int u, int n) { return tile * kTile + 16 * u + n; }
+__device__ __forceinline__ int v_col(int tile, int i, int g) {
+  return tile * kTile + 16 * (i >> 2) + 4 * g + (i & 3);
+}
+
+// Raw index entries of a tile (-1 when the tile is past the split's end).
+struct TileIdx {
+  int k[2];
+  int v[8];
+};
+__device__ __forceinline__ void load_tile_idx(const int32_t* irow, int tile, int t_end,
+                                              int n_valid, int n, int g, TileIdx& r) {
+  const bool ok = tile < t_end;
+#pragma unroll
+  for (int u = 0; u < 2; ++u) r.k[u] = ok ? index_at(irow, k_col(tile, u, n), n_valid) : -1;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) r.v[i] = ok ? index_at(irow, v_col(tile, i, g), n_valid) : -1;
+}
+
+template <int D, int NKV>
+__device__ __forceinline__ void issue_k(const AttnParams& p, const int (&slot)[2],
+                                        const int64_t (&khead)[NKV], int g, TileK<D, NKV>& K) {
+  const char* zero = reinterpret_cast<const char*>(g_qsa_zero_rows);
+#pragma unroll
+  for (int u = 0; u < 2; ++u) {
+    const int64_t off = slot[u] >= 0 ? slot_offset(p, slot[u], p.kb, p.kt) : 0;
+#pragma unroll
+    for (int v = 0; v < NKV; ++v) {
+      const char* base = slot[u] >= 0 ? p.k + off + khead[v] : zero;
+#pragma unroll
+      for (int s = 0; s < D / 32; ++s) K.r[v][u][s] = load_u32x4(base + (32 * s + 8 * g) * 2);
+    }
+  }
+}
+
+template <int D, int NKV>
+__device__ __forceinline__ void issue_v(const AttnParams& p, const int (&slot)[8],
+                                        const int64_t (&vhead)[NKV], int n, TileV<D, NKV>& V) {
+  constexpr int DPL = D / 16;
+  const char* zero = reinterpret_cast<const char*>(g_qsa_zero_rows);
+  V.mask = 0;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    V.mask |= slot[i] >= 0 ? (1u << i) : 0u;
+    const int64_t off = slot[i] >= 0 ? slot_offset(p, slot[i], p.vb, p.vt) : 0;
+#pragma unroll
+    for (int v = 0; v < NKV; ++v) {
+      const char* base = slot[i] >= 0 ? p.v + off + vhead[v] : zero;
+      V.r[v][i] = VRow<D>::load(base + DPL * n * 2);
+    }
+  }
+}
+
+// S^T = K_tile Q^T, then the online-softmax update of head n; returns P^T (the
+// lane's 8 token numerators) as packed bf16 pairs.
+template <int D, int NKV>
+__device__ __forceinline__ u32x4 qk_softmax(const AttnParams& p, const TileK<D, NKV>& K,
+                                            const bf16x8 (&bq)[NKV][D / 32], uint32_t mask,
+                                            float& m_run, float& l_run, f32x4 (&oacc)[D / 16]) {
+  f32x4 sacc[2];
+#pragma unroll
+  for (int u = 0; u < 2; ++u) {
+    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int v = 0; v < NKV; ++v)
+#pragma unroll
+      for (int s = 0; s < D / 32; ++s)
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, K.r[v][u][s]),
+                                                      bq[v][s], acc, 0, 0, 0);
+    sacc[u] = acc;
+  }
+  // Lane holds S[token 16 u + 4 g + r][head n] in sacc[u][r] = token slot 4 u + r.
+  float sc[8];
+  float tmax = -INFINITY;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const float x = sacc[i >> 2][i & 3] * p.scale_log2;
+    sc[i] = (mask >> i) & 1u ? x : -INFINITY;
+    tmax = fmaxf(tmax, sc[i]);
+  }
+  tmax = fmaxf(tmax, shfl_xor_f(tmax, 16));
+  tmax = fmaxf(tmax, shfl_xor_f(tmax, 32));
+  const float m_new = fmaxf(m_run, tmax);
+  const float alpha = fast_exp2(m_run - m_new);
+  float lsum = 0.0f;
+  float pv[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    pv[i] = fast_exp2(sc[i] - m_new);
+    lsum += pv[i];
+  }
+  l_run = l_run * alpha + lsum;
+  m_run = m_new;
+#pragma unroll
+  for (int j = 0; j < D / 16; ++j) oacc[j] *= alpha;
+  u32x4 praw;
+  praw[0] = pack_bf16x2(pv[0], pv[1]);
+  praw[1] = pack_bf16x2(pv[2], pv[3]);
+  praw[2] = pack_bf16x2(pv[4], pv[5]);
+  praw[3] = pack_bf16x2(pv[6], pv[7]);
+  return praw;
+}
+
+// O^T += V_tile^T P^T, the lane's 8x8 V blocks transposed by v_perm_b32.
+template <int D, int NKV>
+__device__ __forceinline__ void pv_mfma(const TileV<D, NKV>& V, u32x4 praw, int vslot,
+                                        f32x4 (&oacc)[D / 16]) {
+#pragma unroll
+  for (int v = 0; v < NKV; ++v) {
+    const u32x4 pm = (vslot == v) ? praw : u32x4{0u, 0u, 0u, 0u};
+    const bf16x8 bp = __builtin_bit_cast(bf16x8, pm);
+#pragma unroll
+    for (int j = 0; j < D / 16; ++j) {
+      const uint32_t sel = (j & 1) ? 0x07060302u : 0x05040100u;
+      u32x4 a;
+#pragma unroll
+      for (int q = 0; q < 4; ++q)
+        a[q] = perm_b32(V.r[v][2 * q + 1][j >> 1], V.r[v][2 * q][j >> 1], sel);
+      oacc[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a), bp,
+                                                        oacc[j], 0, 0, 0);
+    }
+  }
+}
 
 // Two waves per SIMD wherever the registers allow it without spilling.
-template <int D, int NKV>
-__global__ __launch_bounds__(kThreads)
+template <int D, int NKV, int WAVES>
+__global__ __launch_bounds__(64 * WAVES)
 __attribute__((amdgpu_waves_per_eu(D == 128 && NKV == 4 ? 1 : 2)))
 void sparse_attn_kernel(const AttnParams p) {
   constexpr int DPL = D / 16;  // V dims per lane = P.V MFMAs per kv slot
   constexpr int KS = D / 32;   // K steps of the Q.K MFMA
-  typedef typename VRow<D>::type vrow_t;
 
-  __shared__ float s_m[kWaves][16];
-  __shared__ float s_l[kWaves][16];
-  __shared__ float s_o[kWaves][16][D + 4];
+  __shared__ float s_m[WAVES][16];
+  __shared__ float s_l[WAVES][16];
+  __shared__ float s_o[WAVES][16][D + 4];
 
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
@@ -174,7 +316,6 @@ void sparse_attn_kernel(const AttnParams p) {
   const int t_begin = (int)((int64_t)split * tiles / p.num_splits);
   const int t_end = (int)((int64_t)(split + 1) * tiles / p.num_splits);
 
-  const char* zero = reinterpret_cast<const char*>(g_qsa_zero_rows);
   int64_t khead[NKV], vhead[NKV];
 #pragma unroll
   for (int v = 0; v < NKV; ++v) {
@@ -188,110 +329,44 @@ void sparse_attn_kernel(const AttnParams p) {
 #pragma unroll
   for (int j = 0; j < DPL; ++j) oacc[j] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-  int tile = t_begin + wave;
-  int kslot[2], vsl[8];
-  if (tile < t_end) {
+  int t = t_begin + wave;
+  if (t < t_end) {
+    TileIdx idx;
+    int ks[2], vs[8];
+    TileK<D, NKV> K;
+    TileV<D, NKV> V;
+    // Prologue, in issue order: K(t), index entries of t+W, V(t).
+    load_tile_idx(irow, t, t_end, n_valid, n, g, idx);
 #pragma unroll
-    for (int u = 0; u < 2; ++u) kslot[u] = resolve_slot(p, irow, trow, req_ok, tile * kTile + k_col(u, n), n_valid);
+    for (int u = 0; u < 2; ++u) ks[u] = resolve_slot(p, trow, req_ok, idx.k[u]);
 #pragma unroll
-    for (int i = 0; i < 8; ++i) vsl[i] = resolve_slot(p, irow, trow, req_ok, tile * kTile + v_col(i, g), n_valid);
-  }
-
-  for (; tile < t_end; tile += kWaves) {
-    // K rows: tokens 16 u + n (A-operand row = token).
-    u32x4 kr[NKV][2][KS];
+    for (int i = 0; i < 8; ++i) vs[i] = resolve_slot(p, trow, req_ok, idx.v[i]);
+    issue_k<D, NKV>(p, ks, khead, g, K);
+    QSA_SCHED_FENCE();
+    load_tile_idx(irow, t + WAVES, t_end, n_valid, n, g, idx);
+    QSA_SCHED_FENCE();
+    issue_v<D, NKV>(p, vs, vhead, n, V);
+    QSA_SCHED_FENCE();
+    for (; t < t_end; t += WAVES) {
+      const bool has_next = t + WAVES < t_end;
+      const u32x4 praw = qk_softmax<D, NKV>(p, K, bq, V.mask, m_run, l_run, oacc);
+      QSA_SCHED_FENCE();
+      if (has_next) {
 #pragma unroll
-    for (int u = 0; u < 2; ++u) {
-      const int64_t off = kslot[u] >= 0 ? slot_offset(p, kslot[u], p.kb, p.kt) : 0;
+        for (int u = 0; u < 2; ++u) ks[u] = resolve_slot(p, trow, req_ok, idx.k[u]);
 #pragma unroll
-      for (int v = 0; v < NKV; ++v) {
-        const char* base = kslot[u] >= 0 ? p.k + off + khead[v] : zero;
-#pragma unroll
-        for (int s = 0; s < KS; ++s) kr[v][u][s] = load_u32x4(base + (32 * s + 8 * g) * 2);
+        for (int i = 0; i < 8; ++i) vs[i] = resolve_slot(p, trow, req_ok, idx.v[i]);
+        issue_k<D, NKV>(p, ks, khead, g, K);
       }
-    }
-    // V rows: tokens 16 (i / 4) + 4 g + i % 4, dims DPL n .. +DPL-1.
-    vrow_t vr[NKV][8];
-    uint32_t vmask = 0;
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      vmask |= vsl[i] >= 0 ? (1u << i) : 0u;
-      const int64_t off = vsl[i] >= 0 ? slot_offset(p, vsl[i], p.vb, p.vt) : 0;
-#pragma unroll
-      for (int v = 0; v < NKV; ++v) {
-        const char* base = vsl[i] >= 0 ? p.v + off + vhead[v] : zero;
-        vr[v][i] = VRow<D>::load(base + DPL * n * 2);
+      QSA_SCHED_FENCE();
+      pv_mfma<D, NKV>(V, praw, vslot, oacc);
+      QSA_SCHED_FENCE();
+      if (has_next) {
+        load_tile_idx(irow, t + 2 * WAVES, t_end, n_valid, n, g, idx);
+        QSA_SCHED_FENCE();
+        issue_v<D, NKV>(p, vs, vhead, n, V);
       }
-    }
-
-    // Resolve the next tile's slots while this tile's loads are in flight.
-    const int next = tile + kWaves;
-    if (next < t_end) {
-#pragma unroll
-      for (int u = 0; u < 2; ++u) kslot[u] = resolve_slot(p, irow, trow, req_ok, next * kTile + k_col(u, n), n_valid);
-#pragma unroll
-      for (int i = 0; i < 8; ++i) vsl[i] = resolve_slot(p, irow, trow, req_ok, next * kTile + v_col(i, g), n_valid);
-    }
-
-    // S^T for the two 16-token halves; lane holds S[tok 16u + 4g + r][head n].
-    f32x4 sacc[2];
-#pragma unroll
-    for (int u = 0; u < 2; ++u) {
-      f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int v = 0; v < NKV; ++v)
-#pragma unroll
-        for (int s = 0; s < KS; ++s)
-          acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
-              __builtin_bit_cast(bf16x8, kr[v][u][s]), bq[v][s], acc, 0, 0, 0);
-      sacc[u] = acc;
-    }
-
-    // Online softmax (log2 domain) for head n over this tile's 32 tokens.
-    float sc[8];
-    float tmax = -INFINITY;
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const float x = sacc[i >> 2][i & 3] * p.scale_log2;
-      sc[i] = (vmask >> i) & 1u ? x : -INFINITY;
-      tmax = fmaxf(tmax, sc[i]);
-    }
-    tmax = fmaxf(tmax, shfl_xor_f(tmax, 16));
-    tmax = fmaxf(tmax, shfl_xor_f(tmax, 32));
-    const float m_new = fmaxf(m_run, tmax);
-    const float alpha = fast_exp2(m_run - m_new);
-    float lsum = 0.0f;
-    float pv[8];
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      pv[i] = fast_exp2(sc[i] - m_new);
-      lsum += pv[i];
-    }
-    l_run = l_run * alpha + lsum;
-    m_run = m_new;
-#pragma unroll
-    for (int j = 0; j < DPL; ++j) oacc[j] *= alpha;
-
-    u32x4 praw;
-    praw[0] = pack_bf16x2(pv[0], pv[1]);
-    praw[1] = pack_bf16x2(pv[2], pv[3]);
-    praw[2] = pack_bf16x2(pv[4], pv[5]);
-    praw[3] = pack_bf16x2(pv[6], pv[7]);
-
-#pragma unroll
-    for (int v = 0; v < NKV; ++v) {
-      const u32x4 pm = (vslot == v) ? praw : u32x4{0u, 0u, 0u, 0u};
-      const bf16x8 bp = __builtin_bit_cast(bf16x8, pm);
-#pragma unroll
-      for (int j = 0; j < DPL; ++j) {
-        const uint32_t sel = (j & 1) ? 0x07060302u : 0x05040100u;
-        u32x4 a;
-#pragma unroll
-        for (int q = 0; q < 4; ++q)
-          a[q] = perm_b32(vr[v][2 * q + 1][j >> 1], vr[v][2 * q][j >> 1], sel);
-        oacc[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a), bp,
-                                                          oacc[j], 0, 0, 0);
-      }
+      QSA_SCHED_FENCE();
     }
   }
 
@@ -310,35 +385,32 @@ void sparse_attn_kernel(const AttnParams p) {
   }
   __syncthreads();
 
-  // Thread t finalises head t / 16, dims [(t % 16) * DPL, +DPL).
+  // Thread t < 256 finalises head t / 16, dims [(t % 16) * DPL, +DPL).
   const int h = threadIdx.x >> 4;
   const int d0 = (threadIdx.x & 15) * DPL;
-  const bool h_ok = h < p.heads_per_wave;
+  if (threadIdx.x >= 256 || h >= p.heads_per_wave) return;
   const int head = head0 + h;
-  float o[DPL];
+  float mw[WAVES];
   float mx = kInitMax, lsum = 0.0f;
-  if (h_ok) {
-    float mw[kWaves];
 #pragma unroll
-    for (int w = 0; w < kWaves; ++w) {
-      mw[w] = s_m[w][h];
-      mx = fmaxf(mx, mw[w]);
-    }
-#pragma unroll
-    for (int d = 0; d < DPL; ++d) o[d] = 0.0f;
-#pragma unroll
-    for (int w = 0; w < kWaves; ++w) {
-      const float wt = fast_exp2(mw[w] - mx);
-      lsum += wt * s_l[w][h];
-#pragma unroll
-      for (int d = 0; d < DPL; ++d) o[d] += wt * s_o[w][h][d0 + d];
-    }
-    const float inv = lsum > 0.0f ? 1.0f / fmaxf(lsum, 1.0e-20f) : 0.0f;
-#pragma unroll
-    for (int d = 0; d < DPL; ++d) o[d] *= inv;
+  for (int w = 0; w < WAVES; ++w) {
+    mw[w] = s_m[w][h];
+    mx = fmaxf(mx, mw[w]);
   }
+  float o[DPL];
+#pragma unroll
+  for (int d = 0; d < DPL; ++d) o[d] = 0.0f;
+#pragma unroll
+  for (int w = 0; w < WAVES; ++w) {
+    const float wt = fast_exp2(mw[w] - mx);
+    lsum += wt * s_l[w][h];
+#pragma unroll
+    for (int d = 0; d < DPL; ++d) o[d] += wt * s_o[w][h][d0 + d];
+  }
+  const float inv = lsum > 0.0f ? 1.0f / fmaxf(lsum, 1.0e-20f) : 0.0f;
+#pragma unroll
+  for (int d = 0; d < DPL; ++d) o[d] *= inv;
 
-  if (!h_ok) return;
   if (p.num_splits > 1) {
     // Normalised fp32 partial + log2-LSE for the merge kernel (ops/qsa.py:278-303).
     const int64_t prow = ((int64_t)split * p.rows + row) * p.num_q_heads + head;
@@ -458,9 +530,26 @@ bool plan_heads(int num_q_heads, int num_kv_heads, HeadPlan* plan) {
   return true;
 }
 
+// Waves per workgroup: 8 once (row, head group) pairs alone reach 64, so a
+// few splits give every CU one 8-wave workgroup; 4 below that, where more and
+// smaller workgroups spread a small batch wider. On the 64-row, 16-head decode
+// shape 8 waves x 4 splits measured faster than 4 waves x 8 splits. D = 128
+// with 4 kv heads per group needs more than the 256 registers a lane gets at
+// two waves per SIMD, so it always runs 4 waves (one per SIMD).
+bool fits_8_waves(int head_dim, int nkv) { return !(head_dim == 128 && nkv == 4); }
+int waves_for(int rows, const HeadPlan& plan, int head_dim) {
+  return (int64_t)rows * plan.groups >= 64 && fits_8_waves(head_dim, plan.nkv) ? 8 : 4;
+}
+
 template <int D, int NKV>
-hipError_t launch_attn(const AttnParams& p, dim3 grid, hipStream_t stream) {
-  hipLaunchKernelGGL((sparse_attn_kernel<D, NKV>), grid, dim3(kThreads), 0, stream, p);
+hipError_t launch_attn(const AttnParams& p, dim3 grid, int waves, hipStream_t stream) {
+  if constexpr (!(D == 128 && NKV == 4)) {
+    if (waves == 8) {
+      hipLaunchKernelGGL((sparse_attn_kernel<D, NKV, 8>), grid, dim3(512), 0, stream, p);
+      return hipGetLastError();
+    }
+  }
+  hipLaunchKernelGGL((sparse_attn_kernel<D, NKV, 4>), grid, dim3(256), 0, stream, p);
   return hipGetLastError();
 }
 
@@ -482,12 +571,14 @@ using namespace qsa;
 
 extern "C" int qsa_sparse_attention_splits(int rows, int num_q_heads, int num_kv_heads,
                                            int head_dim, int width, int use_decode_kernel) {
-  (void)head_dim;
+  (void)use_decode_kernel;
   HeadPlan plan;
   if (rows <= 0 || !plan_heads(num_q_heads, num_kv_heads, &plan)) return 1;
   const int tiles = (width + kTile - 1) / kTile;
-  const int base = rows * plan.groups;
-  const int target = use_decode_kernel ? 512 : 256;  // workgroups in flight on 256 CUs
+  const int64_t base = (int64_t)rows * plan.groups;
+  // One 8-wave workgroup per CU, or two 4-wave ones, and at least two tiles
+  // per split (a one-tile split pays for a partial and its merge for nothing).
+  const int64_t target = waves_for(rows, plan, head_dim) == 8 ? kCUs : 2 * kCUs;
   int splits = 1;
   while (splits * 2 * base <= target && splits * 2 <= std::max(1, tiles / 2) && splits < 64)
     splits *= 2;
@@ -583,7 +674,6 @@ extern "C" int qsa_sparse_attention(
   p.num_q_heads = num_q_heads;
   p.group = num_q_heads / num_kv_heads;
   p.heads_per_wave = plan.heads_per_wave;
-  p.head_groups = plan.groups;
   p.num_splits = num_splits;
   p.physical = indices_are_physical ? 1 : 0;
   p.scale_log2 = (float)(1.0 / __builtin_sqrt((double)head_dim) * 1.4426950408889634);
@@ -591,16 +681,17 @@ extern "C" int qsa_sparse_attention(
   if (plan.groups > 65535 || num_splits > 65535)
     return fail(QSA_ERR_UNSUPPORTED, "qsa_sparse_attention: grid too large");
   const dim3 grid(rows, num_splits, plan.groups);
+  const int waves = waves_for(rows, plan, head_dim);
   hipStream_t s = static_cast<hipStream_t>(stream);
   hipError_t err = hipSuccess;
   if (head_dim == 128) {
-    if (plan.nkv == 1) err = launch_attn<128, 1>(p, grid, s);
-    else if (plan.nkv == 2) err = launch_attn<128, 2>(p, grid, s);
-    else err = launch_attn<128, 4>(p, grid, s);
+    if (plan.nkv == 1) err = launch_attn<128, 1>(p, grid, waves, s);
+    else if (plan.nkv == 2) err = launch_attn<128, 2>(p, grid, waves, s);
+    else err = launch_attn<128, 4>(p, grid, waves, s);
   } else {
-    if (plan.nkv == 1) err = launch_attn<64, 1>(p, grid, s);
-    else if (plan.nkv == 2) err = launch_attn<64, 2>(p, grid, s);
-    else err = launch_attn<64, 4>(p, grid, s);
+    if (plan.nkv == 1) err = launch_attn<64, 1>(p, grid, waves, s);
+    else if (plan.nkv == 2) err = launch_attn<64, 2>(p, grid, waves, s);
+    else err = launch_attn<64, 4>(p, grid, waves, s);
   }
   if (err != hipSuccess)
     return fail(QSA_ERR_HIP, std::string("qsa_sparse_attention launch: ") + hipGetErrorString(err));

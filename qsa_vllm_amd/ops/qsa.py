@@ -7,8 +7,9 @@ behind ``torch.ops.yulan_qsa_kernels.sparse_attention``.
 
 ``decode_config`` keeps the reference's ``(block_n, target_splits, warps)``
 tuple; only ``target_splits`` is meaningful here (the HIP kernel walks fixed
-32-token tiles with 4 waves), and it caps the split count exactly as the
-reference caps its own (``num_splits = min(pow2floor(tiles), target)``).
+32-token tiles and picks its own waves per workgroup), and it caps the split
+count exactly as the reference caps its own
+(``num_splits = min(pow2floor(tiles), target)``).
 """
 
 from __future__ import annotations
