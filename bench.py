@@ -44,6 +44,12 @@ def parse_args():
     p.add_argument("--traffic", default=os.path.join(os.path.dirname(os.path.abspath(__file__)),
                                                      "profiles", "sparse_attn_decode_32k_traffic.txt"),
                    help="committed rocprofv3 PMC summary giving HBM bytes per attention launch")
+    p.add_argument("--traffic-run", action="store_true",
+                   help="no timing: eager attention launches of the workload plus a calibration "
+                        "copy, for rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE passes")
+    p.add_argument("--traffic-summary", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
+                   help="summarise the counter CSVs of a FETCH_SIZE and a WRITE_SIZE pass of "
+                        "--traffic-run and print the traffic summary")
     return p.parse_args()
 
 
@@ -69,6 +75,9 @@ def main():
         print(f"bench.py measures one GPU only (asked for --gpus {args.gpus}); the QSA path is "
               "built and measured on a single MI355X.", file=sys.stderr)
         return 2
+    if args.traffic_summary:
+        print(traffic_summary(*args.traffic_summary))
+        return 0
     if args.steps <= 0:
         raise SystemExit("--steps must be positive")
 
@@ -121,6 +130,9 @@ def main():
     def step(i):
         select(i)
         attend(i)
+
+    if args.traffic_run:
+        return traffic_run(select, attend, n_sets)
 
     # Eager pass (also initialises allocator pools), then capture.
     for i in range(n_sets):
@@ -244,6 +256,87 @@ def main():
         result["cpu_baseline"] = cpu_baseline(wl, args)
     print(json.dumps(result), flush=True)
     return 0
+
+
+# Calibration copy for the counter passes: an fp32 negation (reads and writes
+# CAL_BYTES once each), recognised in the counter CSV by its kernel name.
+CAL_BYTES = 256 << 20
+CAL_KERNEL = "neg_kernel"
+ATTN_KERNELS = ("sparse_attn_kernel", "merge_kernel")
+
+
+def traffic_run(select, attend, n_sets, rounds=3):
+    import torch
+
+    for i in range(n_sets):
+        select(i)
+    torch.cuda.synchronize()
+    for _ in range(rounds):
+        for i in range(n_sets):
+            attend(i)
+    src = torch.ones(CAL_BYTES // 4, dtype=torch.float32, device="cuda")
+    dst = torch.empty_like(src)
+    for _ in range(rounds):
+        torch.neg(src, out=dst)
+    torch.cuda.synchronize()
+    log(f"traffic run: {rounds * n_sets} attention launches, {rounds} calibration copies "
+        f"of {CAL_BYTES} B")
+    return 0
+
+
+def _counter_means(root, counter):
+    """Mean counter value per dispatch, by kernel group, over a rocprofv3 --pmc run."""
+    import csv
+    import glob
+
+    files = glob.glob(os.path.join(root, "**", "*counter_collection.csv"), recursive=True)
+    if not files:
+        raise SystemExit(f"no counter_collection.csv under {root}")
+    per_dispatch = {}
+    for path in files:
+        with open(path) as fh:
+            for rec in csv.DictReader(fh):
+                if rec.get("Counter_Name") != counter:
+                    continue
+                name = rec["Kernel_Name"]
+                group = next((k for k in ATTN_KERNELS + (CAL_KERNEL,) if k in name), None)
+                if group is None:
+                    continue
+                key = (path, rec["Dispatch_Id"])
+                grp, val = per_dispatch.get(key, (group, 0.0))
+                per_dispatch[key] = (grp, val + float(rec["Counter_Value"]))
+    sums, counts = {}, {}
+    for grp, val in per_dispatch.values():
+        sums[grp] = sums.get(grp, 0.0) + val
+        counts[grp] = counts.get(grp, 0) + 1
+    return {g: (sums[g] / counts[g], counts[g]) for g in sums}
+
+
+def traffic_summary(fetch_dir, write_dir):
+    """HBM bytes per attention launch (attention kernel + split merge), each
+    counter scaled by what it reads for the calibration copy of CAL_BYTES."""
+    fetch = _counter_means(fetch_dir, "FETCH_SIZE")
+    write = _counter_means(write_dir, "WRITE_SIZE")
+    for table, name in ((fetch, "FETCH_SIZE"), (write, "WRITE_SIZE")):
+        missing = [k for k in ATTN_KERNELS[:1] + (CAL_KERNEL,) if k not in table]
+        if missing:
+            raise SystemExit(f"{name} pass lacks dispatches of {missing}")
+    f_scale = CAL_BYTES / (fetch[CAL_KERNEL][0] * 1024.0)
+    w_scale = CAL_BYTES / (write[CAL_KERNEL][0] * 1024.0)
+    lines = [f"calibration: fp32 negation of {CAL_BYTES} B reads FETCH_SIZE "
+             f"{fetch[CAL_KERNEL][0]:.1f} KiB, WRITE_SIZE {write[CAL_KERNEL][0]:.1f} KiB "
+             f"-> scale fetch x{f_scale:.4f}, write x{w_scale:.4f}"]
+    total = 0.0
+    for k in ATTN_KERNELS:
+        if k not in fetch:
+            continue
+        fb = fetch[k][0] * 1024.0 * f_scale
+        wb = write.get(k, (0.0, 0))[0] * 1024.0 * w_scale
+        total += fb + wb
+        lines.append(f"{k}: {fetch[k][1]} dispatches, fetch {fb / 1e6:.2f} MB, "
+                     f"write {wb / 1e6:.2f} MB per dispatch (scaled)")
+    lines.append(f"traffic_bytes_per_launch: {total:.0f}")
+    return "\n".join(lines)
 
 
 def cpu_baseline(wl, args):
