@@ -1,11 +1,16 @@
-"""Decode logits-width buckets for QSA selection.
+"""Logits-width policy of QSA selection.
 
-Restates the column policy of the reference ``graph_dispatch.py:313-342``:
-decode rows whose compressed length fits 32768 columns share one short
-logits width; longer batches use the full page-table capacity. Graph capture
-pins the width through ``capture_column_scope``. The vLLM graph-manager
-patches of the reference (``install_short_decode_dispatch``) belong to the
-serving runtime and are not part of this package.
+Decode scoring writes one fp32 logit per compressed key into a
+``[rows, columns]`` buffer, so the column count decides the buffer and the
+top-k kernel instance. The reference (``graph_dispatch.py:26-34``) uses two
+width classes so captured graphs stay valid across batches: a short class of
+32768 columns whenever the longest sequence's compressed length fits it, and
+the full page-table capacity otherwise. A graph capture pins the class with
+:func:`capture_column_scope`. Prefill sizes its logits by the longest
+sequence, rounded up to 64 columns (``ops/indexer.py:320-321``).
+
+The reference also patches vLLM's graph manager to key graphs by this class;
+that belongs to the serving runtime, not to this package.
 """
 
 from __future__ import annotations
@@ -13,27 +18,40 @@ from __future__ import annotations
 from contextlib import contextmanager
 
 SHORT_DECODE_COLUMNS = 32768
-_capture_columns = None
+_pinned_columns: int | None = None
 
 
 def decode_column_bucket(max_seq_len: int, compress_ratio: int = 4) -> int:
-    """Zero denotes the full page-table capacity; short rows use one selector."""
-    return SHORT_DECODE_COLUMNS if max_seq_len // compress_ratio <= SHORT_DECODE_COLUMNS else 0
+    """Width class of a decode batch: SHORT_DECODE_COLUMNS when its longest
+    compressed length fits in it, else 0, meaning the page-table capacity."""
+    fits_short = max_seq_len // compress_ratio <= SHORT_DECODE_COLUMNS
+    return SHORT_DECODE_COLUMNS if fits_short else 0
 
 
 def decode_logits_columns(max_seq_len: int, compress_ratio: int, capacity: int) -> int:
-    columns = (_capture_columns if _capture_columns is not None
-               else decode_column_bucket(max_seq_len, compress_ratio))
-    return min(columns, capacity) if columns else capacity
+    """Logits columns of a decode call, never more than ``capacity`` (the
+    compressed page table's width times keys per compressed page)."""
+    bucket = _pinned_columns
+    if bucket is None:
+        bucket = decode_column_bucket(max_seq_len, compress_ratio)
+    return capacity if bucket == 0 else min(bucket, capacity)
+
+
+def prefill_logits_width(max_seq_len: int, compress_ratio: int, capacity: int) -> int:
+    """Logits columns of a prefill call: the longest compressed length rounded
+    up to a multiple of 64, at least 64, at most ``capacity``."""
+    keys = -(-max_seq_len // compress_ratio)
+    rounded = -(-keys // 64) * 64
+    return min(max(rounded, 64), capacity)
 
 
 @contextmanager
-def capture_column_scope(columns):
-    """Fix the decode logits width (0 = capacity) while capturing a graph."""
-    global _capture_columns
-    previous = _capture_columns
-    _capture_columns = columns
+def capture_column_scope(columns: int):
+    """Pin the decode width class (0 = capacity) while a graph is captured."""
+    global _pinned_columns
+    saved = _pinned_columns
+    _pinned_columns = columns
     try:
         yield
     finally:
-        _capture_columns = previous
+        _pinned_columns = saved

@@ -51,6 +51,12 @@ def _stream(device):
     return ctypes.c_void_p(torch.cuda.current_stream(device).cuda_stream)
 
 
+def _stride(t, d):
+    """Stride of dim d, 0 for a size-1 dim (never used to address memory; views
+    may carry any value there)."""
+    return 0 if t.size(d) == 1 else t.stride(d)
+
+
 def _require(cond, msg):
     if not cond:
         raise RuntimeError(f"{_NS}: {msg}")
@@ -158,7 +164,7 @@ def _cache_strides(k_cache, name):
     if k_cache.dim() == 4:
         _require(k_cache.size(2) == 1, f"{name} must hold one index head")
     _require(k_cache.stride(-1) == 1, f"{name} must have a unit dim stride")
-    return k_cache.stride(0), k_cache.stride(1)
+    return _stride(k_cache, 0), _stride(k_cache, 1)
 
 
 def _indexer_decode_impl(q, k_cache, page_table, visible, logits, decode_query_len):
@@ -181,7 +187,7 @@ def _indexer_decode_impl(q, k_cache, page_table, visible, logits, decode_query_l
     if rows == 0:
         return
     with torch.cuda.device(dev):
-        _lib.call("qsa_indexer_decode", _ptr(q), q.stride(0), q.stride(1), rows, heads, dim,
+        _lib.call("qsa_indexer_decode", _ptr(q), _stride(q, 0), _stride(q, 1), rows, heads, dim,
                   _ptr(k_cache), cb, ct, k_cache.size(0), k_cache.size(1),
                   _ptr(page_table), page_table.stride(0), page_table.size(1),
                   _ptr(visible), int(decode_query_len), _ptr(logits), logits.stride(0),
@@ -211,7 +217,7 @@ def _indexer_prefill_impl(q, k_cache, page_table, query_start_loc, visible, logi
     if num_rows == 0 or requests == 0:
         return
     with torch.cuda.device(dev):
-        _lib.call("qsa_indexer_prefill", _ptr(q), q.stride(0), q.stride(1), heads, dim,
+        _lib.call("qsa_indexer_prefill", _ptr(q), _stride(q, 0), _stride(q, 1), heads, dim,
                   _ptr(k_cache), cb, ct, k_cache.size(0), k_cache.size(1),
                   _ptr(page_table), page_table.stride(0), page_table.size(1), requests,
                   _ptr(query_start_loc), _ptr(visible), int(query_offset), int(num_rows),
@@ -227,7 +233,7 @@ def _gate_strides(gate, rows, heads, dim):
     _dtype(gate, torch.bfloat16, "output_gate")
     _require(gate.dim() == 3 and tuple(gate.shape[1:]) == (heads, dim) and gate.size(0) >= rows,
              "output_gate must be [rows, heads, dim]")
-    return gate.stride(0), gate.stride(1), gate.stride(2)
+    return _stride(gate, 0), _stride(gate, 1), _stride(gate, 2)
 
 
 def _sparse_attention_impl(q, k_cache, v_cache, indices, block_table, token_to_req, out,
@@ -262,14 +268,14 @@ def _sparse_attention_impl(q, k_cache, v_cache, indices, block_table, token_to_r
     ws = _workspace(nbytes, dev)
     with torch.cuda.device(dev):
         _lib.call(
-            "qsa_sparse_attention", _ptr(q), q.stride(0), q.stride(1), rows, hq, dim,
-            _ptr(k_cache), k_cache.stride(0), k_cache.stride(1), k_cache.stride(2),
-            _ptr(v_cache), v_cache.stride(0), v_cache.stride(1), v_cache.stride(2),
+            "qsa_sparse_attention", _ptr(q), _stride(q, 0), _stride(q, 1), rows, hq, dim,
+            _ptr(k_cache), _stride(k_cache, 0), _stride(k_cache, 1), _stride(k_cache, 2),
+            _ptr(v_cache), _stride(v_cache, 0), _stride(v_cache, 1), _stride(v_cache, 2),
             k_cache.size(0), k_cache.size(1), k_cache.size(2),
             _ptr(indices), indices.stride(0), indices.size(1),
             _ptr(block_table), block_table.stride(0), block_table.size(1), block_table.size(0),
             _ptr(token_to_req), _ptr(valid_counts),
-            _ptr(out), out.stride(0), out.stride(1),
+            _ptr(out), _stride(out, 0), _stride(out, 1),
             _ptr(output_gate), gr, gh, gd,
             int(bool(indices_are_physical)), int(num_splits),
             _ptr(ws), 0 if ws is None else ws.numel(), _stream(dev))
@@ -292,7 +298,7 @@ def _sparse_attention_merge_impl(partial_out, partial_lse, out, output_gate):
         return
     with torch.cuda.device(dev):
         _lib.call("qsa_sparse_attention_merge", _ptr(partial_out), _ptr(partial_lse), splits,
-                  rows, hq, dim, _ptr(out), out.stride(0), out.stride(1), _ptr(output_gate),
+                  rows, hq, dim, _ptr(out), _stride(out, 0), _stride(out, 1), _ptr(output_gate),
                   gr, gh, gd, _stream(dev))
 
 

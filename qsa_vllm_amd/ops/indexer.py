@@ -1,12 +1,16 @@
-"""QSA indexer scoring + fused top-k selection on gfx950.
+"""Index-key scoring and top-k token selection (host side of the QSA indexer).
 
-Same functions, signatures and chunking policy as the reference
-``yulan_qsa_vllm/ops/indexer.py``: ``qsa_select_paged_decode`` (:227-279),
-``qsa_select_paged_prefill`` (:305-343), ``select_paged_tokens`` (:346-393).
-Scoring runs in the HIP kernels behind ``torch.ops.yulan_qsa_kernels.
-indexer_decode`` / ``indexer_prefill`` and selection in ``topk_expand``. The
-fp32 logits workspace is bounded by ``QSA_INDEXER_WORKSPACE_MB`` (default 64),
-as in the reference.
+The entry points keep the names, arguments and results of the reference
+``yulan_qsa_vllm/ops/indexer.py``: ``qsa_select_paged_decode`` (:227-239),
+``qsa_select_paged_prefill`` (:305-318) and ``select_paged_tokens``
+(:346-393). Each call scores queries into an fp32 logits buffer with the HIP
+scoring kernel (``indexer_decode`` / ``indexer_prefill``) and then runs the
+fused top-k + expansion kernel (``topk_expand``) on it.
+
+The logits buffer is capped at ``QSA_INDEXER_WORKSPACE_MB`` MiB (default 64,
+the reference's cap); a call whose rows need more is processed in row spans
+that each fit, reusing the one buffer. Spans only bound memory: every row's
+result is independent of how the rows are grouped.
 """
 
 from __future__ import annotations
@@ -15,14 +19,25 @@ import os
 
 import torch
 
-from ..graph_dispatch import decode_logits_columns
-from .topk import topk_expand as _topk_expand
+from ..graph_dispatch import decode_logits_columns, prefill_logits_width
+from .topk import topk_expand
 
-_INDEXER_WORKSPACE_BYTES = int(os.environ.get("QSA_INDEXER_WORKSPACE_MB", "64")) * 1024 * 1024
+_LOGITS_CAP_BYTES = int(os.environ.get("QSA_INDEXER_WORKSPACE_MB", "64")) << 20
 
 
-def _cdiv(a: int, b: int) -> int:
-    return (a + b - 1) // b
+def _spans(count: int, per_span: int):
+    """[start, end) spans of at most ``per_span`` covering ``range(count)``."""
+    return [(a, min(a + per_span, count)) for a in range(0, count, per_span)]
+
+
+def _expand_rows(logits, rows: slice, visible_blocks, compress_ratio, out, *, query_positions,
+                 sequence_lengths, token_to_req, main_block_table, main_page_size,
+                 valid_counts_out):
+    """``topk_expand`` of the logits of ``rows`` (row-relative to the caller's tensors)."""
+    topk_expand(logits, visible_blocks[rows], query_positions[rows], sequence_lengths,
+                token_to_req[rows], out[rows], compress_ratio,
+                main_block_table=main_block_table, main_page_size=main_page_size,
+                valid_counts_out=None if valid_counts_out is None else valid_counts_out[rows])
 
 
 def qsa_select_paged_decode(
@@ -38,46 +53,24 @@ def qsa_select_paged_decode(
     *, query_positions, sequence_lengths, token_to_req,
     main_block_table=None, main_page_size=1, valid_counts_out=None,
 ) -> None:
-    """Score decode queries and write the expanded selection."""
-    num_requests = q.shape[0] // decode_query_len
-    columns = decode_logits_columns(
-        max_seq_len, compress_ratio, page_table.shape[1] * k_cache.shape[1],
-    )
-    requests_per_chunk = max(
-        1, _INDEXER_WORKSPACE_BYTES // (columns * 4 * decode_query_len)
-    )
-    workspace_rows = min(num_requests, requests_per_chunk) * decode_query_len
-    logits_workspace = torch.empty(
-        (workspace_rows, columns), dtype=torch.float32, device=q.device,
-    )
-    for first_request in range(0, num_requests, requests_per_chunk):
-        last_request = min(first_request + requests_per_chunk, num_requests)
-        first_row = first_request * decode_query_len
-        last_row = last_request * decode_query_len
-        queries = q[first_row:last_row]
-        table = page_table[first_request:last_request]
-        visible = visible_blocks[first_row:last_row]
-        logits = logits_workspace[:last_row - first_row]
+    """Decode selection: request i of ``page_table`` owns rows
+    ``[i * decode_query_len, (i + 1) * decode_query_len)`` of ``q``."""
+    per_req = decode_query_len
+    requests = q.shape[0] // per_req
+    columns = decode_logits_columns(max_seq_len, compress_ratio,
+                                    page_table.shape[1] * k_cache.shape[1])
+    reqs_per_span = max(1, _LOGITS_CAP_BYTES // (4 * columns * per_req))
+    buf = torch.empty(min(requests, reqs_per_span) * per_req, columns, dtype=torch.float32,
+                      device=q.device)
+    for r0, r1 in _spans(requests, reqs_per_span):
+        rows = slice(r0 * per_req, r1 * per_req)
+        logits = buf[:(r1 - r0) * per_req]
         torch.ops.yulan_qsa_kernels.indexer_decode(
-            queries, k_cache, table, visible, logits, decode_query_len)
-        _topk_expand(
-            logits, visible, query_positions[first_row:last_row], sequence_lengths,
-            token_to_req[first_row:last_row], out[first_row:last_row], compress_ratio,
-            main_block_table=main_block_table, main_page_size=main_page_size,
-            valid_counts_out=(valid_counts_out[first_row:last_row]
-                              if valid_counts_out is not None else None),
-        )
-
-
-def _prefill_logits(
-    q, k_cache, page_table, query_start_loc, visible_blocks, logits_workspace,
-    max_query_len, logits_width, query_offset, num_queries,
-):
-    logits = logits_workspace[:num_queries * logits_width].view(num_queries, logits_width)
-    torch.ops.yulan_qsa_kernels.indexer_prefill(
-        q, k_cache, page_table, query_start_loc, visible_blocks, logits,
-        query_offset, num_queries, max_query_len)
-    return logits
+            q[rows], k_cache, page_table[r0:r1], visible_blocks[rows], logits, per_req)
+        _expand_rows(logits, rows, visible_blocks, compress_ratio, out,
+                     query_positions=query_positions, sequence_lengths=sequence_lengths,
+                     token_to_req=token_to_req, main_block_table=main_block_table,
+                     main_page_size=main_page_size, valid_counts_out=valid_counts_out)
 
 
 def qsa_select_paged_prefill(
@@ -94,31 +87,35 @@ def qsa_select_paged_prefill(
     *, query_positions, sequence_lengths, token_to_req,
     main_block_table=None, main_page_size=1, valid_counts_out=None,
 ) -> None:
-    """Packed prefill scoring and fused final token-selection writeout."""
-    rows = q.shape[0]
-    columns = page_table.shape[1] * k_cache.shape[1]
-    logits_width = _cdiv(_cdiv(max_seq_len, compress_ratio), 64) * 64
-    logits_width = min(max(64, logits_width), columns)
-    rows_per_chunk = max(1, _INDEXER_WORKSPACE_BYTES // (logits_width * 4))
-    logits_workspace = torch.empty(
-        min(rows, rows_per_chunk) * logits_width,
-        dtype=torch.float32, device=q.device,
-    )
-    for query_start in range(0, rows, rows_per_chunk):
-        query_end = min(query_start + rows_per_chunk, rows)
-        logits = _prefill_logits(
-            q, k_cache, page_table, query_start_loc, visible_blocks,
-            logits_workspace, max_query_len, logits_width,
-            query_offset=query_start, num_queries=query_end - query_start,
-        )
-        _topk_expand(
-            logits, visible_blocks[query_start:query_end],
-            query_positions[query_start:query_end], sequence_lengths,
-            token_to_req[query_start:query_end], out[query_start:query_end], compress_ratio,
-            main_block_table=main_block_table, main_page_size=main_page_size,
-            valid_counts_out=(valid_counts_out[query_start:query_end]
-                              if valid_counts_out is not None else None),
-        )
+    """Prefill selection: the rows of ``q`` are the packed query tokens of the
+    requests of ``page_table``, request i's starting at row
+    ``query_start_loc[i] - query_start_loc[0]``, each row masked causally by
+    its ``visible_blocks`` entry."""
+    rows_total = q.shape[0]
+    width = prefill_logits_width(max_seq_len, compress_ratio,
+                                 page_table.shape[1] * k_cache.shape[1])
+    rows_per_span = max(1, _LOGITS_CAP_BYTES // (4 * width))
+    buf = torch.empty(min(rows_total, rows_per_span), width, dtype=torch.float32,
+                      device=q.device)
+    for a, b in _spans(rows_total, rows_per_span):
+        logits = buf[:b - a]
+        torch.ops.yulan_qsa_kernels.indexer_prefill(
+            q, k_cache, page_table, query_start_loc, visible_blocks, logits, a, b - a,
+            max_query_len)
+        _expand_rows(logits, slice(a, b), visible_blocks, compress_ratio, out,
+                     query_positions=query_positions, sequence_lengths=sequence_lengths,
+                     token_to_req=token_to_req, main_block_table=main_block_table,
+                     main_page_size=main_page_size, valid_counts_out=valid_counts_out)
+
+
+def _visible_blocks(query_positions, sequence_lengths, token_to_req, compress_ratio):
+    """Complete compressed blocks a row may see: min((pos + 1) // R,
+    seq_len // R) of its request, 0 for padding rows (request < 0)."""
+    req = token_to_req.long()
+    has_req = req >= 0
+    seq = sequence_lengths.index_select(0, req.clamp_min(0))
+    vis = torch.minimum((query_positions + 1) // compress_ratio, seq // compress_ratio)
+    return torch.where(has_req, vis, torch.zeros_like(vis)).to(torch.int32)
 
 
 def select_paged_tokens(
@@ -128,43 +125,41 @@ def select_paged_tokens(
     visible_blocks=None, main_block_table=None, main_page_size=1,
     valid_counts_out=None,
 ):
-    """Select blocks and write expanded decode/prefill tokens in place."""
-    rows = q.shape[0]
+    """Select ``token_topk`` tokens (+ causal tail) per query row into ``out``
+    ([rows, token_topk + compress_ratio - 1] int32, allocated if absent).
+
+    Rows come decode first: the first ``num_decode_tokens`` rows belong to the
+    first ``num_decodes`` requests and take the decode scorer; the remaining
+    rows (requests ``num_decodes`` onward) take the prefill scorer. With
+    ``main_block_table`` the selection is written as physical cache slots.
+    """
+    rows_total = q.shape[0]
     if out is None:
-        out = torch.empty(
-            (rows, token_topk + compress_ratio - 1),
-            dtype=torch.int32, device=q.device,
-        )
-    if not rows:
+        out = torch.empty(rows_total, token_topk + compress_ratio - 1, dtype=torch.int32,
+                          device=q.device)
+    if rows_total == 0:
         return out
     if visible_blocks is None:
-        safe_requests = token_to_req.clamp_min(0).long()
-        visible_blocks = torch.minimum(
-            (query_positions + 1) // compress_ratio,
-            sequence_lengths.index_select(0, safe_requests) // compress_ratio,
-        ).to(torch.int32)
-        visible_blocks = torch.where(token_to_req >= 0, visible_blocks, 0)
-    if num_decode_tokens:
-        qsa_select_paged_decode(
-            q[:num_decode_tokens], k_cache, page_table[:num_decodes],
-            visible_blocks[:num_decode_tokens], token_topk, compress_ratio,
-            decode_query_len, out[:num_decode_tokens], max_seq_len,
-            query_positions=query_positions[:num_decode_tokens],
-            sequence_lengths=sequence_lengths, token_to_req=token_to_req[:num_decode_tokens],
-            main_block_table=main_block_table, main_page_size=main_page_size,
-            valid_counts_out=(valid_counts_out[:num_decode_tokens]
-                              if valid_counts_out is not None else None),
-        )
-    if num_decode_tokens < rows:
-        qsa_select_paged_prefill(
-            q[num_decode_tokens:], k_cache, page_table[num_decodes:],
-            query_start_loc[num_decodes:], visible_blocks[num_decode_tokens:],
-            token_topk, compress_ratio, max_query_len,
-            out[num_decode_tokens:], max_seq_len,
-            query_positions=query_positions[num_decode_tokens:],
-            sequence_lengths=sequence_lengths, token_to_req=token_to_req[num_decode_tokens:],
-            main_block_table=main_block_table, main_page_size=main_page_size,
-            valid_counts_out=(valid_counts_out[num_decode_tokens:]
-                              if valid_counts_out is not None else None),
-        )
+        visible_blocks = _visible_blocks(query_positions, sequence_lengths, token_to_req,
+                                         compress_ratio)
+
+    def row_args(rows: slice):
+        return dict(
+            query_positions=query_positions[rows], sequence_lengths=sequence_lengths,
+            token_to_req=token_to_req[rows], main_block_table=main_block_table,
+            main_page_size=main_page_size,
+            valid_counts_out=None if valid_counts_out is None else valid_counts_out[rows])
+
+    split = num_decode_tokens
+    if split > 0:
+        rows = slice(0, split)
+        qsa_select_paged_decode(q[rows], k_cache, page_table[:num_decodes],
+                                visible_blocks[rows], token_topk, compress_ratio,
+                                decode_query_len, out[rows], max_seq_len, **row_args(rows))
+    if split < rows_total:
+        rows = slice(split, rows_total)
+        qsa_select_paged_prefill(q[rows], k_cache, page_table[num_decodes:],
+                                 query_start_loc[num_decodes:], visible_blocks[rows],
+                                 token_topk, compress_ratio, max_query_len, out[rows],
+                                 max_seq_len, **row_args(rows))
     return out

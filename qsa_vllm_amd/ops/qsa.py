@@ -83,7 +83,9 @@ def qsa_select_paged_tokens(
     decode_query_len: int = 1,
     visible_blocks: torch.Tensor | None = None,
 ) -> torch.Tensor:
-    """Select with the fused HIP top-k and the HIP prefill/decode scoring."""
+    """Entry point of the same name in the reference's ``ops/qsa.py``
+    (:753-782): :func:`select_paged_tokens` without the main-table (physical
+    slot) and valid-count arguments, i.e. logical token ids."""
     from .indexer import select_paged_tokens
 
     return select_paged_tokens(

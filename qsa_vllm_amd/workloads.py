@@ -50,6 +50,7 @@ class QSAShape:
     kv_layout: str = "token_major"
     chunk: int = 0                     # > 0: chunked prefill of `chunk` new tokens per sequence
     prefix: int = 0
+    decode_requests: int = 0           # with chunk > 0: the first requests decode one token
     seed: int = 0
 
     @property
@@ -104,6 +105,7 @@ class QSAWorkload:
     gate: torch.Tensor | None = None
     max_seq_len: int = 0
     max_query_len: int = 1
+    num_decodes: int = 0              # leading decode requests (= their rows: one token each)
     extra: dict = field(default_factory=dict)
 
     @property
@@ -113,6 +115,10 @@ class QSAWorkload:
     @property
     def is_decode(self) -> bool:
         return self.shape.chunk == 0
+
+    @property
+    def num_decode_tokens(self) -> int:
+        return self.num_decodes
 
 
 def _seq_lens(shape: QSAShape, gen: torch.Generator) -> torch.Tensor:
@@ -167,16 +173,22 @@ def make_workload(shape: QSAShape | str, device="cpu", **overrides) -> QSAWorklo
     seq_lens = _seq_lens(shape, cpu_gen)
     b = shape.batch
     if shape.chunk:
-        n_new = shape.chunk
-        positions = torch.cat([torch.arange(int(s) - n_new, int(s)) for s in seq_lens])
-        token_to_req = torch.arange(b, dtype=torch.int32).repeat_interleave(n_new)
-        query_start_loc = torch.arange(0, (b + 1) * n_new, n_new, dtype=torch.int32)
-        max_query_len = n_new
+        # Mixed batch: decode requests (one new token) first, then prefill chunks.
+        n_dec = min(shape.decode_requests, b)
+        q_lens = torch.tensor([1] * n_dec + [shape.chunk] * (b - n_dec), dtype=torch.int64)
+        positions = torch.cat([torch.arange(int(s) - int(n), int(s))
+                               for s, n in zip(seq_lens, q_lens)])
+        token_to_req = torch.arange(b, dtype=torch.int32).repeat_interleave(q_lens)
+        query_start_loc = torch.cat([torch.zeros(1, dtype=torch.int64),
+                                     q_lens.cumsum(0)]).to(torch.int32)
+        max_query_len = int(q_lens.max())
+        num_decodes = n_dec
     else:
         positions = seq_lens - 1
         token_to_req = torch.arange(b, dtype=torch.int32)
         query_start_loc = torch.arange(b + 1, dtype=torch.int32)
         max_query_len = 1
+        num_decodes = b
     rows = positions.numel()
     r = shape.compress_ratio
     visible = torch.minimum((positions + 1) // r, seq_lens[token_to_req.long()] // r).to(torch.int32)
@@ -216,6 +228,7 @@ def make_workload(shape: QSAShape | str, device="cpu", **overrides) -> QSAWorklo
         q=q, q_index=q_index, gate=gate,
         max_seq_len=int(seq_lens.max()),
         max_query_len=max_query_len,
+        num_decodes=num_decodes,
     )
 
 

@@ -1,0 +1,177 @@
+"""The attention-side glue (``qsa_vllm_amd.backend``): cache views, the layer
+call order and the decode / prefill / mixed flags, against the oracle."""
+
+import pytest
+import torch
+
+import oracle
+from qsa_vllm_amd.workloads import make_workload
+
+DEV = "cuda:0"
+MAX_ABS, MEAN_ABS = 2e-2, 2e-3
+
+
+def _backend():
+    from qsa_vllm_amd import backend  # loads libqsa_hip.so (no GPU needed to load it)
+    return backend
+
+
+@pytest.mark.parametrize("heads", [1, 2])
+@pytest.mark.parametrize("layout", ["BLNHC", "BLHNC"])
+def test_main_kv_views_address_the_bound_cache(heads, layout):
+    """backend.py:148-153: the logical [blocks, heads, page, 2D] view the cache is
+    bound as, whatever the physical layout, gives K/V [blocks, page, heads, D]."""
+    backend = _backend()
+    blocks, page, d = 3, 16, 8
+    g = torch.Generator().manual_seed(heads)
+    if layout == "BLNHC":   # physical [blocks, page, heads, 2D]
+        phys = torch.randn(blocks, page, heads, 2 * d, generator=g)
+        bound = phys.permute(0, 2, 1, 3)
+        want_k, want_v = phys[..., :d], phys[..., d:]
+    else:                   # physical [blocks, heads, page, 2D]
+        phys = torch.randn(blocks, heads, page, 2 * d, generator=g)
+        bound = phys
+        want_k, want_v = phys.transpose(1, 2)[..., :d], phys.transpose(1, 2)[..., d:]
+    k, v = backend.main_kv_views(bound, d)
+    assert k.shape == (blocks, page, heads, d) and v.shape == k.shape
+    assert torch.equal(k, want_k) and torch.equal(v, want_v)
+    assert k.data_ptr() == phys.data_ptr() and v.data_ptr() == phys.data_ptr() + d * 4
+    assert k.stride(3) == 1
+    if heads == 1:
+        assert k.stride(2) == d          # canonical stride of the singleton head dim
+
+
+def test_canonical_strides_keep_addresses():
+    backend = _backend()
+    base = torch.arange(2 * 1 * 5 * 1 * 4, dtype=torch.float32).view(2, 5, 4)
+    t = base.unsqueeze(1).unsqueeze(3)        # [2, 1, 5, 1, 4]
+    weird = t.as_strided(t.shape, (20, 777, 4, 999, 1))
+    c = backend.canonicalize_singleton_dim_strides(weird)
+    assert c.stride() == (20, 20, 4, 4, 1)
+    assert torch.equal(c, t)
+
+
+def _check_attn(got, want, what):
+    err = (got.float().cpu() - want).abs()
+    print(f"[backend] {what}: max_abs={err.max().item():.3e} mean_abs={err.mean().item():.3e}",
+          flush=True)
+    assert err.max().item() <= MAX_ABS and err.mean().item() <= MEAN_ABS, what
+
+
+def _compressed_meta(backend, wl):
+    return backend.QSACompressedMetadata(
+        block_table=wl.index_table, token_to_req=wl.token_to_req,
+        logical_positions=wl.positions, seq_lens=wl.seq_lens,
+        query_start_loc=wl.query_start_loc, max_query_len=wl.max_query_len,
+        max_seq_len=wl.max_seq_len, num_decodes=wl.num_decodes,
+        num_decode_tokens=wl.num_decode_tokens, decode_query_len=1,
+        visible_blocks=wl.visible)
+
+
+def _gpu_logits(wl):
+    """The fp32 logits the HIP scorers produce for the workload's rows
+    (decode rows, then prefill rows), each part at its own width."""
+    from qsa_vllm_amd.graph_dispatch import decode_logits_columns, prefill_logits_width
+    s = wl.shape
+    nd = wl.num_decode_tokens
+    cap = wl.index_table.shape[1] * wl.index_cache.shape[1]
+    parts = []
+    if nd:
+        cols = decode_logits_columns(wl.max_seq_len, s.compress_ratio, cap)
+        lg = torch.full((nd, cols), float("nan"), device=DEV)
+        torch.ops.yulan_qsa_kernels.indexer_decode(wl.q_index[:nd], wl.index_cache,
+                                                   wl.index_table[:wl.num_decodes],
+                                                   wl.visible[:nd], lg, 1)
+        parts.append(lg.cpu())
+    if nd < wl.rows:
+        width = prefill_logits_width(wl.max_seq_len, s.compress_ratio, cap)
+        n = wl.rows - nd
+        lg = torch.full((n, width), float("nan"), device=DEV)
+        torch.ops.yulan_qsa_kernels.indexer_prefill(
+            wl.q_index[nd:], wl.index_cache, wl.index_table[wl.num_decodes:],
+            wl.query_start_loc[wl.num_decodes:], wl.visible[nd:], lg, 0, n, wl.max_query_len)
+        parts.append(lg.cpu())
+    return parts
+
+
+def _run_layer(wl, pad_rows=3):
+    backend = _backend()
+    s = wl.shape
+    rows = wl.rows
+    layer = backend.QSALayerState(wl.kv_cache.permute(0, 2, 1, 3)
+                                  if s.kv_layout == "token_major" else wl.kv_cache,
+                                  s.head_dim, rows + pad_rows, s.width)
+    impl = backend.YuLanQSAImpl(s.num_q_heads, s.num_kv_heads, s.head_dim)
+    main = backend.YuLanQSAMetadata(num_actual_tokens=rows, max_query_len=wl.max_query_len,
+                                    block_table=wl.block_table,
+                                    slot_mapping=torch.zeros(rows, dtype=torch.int64, device=DEV))
+    output = torch.full((rows + pad_rows, s.num_q_heads, s.head_dim), float("nan"),
+                        dtype=torch.bfloat16, device=DEV)
+    backend.run_qsa(layer, impl, wl.q_index, wl.index_cache, wl.q, wl.gate, output, main,
+                    _compressed_meta(backend, wl), s.token_topk, s.compress_ratio,
+                    wl.token_to_req)
+    torch.cuda.synchronize()
+    return layer, output
+
+
+def _expected_selection(wl, physical):
+    s = wl.shape
+    nd = wl.num_decode_tokens
+    logits = _gpu_logits(wl)
+    spans = ([(0, nd)] if nd else []) + ([(nd, wl.rows)] if nd < wl.rows else [])
+    idx, cnt = [], []
+    cpu = {n: getattr(wl, n).cpu() for n in ("visible", "positions", "seq_lens", "token_to_req",
+                                              "block_table")}
+    for lg, (a, b) in zip(logits, spans):
+        i, c = oracle.topk_expand(lg, cpu["visible"][a:b], cpu["positions"][a:b],
+                                  cpu["seq_lens"], cpu["token_to_req"][a:b],
+                                  cpu["block_table"] if physical else None, s.width,
+                                  s.compress_ratio, s.page_size, physical)
+        idx.append(i)
+        cnt.append(c)
+    return torch.cat(idx), torch.cat(cnt)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("kv_layout,gate", [("token_major", False), ("head_major", True)])
+def test_run_qsa_uniform_decode(kv_layout, gate):
+    wl = make_workload("cpu_decode_4k", device=DEV, batch=6, kv_layout=kv_layout, gate=gate)
+    print(f"[backend] uniform decode layout={kv_layout} gate={gate}", flush=True)
+    layer, output = _run_layer(wl)
+    want_idx, want_counts = _expected_selection(wl, physical=True)
+    rows = wl.rows
+    assert torch.equal(layer.topk_indices_buffer[:rows].cpu(), want_idx)
+    assert torch.equal(layer.topk_counts_buffer[:rows].cpu(), want_counts)
+    s = wl.shape
+    kv = wl.kv_cache.cpu()
+    if kv_layout == "token_major":
+        k, v = kv[..., :s.head_dim], kv[..., s.head_dim:]
+    else:
+        k, v = kv.transpose(1, 2).split(s.head_dim, dim=-1)
+    want = oracle.sparse_attention(wl.q.cpu(), k, v, want_idx, wl.block_table.cpu(),
+                                   wl.token_to_req.cpu(), indices_are_physical=True,
+                                   valid_counts=want_counts,
+                                   output_gate=None if wl.gate is None else wl.gate.cpu())
+    _check_attn(output[:rows], want, "uniform decode")
+    assert (output[rows:].float() == 0).all(), "rows past num_actual_tokens are zeroed"
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("decode_requests", [0, 3])
+def test_run_qsa_prefill_and_mixed(decode_requests):
+    """max_query_len > 1: logical ids for every row (decode rows included), no counts."""
+    wl = make_workload("prefill_8k_on_16k", device=DEV, batch=5, chunk=40, prefix=0,
+                       seq_len_min=700, seq_len_max=1500, seq_len_dist="uniform",
+                       token_topk=256, decode_requests=decode_requests)
+    print(f"[backend] prefill/mixed decode_requests={decode_requests} rows={wl.rows}", flush=True)
+    layer, output = _run_layer(wl)
+    want_idx, _ = _expected_selection(wl, physical=False)
+    rows = wl.rows
+    got_idx = layer.topk_indices_buffer[:rows].cpu()
+    assert torch.equal(got_idx, want_idx)
+    s = wl.shape
+    kv = wl.kv_cache.cpu()
+    want = oracle.sparse_attention(wl.q.cpu(), kv[..., :s.head_dim], kv[..., s.head_dim:],
+                                   want_idx, wl.block_table.cpu(), wl.token_to_req.cpu())
+    _check_attn(output[:rows], want, "prefill/mixed")
+    assert (output[rows:].float() == 0).all()

@@ -178,9 +178,23 @@ def _random_physical_indices(g, rows, width, num_blocks, page, counts):
 @pytest.mark.parametrize("splits", [1, 3, 8])
 @pytest.mark.parametrize("layout", ["token_major", "head_major"])
 def test_attention_physical_parity(hq, hkv, dim, splits, layout):
-    _note(f"attention physical hq={hq} hkv={hkv} dim={dim} splits={splits} layout={layout}")
-    g = torch.Generator().manual_seed(hq * 31 + hkv * 7 + dim + splits)
-    rows, page, num_blocks, width = 6, 16, 40, 200
+    _physical_case(hq, hkv, dim, splits, layout, rows=6)
+
+
+# 64+ (row, head group) pairs switch the kernel to 8-wave workgroups.
+@pytest.mark.parametrize("hq,hkv,dim", [(16, 2, 128), (8, 1, 128), (4, 4, 128), (32, 2, 128),
+                                         (16, 2, 64), (8, 8, 64)])
+@pytest.mark.parametrize("splits", [1, 3])
+@pytest.mark.parametrize("layout", ["token_major", "head_major"])
+def test_attention_physical_parity_wide_batch(hq, hkv, dim, splits, layout):
+    _physical_case(hq, hkv, dim, splits, layout, rows=72)
+
+
+def _physical_case(hq, hkv, dim, splits, layout, rows):
+    _note(f"attention physical hq={hq} hkv={hkv} dim={dim} splits={splits} layout={layout} "
+          f"rows={rows}")
+    g = torch.Generator().manual_seed(hq * 31 + hkv * 7 + dim + splits + rows)
+    page, num_blocks, width = 16, 40, 200
     if layout == "token_major":
         kv = torch.randn(num_blocks, page, hkv, 2 * dim, generator=g).to(torch.bfloat16)
         k, v = kv[..., :dim], kv[..., dim:]
@@ -189,7 +203,7 @@ def test_attention_physical_parity(hq, hkv, dim, splits, layout):
         k, v = kv.transpose(1, 2).split(dim, dim=-1)
     q = torch.randn(rows, hq, dim, generator=g).to(torch.bfloat16)
     gate = torch.randn(rows, hq, dim, generator=g).to(torch.bfloat16)
-    counts = torch.tensor([width, 0, 1, 33, 150, 199], dtype=torch.int32)
+    counts = torch.tensor([width, 0, 1, 33, 150, 199], dtype=torch.int32).repeat(rows // 6)
     idx = _random_physical_indices(g, rows, width, num_blocks, page, counts)
     table = torch.zeros(1, 1, dtype=torch.int32)
     t2r = torch.zeros(rows, dtype=torch.int32)
@@ -207,21 +221,23 @@ def test_attention_physical_parity(hq, hkv, dim, splits, layout):
             gate.to(DEV) if use_gate else None, counts.to(DEV), True, splits)
         torch.cuda.synchronize()
         _attn_check(out, want, f"gate={use_gate}")
-        assert (out[1].float() == 0).all(), "a row with no valid slot must be zero"
+        assert (out[1::6].float() == 0).all(), "a row with no valid slot must be zero"
 
 
 @pytest.mark.parametrize("splits", [1, 4])
-def test_attention_logical_parity(splits):
-    _note(f"attention logical splits={splits}")
-    g = torch.Generator().manual_seed(40 + splits)
+@pytest.mark.parametrize("reps", [1, 8])
+def test_attention_logical_parity(splits, reps):
+    _note(f"attention logical splits={splits} rows={9 * reps}")
+    g = torch.Generator().manual_seed(40 + splits + reps)
     reqs, hq, hkv, dim, page, num_blocks = 3, 16, 2, 128, 16, 30
     k = torch.randn(num_blocks, page, hkv, dim, generator=g).to(torch.bfloat16)
     v = torch.randn(num_blocks, page, hkv, dim, generator=g).to(torch.bfloat16)
     table = torch.randperm(num_blocks, generator=g)[:reqs * 8].view(reqs, 8).to(torch.int32)
     table[1, 5:] = -1
     table[2, 0] = num_blocks + 4             # an out-of-cache page is invalid
-    rows, width = 9, 100
-    t2r = torch.tensor([0, 0, 1, 1, 2, 2, -1, 3, 0], dtype=torch.int32)  # padding + bad request
+    rows, width = 9 * reps, 100
+    # padding (-1) and out-of-range request rows repeat every 9 rows
+    t2r = torch.tensor([0, 0, 1, 1, 2, 2, -1, 3, 0], dtype=torch.int32).repeat(reps)
     idx = torch.randint(-2, 8 * page + 10, (rows, width), generator=g, dtype=torch.int32)
     q = torch.randn(rows, hq, dim, generator=g).to(torch.bfloat16)
     want = oracle.sparse_attention(q, k, v, idx, table, t2r)
@@ -229,7 +245,8 @@ def test_attention_logical_parity(splits):
                                      t2r.to(DEV), decode_config=(32, splits, 4))
     torch.cuda.synchronize()
     _attn_check(out, want, "logical")
-    assert (out[6:8].float() == 0).all()
+    bad = (t2r < 0) | (t2r >= reqs)
+    assert (out[bad.to(DEV)].float() == 0).all()
 
 
 def test_decode_select_then_attend_small():
