@@ -29,12 +29,15 @@ import time
 
 METRIC = "QSA decode tokens/s + sparse-attn HBM GB/s (% of peak), 32k ctx, 1 MI355X"
 HBM_PEAK_GBPS = 8000.0
-WORKLOAD = "decode_32k"
+BF16_PEAK_TFLOPS = 2500.0
+WORKLOADS = ("decode_32k", "decode_long_skew", "prefill_8k_on_16k")
 
 
 def parse_args():
     p = argparse.ArgumentParser(description=__doc__.split("\n\n")[0])
     p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--workload", default="decode_32k", choices=WORKLOADS,
+                   help="decode_32k is the headline; the others are secondary figures")
     p.add_argument("--steps", type=int, default=200)
     p.add_argument("--warmup", type=int, default=20)
     p.add_argument("--sets", type=int, default=4, help="query sets rotated across steps")
@@ -90,9 +93,11 @@ def main():
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
     t0 = time.time()
-    wl = make_workload(WORKLOAD, device=dev)
+    wl = make_workload(args.workload, device=dev)
     s = wl.shape
     rows = wl.rows
+    if not wl.is_decode:
+        return run_prefill(args, wl)
     sets = [(wl.q, wl.q_index)] + [fresh_queries(wl, 100 + i) for i in range(args.sets - 1)]
     n_sets = len(sets)
     idx = [torch.empty(rows, s.width, dtype=torch.int32, device=dev) for _ in sets]
@@ -102,7 +107,7 @@ def main():
     from qsa_vllm_amd.graph_dispatch import decode_logits_columns
     cols = decode_logits_columns(wl.max_seq_len, s.compress_ratio, cols)
     logits = [torch.empty(rows, cols, dtype=torch.float32, device=dev) for _ in sets]
-    log(f"workload {WORKLOAD} built in {time.time() - t0:.1f}s: rows={rows} "
+    log(f"workload {args.workload} built in {time.time() - t0:.1f}s: rows={rows} "
         f"kv_cache={wl.kv_cache.numel() * 2 / 1e9:.2f} GB")
 
     def select(i):
@@ -208,7 +213,8 @@ def main():
     attn_bytes = sum(attention_bytes(wl, counts[i]) for i in range(n_sets)) / n_sets
     attn_gbps = attn_bytes / (attn_us * 1e-6) / 1e9
     idx_bytes = indexer_bytes(wl)
-    traffic = read_traffic(args.traffic)
+    # The committed counter summary covers the headline workload only.
+    traffic = read_traffic(args.traffic) if args.workload == "decode_32k" else None
 
     result = {
         "metric": METRIC,
@@ -224,10 +230,7 @@ def main():
         "dtype": "bf16",
         "data": "synthetic: seeded N(0,1) activations and caches, permuted block tables",
         "config": {
-            "workload": f"{WORKLOAD}: decode batch {s.batch}, context U[{s.seq_len_min},"
-                        f"{s.seq_len_max}], {s.num_q_heads}q/{s.num_kv_heads}kv x {s.head_dim}, "
-                        f"page {s.page_size}, compress ratio {s.compress_ratio}, top-k "
-                        f"{s.token_topk} tokens, indexer {s.index_heads}x{s.index_dim}",
+            "workload": describe(s),
             "batch": s.batch,
             "query_sets": n_sets,
             "kv_layout": s.kv_layout,
@@ -254,6 +257,126 @@ def main():
     }
     if args.cpu_seconds > 0:
         result["cpu_baseline"] = cpu_baseline(wl, args)
+    print(json.dumps(result), flush=True)
+    return 0
+
+
+def describe(s):
+    if s.seq_len_dist == "uniform":
+        ctx = f"context U[{s.seq_len_min},{s.seq_len_max}]"
+    elif s.seq_len_dist == "lognormal":
+        ctx = (f"context lognormal(median {s.lognormal_median:.0f}, sigma {s.lognormal_sigma}) "
+               f"clipped to [{s.seq_len_min},{s.seq_len_max}]")
+    else:
+        ctx = f"context {s.seq_len_min}"
+    kind = (f"chunked prefill {s.batch} x {s.chunk} new tokens on a {s.prefix}-token prefix"
+            if s.chunk else f"decode batch {s.batch}")
+    return (f"{s.name}: {kind}, {ctx}, {s.num_q_heads}q/{s.num_kv_heads}kv x {s.head_dim}, "
+            f"page {s.page_size}, compress ratio {s.compress_ratio}, top-k {s.token_topk} "
+            f"tokens, indexer {s.index_heads}x{s.index_dim}")
+
+
+def run_prefill(args, wl):
+    """Chunked prefill step: prefill scoring (MFMA) -> logical top-k/expand ->
+    sparse attention over logical ids. The step's rows are the new tokens."""
+    import torch
+
+    from qsa_vllm_amd.graph_dispatch import prefill_logits_width
+    from qsa_vllm_amd.ops import qsa_sparse_paged_attention, select_paged_tokens, topk_expand
+    from qsa_vllm_amd.workloads import indexer_flops
+
+    s = wl.shape
+    rows = wl.rows
+    dev = wl.device
+    idx = torch.empty(rows, s.width, dtype=torch.int32, device=dev)
+    out = torch.zeros_like(wl.q)
+    width = prefill_logits_width(wl.max_seq_len, s.compress_ratio,
+                                 wl.index_table.shape[1] * wl.index_cache.shape[1])
+    logits = torch.empty(rows, width, dtype=torch.float32, device=dev)
+
+    def select():
+        select_paged_tokens(wl.q_index, wl.index_cache, wl.index_table, wl.token_to_req,
+                            wl.positions, wl.seq_lens, s.token_topk, s.compress_ratio, idx,
+                            query_start_loc=wl.query_start_loc, max_query_len=wl.max_query_len,
+                            max_seq_len=wl.max_seq_len, visible_blocks=wl.visible)
+
+    def attend():
+        qsa_sparse_paged_attention(wl.q, wl.k_cache, wl.v_cache, idx, wl.block_table,
+                                   wl.token_to_req, out)
+
+    def index_only():
+        torch.ops.yulan_qsa_kernels.indexer_prefill(wl.q_index, wl.index_cache, wl.index_table,
+                                                    wl.query_start_loc, wl.visible, logits, 0,
+                                                    rows, wl.max_query_len)
+
+    def topk_only():
+        topk_expand(logits, wl.visible, wl.positions, wl.seq_lens, wl.token_to_req, idx,
+                    s.compress_ratio)
+
+    def step():
+        select()
+        attend()
+
+    stream = torch.cuda.current_stream()
+
+    def timed(fn, reps):
+        fn()
+        torch.cuda.synchronize()
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record(stream)
+        for _ in range(reps):
+            fn()
+        b.record(stream)
+        torch.cuda.synchronize()
+        return a.elapsed_time(b) / reps  # ms
+
+    steps = max(1, min(args.steps, 20))
+    for _ in range(min(args.warmup, 3)):
+        step()
+    ms_step = timed(step, steps)
+    idx_ms = timed(index_only, steps)
+    topk_ms = timed(topk_only, steps)
+    attn_ms = timed(attend, steps)
+    if not torch.isfinite(out.float()).all():
+        raise SystemExit("non-finite attention output: results invalid")
+    flops = indexer_flops(wl)
+    valid = int((idx >= 0).sum())
+    gathered = valid * s.num_kv_heads * 2 * s.head_dim * 2
+    tflops = flops / (idx_ms * 1e-3) / 1e12
+    result = {
+        "metric": f"QSA chunked-prefill new tokens/s + prefill indexer bf16 TFLOP/s, 1 MI355X",
+        "value": round(rows / (ms_step * 1e-3), 1),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": steps,
+        "warmup": min(args.warmup, 3),
+        "ms_per_step": round(ms_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic: seeded N(0,1) activations and caches, permuted block tables",
+        "config": {"workload": describe(s), "rows": rows},
+        "roofline": {
+            "kernel": "indexer_prefill_kernel",
+            "bound": "mfma",
+            "achieved": round(tflops, 1),
+            "peak": BF16_PEAK_TFLOPS,
+            "unit": "TFLOP/s",
+            "frac": round(tflops / BF16_PEAK_TFLOPS, 4),
+            "traffic": None,
+            "algorithmic_flops_per_launch": flops,
+            "ms_per_launch": round(idx_ms, 4),
+        },
+        "breakdown_ms": {
+            "indexer_prefill": round(idx_ms, 4),
+            "topk_expand": round(topk_ms, 4),
+            "sparse_attention": round(attn_ms, 4),
+            "step": round(ms_step, 4),
+        },
+        "attention_gathered_gbps": round(gathered / (attn_ms * 1e-3) / 1e9, 1),
+        "attention_gathered_bytes": gathered,
+    }
     print(json.dumps(result), flush=True)
     return 0
 
@@ -367,7 +490,7 @@ def cpu_baseline(wl, args):
         "unit": "tokens/s",
         "cores": threads,
         "kind": "port",
-        "sample": f"{steps} full decode step(s) of the {WORKLOAD} batch ({wl.rows} rows) in "
+        "sample": f"{steps} full decode step(s) of the {wl.shape.name} batch ({wl.rows} rows) in "
                   f"{elapsed:.1f}s: oracle indexer -> top-k/expand -> fp32 sparse attention",
         "cpu": _cpu_model(),
         "torch": torch.__version__,

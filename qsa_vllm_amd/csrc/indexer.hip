@@ -68,55 +68,86 @@ __device__ __forceinline__ float relu_head_sum(const f32x16& acc) {
 }
 
 // ---------------------------------------------------------------------------
-// Decode: grid (programs, rows), one wave per workgroup.
+// Decode: grid (programs, rows), one wave per workgroup, TPW consecutive
+// 32-key tiles per wave.
+//
+// A wave's loads complete in issue order, so they are issued in the order
+// they are needed and all before the first use: the page-table entries of the
+// wave's keys, then Q, then every key row. Each wait then covers exactly the
+// group in hand while the rest stays in flight. All loads are unconditional
+// (invalid keys read the zero block), which keeps the wait counts static.
 // ---------------------------------------------------------------------------
-template <int D, int MB>
+constexpr int kDecodeTilesPerWave = 2;
+
+template <int D, int MB, int TPW>
 __global__ __launch_bounds__(64) void indexer_decode_kernel(const IndexerParams p) {
   constexpr int KS = D / 16;
   const int lane = threadIdx.x;
   const int kk = lane & 31;
   const int half = lane >> 5;
   const int row = blockIdx.y;
-  const int prog = blockIdx.x;
+  const int tile0 = blockIdx.x * TPW;
   const int num_columns = p.table_width * p.cache_page;
   const int vis = min(min(p.visible[row], num_columns), p.logits_cols);
-  if (prog * 32 >= vis) return;
+  if (tile0 * 32 >= vis) return;
   const int req = row / p.decode_query_len;
   const int32_t* trow = p.table + (int64_t)req * p.table_row;
+  const int32_t* zero_i = reinterpret_cast<const int32_t*>(g_qsa_zero_rows);
+  const char* zero = reinterpret_cast<const char*>(g_qsa_zero_rows);
 
-  // A operand: lane holds Q[head 32 mb + kk][16 s + 8 half .. +7].
+  // 1. Page-table entries of this lane's key in each tile.
+  int page[TPW];
+  bool live[TPW];
+#pragma unroll
+  for (int t = 0; t < TPW; ++t) {
+    const int c = (tile0 + t) * 32 + kk;
+    live[t] = c < vis;
+    page[t] = *(live[t] ? trow + p.page_div.div(c) : zero_i);
+  }
+
+  // 2. A operand: lane holds Q[head 32 mb + kk][16 s + 8 half .. +7].
   bf16x8 qa[MB][KS];
 #pragma unroll
   for (int mb = 0; mb < MB; ++mb) {
     const int h = 32 * mb + kk;
-    const uint16_t* qrow = p.q + (int64_t)row * p.q_row + (int64_t)(h < p.num_heads ? h : 0) * p.q_head;
+    const uint16_t* qrow = p.q + (int64_t)row * p.q_row + (int64_t)h * p.q_head;
 #pragma unroll
     for (int s = 0; s < KS; ++s) {
-      u32x4 raw = {0u, 0u, 0u, 0u};
-      if (h < p.num_heads) raw = load_u32x4(qrow + 16 * s + 8 * half);
-      qa[mb][s] = __builtin_bit_cast(bf16x8, raw);
+      const void* src = h < p.num_heads ? (const void*)(qrow + 16 * s + 8 * half) : (const void*)zero;
+      qa[mb][s] = __builtin_bit_cast(bf16x8, load_u32x4(src));
     }
   }
 
-  float* lrow = p.logits + (int64_t)row * p.logits_row;
-  for (int tile = prog; tile * 32 < vis; tile += gridDim.x) {
-    const int c = tile * 32 + kk;
-    const bool live = c < vis;
-    const char* kp = key_ptr(p, trow, c, live);
-    bf16x8 kb[KS];
+  // 3. Every key row of the wave's tiles (B operand: K^T, 16 B per lane per step).
+  bf16x8 kb[TPW][KS];
 #pragma unroll
-    for (int s = 0; s < KS; ++s) kb[s] = __builtin_bit_cast(bf16x8, load_u32x4(kp + (16 * s + 8 * half) * 2));
+  for (int t = 0; t < TPW; ++t) {
+    const int c = (tile0 + t) * 32 + kk;
+    const int lp = p.page_div.div(c);
+    const bool ok = live[t] && page[t] >= 0 && page[t] < p.num_blocks;
+    const char* kp = ok ? p.k + (int64_t)page[t] * p.kb + (int64_t)(c - lp * p.cache_page) * p.kt
+                        : zero;
+#pragma unroll
+    for (int s = 0; s < KS; ++s)
+      kb[t][s] = __builtin_bit_cast(bf16x8, load_u32x4(kp + (16 * s + 8 * half) * 2));
+  }
+  __builtin_amdgcn_sched_barrier(0);  // keep every load ahead of the first MFMA
+
+  float* lrow = p.logits + (int64_t)row * p.logits_row;
+#pragma unroll
+  for (int t = 0; t < TPW; ++t) {
     float sum = 0.0f;
 #pragma unroll
     for (int mb = 0; mb < MB; ++mb) {
       f32x16 acc = {};
 #pragma unroll
       for (int s = 0; s < KS; ++s)
-        acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(qa[mb][s], kb[s], acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(qa[mb][s], kb[t][s], acc, 0, 0, 0);
       sum += relu_head_sum(acc);
     }
     sum += shfl_xor_f(sum, 32);
-    if (half == 0 && live) lrow[c] = sum * p.scale;
+    const int c = (tile0 + t) * 32 + kk;
+    if (half == 0 && live[t]) lrow[c] = sum * p.scale;
   }
 }
 
@@ -272,18 +303,20 @@ extern "C" int qsa_indexer_decode(const void* q, int64_t q_row_stride, int64_t q
   p.logits_row = logits_row_stride;
   p.logits_cols = logits_cols;
   p.scale = (float)(1.0 / __builtin_sqrt((double)head_dim));
+  // One wave per kDecodeTilesPerWave key tiles of a row: every key of the
+  // batch is in flight at once for batches up to tens of thousands of keys.
   const int max_tiles = (std::min(logits_cols, table_width * cache_page) + 31) / 32;
-  int programs = (1024 + rows - 1) / rows;
-  programs = std::max(1, std::min(programs, max_tiles));
+  const int programs = std::max(1, (max_tiles + kDecodeTilesPerWave - 1) / kDecodeTilesPerWave);
   const dim3 grid(programs, rows);
   hipStream_t s = static_cast<hipStream_t>(stream);
   if (rows > 65535) return fail(QSA_ERR_UNSUPPORTED, "qsa_indexer_decode: more than 65535 rows");
+  constexpr int T = kDecodeTilesPerWave;
   if (head_dim == 128) {
-    if (num_heads <= 32) hipLaunchKernelGGL((indexer_decode_kernel<128, 1>), grid, dim3(64), 0, s, p);
-    else hipLaunchKernelGGL((indexer_decode_kernel<128, 2>), grid, dim3(64), 0, s, p);
+    if (num_heads <= 32) hipLaunchKernelGGL((indexer_decode_kernel<128, 1, T>), grid, dim3(64), 0, s, p);
+    else hipLaunchKernelGGL((indexer_decode_kernel<128, 2, T>), grid, dim3(64), 0, s, p);
   } else {
-    if (num_heads <= 32) hipLaunchKernelGGL((indexer_decode_kernel<64, 1>), grid, dim3(64), 0, s, p);
-    else hipLaunchKernelGGL((indexer_decode_kernel<64, 2>), grid, dim3(64), 0, s, p);
+    if (num_heads <= 32) hipLaunchKernelGGL((indexer_decode_kernel<64, 1, T>), grid, dim3(64), 0, s, p);
+    else hipLaunchKernelGGL((indexer_decode_kernel<64, 2, T>), grid, dim3(64), 0, s, p);
   }
   return check_launch("qsa_indexer_decode launch");
 }

@@ -90,21 +90,19 @@ __device__ __forceinline__ float sigmoidf_(float x) { return 1.0f / (1.0f + __ex
 
 #define QSA_SCHED_FENCE() __builtin_amdgcn_sched_barrier(0)
 
-// Index-list entry of column `col`, -1 past the row's valid count.
-__device__ __forceinline__ int index_at(const int32_t* irow, int col, int n_valid) {
-  return col < n_valid ? irow[col] : -1;
-}
-
 // Validated physical slot (page * page_size + offset) of index value `tok`,
-// or -1 (ops/qsa.py:186-212).
+// or -1 (ops/qsa.py:186-212). The block-table load of logical indices is
+// unconditional (an invalid entry reads the zero block and is then rejected)
+// so that the compiler's wait counts stay static.
+template <bool PHYSICAL>
 __device__ __forceinline__ int resolve_slot(const AttnParams& p, const int32_t* trow, bool req_ok,
                                             int tok) {
-  if (tok < 0) return -1;
-  const int lp = p.page_div.div(tok);
-  if (p.physical) return lp < p.num_blocks ? tok : -1;
-  if (!req_ok || lp >= p.table_width) return -1;
-  const int page = trow[lp];
-  return (page >= 0 && page < p.num_blocks) ? page * p.page_size + (tok - lp * p.page_size) : -1;
+  const int lp = p.page_div.div(max(tok, 0));
+  if (PHYSICAL) return (tok >= 0 && lp < p.num_blocks) ? tok : -1;
+  const bool mapped = tok >= 0 && req_ok && lp < p.table_width;
+  const int page = *(mapped ? trow + lp : reinterpret_cast<const int32_t*>(g_qsa_zero_rows));
+  return (mapped && page >= 0 && page < p.num_blocks) ? page * p.page_size + (tok - lp * p.page_size)
+                                                      : -1;
 }
 
 // Byte offset of a validated slot's row in a cache with (block, token) strides.
@@ -144,18 +142,37 @@ __device__ __forceinline__ int v_col(int tile, int i, int g) {
   return tile * kTile + 16 * (i >> 2) + 4 * g + (i & 3);
 }
 
-// Raw index entries of a tile (-1 when the tile is past the split's end).
+// Raw index entries of a tile. Every entry is loaded unconditionally (columns
+// past the valid count or the split read the zero block) with its validity in
+// `ok`, applied only when the entry is used: a skipped load would make the
+// compiler drain every outstanding load at the first use instead of waiting
+// for these loads alone.
 struct TileIdx {
   int k[2];
   int v[8];
+  uint32_t ok;  // bits 0-1: k[u], bits 2-9: v[i]
+  __device__ __forceinline__ int key(int u) const { return (ok >> u) & 1u ? k[u] : -1; }
+  __device__ __forceinline__ int val(int i) const { return (ok >> (2 + i)) & 1u ? v[i] : -1; }
 };
 __device__ __forceinline__ void load_tile_idx(const int32_t* irow, int tile, int t_end,
                                               int n_valid, int n, int g, TileIdx& r) {
-  const bool ok = tile < t_end;
+  const int32_t* zero = reinterpret_cast<const int32_t*>(g_qsa_zero_rows);
+  const bool live = tile < t_end;
+  r.ok = 0;
 #pragma unroll
-  for (int u = 0; u < 2; ++u) r.k[u] = ok ? index_at(irow, k_col(tile, u, n), n_valid) : -1;
+  for (int u = 0; u < 2; ++u) {
+    const int col = k_col(tile, u, n);
+    const bool ok = live && col < n_valid;
+    r.k[u] = *(ok ? irow + col : zero);
+    r.ok |= (uint32_t)ok << u;
+  }
 #pragma unroll
-  for (int i = 0; i < 8; ++i) r.v[i] = ok ? index_at(irow, v_col(tile, i, g), n_valid) : -1;
+  for (int i = 0; i < 8; ++i) {
+    const int col = v_col(tile, i, g);
+    const bool ok = live && col < n_valid;
+    r.v[i] = *(ok ? irow + col : zero);
+    r.ok |= (uint32_t)ok << (2 + i);
+  }
 }
 
 template <int D, int NKV>
@@ -264,7 +281,7 @@ __device__ __forceinline__ void pv_mfma(const TileV<D, NKV>& V, u32x4 praw, int 
 }
 
 // Two waves per SIMD wherever the registers allow it without spilling.
-template <int D, int NKV, int WAVES>
+template <int D, int NKV, int WAVES, bool PHYSICAL>
 __global__ __launch_bounds__(64 * WAVES)
 __attribute__((amdgpu_waves_per_eu(D == 128 && NKV == 4 ? 1 : 2)))
 void sparse_attn_kernel(const AttnParams p) {
@@ -294,10 +311,10 @@ void sparse_attn_kernel(const AttnParams p) {
   bf16x8 bq[NKV][KS];
   {
     const uint16_t* qrow = p.q + (int64_t)row * p.q_row + (int64_t)(head_ok ? qh : 0) * p.q_head;
+    const void* zero = g_qsa_zero_rows;
 #pragma unroll
     for (int s = 0; s < KS; ++s) {
-      u32x4 raw = {0u, 0u, 0u, 0u};
-      if (head_ok) raw = load_u32x4(qrow + 32 * s + 8 * g);
+      const u32x4 raw = load_u32x4(head_ok ? (const void*)(qrow + 32 * s + 8 * g) : zero);
 #pragma unroll
       for (int v = 0; v < NKV; ++v) {
         const u32x4 sel = (vslot == v) ? raw : u32x4{0u, 0u, 0u, 0u};
@@ -338,34 +355,33 @@ void sparse_attn_kernel(const AttnParams p) {
     // Prologue, in issue order: K(t), index entries of t+W, V(t).
     load_tile_idx(irow, t, t_end, n_valid, n, g, idx);
 #pragma unroll
-    for (int u = 0; u < 2; ++u) ks[u] = resolve_slot(p, trow, req_ok, idx.k[u]);
+    for (int u = 0; u < 2; ++u) ks[u] = resolve_slot<PHYSICAL>(p, trow, req_ok, idx.key(u));
 #pragma unroll
-    for (int i = 0; i < 8; ++i) vs[i] = resolve_slot(p, trow, req_ok, idx.v[i]);
+    for (int i = 0; i < 8; ++i) vs[i] = resolve_slot<PHYSICAL>(p, trow, req_ok, idx.val(i));
     issue_k<D, NKV>(p, ks, khead, g, K);
     QSA_SCHED_FENCE();
     load_tile_idx(irow, t + WAVES, t_end, n_valid, n, g, idx);
     QSA_SCHED_FENCE();
     issue_v<D, NKV>(p, vs, vhead, n, V);
     QSA_SCHED_FENCE();
+    // The next tile's loads are issued even on the last trip (its slots are
+    // then all invalid and read the zero block): loads under a branch would
+    // make the compiler's wait counts assume the branch not taken, so P.V(t)
+    // would also wait for K(t+W).
     for (; t < t_end; t += WAVES) {
-      const bool has_next = t + WAVES < t_end;
       const u32x4 praw = qk_softmax<D, NKV>(p, K, bq, V.mask, m_run, l_run, oacc);
       QSA_SCHED_FENCE();
-      if (has_next) {
 #pragma unroll
-        for (int u = 0; u < 2; ++u) ks[u] = resolve_slot(p, trow, req_ok, idx.k[u]);
+      for (int u = 0; u < 2; ++u) ks[u] = resolve_slot<PHYSICAL>(p, trow, req_ok, idx.key(u));
 #pragma unroll
-        for (int i = 0; i < 8; ++i) vs[i] = resolve_slot(p, trow, req_ok, idx.v[i]);
-        issue_k<D, NKV>(p, ks, khead, g, K);
-      }
+      for (int i = 0; i < 8; ++i) vs[i] = resolve_slot<PHYSICAL>(p, trow, req_ok, idx.val(i));
+      issue_k<D, NKV>(p, ks, khead, g, K);
       QSA_SCHED_FENCE();
       pv_mfma<D, NKV>(V, praw, vslot, oacc);
       QSA_SCHED_FENCE();
-      if (has_next) {
-        load_tile_idx(irow, t + 2 * WAVES, t_end, n_valid, n, g, idx);
-        QSA_SCHED_FENCE();
-        issue_v<D, NKV>(p, vs, vhead, n, V);
-      }
+      load_tile_idx(irow, t + 2 * WAVES, t_end, n_valid, n, g, idx);
+      QSA_SCHED_FENCE();
+      issue_v<D, NKV>(p, vs, vhead, n, V);
       QSA_SCHED_FENCE();
     }
   }
@@ -541,16 +557,24 @@ int waves_for(int rows, const HeadPlan& plan, int head_dim) {
   return (int64_t)rows * plan.groups >= 64 && fits_8_waves(head_dim, plan.nkv) ? 8 : 4;
 }
 
-template <int D, int NKV>
-hipError_t launch_attn(const AttnParams& p, dim3 grid, int waves, hipStream_t stream) {
+template <int D, int NKV, bool PHYSICAL>
+hipError_t launch_attn_mode(const AttnParams& p, dim3 grid, int waves, hipStream_t stream) {
   if constexpr (!(D == 128 && NKV == 4)) {
     if (waves == 8) {
-      hipLaunchKernelGGL((sparse_attn_kernel<D, NKV, 8>), grid, dim3(512), 0, stream, p);
+      hipLaunchKernelGGL((sparse_attn_kernel<D, NKV, 8, PHYSICAL>), grid, dim3(512), 0, stream, p);
       return hipGetLastError();
     }
   }
-  hipLaunchKernelGGL((sparse_attn_kernel<D, NKV, 4>), grid, dim3(256), 0, stream, p);
+  hipLaunchKernelGGL((sparse_attn_kernel<D, NKV, 4, PHYSICAL>), grid, dim3(256), 0, stream, p);
   return hipGetLastError();
+}
+
+// Physical and logical indices are separate kernels: the logical form's
+// block-table loads would otherwise make every wait in the loop conservative.
+template <int D, int NKV>
+hipError_t launch_attn(const AttnParams& p, dim3 grid, int waves, hipStream_t stream) {
+  return p.physical ? launch_attn_mode<D, NKV, true>(p, grid, waves, stream)
+                    : launch_attn_mode<D, NKV, false>(p, grid, waves, stream);
 }
 
 int launch_merge(const float* part_out, const float* part_lse, int num_splits, int rows,

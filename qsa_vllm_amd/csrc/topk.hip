@@ -109,40 +109,43 @@ __device__ __forceinline__ int table_entry(const RowMeta& r, int lp) {
 }
 
 // --- loaders ---------------------------------------------------------------
+//
+// Every load here is unconditional: an id outside the row reads the zero
+// block instead of being skipped. That keeps the number of loads a wave has in
+// flight known at compile time, so waiting for the scores does not also wait
+// for the page-table loads issued after them (a skipped, divergent load forces
+// the compiler to drain every outstanding load instead).
 
 struct DirectLoader {  // ids start + i over a contiguous score row
   const float* scores;
   int start;
-  __device__ __forceinline__ int id(int i) const { return start + i; }
+  __device__ __forceinline__ int id_at(int i) const { return start + i; }
   template <int ITEMS>
-  __device__ __forceinline__ void load(int base, int limit, uint32_t (&key)[ITEMS]) const {
-    const float* p = scores + start + base;
-    if (ITEMS % 4 == 0 && base + ITEMS <= limit && (((uintptr_t)p) & 15u) == 0) {
+  __device__ __forceinline__ void load(int base, int limit, uint32_t (&key)[ITEMS],
+                                       int (&id)[ITEMS]) const {
+    const uint32_t* row = reinterpret_cast<const uint32_t*>(scores + start);
 #pragma unroll
-      for (int j = 0; j < ITEMS; j += 4) {
-        const u32x4 v = load_u32x4(p + j);
-        key[j] = v[0];
-        key[j + 1] = v[1];
-        key[j + 2] = v[2];
-        key[j + 3] = v[3];
-      }
-      return;
+    for (int j = 0; j < ITEMS; ++j) {
+      const bool in = base + j < limit;
+      key[j] = *(in ? row + base + j : g_qsa_zero_rows);
+      id[j] = start + base + j;
     }
-#pragma unroll
-    for (int j = 0; j < ITEMS; ++j)
-      key[j] = base + j < limit ? __builtin_bit_cast(uint32_t, p[j]) : 0u;
   }
 };
 
 struct IndirectLoader {  // candidate list of ids into a score row
   const float* scores;
   const int32_t* ids;
-  __device__ __forceinline__ int id(int i) const { return ids[i]; }
+  __device__ __forceinline__ int id_at(int i) const { return ids[i]; }
   template <int ITEMS>
-  __device__ __forceinline__ void load(int base, int limit, uint32_t (&key)[ITEMS]) const {
+  __device__ __forceinline__ void load(int base, int limit, uint32_t (&key)[ITEMS],
+                                       int (&id)[ITEMS]) const {
+    const uint32_t* row = reinterpret_cast<const uint32_t*>(scores);
+    const int32_t* zero = reinterpret_cast<const int32_t*>(g_qsa_zero_rows);
 #pragma unroll
-    for (int j = 0; j < ITEMS; ++j)
-      key[j] = base + j < limit ? __builtin_bit_cast(uint32_t, scores[ids[base + j]]) : 0u;
+    for (int j = 0; j < ITEMS; ++j) id[j] = *(base + j < limit ? ids + base + j : zero);
+#pragma unroll
+    for (int j = 0; j < ITEMS; ++j) key[j] = row[id[j]];  // id 0 stands in past the list
   }
 };
 
@@ -194,10 +197,11 @@ __device__ __forceinline__ void block_scan2(int& a, int& b, TopkShared<THREADS>&
 
 // Exact top-k of `length` (> topk) keys in registers. Writes the selected ids
 // in ascending-id order to sel[0..topk) and the matching prefetched values of
-// aux to sel[topk..2 topk).
-template <int THREADS, int ITEMS, typename Loader>
-__device__ void select_long(const Loader& load, int length, int topk, const uint32_t (&key)[ITEMS],
-                            const int (&aux)[ITEMS], TopkShared<THREADS>& sh, int* sel) {
+// aux (-1 where bit j of aux_ok is clear) to sel[topk..2 topk).
+template <int THREADS, int ITEMS>
+__device__ void select_long(int length, int topk, const uint32_t (&key)[ITEMS],
+                            const int (&id)[ITEMS], const int (&aux)[ITEMS], uint32_t aux_ok,
+                            TopkShared<THREADS>& sh, int* sel) {
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int base = tid * ITEMS;
@@ -308,14 +312,21 @@ __device__ void select_long(const Loader& load, int length, int topk, const uint
       ++n_tie;
     }
     if (rank >= 0) {
-      sel[rank] = load.id(base + j);
-      sel[topk + rank] = aux[j];
+      sel[rank] = id[j];
+      sel[topk + rank] = (aux_ok >> j) & 1u ? aux[j] : -1;
     }
   }
 }
 
 // Writes one expanded output row (coalesced over columns) from ranked block
 // ids in sel[0..topk) and their first-token physical pages in sel[topk..).
+//
+// The common layouts (logical ids, or blocks that lie inside one page with the
+// causal tail's pages prefetched) write the row from LDS alone, one block of
+// columns per thread. A loop with a global load in it would make every
+// iteration wait for all earlier stores: on gfx9 stores count in the same
+// in-order counter as loads, and the compiler cannot tell a skipped load from a
+// pending one.
 __device__ __forceinline__ void write_expanded(const ExpandMeta& m, const RowMeta& r, int row,
                                                int topk, const int* sel, const int* tail_page,
                                                int32_t* out) {
@@ -325,35 +336,58 @@ __device__ __forceinline__ void write_expanded(const ExpandMeta& m, const RowMet
   const int tail_count = p1 - tail_start;
   const int expanded = complete * m.ratio;
   const bool block_in_page = m.physical && (m.page_size % m.ratio == 0);
-  for (int c = threadIdx.x; c < m.out_width; c += blockDim.x) {
-    int v = -1;
-    if (c < expanded) {
-      const int rank = m.ratio_div.div(c);
-      const int o = c - rank * m.ratio;
-      const int block = sel[rank];
-      if (block >= 0) {
-        const int first = block * m.ratio;
-        if (!m.physical) {
-          v = slot_of(m, r, first + o, 0);
-        } else if (block_in_page) {
-          // The block lies inside one page (topk.cu:134-146).
-          const int s0 = slot_of(m, r, first, sel[topk + rank]);
-          v = (s0 >= 0 && first + o < r.seq_len) ? s0 + o : -1;
-        } else {
-          const int t = first + o;
-          v = slot_of(m, r, t, table_entry(r, token_page(m, t)));
+  const bool from_lds = !m.physical || (block_in_page && m.ratio - 1 <= kTailSlots);
+  if (from_lds) {
+    const int64_t cs = m.out_col_stride;
+    // Thread b writes the `ratio` columns of rank b: two LDS reads, then
+    // plain stores (topk.cu:134-146 for the physical form).
+    for (int b = threadIdx.x; b < complete; b += blockDim.x) {
+      const int block = sel[b];
+      const int first = block * m.ratio;
+      int base = first;
+      if (m.physical) {
+        const int pp = sel[topk + b];
+        base = pp >= 0 ? pp * m.page_size + (first - m.page_div.div(max(first, 0)) * m.page_size) : -1;
+      }
+      const int lim = (block < 0 || base < 0) ? 0 : min(m.ratio, r.seq_len - first);
+      int32_t* o = out + (int64_t)b * m.ratio * cs;
+      for (int j = 0; j < m.ratio; ++j, o += cs) *o = j < lim ? base + j : -1;
+    }
+    // Causal tail, then -1 to the end of the row.
+    for (int c = expanded + threadIdx.x; c < m.out_width; c += blockDim.x) {
+      const int off = c - expanded;
+      int v = -1;
+      if (off < tail_count && off < m.ratio - 1)
+        v = slot_of(m, r, tail_start + off, m.physical ? tail_page[off] : 0);
+      out[(int64_t)c * cs] = v;
+    }
+  } else {
+    for (int c = threadIdx.x; c < m.out_width; c += blockDim.x) {
+      int v = -1;
+      if (c < expanded) {
+        const int rank = m.ratio_div.div(c);
+        const int o = c - rank * m.ratio;
+        const int block = sel[rank];
+        if (block >= 0) {
+          const int first = block * m.ratio;
+          if (block_in_page) {
+            const int s0 = slot_of(m, r, first, sel[topk + rank]);
+            v = (s0 >= 0 && first + o < r.seq_len) ? s0 + o : -1;
+          } else {
+            const int t = first + o;
+            v = slot_of(m, r, t, table_entry(r, token_page(m, t)));
+          }
+        }
+      } else {
+        const int off = c - expanded;
+        if (off < tail_count && off < m.ratio - 1) {
+          const int t = tail_start + off;
+          const int pp = off < kTailSlots ? tail_page[off] : table_entry(r, token_page(m, t));
+          v = slot_of(m, r, t, pp);
         }
       }
-    } else {
-      const int off = c - expanded;
-      if (off < tail_count && off < m.ratio - 1) {
-        const int t = tail_start + off;
-        const int pp = !m.physical ? 0
-                       : (off < kTailSlots ? tail_page[off] : table_entry(r, token_page(m, t)));
-        v = slot_of(m, r, t, pp);
-      }
+      out[(int64_t)c * m.out_col_stride] = v;
     }
-    out[(int64_t)c * m.out_col_stride] = v;
   }
   if (m.store_counts && threadIdx.x == 0) m.counts[row] = min(expanded + tail_count, r.seq_len);
 }
@@ -373,24 +407,33 @@ __device__ void process_row(const Loader& load, int limit, int length_raw, int c
     r.pos = (int)m.positions[row];
   }
   uint32_t key[ITEMS];
-  load.template load<ITEMS>(tid * ITEMS, limit, key);
+  int id[ITEMS];
+  load.template load<ITEMS>(tid * ITEMS, limit, key, id);
   if (tid < 256) sh.hist[tid] = 0u;
   for (int b = tid + THREADS; b < 256; b += THREADS) sh.hist[b] = 0u;
 
-  // Page-table entries this thread's blocks and the causal tail will need.
+  // Page-table entries this thread's blocks and the causal tail will need,
+  // loaded unconditionally (validity kept in bit masks, applied at use).
   int aux[ITEMS];
+  uint32_t aux_ok = 0;
   int tail_pp = -1;
+  bool tail_ok = false;
+  const int32_t* zero = reinterpret_cast<const int32_t*>(g_qsa_zero_rows);
   if (EXPAND) {
     const bool mapped = req >= 0 && req < m.num_requests;
     r.seq_len = mapped ? m.sequence_lengths[req] : 0;
     r.table_row = m.physical ? m.table + (int64_t)(mapped ? req : 0) * m.table_row_stride : nullptr;
 #pragma unroll
     for (int j = 0; j < ITEMS; ++j) {
-      const int i = tid * ITEMS + j;
-      aux[j] = (i < limit) ? table_entry(r, token_page(m, load.id(i) * m.ratio)) : -1;
+      const int lp = tid * ITEMS + j < limit ? token_page(m, id[j] * m.ratio) : -1;
+      const bool ok = r.table_row && lp >= 0;
+      aux[j] = *(ok ? r.table_row + lp : zero);
+      aux_ok |= (uint32_t)ok << j;
     }
-    if (tid < kTailSlots && tid < m.ratio - 1)
-      tail_pp = table_entry(r, token_page(m, tail_start_of(r.pos, m.ratio) + tid));
+    const int lp = (tid < kTailSlots && tid < m.ratio - 1)
+                       ? token_page(m, tail_start_of(r.pos, m.ratio) + tid) : -1;
+    tail_ok = r.table_row && lp >= 0;
+    tail_pp = *(tail_ok ? r.table_row + lp : zero);
   } else {
 #pragma unroll
     for (int j = 0; j < ITEMS; ++j) aux[j] = 0;
@@ -398,15 +441,16 @@ __device__ void process_row(const Loader& load, int limit, int length_raw, int c
 
   const int length = length_raw > topk ? min(length_raw, clamp) : length_raw;
   if (length > topk) {
-    select_long<THREADS, ITEMS>(load, length, topk, key, aux, sh, sel);
+    select_long<THREADS, ITEMS>(length, topk, key, id, aux, aux_ok, sh, sel);
   } else {
+    // At most topk entries: the loader's first `length` ids in order, then -1.
     for (int i = tid; i < topk; i += THREADS) {
-      const int id = i < length ? load.id(i) : -1;
-      sel[i] = id;
-      sel[topk + i] = (EXPAND && id >= 0) ? table_entry(r, token_page(m, id * m.ratio)) : -1;
+      const int lid = i < length ? load.id_at(i) : -1;
+      sel[i] = lid;
+      sel[topk + i] = (EXPAND && lid >= 0) ? table_entry(r, token_page(m, lid * m.ratio)) : -1;
     }
   }
-  if (EXPAND && tid < kTailSlots && tid < m.ratio - 1) sh.tail_page[tid] = tail_pp;
+  if (EXPAND && tid < kTailSlots && tid < m.ratio - 1) sh.tail_page[tid] = tail_ok ? tail_pp : -1;
   lds_barrier();
   if (EXPAND) {
     write_expanded(m, r, row, topk, sel, sh.tail_page, out);
