@@ -16,75 +16,20 @@
 // Prefill: consecutive query rows of a request see nearly the same keys, so a
 // 4-wave workgroup owns 16 rows (4 per wave, their Q in registers) and stages
 // each 32-key tile once in LDS, where all 16 rows reuse it (MFMA bound).
-#include "qsa_common.h"
+#include "indexer_device.h"
 #include "../../include/qsa_hip.h"
 
 namespace qsa {
 namespace {
 
-struct IndexerParams {
-  const uint16_t* q;
-  int64_t q_row, q_head;  // elements
-  const char* k;
-  int64_t kb, kt;  // bytes
-  int num_blocks;
-  int cache_page;
-  FastDiv page_div;
-  const int32_t* table;
-  int64_t table_row;
-  int table_width;
-  const int32_t* visible;
-  int num_heads;
-  int decode_query_len;
-  float* logits;
-  int64_t logits_row;
-  int logits_cols;
-  float scale;
-  // prefill only
-  const int32_t* query_start_loc;
-  int num_requests;
-  int query_offset;
-  int num_rows;
-  int key_tiles_per_wg;
-};
-
-// Byte address of compressed key c of a request, or the zero block.
-__device__ __forceinline__ const char* key_ptr(const IndexerParams& p, const int32_t* trow, int c,
-                                               bool live) {
-  const char* zero = reinterpret_cast<const char*>(g_qsa_zero_rows);
-  if (!live) return zero;
-  const int lp = p.page_div.div(c);
-  const int off = c - lp * p.cache_page;
-  const int page = trow[lp];
-  if (page < 0 || page >= p.num_blocks) return zero;
-  return p.k + (int64_t)page * p.kb + (int64_t)off * p.kt;
-}
-
-__device__ __forceinline__ float relu_head_sum(const f32x16& acc) {
-  float s = 0.0f;
-#pragma unroll
-  for (int i = 0; i < 16; ++i) s += fmaxf(acc[i], 0.0f);
-  return s;
-}
-
 // ---------------------------------------------------------------------------
-// Decode: grid (programs, rows), one wave per workgroup, TPW consecutive
-// 32-key tiles per wave.
-//
-// A wave's loads complete in issue order, so they are issued in the order
-// they are needed and all before the first use: the page-table entries of the
-// wave's keys, then Q, then every key row. Each wait then covers exactly the
-// group in hand while the rest stays in flight. All loads are unconditional
-// (invalid keys read the zero block), which keeps the wait counts static.
+// Decode: grid (programs, rows), one wave per workgroup, kDecodeTilesPerWave
+// consecutive 32-key tiles per wave, logits to global memory.
 // ---------------------------------------------------------------------------
 constexpr int kDecodeTilesPerWave = 2;
 
 template <int D, int MB, int TPW>
 __global__ __launch_bounds__(64) void indexer_decode_kernel(const IndexerParams p) {
-  constexpr int KS = D / 16;
-  const int lane = threadIdx.x;
-  const int kk = lane & 31;
-  const int half = lane >> 5;
   const int row = blockIdx.y;
   const int tile0 = blockIdx.x * TPW;
   const int num_columns = p.table_width * p.cache_page;
@@ -92,63 +37,10 @@ __global__ __launch_bounds__(64) void indexer_decode_kernel(const IndexerParams 
   if (tile0 * 32 >= vis) return;
   const int req = row / p.decode_query_len;
   const int32_t* trow = p.table + (int64_t)req * p.table_row;
-  const int32_t* zero_i = reinterpret_cast<const int32_t*>(g_qsa_zero_rows);
-  const char* zero = reinterpret_cast<const char*>(g_qsa_zero_rows);
-
-  // 1. Page-table entries of this lane's key in each tile.
-  int page[TPW];
-  bool live[TPW];
-#pragma unroll
-  for (int t = 0; t < TPW; ++t) {
-    const int c = (tile0 + t) * 32 + kk;
-    live[t] = c < vis;
-    page[t] = *(live[t] ? trow + p.page_div.div(c) : zero_i);
-  }
-
-  // 2. A operand: lane holds Q[head 32 mb + kk][16 s + 8 half .. +7].
-  bf16x8 qa[MB][KS];
-#pragma unroll
-  for (int mb = 0; mb < MB; ++mb) {
-    const int h = 32 * mb + kk;
-    const uint16_t* qrow = p.q + (int64_t)row * p.q_row + (int64_t)h * p.q_head;
-#pragma unroll
-    for (int s = 0; s < KS; ++s) {
-      const void* src = h < p.num_heads ? (const void*)(qrow + 16 * s + 8 * half) : (const void*)zero;
-      qa[mb][s] = __builtin_bit_cast(bf16x8, load_u32x4(src));
-    }
-  }
-
-  // 3. Every key row of the wave's tiles (B operand: K^T, 16 B per lane per step).
-  bf16x8 kb[TPW][KS];
-#pragma unroll
-  for (int t = 0; t < TPW; ++t) {
-    const int c = (tile0 + t) * 32 + kk;
-    const int lp = p.page_div.div(c);
-    const bool ok = live[t] && page[t] >= 0 && page[t] < p.num_blocks;
-    const char* kp = ok ? p.k + (int64_t)page[t] * p.kb + (int64_t)(c - lp * p.cache_page) * p.kt
-                        : zero;
-#pragma unroll
-    for (int s = 0; s < KS; ++s)
-      kb[t][s] = __builtin_bit_cast(bf16x8, load_u32x4(kp + (16 * s + 8 * half) * 2));
-  }
-  __builtin_amdgcn_sched_barrier(0);  // keep every load ahead of the first MFMA
-
+  bf16x8 qa[MB][D / 16];
+  load_q<D, MB>(p, row, qa);
   float* lrow = p.logits + (int64_t)row * p.logits_row;
-#pragma unroll
-  for (int t = 0; t < TPW; ++t) {
-    float sum = 0.0f;
-#pragma unroll
-    for (int mb = 0; mb < MB; ++mb) {
-      f32x16 acc = {};
-#pragma unroll
-      for (int s = 0; s < KS; ++s)
-        acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(qa[mb][s], kb[t][s], acc, 0, 0, 0);
-      sum += relu_head_sum(acc);
-    }
-    sum += shfl_xor_f(sum, 32);
-    const int c = (tile0 + t) * 32 + kk;
-    if (half == 0 && live[t]) lrow[c] = sum * p.scale;
-  }
+  score_tiles<D, MB, TPW>(p, trow, tile0, vis, qa, [&](int c, float v) { lrow[c] = v; });
 }
 
 // ---------------------------------------------------------------------------

@@ -1,463 +1,13 @@
 // Kernel 2: exact per-row top-k block selection + token expansion, gfx950.
 //
-// Semantics follow ops/csrc/topk.cu of the reference plugin:
-//  * order key = raw fp32 bit pattern read as uint32 (topk.cu:262, 331-338),
-//    larger key first, lower id first among equal keys;
-//  * rows with length <= k emit ids 0..length-1 then -1 (topk.cu:187-191);
-//  * selected ids are emitted in ascending id order (topk.cu:328-349);
-//  * expansion, causal tail, physical slot mapping and counts as
-//    ExpandedWriter (topk.cu:97-180).
-//
-// Algorithm (own design for wave64 + LDS). One workgroup per row holds the
-// row's keys in registers (blocked: thread t owns ids [t*ITEMS, t*ITEMS+ITEMS)).
-// A radix select walks 8-bit digits downward from the highest bit in which the
-// row's keys differ (one block min/max). Each pass builds an LDS histogram
-// (atomics with a wave-uniform fast path) and one wave locates the bin holding
-// the k-th largest key with a DPP scan. The walk stops as soon as that bin
-// holds exactly the number of keys still needed - then the selection is every
-// key >= the bin's smallest possible key - or when all 32 bits are fixed, in
-// which case the remaining slots go to the lowest ids with that exact key.
-// A block-wide exclusive scan of (selected, tied) counts in id order gives
-// each selected id its output rank; ranks land in LDS and the whole output row
-// (expanded slots, causal tail, -1 padding) is written with coalesced stores.
-//
-// The kernel is a chain of short dependent steps, so latency is what counts:
-// every independent load (scores, row metadata, the page-table entry of every
-// block a thread holds, the causal tail's pages) is issued at entry, the
-// barriers order LDS only (so those loads stay in flight through the radix
-// passes), derived row metadata is computed only when the row is written, and
-// reductions and scans are DPP sequences.
-//
-// Rows longer than the register-resident capacity use two passes: exact top-k
-// per 8192-column partition, then exact top-k over the partition winners.
-#include "qsa_common.h"
+// Semantics and algorithm: topk_device.h. This file holds the kernels (direct,
+// and partition + merge for rows longer than the register-resident capacity)
+// and the C ABI entry points.
+#include "topk_device.h"
 #include "../../include/qsa_hip.h"
-
-extern "C" __device__ unsigned int __ockl_wfred_min_u32(unsigned int);
-extern "C" __device__ unsigned int __ockl_wfred_max_u32(unsigned int);
-extern "C" __device__ int __ockl_wfscan_add_i32(int, bool);
 
 namespace qsa {
 namespace {
-
-constexpr int kPartitionColumns = 8192;
-constexpr int kMaxDirectColumns = 16384;  // register-resident capacity: 1024 threads x 16 keys
-constexpr int kMaxTopk = 8192;            // selected ids per row staged in LDS
-constexpr int kTailSlots = 64;            // causal-tail pages fetched ahead of time
-
-template <int THREADS>
-struct TopkShared {
-  uint32_t hist[256];
-  uint32_t wmin[THREADS / 64];
-  uint32_t wmax[THREADS / 64];
-  int wsel[THREADS / 64];
-  int wtie[THREADS / 64];
-  int tail_page[kTailSlots];
-  int bin;
-  int remaining;
-  int bin_count;
-};
-
-// --- row metadata -------------------------------------------------------------
-
-struct ExpandMeta {
-  const int64_t* positions;
-  const int32_t* sequence_lengths;
-  const int32_t* token_to_req;
-  const int32_t* table;
-  int32_t* counts;
-  int64_t table_row_stride;
-  int64_t out_col_stride;
-  int num_requests;
-  int table_width;
-  int page_size;
-  FastDiv page_div;
-  int ratio;
-  FastDiv ratio_div;
-  int out_width;
-  int physical;
-  int store_counts;
-};
-
-// Raw per-row inputs of the expansion (topk.cu:166-180); everything derived
-// from them is computed when the row is written.
-struct RowMeta {
-  int seq_len;
-  int pos;
-  const int32_t* table_row;  // null unless physical
-};
-
-__device__ __forceinline__ int tail_start_of(int pos, int ratio) { return ((pos + 1) / ratio) * ratio; }
-
-// Logical page of token t, or -1 when t has no page-table entry to read.
-__device__ __forceinline__ int token_page(const ExpandMeta& m, int t) {
-  if (t < 0) return -1;
-  const int lp = m.page_div.div(t);
-  return lp < m.table_width ? lp : -1;
-}
-
-// Physical slot of token t given its prefetched physical page (topk.cu:116-125).
-__device__ __forceinline__ int slot_of(const ExpandMeta& m, const RowMeta& r, int t, int pp) {
-  if (t < 0 || t >= r.seq_len) return -1;
-  if (!m.physical) return t;
-  if (pp < 0) return -1;
-  return pp * m.page_size + (t - m.page_div.div(t) * m.page_size);
-}
-
-__device__ __forceinline__ int table_entry(const RowMeta& r, int lp) {
-  return (r.table_row && lp >= 0) ? r.table_row[lp] : -1;
-}
-
-// --- loaders ---------------------------------------------------------------
-//
-// Every load here is unconditional: an id outside the row reads the zero
-// block instead of being skipped. That keeps the number of loads a wave has in
-// flight known at compile time, so waiting for the scores does not also wait
-// for the page-table loads issued after them (a skipped, divergent load forces
-// the compiler to drain every outstanding load instead).
-
-struct DirectLoader {  // ids start + i over a contiguous score row
-  const float* scores;
-  int start;
-  __device__ __forceinline__ int id_at(int i) const { return start + i; }
-  template <int ITEMS>
-  __device__ __forceinline__ void load(int base, int limit, uint32_t (&key)[ITEMS],
-                                       int (&id)[ITEMS]) const {
-    const uint32_t* row = reinterpret_cast<const uint32_t*>(scores + start);
-#pragma unroll
-    for (int j = 0; j < ITEMS; ++j) {
-      const bool in = base + j < limit;
-      key[j] = *(in ? row + base + j : g_qsa_zero_rows);
-      id[j] = start + base + j;
-    }
-  }
-};
-
-struct IndirectLoader {  // candidate list of ids into a score row
-  const float* scores;
-  const int32_t* ids;
-  __device__ __forceinline__ int id_at(int i) const { return ids[i]; }
-  template <int ITEMS>
-  __device__ __forceinline__ void load(int base, int limit, uint32_t (&key)[ITEMS],
-                                       int (&id)[ITEMS]) const {
-    const uint32_t* row = reinterpret_cast<const uint32_t*>(scores);
-    const int32_t* zero = reinterpret_cast<const int32_t*>(g_qsa_zero_rows);
-#pragma unroll
-    for (int j = 0; j < ITEMS; ++j) id[j] = *(base + j < limit ? ids + base + j : zero);
-#pragma unroll
-    for (int j = 0; j < ITEMS; ++j) key[j] = row[id[j]];  // id 0 stands in past the list
-  }
-};
-
-// --- block primitives (DPP wave reductions/scans + one LDS exchange) --------
-
-template <int THREADS>
-__device__ __forceinline__ void block_minmax(uint32_t& lo, uint32_t& hi, TopkShared<THREADS>& sh) {
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  lo = __ockl_wfred_min_u32(lo);
-  hi = __ockl_wfred_max_u32(hi);
-  if (lane == 0) {
-    sh.wmin[wave] = lo;
-    sh.wmax[wave] = hi;
-  }
-  lds_barrier();
-  lo = 0xffffffffu;
-  hi = 0u;
-#pragma unroll
-  for (int w = 0; w < THREADS / 64; ++w) {
-    lo = min(lo, sh.wmin[w]);
-    hi = max(hi, sh.wmax[w]);
-  }
-}
-
-// Exclusive scan of two counters over threads in thread order.
-template <int THREADS>
-__device__ __forceinline__ void block_scan2(int& a, int& b, TopkShared<THREADS>& sh) {
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int ea = __ockl_wfscan_add_i32(a, false);
-  const int eb = __ockl_wfscan_add_i32(b, false);
-  if (lane == 63) {
-    sh.wsel[wave] = ea + a;
-    sh.wtie[wave] = eb + b;
-  }
-  lds_barrier();
-  int pa = 0, pb = 0;
-#pragma unroll
-  for (int w = 0; w < THREADS / 64; ++w) {
-    if (w < wave) {
-      pa += sh.wsel[w];
-      pb += sh.wtie[w];
-    }
-  }
-  a = pa + ea;
-  b = pb + eb;
-}
-
-// --- selection --------------------------------------------------------------
-
-// Exact top-k of `length` (> topk) keys in registers. Writes the selected ids
-// in ascending-id order to sel[0..topk) and the matching prefetched values of
-// aux (-1 where bit j of aux_ok is clear) to sel[topk..2 topk).
-template <int THREADS, int ITEMS>
-__device__ void select_long(int length, int topk, const uint32_t (&key)[ITEMS],
-                            const int (&id)[ITEMS], const int (&aux)[ITEMS], uint32_t aux_ok,
-                            TopkShared<THREADS>& sh, int* sel) {
-  const int tid = threadIdx.x;
-  const int lane = tid & 63;
-  const int base = tid * ITEMS;
-  uint32_t active = 0;
-  uint32_t lo = 0xffffffffu, hi = 0u;
-#pragma unroll
-  for (int j = 0; j < ITEMS; ++j) {
-    if (base + j < length) {
-      active |= 1u << j;
-      lo = min(lo, key[j]);
-      hi = max(hi, key[j]);
-    }
-  }
-  block_minmax<THREADS>(lo, hi, sh);
-
-  // Result: selected = {key > thr} + first `remaining` ids with key == thr
-  // (tie mode), or {key >= thr} (ge mode).
-  uint32_t thr = lo;
-  bool ge = false;
-  int remaining = topk;
-  if (lo != hi) {
-    const int high_bit = 31 - __builtin_clz(lo ^ hi);
-    int shift = high_bit > 7 ? high_bit - 7 : 0;
-    uint32_t prefix = shift + 8 >= 32 ? 0u : (lo & ~((1u << (shift + 8)) - 1u));
-    uint32_t cand = active;
-    for (;;) {
-#pragma unroll
-      for (int j = 0; j < ITEMS; ++j) {
-        const bool a = (cand >> j) & 1u;
-        const int d = (int)((key[j] >> shift) & 255u);
-        const uint64_t am = __ballot(a);
-        if (am == 0) continue;
-        const int first = __builtin_ctzll(am);
-        const int d_first = __builtin_amdgcn_readlane(d, first);
-        const uint64_t same = __ballot(a && d == d_first);
-        if (same == am) {
-          if (lane == first) atomicAdd(&sh.hist[d], (uint32_t)__builtin_popcountll(am));
-        } else if (a) {
-          atomicAdd(&sh.hist[d], 1u);
-        }
-      }
-      lds_barrier();
-      if (tid < 64) {
-        // Bin of the remaining-th largest candidate; lane owns bins 4*lane..+3.
-        uint32_t h[4];
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          h[i] = sh.hist[4 * lane + i];
-          sh.hist[4 * lane + i] = 0u;
-        }
-        const int tot = (int)(h[0] + h[1] + h[2] + h[3]);
-        const int excl = __ockl_wfscan_add_i32(tot, false);
-        const int total = __builtin_amdgcn_readlane(excl + tot, 63);
-        int above = total - excl - tot;
-#pragma unroll
-        for (int i = 3; i >= 0; --i) {
-          if (above < remaining && above + (int)h[i] >= remaining) {
-            sh.bin = 4 * lane + i;
-            sh.remaining = remaining - above;
-            sh.bin_count = (int)h[i];
-          }
-          above += (int)h[i];
-        }
-      }
-      lds_barrier();
-      const uint32_t bin = (uint32_t)sh.bin;
-      const int need = sh.remaining;
-      const int in_bin = sh.bin_count;
-      prefix |= bin << shift;
-      if (in_bin == need) {  // the whole bin is taken: every key >= its smallest key
-        thr = prefix;
-        ge = true;
-        break;
-      }
-      uint32_t next = 0;
-#pragma unroll
-      for (int j = 0; j < ITEMS; ++j)
-        if (((cand >> j) & 1u) && ((key[j] >> shift) & 255u) == bin) next |= 1u << j;
-      cand = next;
-      remaining = need;
-      if (shift == 0) {  // all 32 bits fixed: the bin holds one key value
-        thr = prefix;
-        break;
-      }
-      shift = shift >= 8 ? shift - 8 : 0;
-    }
-  }
-
-  int n_sel = 0, n_tie = 0;
-#pragma unroll
-  for (int j = 0; j < ITEMS; ++j) {
-    if ((active >> j) & 1u) {
-      n_sel += ge ? key[j] >= thr : key[j] > thr;
-      n_tie += !ge && key[j] == thr;
-    }
-  }
-  block_scan2<THREADS>(n_sel, n_tie, sh);
-#pragma unroll
-  for (int j = 0; j < ITEMS; ++j) {
-    if (!((active >> j) & 1u)) continue;
-    const bool strict = ge ? key[j] >= thr : key[j] > thr;
-    int rank = -1;
-    if (strict) {
-      rank = n_sel + min(n_tie, remaining);
-      ++n_sel;
-    } else if (!ge && key[j] == thr) {
-      if (n_tie < remaining) rank = n_sel + n_tie;
-      ++n_tie;
-    }
-    if (rank >= 0) {
-      sel[rank] = id[j];
-      sel[topk + rank] = (aux_ok >> j) & 1u ? aux[j] : -1;
-    }
-  }
-}
-
-// Writes one expanded output row (coalesced over columns) from ranked block
-// ids in sel[0..topk) and their first-token physical pages in sel[topk..).
-//
-// The common layouts (logical ids, or blocks that lie inside one page with the
-// causal tail's pages prefetched) write the row from LDS alone, one block of
-// columns per thread. A loop with a global load in it would make every
-// iteration wait for all earlier stores: on gfx9 stores count in the same
-// in-order counter as loads, and the compiler cannot tell a skipped load from a
-// pending one.
-__device__ __forceinline__ void write_expanded(const ExpandMeta& m, const RowMeta& r, int row,
-                                               int topk, const int* sel, const int* tail_page,
-                                               int32_t* out) {
-  const int p1 = r.pos + 1;
-  const int complete = max(0, min(min(p1 / m.ratio, r.seq_len / m.ratio), topk));
-  const int tail_start = tail_start_of(r.pos, m.ratio);
-  const int tail_count = p1 - tail_start;
-  const int expanded = complete * m.ratio;
-  const bool block_in_page = m.physical && (m.page_size % m.ratio == 0);
-  const bool from_lds = !m.physical || (block_in_page && m.ratio - 1 <= kTailSlots);
-  if (from_lds) {
-    const int64_t cs = m.out_col_stride;
-    // Thread b writes the `ratio` columns of rank b: two LDS reads, then
-    // plain stores (topk.cu:134-146 for the physical form).
-    for (int b = threadIdx.x; b < complete; b += blockDim.x) {
-      const int block = sel[b];
-      const int first = block * m.ratio;
-      int base = first;
-      if (m.physical) {
-        const int pp = sel[topk + b];
-        base = pp >= 0 ? pp * m.page_size + (first - m.page_div.div(max(first, 0)) * m.page_size) : -1;
-      }
-      const int lim = (block < 0 || base < 0) ? 0 : min(m.ratio, r.seq_len - first);
-      int32_t* o = out + (int64_t)b * m.ratio * cs;
-      for (int j = 0; j < m.ratio; ++j, o += cs) *o = j < lim ? base + j : -1;
-    }
-    // Causal tail, then -1 to the end of the row.
-    for (int c = expanded + threadIdx.x; c < m.out_width; c += blockDim.x) {
-      const int off = c - expanded;
-      int v = -1;
-      if (off < tail_count && off < m.ratio - 1)
-        v = slot_of(m, r, tail_start + off, m.physical ? tail_page[off] : 0);
-      out[(int64_t)c * cs] = v;
-    }
-  } else {
-    for (int c = threadIdx.x; c < m.out_width; c += blockDim.x) {
-      int v = -1;
-      if (c < expanded) {
-        const int rank = m.ratio_div.div(c);
-        const int o = c - rank * m.ratio;
-        const int block = sel[rank];
-        if (block >= 0) {
-          const int first = block * m.ratio;
-          if (block_in_page) {
-            const int s0 = slot_of(m, r, first, sel[topk + rank]);
-            v = (s0 >= 0 && first + o < r.seq_len) ? s0 + o : -1;
-          } else {
-            const int t = first + o;
-            v = slot_of(m, r, t, table_entry(r, token_page(m, t)));
-          }
-        }
-      } else {
-        const int off = c - expanded;
-        if (off < tail_count && off < m.ratio - 1) {
-          const int t = tail_start + off;
-          const int pp = off < kTailSlots ? tail_page[off] : table_entry(r, token_page(m, t));
-          v = slot_of(m, r, t, pp);
-        }
-      }
-      out[(int64_t)c * m.out_col_stride] = v;
-    }
-  }
-  if (m.store_counts && threadIdx.x == 0) m.counts[row] = min(expanded + tail_count, r.seq_len);
-}
-
-// One row: issue every independent load first, select, then write the row.
-// `limit` bounds the speculative score loads; rows longer than topk must have
-// length <= min(limit, THREADS * ITEMS).
-template <int THREADS, int ITEMS, bool EXPAND, typename Loader>
-__device__ void process_row(const Loader& load, int limit, int length_raw, int clamp, int topk,
-                            const ExpandMeta& m, int row, int32_t* out,
-                            TopkShared<THREADS>& sh, int* sel) {
-  const int tid = threadIdx.x;
-  RowMeta r = {0, 0, nullptr};
-  int req = -1;
-  if (EXPAND) {
-    req = m.token_to_req[row];
-    r.pos = (int)m.positions[row];
-  }
-  uint32_t key[ITEMS];
-  int id[ITEMS];
-  load.template load<ITEMS>(tid * ITEMS, limit, key, id);
-  if (tid < 256) sh.hist[tid] = 0u;
-  for (int b = tid + THREADS; b < 256; b += THREADS) sh.hist[b] = 0u;
-
-  // Page-table entries this thread's blocks and the causal tail will need,
-  // loaded unconditionally (validity kept in bit masks, applied at use).
-  int aux[ITEMS];
-  uint32_t aux_ok = 0;
-  int tail_pp = -1;
-  bool tail_ok = false;
-  const int32_t* zero = reinterpret_cast<const int32_t*>(g_qsa_zero_rows);
-  if (EXPAND) {
-    const bool mapped = req >= 0 && req < m.num_requests;
-    r.seq_len = mapped ? m.sequence_lengths[req] : 0;
-    r.table_row = m.physical ? m.table + (int64_t)(mapped ? req : 0) * m.table_row_stride : nullptr;
-#pragma unroll
-    for (int j = 0; j < ITEMS; ++j) {
-      const int lp = tid * ITEMS + j < limit ? token_page(m, id[j] * m.ratio) : -1;
-      const bool ok = r.table_row && lp >= 0;
-      aux[j] = *(ok ? r.table_row + lp : zero);
-      aux_ok |= (uint32_t)ok << j;
-    }
-    const int lp = (tid < kTailSlots && tid < m.ratio - 1)
-                       ? token_page(m, tail_start_of(r.pos, m.ratio) + tid) : -1;
-    tail_ok = r.table_row && lp >= 0;
-    tail_pp = *(tail_ok ? r.table_row + lp : zero);
-  } else {
-#pragma unroll
-    for (int j = 0; j < ITEMS; ++j) aux[j] = 0;
-  }
-
-  const int length = length_raw > topk ? min(length_raw, clamp) : length_raw;
-  if (length > topk) {
-    select_long<THREADS, ITEMS>(length, topk, key, id, aux, aux_ok, sh, sel);
-  } else {
-    // At most topk entries: the loader's first `length` ids in order, then -1.
-    for (int i = tid; i < topk; i += THREADS) {
-      const int lid = i < length ? load.id_at(i) : -1;
-      sel[i] = lid;
-      sel[topk + i] = (EXPAND && lid >= 0) ? table_entry(r, token_page(m, lid * m.ratio)) : -1;
-    }
-  }
-  if (EXPAND && tid < kTailSlots && tid < m.ratio - 1) sh.tail_page[tid] = tail_ok ? tail_pp : -1;
-  lds_barrier();
-  if (EXPAND) {
-    write_expanded(m, r, row, topk, sel, sh.tail_page, out);
-  } else {
-    for (int c = tid; c < topk; c += THREADS) out[c] = sel[c];
-  }
-}
 
 // --- kernels ---------------------------------------------------------------
 
