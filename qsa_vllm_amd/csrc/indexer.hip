@@ -4,18 +4,19 @@
 // compressed keys of row r (ops/indexer.py:24-114 decode, :117-223 prefill),
 // bf16 inputs, fp32 accumulation, written only for c < visible[r].
 //
-// Both kernels use v_mfma_f32_32x32x16_bf16 with the index heads on M and 32
-// keys on N: A = Q[32 heads][16 dims] stays in registers for the whole row,
-// B = K^T[16 dims][32 keys] is one 16 B load per lane per K step. The 32x32
-// accumulator holds 16 heads of one key per lane, so the ReLU head-sum is 16
-// in-lane adds plus one cross-half shuffle, and lanes 0..31 then hold the 32
-// logits of the tile for one coalesced 128 B store.
-//
 // Decode: a row's keys are only read once, so each wave streams key tiles of
-// one row straight from HBM (GEMV-like, bandwidth bound).
+// one row straight from HBM (GEMV-like, bandwidth bound), with the 16-key
+// v_mfma_f32_16x16x32_bf16 layout of indexer_device.h: each load instruction
+// reads 16 keys x 64 contiguous bytes.
+//
 // Prefill: consecutive query rows of a request see nearly the same keys, so a
 // 4-wave workgroup owns 16 rows (4 per wave, their Q in registers) and stages
-// each 32-key tile once in LDS, where all 16 rows reuse it (MFMA bound).
+// each 32-key tile once in LDS, where all 16 rows reuse it (MFMA bound). It
+// uses v_mfma_f32_32x32x16_bf16 with the index heads on M and 32 keys on N:
+// A = Q[32 heads][16 dims] stays in registers, B = K^T[16 dims][32 keys] comes
+// from LDS. The 32x32 accumulator holds 16 heads of one key per lane, so the
+// ReLU head-sum is 16 in-lane adds plus one cross-half shuffle, and lanes
+// 0..31 then hold the 32 logits of the tile for one coalesced 128 B store.
 #include "indexer_device.h"
 #include "../../include/qsa_hip.h"
 
@@ -24,23 +25,23 @@ namespace {
 
 // ---------------------------------------------------------------------------
 // Decode: grid (programs, rows), one wave per workgroup, kDecodeTilesPerWave
-// consecutive 32-key tiles per wave, logits to global memory.
+// consecutive 16-key tiles per wave, logits to global memory.
 // ---------------------------------------------------------------------------
-constexpr int kDecodeTilesPerWave = 2;
+constexpr int kDecodeTilesPerWave = 4;
 
-template <int D, int MB, int TPW>
+template <int D, int HB, int TPW>
 __global__ __launch_bounds__(64) void indexer_decode_kernel(const IndexerParams p) {
   const int row = blockIdx.y;
   const int tile0 = blockIdx.x * TPW;
   const int num_columns = p.table_width * p.cache_page;
   const int vis = min(min(p.visible[row], num_columns), p.logits_cols);
-  if (tile0 * 32 >= vis) return;
+  if (tile0 * kKeysPerTile >= vis) return;
   const int req = row / p.decode_query_len;
   const int32_t* trow = p.table + (int64_t)req * p.table_row;
-  bf16x8 qa[MB][D / 16];
-  load_q<D, MB>(p, row, qa);
+  bf16x8 qa[HB][D / 32];
+  load_q<D, HB>(p, row, qa);
   float* lrow = p.logits + (int64_t)row * p.logits_row;
-  score_tiles<D, MB, TPW>(p, trow, tile0, vis, qa, [&](int c, float v) { lrow[c] = v; });
+  score_tiles<D, HB, TPW>(p, trow, tile0, vis, qa, [&](int c, float v) { lrow[c] = v; });
 }
 
 // ---------------------------------------------------------------------------
@@ -197,18 +198,25 @@ extern "C" int qsa_indexer_decode(const void* q, int64_t q_row_stride, int64_t q
   p.scale = (float)(1.0 / __builtin_sqrt((double)head_dim));
   // One wave per kDecodeTilesPerWave key tiles of a row: every key of the
   // batch is in flight at once for batches up to tens of thousands of keys.
-  const int max_tiles = (std::min(logits_cols, table_width * cache_page) + 31) / 32;
+  const int max_tiles = (std::min(logits_cols, table_width * cache_page) + kKeysPerTile - 1) /
+                        kKeysPerTile;
   const int programs = std::max(1, (max_tiles + kDecodeTilesPerWave - 1) / kDecodeTilesPerWave);
   const dim3 grid(programs, rows);
   hipStream_t s = static_cast<hipStream_t>(stream);
   if (rows > 65535) return fail(QSA_ERR_UNSUPPORTED, "qsa_indexer_decode: more than 65535 rows");
   constexpr int T = kDecodeTilesPerWave;
+  // Head blocks of 16: up to 64 index heads.
+  const int hb = (num_heads + 15) / 16;
   if (head_dim == 128) {
-    if (num_heads <= 32) hipLaunchKernelGGL((indexer_decode_kernel<128, 1, T>), grid, dim3(64), 0, s, p);
-    else hipLaunchKernelGGL((indexer_decode_kernel<128, 2, T>), grid, dim3(64), 0, s, p);
+    if (hb == 1) hipLaunchKernelGGL((indexer_decode_kernel<128, 1, T>), grid, dim3(64), 0, s, p);
+    else if (hb == 2) hipLaunchKernelGGL((indexer_decode_kernel<128, 2, T>), grid, dim3(64), 0, s, p);
+    else if (hb == 3) hipLaunchKernelGGL((indexer_decode_kernel<128, 3, T>), grid, dim3(64), 0, s, p);
+    else hipLaunchKernelGGL((indexer_decode_kernel<128, 4, T>), grid, dim3(64), 0, s, p);
   } else {
-    if (num_heads <= 32) hipLaunchKernelGGL((indexer_decode_kernel<64, 1, T>), grid, dim3(64), 0, s, p);
-    else hipLaunchKernelGGL((indexer_decode_kernel<64, 2, T>), grid, dim3(64), 0, s, p);
+    if (hb == 1) hipLaunchKernelGGL((indexer_decode_kernel<64, 1, T>), grid, dim3(64), 0, s, p);
+    else if (hb == 2) hipLaunchKernelGGL((indexer_decode_kernel<64, 2, T>), grid, dim3(64), 0, s, p);
+    else if (hb == 3) hipLaunchKernelGGL((indexer_decode_kernel<64, 3, T>), grid, dim3(64), 0, s, p);
+    else hipLaunchKernelGGL((indexer_decode_kernel<64, 4, T>), grid, dim3(64), 0, s, p);
   }
   return check_launch("qsa_indexer_decode launch");
 }
@@ -258,7 +266,8 @@ extern "C" int qsa_indexer_prefill(const void* q, int64_t q_row_stride, int64_t 
   p.key_tiles_per_wg = 8;
   const int row_span = std::max(1, std::min(num_rows, max_query_len > 0 ? max_query_len : num_rows));
   const int row_tiles = (row_span + kPrefillRows - 1) / kPrefillRows;
-  const int max_tiles = (std::min(logits_cols, table_width * cache_page) + 31) / 32;
+  const int max_tiles = (std::min(logits_cols, table_width * cache_page) + kKeysPerTile - 1) /
+                        kKeysPerTile;
   const int key_chunks = (max_tiles + p.key_tiles_per_wg - 1) / p.key_tiles_per_wg;
   if (row_tiles > 65535 || key_chunks > 65535)
     return fail(QSA_ERR_UNSUPPORTED, "qsa_indexer_prefill: grid too large");

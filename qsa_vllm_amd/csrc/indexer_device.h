@@ -4,12 +4,6 @@
 // compressed keys of row r (ops/indexer.py:24-114 decode, :117-223 prefill),
 // bf16 inputs, fp32 accumulation.
 //
-// v_mfma_f32_32x32x16_bf16 with the index heads on M and 32 keys on N:
-// A = Q[32 heads][16 dims] stays in registers for the whole row, B = K^T[16
-// dims][32 keys] is one 16 B load per lane per K step. The 32x32 accumulator
-// holds 16 heads of one key per lane, so the ReLU head-sum is 16 in-lane adds
-// plus one cross-half shuffle, and lanes 0..31 then hold the 32 logits of the
-// tile.
 #pragma once
 
 #include "qsa_common.h"
@@ -62,95 +56,106 @@ __device__ __forceinline__ float relu_head_sum(const f32x16& acc) {
   return s;
 }
 
-// A operand: lane holds Q[row][head 32 mb + kk][16 s + 8 half .. +7]; heads
-// past num_heads read the zero block.
-template <int D, int MB>
-__device__ __forceinline__ void load_q(const IndexerParams& p, int row, bf16x8 (&qa)[MB][D / 16]) {
-  const int kk = threadIdx.x & 31;
-  const int half = (threadIdx.x >> 5) & 1;
+// ---------------------------------------------------------------------------
+// Decode scoring: v_mfma_f32_16x16x32_bf16 with 16 index heads on M and 16
+// keys on N. B = K^T[32 dims][16 keys]: lane (n, g) = (lane & 15, lane >> 4)
+// holds key n's dims 32 s + 8 g .. +7, so one load instruction reads 16 keys
+// x 64 contiguous bytes (a wave streams whole 256 B key rows in 4 loads). A =
+// Q[16 heads][32 dims] per head block stays in registers. The 16x16
+// accumulator gives lane (n, g) heads 4 g .. 4 g + 3 of key n: the ReLU
+// head-sum is in-lane adds over head blocks and those 4 heads plus two
+// cross-group shuffles, after which lanes 0..15 hold 16 consecutive logits.
+// ---------------------------------------------------------------------------
+constexpr int kKeysPerTile = 16;
+
+// A operand for head block hb: lane (m, g) holds Q[row][16 hb + m][32 s + 8 g
+// .. +7]; heads past num_heads read the zero block.
+template <int D, int HB>
+__device__ __forceinline__ void load_q(const IndexerParams& p, int row, bf16x8 (&qa)[HB][D / 32]) {
+  const int m = threadIdx.x & 15;
+  const int g = (threadIdx.x >> 4) & 3;
   const char* zero = reinterpret_cast<const char*>(g_qsa_zero_rows);
 #pragma unroll
-  for (int mb = 0; mb < MB; ++mb) {
-    const int h = 32 * mb + kk;
+  for (int hb = 0; hb < HB; ++hb) {
+    const int h = 16 * hb + m;
     const uint16_t* qrow = p.q + (int64_t)row * p.q_row + (int64_t)h * p.q_head;
 #pragma unroll
-    for (int s = 0; s < D / 16; ++s) {
-      const void* src = h < p.num_heads ? (const void*)(qrow + 16 * s + 8 * half) : (const void*)zero;
-      qa[mb][s] = __builtin_bit_cast(bf16x8, load_u32x4(src));
+    for (int s = 0; s < D / 32; ++s) {
+      const void* src = h < p.num_heads ? (const void*)(qrow + 32 * s + 8 * g) : (const void*)zero;
+      qa[hb][s] = __builtin_bit_cast(bf16x8, load_u32x4(src));
     }
   }
 }
 
-// Issues the loads of one 32-key tile's B operand: this lane's key c (page
-// entry `page` of its request, live when c is visible), 16 B per K step.
-template <int D>
-__device__ __forceinline__ void issue_key_tile(const IndexerParams& p, int c, int page, bool live,
-                                               bf16x8 (&kb)[D / 16]) {
-  const int half = (threadIdx.x >> 5) & 1;
-  const int lp = p.page_div.div(c);
-  const bool ok = live && page >= 0 && page < p.num_blocks;
-  const char* kp = ok ? p.k + (int64_t)page * p.kb + (int64_t)(c - lp * p.cache_page) * p.kt
-                      : reinterpret_cast<const char*>(g_qsa_zero_rows);
-#pragma unroll
-  for (int s = 0; s < D / 16; ++s)
-    kb[s] = __builtin_bit_cast(bf16x8, load_u32x4(kp + (16 * s + 8 * half) * 2));
-}
-
-// Page-table entry of this lane's key c (zero block when c is not visible).
+// Page-table entry of key c (zero block when c is not visible).
 __device__ __forceinline__ int key_page(const IndexerParams& p, const int32_t* trow, int c,
                                         bool live) {
   return *(live ? trow + p.page_div.div(c) : reinterpret_cast<const int32_t*>(g_qsa_zero_rows));
 }
 
-// The logit of this lane's key (valid in lanes 0..31): ReLU head-sum of the
-// 32x32 tile product, one cross-half shuffle, times D^-0.5.
-template <int D, int MB>
-__device__ __forceinline__ float tile_logit(const IndexerParams& p, const bf16x8 (&qa)[MB][D / 16],
-                                            const bf16x8 (&kb)[D / 16]) {
+// Issues the B-operand loads of this lane's key c of a tile.
+template <int D>
+__device__ __forceinline__ void issue_key_tile(const IndexerParams& p, int c, int page, bool live,
+                                               bf16x8 (&kb)[D / 32]) {
+  const int g = (threadIdx.x >> 4) & 3;
+  const int lp = p.page_div.div(c);
+  const bool ok = live && page >= 0 && page < p.num_blocks;
+  const char* kp = ok ? p.k + (int64_t)page * p.kb + (int64_t)(c - lp * p.cache_page) * p.kt
+                      : reinterpret_cast<const char*>(g_qsa_zero_rows);
+#pragma unroll
+  for (int s = 0; s < D / 32; ++s)
+    kb[s] = __builtin_bit_cast(bf16x8, load_u32x4(kp + (32 * s + 8 * g) * 2));
+}
+
+// The logit of this lane's key (every lane of a 16-lane column holds it).
+template <int D, int HB>
+__device__ __forceinline__ float tile_logit(const IndexerParams& p, const bf16x8 (&qa)[HB][D / 32],
+                                            const bf16x8 (&kb)[D / 32]) {
   float sum = 0.0f;
 #pragma unroll
-  for (int mb = 0; mb < MB; ++mb) {
-    f32x16 acc = {};
+  for (int hb = 0; hb < HB; ++hb) {
+    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int s = 0; s < D / 16; ++s)
-      acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(qa[mb][s], kb[s], acc, 0, 0, 0);
-    sum += relu_head_sum(acc);
+    for (int s = 0; s < D / 32; ++s)
+      acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(qa[hb][s], kb[s], acc, 0, 0, 0);
+    sum += fmaxf(acc[0], 0.0f) + fmaxf(acc[1], 0.0f) + fmaxf(acc[2], 0.0f) + fmaxf(acc[3], 0.0f);
   }
+  sum += shfl_xor_f(sum, 16);
   sum += shfl_xor_f(sum, 32);
   return sum * p.scale;
 }
 
-// Scores TPW consecutive 32-key tiles of one row starting at tile0 (keys
+// Scores TPW consecutive 16-key tiles of one row starting at tile0 (keys
 // c < vis are live; trow is the row's page-table row) and calls
-// sink(c, logit) for every live key, from lanes 0..31.
+// sink(c, logit) for every live key, from lanes 0..15.
 //
 // A wave's loads complete in issue order, so they are issued in the order
 // they are needed and all before the first use: the page-table entries of
 // the wave's keys, then every key row. Each wait then covers exactly the
 // group in hand while the rest stays in flight. All loads are unconditional
 // (invalid keys read the zero block), which keeps the wait counts static.
-template <int D, int MB, int TPW, typename Sink>
+template <int D, int HB, int TPW, typename Sink>
 __device__ __forceinline__ void score_tiles(const IndexerParams& p, const int32_t* trow, int tile0,
-                                            int vis, const bf16x8 (&qa)[MB][D / 16], Sink sink) {
-  const int kk = threadIdx.x & 31;
-  const int half = (threadIdx.x >> 5) & 1;
+                                            int vis, const bf16x8 (&qa)[HB][D / 32], Sink sink) {
+  const int n = threadIdx.x & 15;
   int page[TPW];
   bool live[TPW];
 #pragma unroll
   for (int t = 0; t < TPW; ++t) {
-    const int c = (tile0 + t) * 32 + kk;
+    const int c = (tile0 + t) * kKeysPerTile + n;
     live[t] = c < vis;
     page[t] = key_page(p, trow, c, live[t]);
   }
-  bf16x8 kb[TPW][D / 16];
+  bf16x8 kb[TPW][D / 32];
 #pragma unroll
-  for (int t = 0; t < TPW; ++t) issue_key_tile<D>(p, (tile0 + t) * 32 + kk, page[t], live[t], kb[t]);
+  for (int t = 0; t < TPW; ++t)
+    issue_key_tile<D>(p, (tile0 + t) * kKeysPerTile + n, page[t], live[t], kb[t]);
   __builtin_amdgcn_sched_barrier(0);  // keep every load ahead of the first MFMA
 #pragma unroll
   for (int t = 0; t < TPW; ++t) {
-    const float v = tile_logit<D, MB>(p, qa, kb[t]);
-    const int c = (tile0 + t) * 32 + kk;
-    if (half == 0 && live[t]) sink(c, v);
+    const float v = tile_logit<D, HB>(p, qa, kb[t]);
+    const int c = (tile0 + t) * kKeysPerTile + n;
+    if (threadIdx.x < 16 && live[t]) sink(c, v);
   }
 }
 
