@@ -100,9 +100,14 @@ int launch_topk(TopkArgs a, int rows, int cols, void* workspace, size_t workspac
   const size_t lds = (size_t)2 * a.topk * sizeof(int);
   hipError_t err;
   if (cols <= kMaxDirectColumns) {
-    if (cols <= 1024) err = launch_direct<256, 4, EXPAND>(a, rows, lds, s);
-    else if (cols <= 2048) err = launch_direct<256, 8, EXPAND>(a, rows, lds, s);
-    else if (cols <= 4096) err = launch_direct<512, 8, EXPAND>(a, rows, lds, s);
+    // Wider workgroups shorten the per-thread serial parts (histogram
+    // updates, rank emission, row writes). Measured on 64 rows, top 128 with
+    // expansion: 1024 columns 512 x 2 6.5 us (256 x 4 7.1); 2048 columns
+    // 512 x 4 7.8 us (256 x 8 9.1, 1024 x 2 8.5); 4096 columns 1024 x 4
+    // 9.2 us (512 x 8 10.5); 8192 columns 1024 x 8 16.9 us (512 x 16 18.5).
+    if (cols <= 1024) err = launch_direct<512, 2, EXPAND>(a, rows, lds, s);
+    else if (cols <= 2048) err = launch_direct<512, 4, EXPAND>(a, rows, lds, s);
+    else if (cols <= 4096) err = launch_direct<1024, 4, EXPAND>(a, rows, lds, s);
     else if (cols <= 8192) err = launch_direct<1024, 8, EXPAND>(a, rows, lds, s);
     else err = launch_direct<1024, 16, EXPAND>(a, rows, lds, s);
     if (err != hipSuccess) return fail(QSA_ERR_HIP, std::string("qsa_topk launch: ") + hipGetErrorString(err));
