@@ -9,16 +9,18 @@
 // v_mfma_f32_16x16x32_bf16 layout of indexer_device.h: each load instruction
 // reads 16 keys x 64 contiguous bytes.
 //
-// Prefill: consecutive query rows of a request see nearly the same keys, so a
-// 4-wave workgroup owns 16 rows (4 per wave, their Q in registers) and stages
-// each 32-key tile once in LDS, where all 16 rows reuse it (MFMA bound). It
+// Prefill: consecutive query rows of a request see nearly the same keys, so an
+// 8-wave workgroup owns 32 rows (4 per wave, their Q in registers) and stages
+// each 64-key tile once in LDS, where all 32 rows reuse it (MFMA bound). It
 // uses v_mfma_f32_32x32x16_bf16 with the index heads on M and 32 keys on N:
 // A = Q[32 heads][16 dims] stays in registers, B = K^T[16 dims][32 keys] comes
 // from LDS. The 32x32 accumulator holds 16 heads of one key per lane, so the
 // ReLU head-sum is 16 in-lane adds plus one cross-half shuffle, and lanes
-// 0..31 then hold the 32 logits of the tile for one coalesced 128 B store.
+// 0..31 then hold 32 consecutive logits of a row.
 #include "indexer_device.h"
 #include "../../include/qsa_hip.h"
+
+extern "C" __device__ unsigned int __ockl_wfred_max_u32(unsigned int);
 
 namespace qsa {
 namespace {
@@ -45,17 +47,36 @@ __global__ __launch_bounds__(64) void indexer_decode_kernel(const IndexerParams 
 }
 
 // ---------------------------------------------------------------------------
-// Prefill: grid (requests, row tiles of 16, key-tile chunks), 4 waves.
+// Prefill: grid (requests, row tiles of 32, key chunks), 8 waves x 4 rows.
+//
+// Per 64-key tile, the workgroup stages the keys once in LDS (double
+// buffered) and every wave multiplies them against its 4 rows' Q (held in
+// registers for the whole chunk): 2 key blocks x 4 rows x 8 K steps = 64
+// MFMAs per 8 KB B-operand read from LDS. The next tile's keys are loaded
+// into registers while the current tile computes, and its page-table entries
+// one tile earlier still, so the MFMAs never wait on a dependent load chain.
+// One LDS-only barrier per tile keeps those loads in flight. All loads and
+// stores are unconditional (invalid keys read the zero block, masked logits go
+// to a discard slot) so every wait count is static.
 // ---------------------------------------------------------------------------
-constexpr int kPrefillRowsPerWave = 4;
-constexpr int kPrefillWaves = 4;
-constexpr int kPrefillRows = kPrefillRowsPerWave * kPrefillWaves;
+constexpr int kPfRowsPerWave = 4;
+constexpr int kPfWaves = 8;
+constexpr int kPfThreads = 64 * kPfWaves;
+constexpr int kPfRows = kPfRowsPerWave * kPfWaves;
+constexpr int kPfTileKeys = 64;
+
+// Per-lane sink for logits a lane must not write (columns past its row's
+// visible count): keeps the store unconditional.
+static __device__ float g_qsa_discard[kPfThreads];
 
 template <int D>
-__global__ __launch_bounds__(256) void indexer_prefill_kernel(const IndexerParams p) {
+__global__ __launch_bounds__(kPfThreads) void indexer_prefill_kernel(const IndexerParams p) {
   constexpr int KS = D / 16;
-  constexpr int ROW_BYTES = D * 2 + 16;  // padded LDS row: conflict-free 16 B reads
-  __shared__ __attribute__((aligned(16))) char s_keys[32 * ROW_BYTES];
+  constexpr int ROW_BYTES = D * 2 + 16;                // padded: conflict-free 16 B reads
+  constexpr int CH = D * 2 / 16;                       // 16 B chunks per key row
+  constexpr int PER_THREAD = kPfTileKeys * CH / kPfThreads;
+  static_assert(PER_THREAD * kPfThreads == kPfTileKeys * CH, "tile must split evenly");
+  __shared__ __attribute__((aligned(16))) char s_keys[2][kPfTileKeys * ROW_BYTES];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -67,75 +88,111 @@ __global__ __launch_bounds__(256) void indexer_prefill_kernel(const IndexerParam
   const int query_end = p.query_offset + p.num_rows;
   const int req_start = max(p.query_start_loc[req] - base, p.query_offset);
   const int req_end = min(p.query_start_loc[req + 1] - base, query_end);
-  const int tile_row0 = req_start + blockIdx.y * kPrefillRows;
+  const int tile_row0 = req_start + blockIdx.y * kPfRows;
   if (tile_row0 >= req_end) return;
 
   const int num_columns = p.table_width * p.cache_page;
   const int32_t* trow = p.table + (int64_t)req * p.table_row;
+  const int32_t* zero_i = reinterpret_cast<const int32_t*>(g_qsa_zero_rows);
+  const char* zero = reinterpret_cast<const char*>(g_qsa_zero_rows);
 
-  // This wave's rows and their visible counts.
-  int rvis[kPrefillRowsPerWave];
-  int wave_vis = 0;
+  // Visible keys of the workgroup's 32 rows: lane l of every wave reads row
+  // l % 32, so each wave finds the workgroup maximum on its own.
+  const int vr = tile_row0 + kk;
+  const int my_vis = vr < req_end ? min(min(p.visible[vr], num_columns), p.logits_cols) : 0;
+  const int wg_vis = (int)__ockl_wfred_max_u32((uint32_t)my_vis);
+  int rvis[kPfRowsPerWave];
 #pragma unroll
-  for (int i = 0; i < kPrefillRowsPerWave; ++i) {
-    const int r = tile_row0 + wave * kPrefillRowsPerWave + i;
-    rvis[i] = r < req_end ? min(min(p.visible[r], num_columns), p.logits_cols) : 0;
-    wave_vis = max(wave_vis, rvis[i]);
-  }
-  // Key range of the workgroup (all 16 rows).
-  int wg_vis = 0;
-  for (int i = 0; i < kPrefillRows; ++i) {
-    const int r = tile_row0 + i;
-    if (r < req_end) wg_vis = max(wg_vis, min(min(p.visible[r], num_columns), p.logits_cols));
-  }
+  for (int i = 0; i < kPfRowsPerWave; ++i)
+    rvis[i] = __builtin_amdgcn_readlane(my_vis, wave * kPfRowsPerWave + i);
   const int t_begin = blockIdx.z * p.key_tiles_per_wg;
-  const int t_end = min(t_begin + p.key_tiles_per_wg, (wg_vis + 31) / 32);
+  const int t_end = min(t_begin + p.key_tiles_per_wg, (wg_vis + kPfTileKeys - 1) / kPfTileKeys);
   if (t_begin >= t_end) return;
 
-  bf16x8 qa[kPrefillRowsPerWave][KS];
+  // This thread's staging chunks: key (tid + kPfThreads j) / CH, chunk % CH.
+  auto page_of = [&](int tile, int j) {
+    const int c = tile * kPfTileKeys + (tid + kPfThreads * j) / CH;
+    return *(c < wg_vis ? trow + p.page_div.div(c) : zero_i);
+  };
+  auto load_keys = [&](int tile, const int (&pg)[PER_THREAD], u32x4 (&st)[PER_THREAD]) {
 #pragma unroll
-  for (int i = 0; i < kPrefillRowsPerWave; ++i) {
-    const int r = tile_row0 + wave * kPrefillRowsPerWave + i;
-    const bool ok = r < req_end && kk < p.num_heads;
-    const uint16_t* qrow = p.q + (int64_t)(ok ? r : 0) * p.q_row + (int64_t)(ok ? kk : 0) * p.q_head;
-#pragma unroll
-    for (int s = 0; s < KS; ++s) {
-      u32x4 raw = {0u, 0u, 0u, 0u};
-      if (ok) raw = load_u32x4(qrow + 16 * s + 8 * half);
-      qa[i][s] = __builtin_bit_cast(bf16x8, raw);
+    for (int j = 0; j < PER_THREAD; ++j) {
+      const int e = tid + kPfThreads * j;
+      const int c = tile * kPfTileKeys + e / CH;
+      const int lp = p.page_div.div(c);
+      const bool ok = c < wg_vis && pg[j] >= 0 && pg[j] < p.num_blocks;
+      const char* kp = ok ? p.k + (int64_t)pg[j] * p.kb + (int64_t)(c - lp * p.cache_page) * p.kt
+                          : zero;
+      st[j] = load_u32x4(kp + (e % CH) * 16);
     }
-  }
+  };
+  auto store_keys = [&](int buf, const u32x4 (&st)[PER_THREAD]) {
+#pragma unroll
+    for (int j = 0; j < PER_THREAD; ++j) {
+      const int e = tid + kPfThreads * j;
+      *reinterpret_cast<u32x4*>(&s_keys[buf][(e / CH) * ROW_BYTES + (e % CH) * 16]) = st[j];
+    }
+  };
 
-  // Cooperative tile load: thread t copies 16 B chunks of key (t / CH).
-  constexpr int CH = D * 2 / 16;  // 16 B chunks per key row
-  for (int tile = t_begin; tile < t_end; ++tile) {
-    __syncthreads();
-    for (int e = tid; e < 32 * CH; e += 256) {
-      const int key = e / CH, ch = e % CH;
-      const int c = tile * 32 + key;
-      const char* kp = key_ptr(p, trow, c, c < wg_vis);
-      *reinterpret_cast<u32x4*>(s_keys + key * ROW_BYTES + ch * 16) = load_u32x4(kp + ch * 16);
-    }
-    __syncthreads();
-    if (tile * 32 >= wave_vis) continue;
-    bf16x8 kb[KS];
+  // Prologue: pages of the first two tiles, keys of the first, Q.
+  int pg_cur[PER_THREAD], pg_next[PER_THREAD];
+#pragma unroll
+  for (int j = 0; j < PER_THREAD; ++j) pg_cur[j] = page_of(t_begin, j);
+#pragma unroll
+  for (int j = 0; j < PER_THREAD; ++j) pg_next[j] = page_of(t_begin + 1, j);
+  u32x4 st[PER_THREAD];
+  load_keys(t_begin, pg_cur, st);
+
+  bf16x8 qa[kPfRowsPerWave][KS];
+#pragma unroll
+  for (int i = 0; i < kPfRowsPerWave; ++i) {
+    const int r = tile_row0 + wave * kPfRowsPerWave + i;
+    const bool ok = r < req_end && kk < p.num_heads;
+    const uint16_t* qrow = p.q + (int64_t)r * p.q_row + (int64_t)kk * p.q_head;
 #pragma unroll
     for (int s = 0; s < KS; ++s)
-      kb[s] = __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4*>(
-                                             s_keys + kk * ROW_BYTES + (16 * s + 8 * half) * 2));
-    const int c = tile * 32 + kk;
+      qa[i][s] = __builtin_bit_cast(
+          bf16x8, load_u32x4(ok ? (const void*)(qrow + 16 * s + 8 * half) : (const void*)zero));
+  }
+  store_keys(0, st);
+  lds_barrier();
+
+  float* discard = g_qsa_discard + tid;
+  for (int tile = t_begin; tile < t_end; ++tile) {
+    const int buf = (tile - t_begin) & 1;
+    // Next tile's keys and the page entries of the one after.
+    load_keys(tile + 1, pg_next, st);
 #pragma unroll
-    for (int i = 0; i < kPrefillRowsPerWave; ++i) {
-      f32x16 acc = {};
+    for (int j = 0; j < PER_THREAD; ++j) pg_next[j] = page_of(tile + 2, j);
+    __builtin_amdgcn_sched_barrier(0);
+
+#pragma unroll
+    for (int kb_i = 0; kb_i < kPfTileKeys / 32; ++kb_i) {
+      const char* krow = &s_keys[buf][(kb_i * 32 + kk) * ROW_BYTES];
+      bf16x8 kb[KS];
 #pragma unroll
       for (int s = 0; s < KS; ++s)
-        acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(qa[i][s], kb[s], acc, 0, 0, 0);
-      float sum = relu_head_sum(acc);
-      sum += shfl_xor_f(sum, 32);
-      const int r = tile_row0 + wave * kPrefillRowsPerWave + i;
-      if (half == 0 && c < rvis[i])
-        p.logits[(int64_t)(r - p.query_offset) * p.logits_row + c] = sum * p.scale;
+        kb[s] = __builtin_bit_cast(bf16x8,
+                                   *reinterpret_cast<const u32x4*>(krow + (16 * s + 8 * half) * 2));
+      const int c = tile * kPfTileKeys + kb_i * 32 + kk;
+#pragma unroll
+      for (int i = 0; i < kPfRowsPerWave; ++i) {
+        f32x16 acc = {};
+#pragma unroll
+        for (int s = 0; s < KS; ++s)
+          acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(qa[i][s], kb[s], acc, 0, 0, 0);
+        float sum = relu_head_sum(acc);
+        sum += shfl_xor_f(sum, 32);
+        const int r = tile_row0 + wave * kPfRowsPerWave + i;
+        float* dst = (half == 0 && c < rvis[i])
+                         ? p.logits + (int64_t)(r - p.query_offset) * p.logits_row + c
+                         : discard;
+        *dst = sum * p.scale;
+      }
     }
+    __builtin_amdgcn_sched_barrier(0);
+    store_keys(buf ^ 1, st);
+    lds_barrier();
   }
 }
 
@@ -263,17 +320,24 @@ extern "C" int qsa_indexer_prefill(const void* q, int64_t q_row_stride, int64_t 
   p.num_requests = num_requests;
   p.query_offset = query_offset;
   p.num_rows = num_rows;
-  p.key_tiles_per_wg = 8;
   const int row_span = std::max(1, std::min(num_rows, max_query_len > 0 ? max_query_len : num_rows));
-  const int row_tiles = (row_span + kPrefillRows - 1) / kPrefillRows;
-  const int max_tiles = (std::min(logits_cols, table_width * cache_page) + kKeysPerTile - 1) /
-                        kKeysPerTile;
-  const int key_chunks = (max_tiles + p.key_tiles_per_wg - 1) / p.key_tiles_per_wg;
+  const int row_tiles = (row_span + kPfRows - 1) / kPfRows;
+  const int max_tiles = (std::min(logits_cols, table_width * cache_page) + kPfTileKeys - 1) /
+                        kPfTileKeys;
+  // Whole key ranges per workgroup (Q is loaded once) unless that leaves
+  // fewer than ~2 workgroups per CU; then split the keys into chunks.
+  const int64_t row_wgs = (int64_t)num_requests * row_tiles;
+  int chunks = (int)std::min<int64_t>(std::max<int64_t>(1, 512 / std::max<int64_t>(1, row_wgs)),
+                                      std::max(1, max_tiles));
+  p.key_tiles_per_wg = std::max(1, (max_tiles + chunks - 1) / chunks);
+  const int key_chunks = (std::max(1, max_tiles) + p.key_tiles_per_wg - 1) / p.key_tiles_per_wg;
   if (row_tiles > 65535 || key_chunks > 65535)
     return fail(QSA_ERR_UNSUPPORTED, "qsa_indexer_prefill: grid too large");
   const dim3 grid(num_requests, row_tiles, key_chunks);
   hipStream_t s = static_cast<hipStream_t>(stream);
-  if (head_dim == 128) hipLaunchKernelGGL((indexer_prefill_kernel<128>), grid, dim3(256), 0, s, p);
-  else hipLaunchKernelGGL((indexer_prefill_kernel<64>), grid, dim3(256), 0, s, p);
+  if (head_dim == 128)
+    hipLaunchKernelGGL((indexer_prefill_kernel<128>), grid, dim3(kPfThreads), 0, s, p);
+  else
+    hipLaunchKernelGGL((indexer_prefill_kernel<64>), grid, dim3(kPfThreads), 0, s, p);
   return check_launch("qsa_indexer_prefill launch");
 }

@@ -11,6 +11,10 @@ namespace {
 
 // --- kernels ---------------------------------------------------------------
 
+// Rows at which the chip is full and throughput, not one row's latency, sets
+// the time (launch shapes and the row writer switch there).
+constexpr int kManyRows = 1024;
+
 struct TopkArgs {
   const float* scores;
   int64_t score_row_stride;
@@ -100,14 +104,22 @@ int launch_topk(TopkArgs a, int rows, int cols, void* workspace, size_t workspac
   const size_t lds = (size_t)2 * a.topk * sizeof(int);
   hipError_t err;
   if (cols <= kMaxDirectColumns) {
-    // Wider workgroups shorten the per-thread serial parts (histogram
-    // updates, rank emission, row writes). Measured on 64 rows, top 128 with
-    // expansion: 1024 columns 512 x 2 6.5 us (256 x 4 7.1); 2048 columns
-    // 512 x 4 7.8 us (256 x 8 9.1, 1024 x 2 8.5); 4096 columns 1024 x 4
-    // 9.2 us (512 x 8 10.5); 8192 columns 1024 x 8 16.9 us (512 x 16 18.5).
-    if (cols <= 1024) err = launch_direct<512, 2, EXPAND>(a, rows, lds, s);
-    else if (cols <= 2048) err = launch_direct<512, 4, EXPAND>(a, rows, lds, s);
-    else if (cols <= 4096) err = launch_direct<1024, 4, EXPAND>(a, rows, lds, s);
+    // Few rows (a decode batch) leave most CUs idle and the time is one row's
+    // latency: wider workgroups shorten the per-thread serial parts
+    // (histogram updates, rank emission, row writes). Measured on 64 rows,
+    // top 128 with expansion: 1024 columns 512 x 2 6.5 us (256 x 4 7.1);
+    // 2048 columns 512 x 4 7.8 us (256 x 8 9.1, 1024 x 2 8.5); 4096 columns
+    // 1024 x 4 9.2 us (512 x 8 10.5); 8192 columns 1024 x 8 16.9 us (512 x 16
+    // 18.5). Many rows (prefill) fill the chip and the time is throughput:
+    // narrower workgroups do less redundant per-workgroup work (32768 rows x
+    // 1536 columns: 256 x 8 0.22 ms, 512 x 4 0.41 ms).
+    const bool latency_bound = rows < kManyRows;
+    if (cols <= 1024 && latency_bound) err = launch_direct<512, 2, EXPAND>(a, rows, lds, s);
+    else if (cols <= 1024) err = launch_direct<256, 4, EXPAND>(a, rows, lds, s);
+    else if (cols <= 2048 && latency_bound) err = launch_direct<512, 4, EXPAND>(a, rows, lds, s);
+    else if (cols <= 2048) err = launch_direct<256, 8, EXPAND>(a, rows, lds, s);
+    else if (cols <= 4096 && latency_bound) err = launch_direct<1024, 4, EXPAND>(a, rows, lds, s);
+    else if (cols <= 4096) err = launch_direct<512, 8, EXPAND>(a, rows, lds, s);
     else if (cols <= 8192) err = launch_direct<1024, 8, EXPAND>(a, rows, lds, s);
     else err = launch_direct<1024, 16, EXPAND>(a, rows, lds, s);
     if (err != hipSuccess) return fail(QSA_ERR_HIP, std::string("qsa_topk launch: ") + hipGetErrorString(err));
@@ -216,6 +228,7 @@ extern "C" int qsa_topk_expand(const float* scores, int64_t score_row_stride, in
   a.meta.out_width = output_width;
   a.meta.physical = physical ? 1 : 0;
   a.meta.store_counts = store_counts ? 1 : 0;
+  a.meta.coalesce = rows >= kManyRows ? 1 : 0;
   return launch_topk<true>(a, rows, cols, workspace, workspace_bytes,
                            static_cast<hipStream_t>(stream));
 }

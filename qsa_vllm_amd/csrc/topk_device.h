@@ -77,6 +77,7 @@ struct ExpandMeta {
   int out_width;
   int physical;
   int store_counts;
+  int coalesce;  // write rows column-major across threads (many rows) or block per thread
 };
 
 // Raw per-row inputs of the expansion (topk.cu:166-180); everything derived
@@ -341,10 +342,39 @@ __device__ __forceinline__ void write_expanded(const ExpandMeta& m, const RowMet
   const int expanded = complete * m.ratio;
   const bool block_in_page = m.physical && (m.page_size % m.ratio == 0);
   const bool from_lds = !m.physical || (block_in_page && m.ratio - 1 <= kTailSlots);
-  if (from_lds) {
+  if (from_lds && m.coalesce) {
+    // Many rows: the chip is full and stores dominate, so consecutive threads
+    // write consecutive columns.
     const int64_t cs = m.out_col_stride;
-    // Thread b writes the `ratio` columns of rank b: two LDS reads, then
-    // plain stores (topk.cu:134-146 for the physical form).
+    for (int c = threadIdx.x; c < m.out_width; c += blockDim.x) {
+      int v = -1;
+      if (c < expanded) {
+        const int rank = m.ratio_div.div(c);
+        const int o = c - rank * m.ratio;
+        const int block = sel[rank];
+        const int t = block * m.ratio + o;
+        if (block >= 0 && t < r.seq_len) {
+          if (!m.physical) {
+            v = t;
+          } else {
+            // The block lies inside one page (topk.cu:134-146).
+            const int pp = sel[topk + rank];
+            const int first = block * m.ratio;
+            v = pp >= 0 ? pp * m.page_size + (first - m.page_div.div(first) * m.page_size) + o : -1;
+          }
+        }
+      } else {
+        const int off = c - expanded;
+        if (off < tail_count && off < m.ratio - 1)
+          v = slot_of(m, r, tail_start + off, m.physical ? tail_page[off] : 0);
+      }
+      out[(int64_t)c * cs] = v;
+    }
+  } else if (from_lds) {
+    const int64_t cs = m.out_col_stride;
+    // Few rows: one row's latency is the time. Thread b writes the `ratio`
+    // columns of rank b: two LDS reads, then plain stores (topk.cu:134-146
+    // for the physical form).
     for (int b = threadIdx.x; b < complete; b += blockDim.x) {
       const int block = sel[b];
       const int first = block * m.ratio;

@@ -59,6 +59,30 @@ def test_topk_bit_exact(cols, k, mode):
     assert torch.equal(out.cpu(), want)
 
 
+# 1024+ rows switch top-k to its throughput launch shapes and row writer.
+@pytest.mark.parametrize("cols,ratio,page,physical", [(1000, 16, 16, True), (2048, 16, 16, False),
+                                                      (3000, 4, 6, True), (2048, 4, 8, True)])
+def test_topk_expand_many_rows(cols, ratio, page, physical):
+    _note(f"topk_expand many rows cols={cols} ratio={ratio} page={page} physical={physical}")
+    g = torch.Generator().manual_seed(cols + ratio + page)
+    rows, k = 1100, 64
+    seq, t2r, pos, vis, table, scores = _expand_case(g, rows, cols, ratio, page, k, physical, reqs=9)
+    width = k * ratio + ratio - 1
+    want, want_counts = oracle.topk_expand(scores, vis, pos, seq, t2r, table, width, ratio, page,
+                                           physical)
+    out = torch.full((rows, width), -9, dtype=torch.int32, device=DEV)
+    counts = torch.full((rows,), -9, dtype=torch.int32, device=DEV)
+    topk_expand(scores.to(DEV), vis.to(DEV), pos.to(DEV), seq.to(DEV), t2r.to(DEV), out, ratio,
+                main_block_table=table.to(DEV) if physical else None, main_page_size=page,
+                valid_counts_out=counts)
+    plain = torch.full((rows, k), -9, dtype=torch.int32, device=DEV)
+    topk(scores.to(DEV), vis.to(DEV), plain)
+    torch.cuda.synchronize()
+    assert torch.equal(out.cpu(), want)
+    assert torch.equal(counts.cpu(), want_counts)
+    assert torch.equal(plain.cpu(), oracle.topk_ids(scores, vis, k))
+
+
 def _expand_case(g, rows, cols, ratio, page, k, physical, reqs=5):
     seq = torch.randint(0, cols * ratio + 40, (reqs,), generator=g, dtype=torch.int32)
     t2r = torch.randint(-1, reqs + 1, (rows,), generator=g, dtype=torch.int32)
