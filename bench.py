@@ -50,6 +50,10 @@ def parse_args():
     p.add_argument("--traffic-run", action="store_true",
                    help="no timing: eager attention launches of the workload plus a calibration "
                         "copy, for rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE passes")
+    p.add_argument("--pmc-run", action="store_true",
+                   help="no timing: three eager steps of the workload, for rocprofv3 --pmc runs")
+    p.add_argument("--pmc-summary", metavar="DIR",
+                   help="mean of every counter per QSA kernel over a rocprofv3 --pmc run")
     p.add_argument("--traffic-summary", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
                    help="summarise the counter CSVs of a FETCH_SIZE and a WRITE_SIZE pass of "
                         "--traffic-run and print the traffic summary")
@@ -80,6 +84,9 @@ def main():
         return 2
     if args.traffic_summary:
         print(traffic_summary(*args.traffic_summary))
+        return 0
+    if args.pmc_summary:
+        print(pmc_summary(args.pmc_summary))
         return 0
     if args.steps <= 0:
         raise SystemExit("--steps must be positive")
@@ -138,6 +145,13 @@ def main():
 
     if args.traffic_run:
         return traffic_run(select, attend, n_sets)
+    if args.pmc_run:
+        for _ in range(3):
+            for i in range(n_sets):
+                step(i)
+        torch.cuda.synchronize()
+        log(f"pmc run: {3 * n_sets} eager decode steps")
+        return 0
 
     # Eager pass (also initialises allocator pools), then capture.
     for i in range(n_sets):
@@ -317,6 +331,13 @@ def run_prefill(args, wl):
         select()
         attend()
 
+    if args.pmc_run:
+        for _ in range(3):
+            step()
+        torch.cuda.synchronize()
+        log("pmc run: 3 eager prefill steps")
+        return 0
+
     stream = torch.cuda.current_stream()
 
     def timed(fn, reps):
@@ -433,6 +454,36 @@ def _counter_means(root, counter):
         sums[grp] = sums.get(grp, 0.0) + val
         counts[grp] = counts.get(grp, 0) + 1
     return {g: (sums[g] / counts[g], counts[g]) for g in sums}
+
+
+QSA_KERNELS = ("sparse_attn_kernel", "merge_kernel", "topk_direct_kernel",
+               "topk_partition_kernel", "topk_merge_kernel", "indexer_decode_kernel",
+               "indexer_prefill_kernel")
+
+
+def pmc_summary(root):
+    """Mean value per dispatch of every collected counter, per QSA kernel."""
+    import csv
+    import glob
+
+    files = glob.glob(os.path.join(root, "**", "*counter_collection.csv"), recursive=True)
+    if not files:
+        raise SystemExit(f"no counter_collection.csv under {root}")
+    per = {}  # (kernel, counter) -> {dispatch: value}
+    for path in files:
+        with open(path) as fh:
+            for rec in csv.DictReader(fh):
+                name = next((k for k in QSA_KERNELS if k in rec["Kernel_Name"]), None)
+                if name is None:
+                    continue
+                d = per.setdefault((name, rec["Counter_Name"]), {})
+                key = (path, rec["Dispatch_Id"])
+                d[key] = d.get(key, 0.0) + float(rec["Counter_Value"])
+    lines = []
+    for (name, counter), d in sorted(per.items()):
+        vals = list(d.values())
+        lines.append(f"{name} {counter}: mean {sum(vals) / len(vals):.6g} over {len(vals)} dispatches")
+    return "\n".join(lines)
 
 
 def traffic_summary(fetch_dir, write_dir):

@@ -181,8 +181,7 @@ __global__ __launch_bounds__(kPfThreads) void indexer_prefill_kernel(const Index
 #pragma unroll
         for (int s = 0; s < KS; ++s)
           acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(qa[i][s], kb[s], acc, 0, 0, 0);
-        float sum = relu_head_sum(acc);
-        sum += shfl_xor_f(sum, 32);
+        const float sum = sum_wave_halves(relu_head_sum(acc));
         const int r = tile_row0 + wave * kPfRowsPerWave + i;
         float* dst = (half == 0 && c < rvis[i])
                          ? p.logits + (int64_t)(r - p.query_offset) * p.logits_row + c

@@ -121,8 +121,7 @@ __device__ __forceinline__ float tile_logit(const IndexerParams& p, const bf16x8
     sum += fmaxf(acc[0], 0.0f) + fmaxf(acc[1], 0.0f) + fmaxf(acc[2], 0.0f) + fmaxf(acc[3], 0.0f);
   }
   sum += shfl_xor_f(sum, 16);
-  sum += shfl_xor_f(sum, 32);
-  return sum * p.scale;
+  return sum_wave_halves(sum) * p.scale;
 }
 
 // Scores TPW consecutive 16-key tiles of one row starting at tile0 (keys

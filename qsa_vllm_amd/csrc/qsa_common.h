@@ -60,7 +60,21 @@ __device__ __forceinline__ void lds_barrier() {
 }
 
 __device__ __forceinline__ float shfl_xor_f(float v, int mask) { return __shfl_xor(v, mask, 64); }
-__device__ __forceinline__ int shfl_xor_i(int v, int mask) { return __shfl_xor(v, mask, 64); }
+
+// v[lane] + v[lane ^ 32] in every lane, without the LDS crossbar.
+// v_permlane32_swap a, b exchanges the upper half of a with the lower half of
+// b; with a and b both holding v, a becomes (v[0..31], v[0..31]) and b
+// (v[32..63], v[32..63]), so a + b adds each lane to its partner (lower half
+// first in every lane, so both halves get the same bits). Written as inline
+// asm with both operands read-write so they get distinct registers (a swap of
+// a register with itself is a rotation); the nops cover the VALU-write ->
+// cross-lane-read hazard on either side.
+__device__ __forceinline__ float sum_wave_halves(float v) {
+  uint32_t a = __builtin_bit_cast(uint32_t, v);
+  uint32_t b = a;
+  asm volatile("s_nop 1\n\tv_permlane32_swap_b32 %0, %1\n\ts_nop 1" : "+v"(a), "+v"(b));
+  return __builtin_bit_cast(float, a) + __builtin_bit_cast(float, b);
+}
 
 __device__ __forceinline__ u32x4 load_u32x4(const void* p) {
   return *reinterpret_cast<const u32x4*>(p);

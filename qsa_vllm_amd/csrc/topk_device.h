@@ -47,10 +47,16 @@ constexpr int kMaxTopk = 8192;            // selected ids per row staged in LDS
 constexpr int kTailSlots = 64;            // causal-tail pages fetched ahead of time
 
 constexpr int kHistBuffers = 3;  // radix pass k counts into buffer k % 3
+#ifndef QSA_TOPK_DIGIT_BITS
+#define QSA_TOPK_DIGIT_BITS 8
+#endif
+constexpr int kDigitBits = QSA_TOPK_DIGIT_BITS;  // radix digit width
+constexpr int kBins = 1 << kDigitBits;
+constexpr int kBinsPerLane = kBins / 64;  // every wave scans the whole histogram
 
 template <int THREADS>
 struct TopkShared {
-  alignas(16) uint32_t hist[kHistBuffers][256];
+  alignas(16) uint32_t hist[kHistBuffers][kBins];
   uint32_t wmin[THREADS / 64];
   uint32_t wmax[THREADS / 64];
   int wsel[THREADS / 64];
@@ -224,9 +230,10 @@ __device__ void select_long(int length, int topk, const uint32_t (&key)[ITEMS],
   bool ge = false;
   int remaining = topk;
   if (lo != hi) {
+    constexpr uint32_t kDigitMask = kBins - 1;
     const int high_bit = 31 - __builtin_clz(lo ^ hi);
-    int shift = high_bit > 7 ? high_bit - 7 : 0;
-    uint32_t prefix = shift + 8 >= 32 ? 0u : (lo & ~((1u << (shift + 8)) - 1u));
+    int shift = high_bit > kDigitBits - 1 ? high_bit - (kDigitBits - 1) : 0;
+    uint32_t prefix = shift + kDigitBits >= 32 ? 0u : (lo & ~((1u << (shift + kDigitBits)) - 1u));
     uint32_t cand = active;
     // One barrier per pass: every wave reads the whole histogram and finds
     // the bin itself (identical results), and pass k counts into buffer
@@ -238,7 +245,7 @@ __device__ void select_long(int length, int topk, const uint32_t (&key)[ITEMS],
 #pragma unroll
       for (int j = 0; j < ITEMS; ++j) {
         const bool a = (cand >> j) & 1u;
-        const int d = (int)((key[j] >> shift) & 255u);
+        const int d = (int)((key[j] >> shift) & kDigitMask);
         const uint64_t am = __ballot(a);
         if (am == 0) continue;
         const int first = __builtin_ctzll(am);
@@ -252,20 +259,33 @@ __device__ void select_long(int length, int topk, const uint32_t (&key)[ITEMS],
       }
       lds_barrier();
       if (pass > 0 && tid < 64) {
-        uint32_t* old = sh.hist[(pass - 1) % kHistBuffers];
-        *reinterpret_cast<u32x4*>(old + 4 * lane) = u32x4{0u, 0u, 0u, 0u};
+        uint32_t* old = sh.hist[(pass - 1) % kHistBuffers] + kBinsPerLane * lane;
+#pragma unroll
+        for (int i = 0; i < kBinsPerLane; i += 4)
+          *reinterpret_cast<u32x4*>(old + i) = u32x4{0u, 0u, 0u, 0u};
       }
-      // Bin of the remaining-th largest candidate; lane owns bins 4*lane..+3.
-      const u32x4 h = *reinterpret_cast<const u32x4*>(hist + 4 * lane);
-      const int tot = (int)(h[0] + h[1] + h[2] + h[3]);
+      // Bin of the remaining-th largest candidate; lane owns kBinsPerLane
+      // consecutive bins.
+      uint32_t h[kBinsPerLane];
+#pragma unroll
+      for (int i = 0; i < kBinsPerLane; i += 4) {
+        const u32x4 v = *reinterpret_cast<const u32x4*>(hist + kBinsPerLane * lane + i);
+        h[i] = v[0];
+        h[i + 1] = v[1];
+        h[i + 2] = v[2];
+        h[i + 3] = v[3];
+      }
+      int tot = 0;
+#pragma unroll
+      for (int i = 0; i < kBinsPerLane; ++i) tot += (int)h[i];
       const int excl = __ockl_wfscan_add_i32(tot, false);
       const int total = __builtin_amdgcn_readlane(excl + tot, 63);
       int above = total - excl - tot;  // candidates in higher lanes' bins
       int hit = -1, hit_need = 0, hit_count = 0;
 #pragma unroll
-      for (int i = 3; i >= 0; --i) {
+      for (int i = kBinsPerLane - 1; i >= 0; --i) {
         if (above < remaining && above + (int)h[i] >= remaining) {
-          hit = 4 * lane + i;
+          hit = kBinsPerLane * lane + i;
           hit_need = remaining - above;
           hit_count = (int)h[i];
         }
@@ -284,14 +304,14 @@ __device__ void select_long(int length, int topk, const uint32_t (&key)[ITEMS],
       uint32_t next = 0;
 #pragma unroll
       for (int j = 0; j < ITEMS; ++j)
-        if (((cand >> j) & 1u) && ((key[j] >> shift) & 255u) == bin) next |= 1u << j;
+        if (((cand >> j) & 1u) && ((key[j] >> shift) & kDigitMask) == bin) next |= 1u << j;
       cand = next;
       remaining = need;
       if (shift == 0) {  // all 32 bits fixed: the bin holds one key value
         thr = prefix;
         break;
       }
-      shift = shift >= 8 ? shift - 8 : 0;
+      shift = shift >= kDigitBits ? shift - kDigitBits : 0;
     }
   }
 
@@ -472,7 +492,7 @@ __device__ __forceinline__ void prefetch_row(const ExpandMeta& m, int row, int l
 
 template <int THREADS>
 __device__ __forceinline__ void clear_histograms(TopkShared<THREADS>& sh) {
-  for (int b = threadIdx.x; b < kHistBuffers * 256; b += THREADS) (&sh.hist[0][0])[b] = 0u;
+  for (int b = threadIdx.x; b < kHistBuffers * kBins; b += THREADS) (&sh.hist[0][0])[b] = 0u;
 }
 
 // Select and write one row from keys already in registers. The histograms
