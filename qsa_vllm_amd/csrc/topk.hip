@@ -36,60 +36,78 @@ __device__ __forceinline__ int row_length(const TopkArgs& a, int row) {
   return length > a.topk ? min(length, a.cols) : length;
 }
 
-template <int THREADS, int ITEMS, bool EXPAND>
+// The selected ids (2 * topk ints) share LDS with the key stage when they fit
+// in it (the stage is dead by then); otherwise they get dynamic LDS.
+template <int THREADS, int ITEMS>
+constexpr bool sel_in_stage(int topk) { return 2 * topk <= THREADS * ITEMS; }
+
+#define QSA_TOPK_LDS(THREADS, ITEMS, PAGES)              \
+  __shared__ TopkShared<THREADS> sh;                     \
+  __shared__ TopkStage<THREADS, ITEMS, PAGES> st;        \
+  extern __shared__ int dyn_sel[];                       \
+  int* sel = sel_in_stage<THREADS, ITEMS>(a.topk) ? reinterpret_cast<int*>(st.key) : dyn_sel
+
+template <int THREADS, int ITEMS, bool EXPAND, bool PAGES>
 __global__ __launch_bounds__(THREADS) void topk_direct_kernel(const TopkArgs a) {
-  __shared__ TopkShared<THREADS> sh;
-  extern __shared__ int sel[];
+  QSA_TOPK_LDS(THREADS, ITEMS, PAGES);
   const int row = blockIdx.x;
   const float* srow = a.scores + (int64_t)row * a.score_row_stride;
-  process_row<THREADS, ITEMS, EXPAND>(DirectLoader{srow, 0}, a.cols, a.lengths[row], a.cols,
-                                      a.topk, a.meta, row, a.out + (int64_t)row * a.out_row_stride,
-                                      sh, sel);
+  process_row<THREADS, ITEMS, EXPAND, PAGES>(DirectLoader{srow, 0}, a.cols, a.lengths[row], a.cols,
+                                             a.topk, a.meta, row,
+                                             a.out + (int64_t)row * a.out_row_stride, sh, st, sel);
 }
 
 // Pass 1 of long rows: rows short enough for one pass finish in partition 0.
-template <int THREADS, int ITEMS, bool EXPAND>
+template <int THREADS, int ITEMS, bool EXPAND, bool PAGES>
 __global__ __launch_bounds__(THREADS) void topk_partition_kernel(const TopkArgs a) {
-  __shared__ TopkShared<THREADS> sh;
-  extern __shared__ int sel[];
+  QSA_TOPK_LDS(THREADS, ITEMS, PAGES);
   const int row = blockIdx.x;
   const int part = blockIdx.y;
   const int length = row_length(a, row);
   const float* srow = a.scores + (int64_t)row * a.score_row_stride;
   if (length <= kPartitionColumns) {
     if (part == 0)
-      process_row<THREADS, ITEMS, EXPAND>(DirectLoader{srow, 0}, length, length, length, a.topk,
-                                          a.meta, row, a.out + (int64_t)row * a.out_row_stride,
-                                          sh, sel);
+      process_row<THREADS, ITEMS, EXPAND, PAGES>(DirectLoader{srow, 0}, length, length, length,
+                                                 a.topk, a.meta, row,
+                                                 a.out + (int64_t)row * a.out_row_stride, sh, st, sel);
     return;
   }
   const int start = part * kPartitionColumns;
   if (start >= length) return;
   const int count = min(kPartitionColumns, length - start);
   int32_t* prow = a.partial + ((int64_t)row * a.parts + part) * a.topk;
-  process_row<THREADS, ITEMS, false>(DirectLoader{srow, start}, count, count, count, a.topk,
-                                     a.meta, row, prow, sh, sel);
+  process_row<THREADS, ITEMS, false, false>(DirectLoader{srow, start}, count, count, count, a.topk,
+                                            a.meta, row, prow, sh, st, sel);
 }
 
 // Pass 2: exact top-k over the concatenated partition winners (ascending ids).
-template <int THREADS, int ITEMS, bool EXPAND>
+template <int THREADS, int ITEMS, bool EXPAND, bool PAGES>
 __global__ __launch_bounds__(THREADS) void topk_merge_kernel(const TopkArgs a) {
-  __shared__ TopkShared<THREADS> sh;
-  extern __shared__ int sel[];
+  QSA_TOPK_LDS(THREADS, ITEMS, PAGES);
   const int row = blockIdx.x;
   const int length = row_length(a, row);
   if (length <= kPartitionColumns) return;
   const int count = (length / kPartitionColumns) * a.topk + min(length % kPartitionColumns, a.topk);
   const float* srow = a.scores + (int64_t)row * a.score_row_stride;
   const IndirectLoader load{srow, a.partial + (int64_t)row * a.parts * a.topk};
-  process_row<THREADS, ITEMS, EXPAND>(load, count, count, count, a.topk, a.meta, row,
-                                      a.out + (int64_t)row * a.out_row_stride, sh, sel);
+  process_row<THREADS, ITEMS, EXPAND, PAGES>(load, count, count, count, a.topk, a.meta, row,
+                                             a.out + (int64_t)row * a.out_row_stride, sh, st, sel);
+}
+
+template <int THREADS, int ITEMS>
+size_t dyn_lds(int topk) {
+  return sel_in_stage<THREADS, ITEMS>(topk) ? 0 : (size_t)2 * topk * sizeof(int);
 }
 
 template <int THREADS, int ITEMS, bool EXPAND>
-hipError_t launch_direct(const TopkArgs& a, int rows, size_t lds, hipStream_t s) {
-  hipLaunchKernelGGL((topk_direct_kernel<THREADS, ITEMS, EXPAND>), dim3(rows), dim3(THREADS), lds,
-                     s, a);
+hipError_t launch_direct(const TopkArgs& a, int rows, hipStream_t s) {
+  const size_t lds = dyn_lds<THREADS, ITEMS>(a.topk);
+  if (EXPAND && a.meta.physical)
+    hipLaunchKernelGGL((topk_direct_kernel<THREADS, ITEMS, true, true>), dim3(rows), dim3(THREADS),
+                       lds, s, a);
+  else
+    hipLaunchKernelGGL((topk_direct_kernel<THREADS, ITEMS, EXPAND, false>), dim3(rows),
+                       dim3(THREADS), lds, s, a);
   return hipGetLastError();
 }
 
@@ -101,7 +119,6 @@ int launch_topk(TopkArgs a, int rows, int cols, void* workspace, size_t workspac
   if (rows == 0) return QSA_OK;
   if (a.topk > kMaxTopk)
     return fail(QSA_ERR_UNSUPPORTED, "qsa_topk: more than 8192 selected blocks per row");
-  const size_t lds = (size_t)2 * a.topk * sizeof(int);
   hipError_t err;
   if (cols <= kMaxDirectColumns) {
     // Few rows (a decode batch) leave most CUs idle and the time is one row's
@@ -114,14 +131,14 @@ int launch_topk(TopkArgs a, int rows, int cols, void* workspace, size_t workspac
     // narrower workgroups do less redundant per-workgroup work (32768 rows x
     // 1536 columns: 256 x 8 0.22 ms, 512 x 4 0.41 ms).
     const bool latency_bound = rows < kManyRows;
-    if (cols <= 1024 && latency_bound) err = launch_direct<512, 2, EXPAND>(a, rows, lds, s);
-    else if (cols <= 1024) err = launch_direct<256, 4, EXPAND>(a, rows, lds, s);
-    else if (cols <= 2048 && latency_bound) err = launch_direct<512, 4, EXPAND>(a, rows, lds, s);
-    else if (cols <= 2048) err = launch_direct<256, 8, EXPAND>(a, rows, lds, s);
-    else if (cols <= 4096 && latency_bound) err = launch_direct<1024, 4, EXPAND>(a, rows, lds, s);
-    else if (cols <= 4096) err = launch_direct<512, 8, EXPAND>(a, rows, lds, s);
-    else if (cols <= 8192) err = launch_direct<1024, 8, EXPAND>(a, rows, lds, s);
-    else err = launch_direct<1024, 16, EXPAND>(a, rows, lds, s);
+    if (cols <= 1024 && latency_bound) err = launch_direct<512, 2, EXPAND>(a, rows, s);
+    else if (cols <= 1024) err = launch_direct<256, 4, EXPAND>(a, rows, s);
+    else if (cols <= 2048 && latency_bound) err = launch_direct<512, 4, EXPAND>(a, rows, s);
+    else if (cols <= 2048) err = launch_direct<256, 8, EXPAND>(a, rows, s);
+    else if (cols <= 4096 && latency_bound) err = launch_direct<1024, 4, EXPAND>(a, rows, s);
+    else if (cols <= 4096) err = launch_direct<512, 8, EXPAND>(a, rows, s);
+    else if (cols <= 8192) err = launch_direct<1024, 8, EXPAND>(a, rows, s);
+    else err = launch_direct<1024, 16, EXPAND>(a, rows, s);
     if (err != hipSuccess) return fail(QSA_ERR_HIP, std::string("qsa_topk launch: ") + hipGetErrorString(err));
     return QSA_OK;
   }
@@ -135,11 +152,21 @@ int launch_topk(TopkArgs a, int rows, int cols, void* workspace, size_t workspac
     return fail(QSA_ERR_WORKSPACE, "qsa_topk: workspace too small for partition winners");
   a.partial = static_cast<int32_t*>(workspace);
   a.parts = parts;
-  hipLaunchKernelGGL((topk_partition_kernel<1024, 8, EXPAND>), dim3(rows, parts), dim3(1024), lds,
-                     s, a);
+  const bool pages = EXPAND && a.meta.physical;
+  if (pages)
+    hipLaunchKernelGGL((topk_partition_kernel<1024, 8, true, true>), dim3(rows, parts), dim3(1024),
+                       (dyn_lds<1024, 8>(a.topk)), s, a);
+  else
+    hipLaunchKernelGGL((topk_partition_kernel<1024, 8, EXPAND, false>), dim3(rows, parts),
+                       dim3(1024), (dyn_lds<1024, 8>(a.topk)), s, a);
   if ((err = hipGetLastError()) != hipSuccess)
     return fail(QSA_ERR_HIP, std::string("qsa_topk partition launch: ") + hipGetErrorString(err));
-  hipLaunchKernelGGL((topk_merge_kernel<1024, 16, EXPAND>), dim3(rows), dim3(1024), lds, s, a);
+  if (pages)
+    hipLaunchKernelGGL((topk_merge_kernel<1024, 16, true, true>), dim3(rows), dim3(1024),
+                       (dyn_lds<1024, 16>(a.topk)), s, a);
+  else
+    hipLaunchKernelGGL((topk_merge_kernel<1024, 16, EXPAND, false>), dim3(rows), dim3(1024),
+                       (dyn_lds<1024, 16>(a.topk)), s, a);
   if ((err = hipGetLastError()) != hipSuccess)
     return fail(QSA_ERR_HIP, std::string("qsa_topk merge launch: ") + hipGetErrorString(err));
   return QSA_OK;

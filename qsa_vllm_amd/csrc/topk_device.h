@@ -8,10 +8,13 @@
 //  * expansion, causal tail, physical slot mapping and counts as
 //    ExpandedWriter (topk.cu:97-180).
 //
-// Algorithm (own design for wave64 + LDS). One workgroup per row holds the
-// row's keys in registers (blocked: thread t owns ids [t*ITEMS, t*ITEMS+ITEMS)).
-// A radix select walks 8-bit digits downward from the highest bit in which the
-// row's keys differ (one block min/max). Each pass builds an LDS histogram
+// Algorithm (own design for wave64 + LDS). One workgroup per row loads the
+// row coalesced into LDS and holds its keys in registers (blocked: thread t
+// owns ids [t*ITEMS, t*ITEMS+ITEMS)). Each full wave bounds the m-th largest
+// of its threads' maxima from below (m * full waves >= k); keys under the
+// smallest bound cannot be selected and are dropped. A radix select walks
+// 8-bit digits downward from the highest bit in which the remaining keys
+// differ (one block min/max). Each pass builds an LDS histogram
 // (atomics with a wave-uniform fast path); after one barrier every wave reads
 // it and locates the bin holding the k-th largest key with a DPP scan. The walk stops as soon as that bin
 // holds exactly the number of keys still needed - then the selection is every
@@ -53,12 +56,16 @@ constexpr int kHistBuffers = 3;  // radix pass k counts into buffer k % 3
 constexpr int kDigitBits = QSA_TOPK_DIGIT_BITS;  // radix digit width
 constexpr int kBins = 1 << kDigitBits;
 constexpr int kBinsPerLane = kBins / 64;  // every wave scans the whole histogram
+#ifndef QSA_TOPK_PRUNE
+#define QSA_TOPK_PRUNE 1
+#endif
 
 template <int THREADS>
 struct TopkShared {
   alignas(16) uint32_t hist[kHistBuffers][kBins];
   uint32_t wmin[THREADS / 64];
   uint32_t wmax[THREADS / 64];
+  uint32_t wfloor[THREADS / 64];
   int wsel[THREADS / 64];
   int wtie[THREADS / 64];
   int tail_page[kTailSlots];
@@ -115,65 +122,96 @@ __device__ __forceinline__ int table_entry(const RowMeta& r, int lp) {
   return (r.table_row && lp >= 0) ? r.table_row[lp] : -1;
 }
 
-// --- loaders ---------------------------------------------------------------
+// --- staging -----------------------------------------------------------------
 //
-// Every load here is unconditional: an id outside the row reads the zero
-// block instead of being skipped. That keeps the number of loads a wave has in
-// flight known at compile time, so waiting for the scores does not also wait
-// for the page-table loads issued after them (a skipped, divergent load forces
-// the compiler to drain every outstanding load instead).
+// One row chunk of at most THREADS * ITEMS candidates passes through LDS.
+// Element e is loaded by thread e % THREADS, so a wave-wide load reads 256
+// consecutive bytes (a thread reading its own ITEMS consecutive words instead
+// makes every load instruction touch ITEMS times as many cache lines), and is
+// read back by thread e / ITEMS, which owns ITEMS consecutive ids as the
+// selection and its id-ordered ranking need. With the expansion, the physical
+// page of each element's first token is staged beside it and read back only
+// for the selected elements.
+//
+// Every global load is unconditional: an element outside the row reads the
+// zero block instead of being skipped. That keeps the number of loads a wave
+// has in flight known at compile time, so waiting for the scores does not also
+// wait for the page-table loads issued after them (a skipped, divergent load
+// forces the compiler to drain every outstanding load instead).
+template <int THREADS, int ITEMS, bool PAGES>
+struct TopkStage {
+  alignas(16) uint32_t key[THREADS * ITEMS];  // also holds sel[] once the keys are read back
+  int page[PAGES ? THREADS * ITEMS : 1];
+};
 
 struct DirectLoader {  // ids start + i over a contiguous score row
   const float* scores;
   int start;
   __device__ __forceinline__ int id_at(int i) const { return start + i; }
-  template <int ITEMS>
-  __device__ __forceinline__ void load(int base, int limit, uint32_t (&key)[ITEMS],
-                                       int (&id)[ITEMS]) const {
-    const uint32_t* row = reinterpret_cast<const uint32_t*>(scores + start);
-#pragma unroll
-    for (int j = 0; j < ITEMS; ++j) {
-      const bool in = base + j < limit;
-      key[j] = *(in ? row + base + j : g_qsa_zero_rows);
-      id[j] = start + base + j;
-    }
-  }
 };
 
 struct IndirectLoader {  // candidate list of ids into a score row
   const float* scores;
   const int32_t* ids;
   __device__ __forceinline__ int id_at(int i) const { return ids[i]; }
-  template <int ITEMS>
-  __device__ __forceinline__ void load(int base, int limit, uint32_t (&key)[ITEMS],
-                                       int (&id)[ITEMS]) const {
-    const uint32_t* row = reinterpret_cast<const uint32_t*>(scores);
-    const int32_t* zero = reinterpret_cast<const int32_t*>(g_qsa_zero_rows);
-#pragma unroll
-    for (int j = 0; j < ITEMS; ++j) id[j] = *(base + j < limit ? ids + base + j : zero);
-#pragma unroll
-    for (int j = 0; j < ITEMS; ++j) key[j] = row[id[j]];  // id 0 stands in past the list
-  }
 };
 
 // --- block primitives (DPP wave reductions/scans + one LDS exchange) --------
 
+// A lower bound on the m-th largest (1 <= m <= 64) of the 64 lanes' values:
+// radix descent with ballots over the kFloorBits bits below the lanes' common
+// prefix; the bits under them stay zero, which can only lower the result.
+// Every value is uniform across the wave.
+#ifndef QSA_TOPK_FLOOR_BITS
+#define QSA_TOPK_FLOOR_BITS 5
+#endif
+constexpr int kFloorBits = QSA_TOPK_FLOOR_BITS;
+__device__ __forceinline__ uint32_t wave_floor_mth_largest(uint32_t v, int m) {
+  const uint32_t vmax = __ockl_wfred_max_u32(v);
+  const uint32_t vmin = __ockl_wfred_min_u32(v);
+  if (vmax == vmin) return vmax;
+  const int top = 31 - __builtin_clz(vmax ^ vmin);
+  uint32_t value = top == 31 ? 0u : vmax & ~((2u << top) - 1u);
+  uint64_t cand = ~0ull;  // lanes equal to `value` on the bits fixed so far
+  int need = m;
+#pragma unroll
+  for (int i = 0; i < kFloorBits; ++i) {
+    const int b = top - i;
+    if (b < 0) break;
+    const uint64_t ones = cand & __ballot((v >> b) & 1u);
+    const int c = __builtin_popcountll(ones);
+    if (c >= need) {
+      cand = ones;
+      value |= 1u << b;
+    } else {
+      cand &= ~ones;
+      need -= c;
+    }
+  }
+  return value;
+}
+
+// Block min, max and min of the per-wave floors, one barrier.
 template <int THREADS>
-__device__ __forceinline__ void block_minmax(uint32_t& lo, uint32_t& hi, TopkShared<THREADS>& sh) {
+__device__ __forceinline__ void block_bounds(uint32_t& lo, uint32_t& hi, uint32_t& floor,
+                                             TopkShared<THREADS>& sh) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   lo = __ockl_wfred_min_u32(lo);
   hi = __ockl_wfred_max_u32(hi);
   if (lane == 0) {
     sh.wmin[wave] = lo;
     sh.wmax[wave] = hi;
+    sh.wfloor[wave] = floor;
   }
   lds_barrier();
   lo = 0xffffffffu;
   hi = 0u;
+  floor = 0xffffffffu;
 #pragma unroll
   for (int w = 0; w < THREADS / 64; ++w) {
     lo = min(lo, sh.wmin[w]);
     hi = max(hi, sh.wmax[w]);
+    floor = min(floor, sh.wfloor[w]);
   }
 }
 
@@ -203,12 +241,12 @@ __device__ __forceinline__ void block_scan2(int& a, int& b, TopkShared<THREADS>&
 // --- selection --------------------------------------------------------------
 
 // Exact top-k of `length` (> topk) keys in registers. Writes the selected ids
-// in ascending-id order to sel[0..topk) and the matching prefetched values of
-// aux (-1 where bit j of aux_ok is clear) to sel[topk..2 topk).
-template <int THREADS, int ITEMS>
+// in ascending-id order to sel[0..topk) and, with PAGES, the staged page of
+// each (page[e] for the element at position e) to sel[topk..2 topk).
+template <int THREADS, int ITEMS, bool PAGES>
 __device__ void select_long(int length, int topk, const uint32_t (&key)[ITEMS],
-                            const int (&id)[ITEMS], const int (&aux)[ITEMS], uint32_t aux_ok,
-                            TopkShared<THREADS>& sh, int* sel) {
+                            const int (&id)[ITEMS], const int* page, TopkShared<THREADS>& sh,
+                            int* sel) {
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int base = tid * ITEMS;
@@ -222,7 +260,23 @@ __device__ void select_long(int length, int topk, const uint32_t (&key)[ITEMS],
       hi = max(hi, key[j]);
     }
   }
-  block_minmax<THREADS>(lo, hi, sh);
+  // Lower bound on the topk-th largest key. Active threads are a prefix, so
+  // waves [0, full) have 64 active lanes, each holding its thread maximum
+  // (`hi` here, a distinct element). If each of those waves bounds the m-th
+  // largest of its maxima from below, with m * full >= topk, at least topk
+  // distinct elements are >= the smallest of these floors: keys below it
+  // cannot be selected and never enter the histograms.
+  uint32_t floor = 0u;  // 0: no bound
+#if QSA_TOPK_PRUNE
+  {
+    const int threads_active = min(THREADS, (length + ITEMS - 1) / ITEMS);
+    const int full = threads_active / 64;
+    const int m = full > 0 ? (topk + full - 1) / full : 65;
+    if (m <= 64) floor = (tid >> 6) < full ? wave_floor_mth_largest(hi, m) : 0xffffffffu;
+  }
+#endif
+  block_bounds<THREADS>(lo, hi, floor, sh);
+  lo = max(lo, floor);  // smallest candidate bound; lo <= hi still holds
 
   // Result: selected = {key > thr} + first `remaining` ids with key == thr
   // (tie mode), or {key >= thr} (ge mode).
@@ -234,7 +288,10 @@ __device__ void select_long(int length, int topk, const uint32_t (&key)[ITEMS],
     const int high_bit = 31 - __builtin_clz(lo ^ hi);
     int shift = high_bit > kDigitBits - 1 ? high_bit - (kDigitBits - 1) : 0;
     uint32_t prefix = shift + kDigitBits >= 32 ? 0u : (lo & ~((1u << (shift + kDigitBits)) - 1u));
-    uint32_t cand = active;
+    uint32_t cand = 0;
+#pragma unroll
+    for (int j = 0; j < ITEMS; ++j)
+      if (((active >> j) & 1u) && key[j] >= lo) cand |= 1u << j;
     // One barrier per pass: every wave reads the whole histogram and finds
     // the bin itself (identical results), and pass k counts into buffer
     // k % 3, so the buffer read in pass k - 1 can be cleared during pass k
@@ -296,8 +353,8 @@ __device__ void select_long(int length, int topk, const uint32_t (&key)[ITEMS],
       const int need = __builtin_amdgcn_readlane(hit_need, src);
       const int in_bin = __builtin_amdgcn_readlane(hit_count, src);
       prefix |= bin << shift;
-      if (in_bin == need) {  // the whole bin is taken: every key >= its smallest key
-        thr = prefix;
+      if (in_bin == need) {  // the whole bin is taken: every candidate >= its smallest key
+        thr = max(prefix, lo);
         ge = true;
         break;
       }
@@ -338,7 +395,7 @@ __device__ void select_long(int length, int topk, const uint32_t (&key)[ITEMS],
     }
     if (rank >= 0) {
       sel[rank] = id[j];
-      sel[topk + rank] = (aux_ok >> j) & 1u ? aux[j] : -1;
+      sel[topk + rank] = PAGES ? page[base + j] : -1;
     }
   }
 }
@@ -446,48 +503,35 @@ __device__ __forceinline__ void write_expanded(const ExpandMeta& m, const RowMet
   if (m.store_counts && threadIdx.x == 0) m.counts[row] = min(expanded + tail_count, r.seq_len);
 }
 
-// Everything the expansion of one row needs from global memory besides the
-// scores: row metadata, the page-table entry of every candidate block this
-// thread holds and the causal tail's pages. Loads are unconditional (validity
-// kept in bit masks, applied at use) so they can be issued early and stay in
-// flight without forcing conservative waits.
-template <int ITEMS>
+// Row metadata and causal-tail pages of the expansion, loaded while the
+// scores are in flight.
 struct RowPrefetch {
   RowMeta r;
-  int aux[ITEMS];
-  uint32_t aux_ok;
   int tail_pp;
   bool tail_ok;
 };
 
-template <int ITEMS, bool EXPAND>
-__device__ __forceinline__ void prefetch_row(const ExpandMeta& m, int row, int limit,
-                                             const int (&id)[ITEMS], RowPrefetch<ITEMS>& f) {
-  const int tid = threadIdx.x;
-  f.r = RowMeta{0, 0, nullptr};
-  f.aux_ok = 0;
-  f.tail_pp = -1;
-  f.tail_ok = false;
-#pragma unroll
-  for (int j = 0; j < ITEMS; ++j) f.aux[j] = 0;
-  if (!EXPAND) return;
-  const int req = m.token_to_req[row];
-  f.r.pos = (int)m.positions[row];
+template <bool EXPAND>
+__device__ __forceinline__ RowPrefetch prefetch_tail(const ExpandMeta& m, int req, int pos) {
+  RowPrefetch f{RowMeta{0, pos, nullptr}, -1, false};
+  if (!EXPAND) return f;
   const bool mapped = req >= 0 && req < m.num_requests;
   f.r.seq_len = mapped ? m.sequence_lengths[req] : 0;
   f.r.table_row = m.physical ? m.table + (int64_t)(mapped ? req : 0) * m.table_row_stride : nullptr;
-  const int32_t* zero = reinterpret_cast<const int32_t*>(g_qsa_zero_rows);
-#pragma unroll
-  for (int j = 0; j < ITEMS; ++j) {
-    const int lp = tid * ITEMS + j < limit ? token_page(m, id[j] * m.ratio) : -1;
-    const bool ok = f.r.table_row && lp >= 0;
-    f.aux[j] = *(ok ? f.r.table_row + lp : zero);
-    f.aux_ok |= (uint32_t)ok << j;
-  }
-  const int lp = (tid < kTailSlots && tid < m.ratio - 1)
-                     ? token_page(m, tail_start_of(f.r.pos, m.ratio) + tid) : -1;
+  const int tid = threadIdx.x;
+  const int lp = (tid < kTailSlots && tid < m.ratio - 1) ? token_page(m, tail_start_of(pos, m.ratio) + tid)
+                                                          : -1;
   f.tail_ok = f.r.table_row && lp >= 0;
-  f.tail_pp = *(f.tail_ok ? f.r.table_row + lp : zero);
+  f.tail_pp = *(f.tail_ok ? f.r.table_row + lp : reinterpret_cast<const int32_t*>(g_qsa_zero_rows));
+  return f;
+}
+
+// Physical page of block id's first token (-1 without one); unconditional load.
+__device__ __forceinline__ int block_page(const ExpandMeta& m, const RowMeta& r, int id, bool in) {
+  const int lp = in ? token_page(m, id * m.ratio) : -1;
+  const bool ok = r.table_row && lp >= 0;
+  const int v = *(ok ? r.table_row + lp : reinterpret_cast<const int32_t*>(g_qsa_zero_rows));
+  return ok ? v : -1;
 }
 
 template <int THREADS>
@@ -495,23 +539,108 @@ __device__ __forceinline__ void clear_histograms(TopkShared<THREADS>& sh) {
   for (int b = threadIdx.x; b < kHistBuffers * kBins; b += THREADS) (&sh.hist[0][0])[b] = 0u;
 }
 
-// Select and write one row from keys already in registers. The histograms
-// must be clear and visible to every wave (a barrier after clear_histograms).
-template <int THREADS, int ITEMS, bool EXPAND, typename Loader>
+// Scores of elements [0, limit) of a contiguous row into the stage, then each
+// thread's ITEMS consecutive keys back into registers. Ends with the barrier
+// that also publishes the cleared histograms.
+template <int THREADS, int ITEMS, bool EXPAND, bool PAGES, typename Stage>
+__device__ __forceinline__ RowPrefetch stage_row(const DirectLoader& load, int limit,
+                                                 const ExpandMeta& m, int row, uint32_t (&key)[ITEMS],
+                                                 int (&id)[ITEMS], TopkShared<THREADS>& sh, Stage& st) {
+  const int tid = threadIdx.x;
+  // Row metadata first: the tail and page loads depend on it, the scores do not.
+  const int req = EXPAND ? m.token_to_req[row] : 0;
+  const int pos = EXPAND ? (int)m.positions[row] : 0;
+  const uint32_t* src = reinterpret_cast<const uint32_t*>(load.scores + load.start);
+  uint32_t v[ITEMS];
+#pragma unroll
+  for (int i = 0; i < ITEMS; ++i) {
+    const int e = i * THREADS + tid;
+    v[i] = *(e < limit ? src + e : g_qsa_zero_rows);
+  }
+  const RowPrefetch f = prefetch_tail<EXPAND>(m, req, pos);
+  int pg[ITEMS];
+  if (PAGES) {
+#pragma unroll
+    for (int i = 0; i < ITEMS; ++i) {
+      const int e = i * THREADS + tid;
+      pg[i] = block_page(m, f.r, load.start + e, e < limit);
+    }
+  }
+  clear_histograms(sh);
+#pragma unroll
+  for (int i = 0; i < ITEMS; ++i) st.key[i * THREADS + tid] = v[i];
+  if (PAGES) {
+#pragma unroll
+    for (int i = 0; i < ITEMS; ++i) st.page[i * THREADS + tid] = pg[i];
+  }
+  lds_barrier();
+  static_assert(ITEMS % 2 == 0, "keys are read back in pairs or quads");
+#pragma unroll
+  for (int j = 0; j < ITEMS; j += (ITEMS % 4 == 0 ? 4 : 2)) {
+    if (ITEMS % 4 == 0) {
+      const u32x4 q = *reinterpret_cast<const u32x4*>(&st.key[tid * ITEMS + j]);
+      key[j] = q[0];
+      key[j + 1] = q[1];
+      key[j + 2] = q[2];
+      key[j + 3] = q[3];
+    } else {
+      const u32x2 q = *reinterpret_cast<const u32x2*>(&st.key[tid * ITEMS + j]);
+      key[j] = q[0];
+      key[j + 1] = q[1];
+    }
+  }
+#pragma unroll
+  for (int j = 0; j < ITEMS; ++j) id[j] = load.start + tid * ITEMS + j;
+  return f;
+}
+
+// Candidate list: thread t gathers the ids at list positions [t*ITEMS,
+// t*ITEMS+ITEMS) and their scores (and pages) directly.
+template <int THREADS, int ITEMS, bool EXPAND, bool PAGES, typename Stage>
+__device__ __forceinline__ RowPrefetch stage_row(const IndirectLoader& load, int limit,
+                                                 const ExpandMeta& m, int row, uint32_t (&key)[ITEMS],
+                                                 int (&id)[ITEMS], TopkShared<THREADS>& sh, Stage& st) {
+  const int tid = threadIdx.x;
+  const int base = tid * ITEMS;
+  const int req = EXPAND ? m.token_to_req[row] : 0;
+  const int pos = EXPAND ? (int)m.positions[row] : 0;
+  const uint32_t* src = reinterpret_cast<const uint32_t*>(load.scores);
+  const int32_t* zero = reinterpret_cast<const int32_t*>(g_qsa_zero_rows);
+#pragma unroll
+  for (int j = 0; j < ITEMS; ++j) id[j] = *(base + j < limit ? load.ids + base + j : zero);
+#pragma unroll
+  for (int j = 0; j < ITEMS; ++j) key[j] = src[id[j]];  // id 0 stands in past the list
+  const RowPrefetch f = prefetch_tail<EXPAND>(m, req, pos);
+  clear_histograms(sh);
+  if (PAGES) {
+#pragma unroll
+    for (int j = 0; j < ITEMS; ++j) st.page[base + j] = block_page(m, f.r, id[j], base + j < limit);
+  }
+  lds_barrier();
+  return f;
+}
+
+// Select and write one row from staged keys. `sel` (2 * topk ints) may alias
+// the key stage, which is dead once the keys are in registers.
+template <int THREADS, int ITEMS, bool EXPAND, bool PAGES, typename Loader, typename Stage>
 __device__ void finish_row(const Loader& load, const uint32_t (&key)[ITEMS], const int (&id)[ITEMS],
-                           const RowPrefetch<ITEMS>& f, int length_raw, int clamp, int topk,
-                           const ExpandMeta& m, int row, int32_t* out, TopkShared<THREADS>& sh,
-                           int* sel) {
+                           const RowPrefetch& f, const Stage& st, int staged,
+                           int length_raw, int clamp, int topk, const ExpandMeta& m, int row,
+                           int32_t* out, TopkShared<THREADS>& sh, int* sel) {
   const int tid = threadIdx.x;
   const int length = length_raw > topk ? min(length_raw, clamp) : length_raw;
   if (length > topk) {
-    select_long<THREADS, ITEMS>(length, topk, key, id, f.aux, f.aux_ok, sh, sel);
+    select_long<THREADS, ITEMS, PAGES>(length, topk, key, id, st.page, sh, sel);
   } else {
     // At most topk entries: the loader's first `length` ids in order, then -1.
+    lds_barrier();  // every wave has read its keys back before sel overwrites them
+    // Lengths of at most topk are not clamped to the row, so ids past the
+    // staged elements read their page directly.
     for (int i = tid; i < topk; i += THREADS) {
       const int lid = i < length ? load.id_at(i) : -1;
       sel[i] = lid;
-      sel[topk + i] = (EXPAND && lid >= 0) ? table_entry(f.r, token_page(m, lid * m.ratio)) : -1;
+      sel[topk + i] = (PAGES && lid >= 0) ? (i < staged ? st.page[i] : block_page(m, f.r, lid, true))
+                                          : -1;
     }
   }
   if (EXPAND && tid < kTailSlots && tid < m.ratio - 1) sh.tail_page[tid] = f.tail_ok ? f.tail_pp : -1;
@@ -523,20 +652,19 @@ __device__ void finish_row(const Loader& load, const uint32_t (&key)[ITEMS], con
   }
 }
 
-// One row of scores in global memory: scores first, then the expansion's
-// loads, then select and write.
-template <int THREADS, int ITEMS, bool EXPAND, typename Loader>
+// One row: stage the scores (and pages), select, write. PAGES stages the
+// physical page of every candidate (the expansion maps to physical slots); the
+// stage must then have room for them.
+template <int THREADS, int ITEMS, bool EXPAND, bool PAGES, typename Loader, typename Stage>
 __device__ void process_row(const Loader& load, int limit, int length_raw, int clamp, int topk,
-                            const ExpandMeta& m, int row, int32_t* out,
-                            TopkShared<THREADS>& sh, int* sel) {
+                            const ExpandMeta& m, int row, int32_t* out, TopkShared<THREADS>& sh,
+                            Stage& st, int* sel) {
   uint32_t key[ITEMS];
   int id[ITEMS];
-  load.template load<ITEMS>(threadIdx.x * ITEMS, limit, key, id);
-  clear_histograms(sh);
-  RowPrefetch<ITEMS> f;
-  prefetch_row<ITEMS, EXPAND>(m, row, limit, id, f);
-  finish_row<THREADS, ITEMS, EXPAND>(load, key, id, f, length_raw, clamp, topk, m, row, out, sh,
-                                     sel);
+  const RowPrefetch f =
+      stage_row<THREADS, ITEMS, EXPAND, PAGES>(load, limit, m, row, key, id, sh, st);
+  finish_row<THREADS, ITEMS, EXPAND, PAGES>(load, key, id, f, st, limit, length_raw, clamp, topk, m,
+                                            row, out, sh, sel);
 }
 
 }  // namespace
