@@ -12,7 +12,7 @@ namespace {
 // --- kernels ---------------------------------------------------------------
 
 // Rows at which the chip is full and throughput, not one row's latency, sets
-// the time (launch shapes and the row writer switch there).
+// the time (the launch shapes switch there).
 constexpr int kManyRows = 1024;
 
 struct TopkArgs {
@@ -255,7 +255,6 @@ extern "C" int qsa_topk_expand(const float* scores, int64_t score_row_stride, in
   a.meta.out_width = output_width;
   a.meta.physical = physical ? 1 : 0;
   a.meta.store_counts = store_counts ? 1 : 0;
-  a.meta.coalesce = rows >= kManyRows ? 1 : 0;
   return launch_topk<true>(a, rows, cols, workspace, workspace_bytes,
                            static_cast<hipStream_t>(stream));
 }

@@ -90,7 +90,6 @@ struct ExpandMeta {
   int out_width;
   int physical;
   int store_counts;
-  int coalesce;  // write rows column-major across threads (many rows) or block per thread
 };
 
 // Raw per-row inputs of the expansion (topk.cu:166-180); everything derived
@@ -120,6 +119,12 @@ __device__ __forceinline__ int slot_of(const ExpandMeta& m, const RowMeta& r, in
 
 __device__ __forceinline__ int table_entry(const RowMeta& r, int lp) {
   return (r.table_row && lp >= 0) ? r.table_row[lp] : -1;
+}
+
+// Physical slot of block id's first token given that token's page (-1: none).
+__device__ __forceinline__ int first_slot(const ExpandMeta& m, int pp, int id) {
+  const int first = id * m.ratio;
+  return pp >= 0 ? pp * m.page_size + (first - m.page_div.div(first) * m.page_size) : -1;
 }
 
 // --- staging -----------------------------------------------------------------
@@ -241,12 +246,13 @@ __device__ __forceinline__ void block_scan2(int& a, int& b, TopkShared<THREADS>&
 // --- selection --------------------------------------------------------------
 
 // Exact top-k of `length` (> topk) keys in registers. Writes the selected ids
-// in ascending-id order to sel[0..topk) and, with PAGES, the staged page of
-// each (page[e] for the element at position e) to sel[topk..2 topk).
+// in ascending-id order to sel[0..topk) and, with PAGES, the physical slot of
+// each one's first token (from page[e], the staged page of the element at
+// position e) to sel[topk..2 topk).
 template <int THREADS, int ITEMS, bool PAGES>
 __device__ void select_long(int length, int topk, const uint32_t (&key)[ITEMS],
-                            const int (&id)[ITEMS], const int* page, TopkShared<THREADS>& sh,
-                            int* sel) {
+                            const int (&id)[ITEMS], const int* page, const ExpandMeta& m,
+                            TopkShared<THREADS>& sh, int* sel) {
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int base = tid * ITEMS;
@@ -395,20 +401,20 @@ __device__ void select_long(int length, int topk, const uint32_t (&key)[ITEMS],
     }
     if (rank >= 0) {
       sel[rank] = id[j];
-      sel[topk + rank] = PAGES ? page[base + j] : -1;
+      sel[topk + rank] = PAGES ? first_slot(m, page[base + j], id[j]) : -1;
     }
   }
 }
 
-// Writes one expanded output row (coalesced over columns) from ranked block
-// ids in sel[0..topk) and their first-token physical pages in sel[topk..).
+// Writes one expanded output row from ranked block ids in sel[0..topk) and
+// the physical slots of their first tokens in sel[topk..) (-1 without one).
+// Consecutive threads write consecutive columns.
 //
 // The common layouts (logical ids, or blocks that lie inside one page with the
-// causal tail's pages prefetched) write the row from LDS alone, one block of
-// columns per thread. A loop with a global load in it would make every
-// iteration wait for all earlier stores: on gfx9 stores count in the same
-// in-order counter as loads, and the compiler cannot tell a skipped load from a
-// pending one.
+// causal tail's pages prefetched) write the row from LDS alone, in a loop with
+// no global load: on gfx9 stores count in the same in-order counter as loads,
+// and the compiler cannot tell a skipped load from a pending one, so a load
+// anywhere in the loop would make every iteration wait for all earlier stores.
 __device__ __forceinline__ void write_expanded(const ExpandMeta& m, const RowMeta& r, int row,
                                                int topk, const int* sel, const int* tail_page,
                                                int32_t* out) {
@@ -419,10 +425,8 @@ __device__ __forceinline__ void write_expanded(const ExpandMeta& m, const RowMet
   const int expanded = complete * m.ratio;
   const bool block_in_page = m.physical && (m.page_size % m.ratio == 0);
   const bool from_lds = !m.physical || (block_in_page && m.ratio - 1 <= kTailSlots);
-  if (from_lds && m.coalesce) {
-    // Many rows: the chip is full and stores dominate, so consecutive threads
-    // write consecutive columns.
-    const int64_t cs = m.out_col_stride;
+  const int64_t cs = m.out_col_stride;
+  if (from_lds) {
     for (int c = threadIdx.x; c < m.out_width; c += blockDim.x) {
       int v = -1;
       if (c < expanded) {
@@ -433,11 +437,9 @@ __device__ __forceinline__ void write_expanded(const ExpandMeta& m, const RowMet
         if (block >= 0 && t < r.seq_len) {
           if (!m.physical) {
             v = t;
-          } else {
-            // The block lies inside one page (topk.cu:134-146).
-            const int pp = sel[topk + rank];
-            const int first = block * m.ratio;
-            v = pp >= 0 ? pp * m.page_size + (first - m.page_div.div(first) * m.page_size) + o : -1;
+          } else {  // the block lies inside one page (topk.cu:134-146)
+            const int s0 = sel[topk + rank];
+            v = s0 >= 0 ? s0 + o : -1;
           }
         }
       } else {
@@ -447,31 +449,6 @@ __device__ __forceinline__ void write_expanded(const ExpandMeta& m, const RowMet
       }
       out[(int64_t)c * cs] = v;
     }
-  } else if (from_lds) {
-    const int64_t cs = m.out_col_stride;
-    // Few rows: one row's latency is the time. Thread b writes the `ratio`
-    // columns of rank b: two LDS reads, then plain stores (topk.cu:134-146
-    // for the physical form).
-    for (int b = threadIdx.x; b < complete; b += blockDim.x) {
-      const int block = sel[b];
-      const int first = block * m.ratio;
-      int base = first;
-      if (m.physical) {
-        const int pp = sel[topk + b];
-        base = pp >= 0 ? pp * m.page_size + (first - m.page_div.div(max(first, 0)) * m.page_size) : -1;
-      }
-      const int lim = (block < 0 || base < 0) ? 0 : min(m.ratio, r.seq_len - first);
-      int32_t* o = out + (int64_t)b * m.ratio * cs;
-      for (int j = 0; j < m.ratio; ++j, o += cs) *o = j < lim ? base + j : -1;
-    }
-    // Causal tail, then -1 to the end of the row.
-    for (int c = expanded + threadIdx.x; c < m.out_width; c += blockDim.x) {
-      const int off = c - expanded;
-      int v = -1;
-      if (off < tail_count && off < m.ratio - 1)
-        v = slot_of(m, r, tail_start + off, m.physical ? tail_page[off] : 0);
-      out[(int64_t)c * cs] = v;
-    }
   } else {
     for (int c = threadIdx.x; c < m.out_width; c += blockDim.x) {
       int v = -1;
@@ -479,13 +456,12 @@ __device__ __forceinline__ void write_expanded(const ExpandMeta& m, const RowMet
         const int rank = m.ratio_div.div(c);
         const int o = c - rank * m.ratio;
         const int block = sel[rank];
-        if (block >= 0) {
-          const int first = block * m.ratio;
+        const int t = block * m.ratio + o;
+        if (block >= 0 && t < r.seq_len) {
           if (block_in_page) {
-            const int s0 = slot_of(m, r, first, sel[topk + rank]);
-            v = (s0 >= 0 && first + o < r.seq_len) ? s0 + o : -1;
+            const int s0 = sel[topk + rank];
+            v = s0 >= 0 ? s0 + o : -1;
           } else {
-            const int t = first + o;
             v = slot_of(m, r, t, table_entry(r, token_page(m, t)));
           }
         }
@@ -497,7 +473,7 @@ __device__ __forceinline__ void write_expanded(const ExpandMeta& m, const RowMet
           v = slot_of(m, r, t, pp);
         }
       }
-      out[(int64_t)c * m.out_col_stride] = v;
+      out[(int64_t)c * cs] = v;
     }
   }
   if (m.store_counts && threadIdx.x == 0) m.counts[row] = min(expanded + tail_count, r.seq_len);
@@ -630,7 +606,7 @@ __device__ void finish_row(const Loader& load, const uint32_t (&key)[ITEMS], con
   const int tid = threadIdx.x;
   const int length = length_raw > topk ? min(length_raw, clamp) : length_raw;
   if (length > topk) {
-    select_long<THREADS, ITEMS, PAGES>(length, topk, key, id, st.page, sh, sel);
+    select_long<THREADS, ITEMS, PAGES>(length, topk, key, id, st.page, m, sh, sel);
   } else {
     // At most topk entries: the loader's first `length` ids in order, then -1.
     lds_barrier();  // every wave has read its keys back before sel overwrites them
@@ -639,8 +615,9 @@ __device__ void finish_row(const Loader& load, const uint32_t (&key)[ITEMS], con
     for (int i = tid; i < topk; i += THREADS) {
       const int lid = i < length ? load.id_at(i) : -1;
       sel[i] = lid;
-      sel[topk + i] = (PAGES && lid >= 0) ? (i < staged ? st.page[i] : block_page(m, f.r, lid, true))
-                                          : -1;
+      sel[topk + i] = (PAGES && lid >= 0)
+                          ? first_slot(m, i < staged ? st.page[i] : block_page(m, f.r, lid, true), lid)
+                          : -1;
     }
   }
   if (EXPAND && tid < kTailSlots && tid < m.ratio - 1) sh.tail_page[tid] = f.tail_ok ? f.tail_pp : -1;
