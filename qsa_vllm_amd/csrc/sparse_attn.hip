@@ -11,27 +11,34 @@
 //   S^T[tok][head] = K_tile (A, 16 tokens x 32 dims) * Q^T (B, 32 dims x 16 heads)
 //       v_mfma_f32_16x16x32_bf16, K read straight from HBM into the A operand
 //       (16 B per lane, 64 B contiguous per token per instruction);
-//       the NKV kv heads accumulate into one S because each lane's Q column
-//       is zero for the kv heads it does not belong to.
+//       one accumulator per kv head, each lane keeping the one its head
+//       attends with.
 //   O^T[dim][head] += V_tile^T (A, 16 dims x 32 tokens) * P^T (B, 32 tok x 16 heads)
 //       each lane loads an 8 token x DPL dim block of V (one 16 B row load per
 //       token) and transposes it in registers with v_perm_b32; P^T is exactly
 //       the lane's own softmax numerators, so P never leaves registers and the
 //       per-head rescale factor lives in the lane that owns that head.
 //
+// Index entries. A lane loads the index entries of its two K tokens only; the
+// slots of its eight V tokens are K slots of lanes in the same 16-lane row
+// and arrive by ds_bpermute.
+//
 // Load schedule. A wave's global loads complete in issue order, so the tile
 // loop is a two-stage pipeline over the K and V halves of a tile:
 //
-//   Q.K + softmax (t) | resolve slots, issue K (t+W) | P.V (t) |
-//   issue index loads (t+2W), issue V (t+W)
+//   Q.K + softmax (t) | slots, issue K (t+W) | P.V (t) |
+//   issue index loads (t+2W), permute V slots, issue V (t+W)
+//
+// Logical indices add a third stage for their block-table entries (index
+// entries of t+3W, table entries of t+2W, K/V of t+W in flight), so the table
+// loads never wait behind the tile in flight.
 //
 // Every wait is for the oldest group in flight, and the next tile's K (V)
 // bytes stream in while P.V (the next Q.K) computes, so a wave never leaves
 // the memory system idle behind its own arithmetic. sched_barrier pins that
 // issue order against the scheduler. Invalid slots read a block of zeros in
 // device memory instead of K/V, so no per-element masking is needed beyond
-// the -inf score. Logical indices add a dependent block-table load per slot;
-// it waits behind the tile in flight, so the physical form is the fast one.
+// the -inf score.
 //
 // The waves merge (max, sum, O) through LDS. With one split the workgroup
 // writes the bf16 output (and gate); with several it writes an fp32 partial +
@@ -90,17 +97,26 @@ __device__ __forceinline__ float sigmoidf_(float x) { return 1.0f / (1.0f + __ex
 
 #define QSA_SCHED_FENCE() __builtin_amdgcn_sched_barrier(0)
 
-// Validated physical slot (page * page_size + offset) of index value `tok`,
-// or -1 (ops/qsa.py:186-212). The block-table load of logical indices is
-// unconditional (an invalid entry reads the zero block and is then rejected)
-// so that the compiler's wait counts stay static.
-template <bool PHYSICAL>
-__device__ __forceinline__ int resolve_slot(const AttnParams& p, const int32_t* trow, bool req_ok,
-                                            int tok) {
+// Validated slot (page * page_size + offset) of a physical index value, or
+// -1 (ops/qsa.py:186-212).
+__device__ __forceinline__ int physical_slot(const AttnParams& p, int tok) {
   const int lp = p.page_div.div(max(tok, 0));
-  if (PHYSICAL) return (tok >= 0 && lp < p.num_blocks) ? tok : -1;
+  return (tok >= 0 && lp < p.num_blocks) ? tok : -1;
+}
+
+// Logical indices in two steps (ops/qsa.py:186-212), so the block-table loads
+// can be issued a whole tile ahead of the K/V loads that need them: the table
+// entries of a tile's index values (unconditional loads, the zero block where
+// an entry is not mapped), then the validated slots.
+__device__ __forceinline__ int table_page(const AttnParams& p, const int32_t* trow, bool req_ok,
+                                          int tok) {
+  const int lp = p.page_div.div(max(tok, 0));
   const bool mapped = tok >= 0 && req_ok && lp < p.table_width;
-  const int page = *(mapped ? trow + lp : reinterpret_cast<const int32_t*>(g_qsa_zero_rows));
+  return *(mapped ? trow + lp : reinterpret_cast<const int32_t*>(g_qsa_zero_rows));
+}
+__device__ __forceinline__ int logical_slot(const AttnParams& p, bool req_ok, int tok, int page) {
+  const int lp = p.page_div.div(max(tok, 0));
+  const bool mapped = tok >= 0 && req_ok && lp < p.table_width;
   return (mapped && page >= 0 && page < p.num_blocks) ? page * p.page_size + (tok - lp * p.page_size)
                                                       : -1;
 }
@@ -138,24 +154,19 @@ struct TileV {
 };
 
 __device__ __forceinline__ int k_col(int tile, int u, int n) { return tile * kTile + 16 * u + n; }
-__device__ __forceinline__ int v_col(int tile, int i, int g) {
-  return tile * kTile + 16 * (i >> 2) + 4 * g + (i & 3);
-}
 
-// Raw index entries of a tile. Every entry is loaded unconditionally (columns
-// past the valid count or the split read the zero block) with its validity in
-// `ok`, applied only when the entry is used: a skipped load would make the
-// compiler drain every outstanding load at the first use instead of waiting
-// for these loads alone.
+// Raw index entries of a tile's K tokens 16 u + n. Every entry is loaded
+// unconditionally (columns past the valid count or the split read the zero
+// block) with its validity in `ok`, applied only when the entry is used: a
+// skipped load would make the compiler drain every outstanding load at the
+// first use instead of waiting for these loads alone.
 struct TileIdx {
   int k[2];
-  int v[8];
-  uint32_t ok;  // bits 0-1: k[u], bits 2-9: v[i]
+  uint32_t ok;  // bit u: k[u]
   __device__ __forceinline__ int key(int u) const { return (ok >> u) & 1u ? k[u] : -1; }
-  __device__ __forceinline__ int val(int i) const { return (ok >> (2 + i)) & 1u ? v[i] : -1; }
 };
 __device__ __forceinline__ void load_tile_idx(const int32_t* irow, int tile, int t_end,
-                                              int n_valid, int n, int g, TileIdx& r) {
+                                              int n_valid, int n, TileIdx& r) {
   const int32_t* zero = reinterpret_cast<const int32_t*>(g_qsa_zero_rows);
   const bool live = tile < t_end;
   r.ok = 0;
@@ -166,13 +177,15 @@ __device__ __forceinline__ void load_tile_idx(const int32_t* irow, int tile, int
     r.k[u] = *(ok ? irow + col : zero);
     r.ok |= (uint32_t)ok << u;
   }
+}
+
+// Slots of the lane's V tokens 16 (i / 4) + 4 g + i % 4: each is the K token
+// 16 u + n of lane 16 g + n with u = i / 4, n = 4 g + i % 4, in the same row
+// of 16 lanes.
+__device__ __forceinline__ void v_slots_from_k(const int (&ks)[2], int g, int (&vs)[8]) {
 #pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    const int col = v_col(tile, i, g);
-    const bool ok = live && col < n_valid;
-    r.v[i] = *(ok ? irow + col : zero);
-    r.ok |= (uint32_t)ok << (2 + i);
-  }
+  for (int i = 0; i < 8; ++i)
+    vs[i] = __builtin_amdgcn_ds_bpermute((20 * g + (i & 3)) * 4, ks[i >> 2]);
 }
 
 template <int D, int NKV>
@@ -210,22 +223,26 @@ __device__ __forceinline__ void issue_v(const AttnParams& p, const int (&slot)[8
 }
 
 // S^T = K_tile Q^T, then the online-softmax update of head n; returns P^T (the
-// lane's 8 token numerators) as packed bf16 pairs.
+// lane's 8 token numerators) as packed bf16 pairs. Each kv head's scores are
+// computed for all 16 head columns and every lane keeps its own head's kv.
 template <int D, int NKV>
 __device__ __forceinline__ u32x4 qk_softmax(const AttnParams& p, const TileK<D, NKV>& K,
-                                            const bf16x8 (&bq)[NKV][D / 32], uint32_t mask,
+                                            const bf16x8 (&bq)[D / 32], int vslot, uint32_t mask,
                                             float& m_run, float& l_run, f32x4 (&oacc)[D / 16]) {
   f32x4 sacc[2];
 #pragma unroll
   for (int u = 0; u < 2; ++u) {
-    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+    f32x4 sel = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int v = 0; v < NKV; ++v)
+    for (int v = 0; v < NKV; ++v) {
+      f32x4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int s = 0; s < D / 32; ++s)
         acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, K.r[v][u][s]),
-                                                      bq[v][s], acc, 0, 0, 0);
-    sacc[u] = acc;
+                                                      bq[s], acc, 0, 0, 0);
+      sel = vslot == v ? acc : sel;
+    }
+    sacc[u] = sel;
   }
   // Lane holds S[token 16 u + 4 g + r][head n] in sacc[u][r] = token slot 4 u + r.
   float sc[8];
@@ -306,21 +323,15 @@ void sparse_attn_kernel(const AttnParams p) {
   const int qh = head0 + n;
   const int vslot = head_ok ? qh / p.group - kv0 : -1;
 
-  // Q^T as the B operand: lane holds Q[qh][32 s + 8 g .. +7], zero for the
-  // kv slots this head does not attend with.
-  bf16x8 bq[NKV][KS];
+  // Q^T as the B operand: lane holds Q[qh][32 s + 8 g .. +7].
+  bf16x8 bq[KS];
   {
     const uint16_t* qrow = p.q + (int64_t)row * p.q_row + (int64_t)(head_ok ? qh : 0) * p.q_head;
     const void* zero = g_qsa_zero_rows;
 #pragma unroll
-    for (int s = 0; s < KS; ++s) {
-      const u32x4 raw = load_u32x4(head_ok ? (const void*)(qrow + 32 * s + 8 * g) : zero);
-#pragma unroll
-      for (int v = 0; v < NKV; ++v) {
-        const u32x4 sel = (vslot == v) ? raw : u32x4{0u, 0u, 0u, 0u};
-        bq[v][s] = __builtin_bit_cast(bf16x8, sel);
-      }
-    }
+    for (int s = 0; s < KS; ++s)
+      bq[s] = __builtin_bit_cast(
+          bf16x8, load_u32x4(head_ok ? (const void*)(qrow + 32 * s + 8 * g) : zero));
   }
 
   int n_valid = p.width;
@@ -347,20 +358,64 @@ void sparse_attn_kernel(const AttnParams p) {
   for (int j = 0; j < DPL; ++j) oacc[j] = f32x4{0.f, 0.f, 0.f, 0.f};
 
   int t = t_begin + wave;
-  if (t < t_end) {
+  if (!PHYSICAL && t < t_end) {
+    // Three stages: index entries of t+3W, table entries of t+2W, K/V of t+W
+    // are in flight while tile t computes. Issue order per trip: K(t+W),
+    // table(t+2W), index(t+3W), V(t+W); each wait is for the oldest group.
+    TileIdx ia, ib;  // index entries of t+W (table entries in flight) and of t+2W
+    int pa[2];       // table entries of t+W
+    int ks[2], vs[8];
+    TileK<D, NKV> K;
+    TileV<D, NKV> V;
+    load_tile_idx(irow, t, t_end, n_valid, n, ia);
+#pragma unroll
+    for (int u = 0; u < 2; ++u) pa[u] = table_page(p, trow, req_ok, ia.key(u));
+#pragma unroll
+    for (int u = 0; u < 2; ++u) ks[u] = logical_slot(p, req_ok, ia.key(u), pa[u]);
+    v_slots_from_k(ks, g, vs);
+    load_tile_idx(irow, t + WAVES, t_end, n_valid, n, ia);
+    QSA_SCHED_FENCE();
+    issue_k<D, NKV>(p, ks, khead, g, K);
+    QSA_SCHED_FENCE();
+#pragma unroll
+    for (int u = 0; u < 2; ++u) pa[u] = table_page(p, trow, req_ok, ia.key(u));
+    QSA_SCHED_FENCE();
+    load_tile_idx(irow, t + 2 * WAVES, t_end, n_valid, n, ib);
+    QSA_SCHED_FENCE();
+    issue_v<D, NKV>(p, vs, vhead, n, V);
+    QSA_SCHED_FENCE();
+    for (; t < t_end; t += WAVES) {
+      const u32x4 praw = qk_softmax<D, NKV>(p, K, bq, vslot, V.mask, m_run, l_run, oacc);
+      QSA_SCHED_FENCE();
+#pragma unroll
+      for (int u = 0; u < 2; ++u) ks[u] = logical_slot(p, req_ok, ia.key(u), pa[u]);
+      issue_k<D, NKV>(p, ks, khead, g, K);
+      QSA_SCHED_FENCE();
+      pv_mfma<D, NKV>(V, praw, vslot, oacc);
+      QSA_SCHED_FENCE();
+#pragma unroll
+      for (int u = 0; u < 2; ++u) pa[u] = table_page(p, trow, req_ok, ib.key(u));
+      ia = ib;  // arrived: its table entries were just addressed from it
+      QSA_SCHED_FENCE();
+      load_tile_idx(irow, t + 3 * WAVES, t_end, n_valid, n, ib);
+      QSA_SCHED_FENCE();
+      v_slots_from_k(ks, g, vs);
+      issue_v<D, NKV>(p, vs, vhead, n, V);
+      QSA_SCHED_FENCE();
+    }
+  } else if (PHYSICAL && t < t_end) {
     TileIdx idx;
     int ks[2], vs[8];
     TileK<D, NKV> K;
     TileV<D, NKV> V;
     // Prologue, in issue order: K(t), index entries of t+W, V(t).
-    load_tile_idx(irow, t, t_end, n_valid, n, g, idx);
+    load_tile_idx(irow, t, t_end, n_valid, n, idx);
 #pragma unroll
-    for (int u = 0; u < 2; ++u) ks[u] = resolve_slot<PHYSICAL>(p, trow, req_ok, idx.key(u));
-#pragma unroll
-    for (int i = 0; i < 8; ++i) vs[i] = resolve_slot<PHYSICAL>(p, trow, req_ok, idx.val(i));
+    for (int u = 0; u < 2; ++u) ks[u] = physical_slot(p, idx.key(u));
     issue_k<D, NKV>(p, ks, khead, g, K);
+    v_slots_from_k(ks, g, vs);
     QSA_SCHED_FENCE();
-    load_tile_idx(irow, t + WAVES, t_end, n_valid, n, g, idx);
+    load_tile_idx(irow, t + WAVES, t_end, n_valid, n, idx);
     QSA_SCHED_FENCE();
     issue_v<D, NKV>(p, vs, vhead, n, V);
     QSA_SCHED_FENCE();
@@ -369,18 +424,17 @@ void sparse_attn_kernel(const AttnParams p) {
     // make the compiler's wait counts assume the branch not taken, so P.V(t)
     // would also wait for K(t+W).
     for (; t < t_end; t += WAVES) {
-      const u32x4 praw = qk_softmax<D, NKV>(p, K, bq, V.mask, m_run, l_run, oacc);
+      const u32x4 praw = qk_softmax<D, NKV>(p, K, bq, vslot, V.mask, m_run, l_run, oacc);
       QSA_SCHED_FENCE();
 #pragma unroll
-      for (int u = 0; u < 2; ++u) ks[u] = resolve_slot<PHYSICAL>(p, trow, req_ok, idx.key(u));
-#pragma unroll
-      for (int i = 0; i < 8; ++i) vs[i] = resolve_slot<PHYSICAL>(p, trow, req_ok, idx.val(i));
+      for (int u = 0; u < 2; ++u) ks[u] = physical_slot(p, idx.key(u));
       issue_k<D, NKV>(p, ks, khead, g, K);
       QSA_SCHED_FENCE();
       pv_mfma<D, NKV>(V, praw, vslot, oacc);
       QSA_SCHED_FENCE();
-      load_tile_idx(irow, t + 2 * WAVES, t_end, n_valid, n, g, idx);
+      load_tile_idx(irow, t + 2 * WAVES, t_end, n_valid, n, idx);
       QSA_SCHED_FENCE();
+      v_slots_from_k(ks, g, vs);
       issue_v<D, NKV>(p, vs, vhead, n, V);
       QSA_SCHED_FENCE();
     }

@@ -12,8 +12,10 @@ namespace {
 // --- kernels ---------------------------------------------------------------
 
 // Rows at which the chip is full and throughput, not one row's latency, sets
-// the time (the launch shapes switch there).
+// the time (the launch shapes switch there), and rows beyond which the
+// narrowest shapes win for rows of up to 2048 columns.
 constexpr int kManyRows = 1024;
+constexpr int kFullChipRows = 4096;
 
 struct TopkArgs {
   const float* scores;
@@ -123,17 +125,19 @@ int launch_topk(TopkArgs a, int rows, int cols, void* workspace, size_t workspac
   if (cols <= kMaxDirectColumns) {
     // Few rows (a decode batch) leave most CUs idle and the time is one row's
     // latency: wider workgroups shorten the per-thread serial parts
-    // (histogram updates, rank emission, row writes). Measured on 64 rows,
-    // top 128 with expansion: 1024 columns 512 x 2 6.5 us (256 x 4 7.1);
-    // 2048 columns 512 x 4 7.8 us (256 x 8 9.1, 1024 x 2 8.5); 4096 columns
-    // 1024 x 4 9.2 us (512 x 8 10.5); 8192 columns 1024 x 8 16.9 us (512 x 16
-    // 18.5). Many rows (prefill) fill the chip and the time is throughput:
-    // narrower workgroups do less redundant per-workgroup work (32768 rows x
-    // 1536 columns: 256 x 8 0.22 ms, 512 x 4 0.41 ms).
+    // (histogram updates, rank emission). Measured on 64 rows, top 128 with
+    // physical expansion: 1024 columns 512 x 2 6.6 us (1024 x 2 7.5, 256 x 4
+    // 8.0); 2048 columns 512 x 4 7.9 us (1024 x 2 8.1, 1024 x 4 8.6); 4096
+    // columns 1024 x 4 10.0 us (512 x 8 9.9); 8192 columns 1024 x 8 13.1 us
+    // (512 x 16 14.8). Many rows fill the chip and the time is throughput:
+    // narrower workgroups do less redundant per-workgroup work (rows of random
+    // length up to the width: 32768 x 1536 256 x 8 0.26 ms, 512 x 4 0.31 ms;
+    // 32768 x 1024 256 x 4 0.18 ms, 512 x 2 0.27 ms), while up to about two
+    // thousand rows 512 x 4 still wins (1024 x 2048: 16.8 us, 256 x 8 18.0).
     const bool latency_bound = rows < kManyRows;
     if (cols <= 1024 && latency_bound) err = launch_direct<512, 2, EXPAND>(a, rows, s);
     else if (cols <= 1024) err = launch_direct<256, 4, EXPAND>(a, rows, s);
-    else if (cols <= 2048 && latency_bound) err = launch_direct<512, 4, EXPAND>(a, rows, s);
+    else if (cols <= 2048 && rows < kFullChipRows) err = launch_direct<512, 4, EXPAND>(a, rows, s);
     else if (cols <= 2048) err = launch_direct<256, 8, EXPAND>(a, rows, s);
     else if (cols <= 4096 && latency_bound) err = launch_direct<1024, 4, EXPAND>(a, rows, s);
     else if (cols <= 4096) err = launch_direct<512, 8, EXPAND>(a, rows, s);
