@@ -77,6 +77,68 @@ int qsa_topk_expand(const float* scores, int64_t score_row_stride, int rows, int
                     void* workspace, size_t workspace_bytes, void* stream);
 
 /* ------------------------------------------------------------------------ */
+/* Kernel 0: indexer preparation and cache producers                          */
+/* ------------------------------------------------------------------------ */
+
+/*
+ * Replaces the launch of _qsa_prepare_kernel in qsa_prepare
+ * (ops/prepare.py:177-225; kernel :49-174, numerics :16-46).
+ *
+ * index_qk [num_tokens, (num_index_heads + 1) * index_head_dim] bf16 (token
+ * stride index_token_stride, unit dim stride): the index queries, then the
+ * raw index key. positions / logical_positions int64; slot mappings int64
+ * (-1: no write); state_table, query_start_loc, k_work int32; k_work is
+ * [num_k_work, 2] (request, group within request), request < 0 for padding.
+ * Writes index_q_out [num_tokens, num_index_heads, index_head_dim] (RMSNorm +
+ * partial RoPE of every query head), one normalised mean-pooled key per
+ * compression group into compressed_cache [blocks, comp_page_size, dim],
+ * the last min(query_len, state_size) raw keys of each request into its ring
+ * state_cache [blocks, state_size, dim], and main_key / main_value rows
+ * [tokens, main_kv_heads, main_head_dim] into main_key_cache /
+ * main_value_cache [blocks, main_page_size, main_kv_heads, main_head_dim].
+ * cos_sin is [max_positions, rotary_dim] bf16 (cos, then sin). Strides are in
+ * elements; every tensor is 16-byte aligned with unit dim stride.
+ * index_head_dim and main_head_dim are 64 or 128; rotary_dim a multiple of 16.
+ */
+int qsa_indexer_prepare(const void* index_qk, int64_t index_token_stride, int num_tokens,
+                        const int64_t* positions, int64_t position_stride,
+                        const void* q_norm_weight, const void* k_norm_weight,
+                        const void* cos_sin, int max_positions, float eps,
+                        void* index_q_out,
+                        void* state_cache, int64_t state_block_stride,
+                        int64_t state_token_stride, int state_size, int num_state_blocks,
+                        const int64_t* state_slots, const int32_t* state_table,
+                        int64_t state_table_stride, const int32_t* query_start_loc,
+                        const int64_t* logical_positions, int num_requests,
+                        void* compressed_cache, int64_t comp_block_stride,
+                        int64_t comp_token_stride, int comp_page_size, int num_comp_blocks,
+                        const int64_t* compressed_slots, const int32_t* k_work, int num_k_work,
+                        const void* main_key, int64_t main_key_token_stride,
+                        int64_t main_key_head_stride,
+                        const void* main_value, int64_t main_value_token_stride,
+                        int64_t main_value_head_stride,
+                        void* main_key_cache, int64_t main_key_cache_block_stride,
+                        int64_t main_key_cache_token_stride, int64_t main_key_cache_head_stride,
+                        void* main_value_cache, int64_t main_value_cache_block_stride,
+                        int64_t main_value_cache_token_stride,
+                        int64_t main_value_cache_head_stride,
+                        const int64_t* main_slots, int main_page_size, int num_main_blocks,
+                        int num_index_heads, int index_head_dim, int rotary_dim,
+                        int compress_ratio, int main_kv_heads, int main_head_dim,
+                        void* stream);
+
+/*
+ * Replaces indexer_norm_rope and its kernel _norm_rope
+ * (ops/normalization.py:33-83): RMSNorm + partial RoPE of every row of
+ * values [tokens, heads, dim] (unit dim stride) into a contiguous out.
+ */
+int qsa_indexer_norm_rope(const void* values, int64_t token_stride, int64_t head_stride,
+                          int tokens, int heads, int dim, const void* weight,
+                          const int64_t* positions, int64_t position_stride,
+                          const void* cos_sin, int max_positions, float eps, int rotary_dim,
+                          void* out, void* stream);
+
+/* ------------------------------------------------------------------------ */
 /* Kernel 1: indexer scoring                                                 */
 /* ------------------------------------------------------------------------ */
 

@@ -39,6 +39,37 @@ SIGNATURES = {
                                 c_i32, c_ptr, c_i32, c_i32,
                                 c_i32, c_i32,
                                 c_ptr, c_size, c_ptr]),
+    "qsa_indexer_prepare": (c_i32, [c_ptr, c_i64, c_i32,
+                                    c_ptr, c_i64,
+                                    c_ptr, c_ptr,
+                                    c_ptr, c_i32, ctypes.c_float,
+                                    c_ptr,
+                                    c_ptr, c_i64,
+                                    c_i64, c_i32, c_i32,
+                                    c_ptr, c_ptr,
+                                    c_i64, c_ptr,
+                                    c_ptr, c_i32,
+                                    c_ptr, c_i64,
+                                    c_i64, c_i32, c_i32,
+                                    c_ptr, c_ptr, c_i32,
+                                    c_ptr, c_i64,
+                                    c_i64,
+                                    c_ptr, c_i64,
+                                    c_i64,
+                                    c_ptr, c_i64,
+                                    c_i64, c_i64,
+                                    c_ptr, c_i64,
+                                    c_i64,
+                                    c_i64,
+                                    c_ptr, c_i32, c_i32,
+                                    c_i32, c_i32, c_i32,
+                                    c_i32, c_i32, c_i32,
+                                    c_ptr]),
+    "qsa_indexer_norm_rope": (c_i32, [c_ptr, c_i64, c_i64,
+                                      c_i32, c_i32, c_i32, c_ptr,
+                                      c_ptr, c_i64,
+                                      c_ptr, c_i32, ctypes.c_float, c_i32,
+                                      c_ptr, c_ptr]),
     "qsa_indexer_decode": (c_i32, [c_ptr, c_i64, c_i64,
                                    c_i32, c_i32, c_i32, c_ptr,
                                    c_i64, c_i64,

@@ -1,0 +1,476 @@
+// Kernel 0: indexer preparation and cache producers, gfx950.
+//
+// qsa_prepare (ops/prepare.py:49-174, launch :177-225) in one launch with
+// three roles, each on 16-lane row groups (lane j of a group holds dims
+// 8 j .. 8 j + 7 of one 64- or 128-dim row, one 16 B load or store):
+//
+//  * index queries: RMSNorm + partial RoPE of every (token, index head) row
+//    of the projection into a contiguous [tokens, heads, dim] output;
+//  * compression groups (one per k_work item): mean of the group's raw index
+//    keys (this step's projection, or the request's raw-key ring for members
+//    before the chunk), RMSNorm + RoPE at the group's first position, store
+//    into the compressed cache; work item 0 of a request then commits the
+//    chunk's last raw keys into the ring, after its own ring reads;
+//  * main K/V: copy of each (token, kv head) key and value row into its
+//    cache slot.
+//
+// indexer_norm_rope (ops/normalization.py:33-83) is the query role alone on
+// an arbitrary strided [tokens, heads, dim] input.
+//
+// Numerics (ops/prepare.py:16-46, ops/normalization.py:44-68). Each fp32
+// product and sum rounds on its own and the post-norm steps round to bf16
+// (the reference compiles with enable_fp_fusion=False), so contraction is off
+// in this file. The sum of squares is formed exactly (bf16 squares are exact
+// in fp32 and their sum is accumulated in double), rounded once to fp32, and
+// the inverse RMS is the correctly rounded 1/sqrt: a definition the CPU
+// oracle reproduces bit for bit. The reference's fp32 tree sum and
+// approximate rsqrt can differ from it in the last fp32 bits, which moves a
+// bf16 output by one unit only when it lies that close to a rounding
+// boundary.
+#pragma clang fp contract(off)
+
+#include "qsa_common.h"
+#include "../../include/qsa_hip.h"
+
+namespace qsa {
+namespace {
+
+constexpr int kGroupLanes = 16;
+constexpr int kPrepThreads = 256;
+constexpr int kGroupsPerBlock = kPrepThreads / kGroupLanes;
+
+struct NormRope {
+  const uint16_t* weight;   // [dim] bf16 gamma
+  const uint16_t* cos_sin;  // [max_positions, rotary] bf16: cos then sin
+  int64_t max_positions;
+  float eps;
+  int dim;
+  int rotary;
+};
+
+__device__ __forceinline__ void unpack8(const u32x4& v, float (&f)[8]) {
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    f[2 * i] = bf16_lo(v[i]);
+    f[2 * i + 1] = bf16_hi(v[i]);
+  }
+}
+
+__device__ __forceinline__ u32x4 pack8(const float (&f)[8]) {
+  u32x4 v;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) v[i] = pack_bf16x2(f[2 * i], f[2 * i + 1]);
+  return v;
+}
+
+__device__ __forceinline__ float round_bf16(float x) { return bf16_lo(pack_bf16x2(x, 0.0f)); }
+
+// Sum over the 16 lanes of a row group (lanes 16 k .. 16 k + 15).
+__device__ __forceinline__ double group_sum(double v) {
+#pragma unroll
+  for (int m = 1; m < kGroupLanes; m <<= 1) v += __shfl_xor(v, m, kGroupLanes);
+  return v;
+}
+
+// RMSNorm + partial RoPE of one row held by a 16-lane group; lane j holds
+// dims 8 j .. 8 j + 7 in x (zeros past the row). Every lane of the group
+// must call it (it shuffles within the group).
+__device__ __forceinline__ u32x4 norm_rope_row(const NormRope& nr, u32x4 x, int64_t pos, int j) {
+  float f[8];
+  unpack8(x, f);
+  double ss = 0.0;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) ss += (double)(f[i] * f[i]);  // each square is exact
+  ss = group_sum(ss);
+  const float mean = __fdiv_rn((float)ss, (float)nr.dim);
+  const float inv = (float)__ddiv_rn(1.0, __dsqrt_rn((double)__fadd_rn(mean, nr.eps)));
+
+  const bool live = 8 * j < nr.dim;
+  const u32x4 graw = *reinterpret_cast<const u32x4*>(
+      live ? (const void*)(nr.weight + 8 * j) : (const void*)g_qsa_zero_rows);
+  float gamma[8];
+  unpack8(graw, gamma);
+  float scaled[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) scaled[i] = round_bf16(round_bf16(f[i] * inv) * gamma[i]);
+  const u32x4 sc = pack8(scaled);
+
+  // Rotate-half partner: dims d < half pair with d + half, the rest of the
+  // rotary dims with d - half, i.e. lane j +/- half / 8 of the same group.
+  const int half = nr.rotary / 2;
+  const bool rot = 8 * j < nr.rotary;
+  const bool first_half = 8 * j < half;
+  const int lane = threadIdx.x & 63;
+  const int src = rot ? (first_half ? lane + half / 8 : lane - half / 8) : lane;
+  u32x4 pr;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) pr[i] = __builtin_amdgcn_ds_bpermute(4 * src, sc[i]);
+  const bool pos_ok = pos >= 0 && pos < nr.max_positions;
+  const int channel = (8 * j) % max(half, 1);
+  const uint16_t* cs = nr.cos_sin + (pos_ok ? pos : 0) * nr.rotary + channel;
+  const bool cs_ok = rot && pos_ok;
+  const u32x4 craw = *reinterpret_cast<const u32x4*>(cs_ok ? (const void*)cs : (const void*)g_qsa_zero_rows);
+  const u32x4 sraw =
+      *reinterpret_cast<const u32x4*>(cs_ok ? (const void*)(cs + half) : (const void*)g_qsa_zero_rows);
+  if (!rot) return sc;
+  float partner[8], cosv[8], sinv[8], out[8];
+  unpack8(pr, partner);
+  unpack8(craw, cosv);
+  unpack8(sraw, sinv);
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const float rotated = first_half ? -partner[i] : partner[i];
+    const float a = round_bf16(scaled[i] * cosv[i]);
+    const float b = round_bf16(rotated * sinv[i]);
+    out[i] = a + b;  // rounded to bf16 by pack8
+  }
+  return pack8(out);
+}
+
+// Row load (zeros for lanes past the row or when !ok).
+__device__ __forceinline__ u32x4 load_row(const uint16_t* row, int j, int dim, bool ok) {
+  return *reinterpret_cast<const u32x4*>(ok && 8 * j < dim ? (const void*)(row + 8 * j)
+                                                           : (const void*)g_qsa_zero_rows);
+}
+
+__device__ __forceinline__ void store_row(uint16_t* row, int j, int dim, u32x4 v) {
+  if (8 * j < dim) *reinterpret_cast<u32x4*>(row + 8 * j) = v;
+}
+
+struct PrepareArgs {
+  NormRope q_nr, k_nr;
+  const uint16_t* index_qk;
+  int64_t index_token_stride;  // elements
+  int num_tokens;
+  const int64_t* positions;
+  int64_t position_stride;
+  uint16_t* index_q_out;  // [tokens, heads, dim]
+  int num_heads;
+  int dim;
+  // raw-key ring
+  uint16_t* state;
+  int64_t state_block_stride, state_token_stride;  // elements
+  int state_size;
+  int num_state_blocks;
+  const int64_t* state_slots;
+  const int32_t* state_table;
+  int64_t state_table_stride;
+  const int32_t* query_start_loc;
+  const int64_t* logical_positions;
+  int num_requests;
+  // compressed keys
+  uint16_t* comp;
+  int64_t comp_block_stride, comp_token_stride;
+  int comp_page;
+  int num_comp_blocks;
+  const int64_t* comp_slots;
+  const int32_t* k_work;
+  int num_k_work;
+  int ratio;
+  // main K/V
+  const uint16_t* mk;
+  int64_t mk_token, mk_head;
+  const uint16_t* mv;
+  int64_t mv_token, mv_head;
+  uint16_t* mkc;
+  int64_t mkc_block, mkc_token, mkc_head;
+  uint16_t* mvc;
+  int64_t mvc_block, mvc_token, mvc_head;
+  const int64_t* main_slots;
+  int main_page;
+  int num_main_blocks;
+  int main_heads;
+  int main_dim;
+  // block ranges of the roles
+  int k_blocks, q_blocks;
+};
+
+// Compression group `w` of request q (ops/prepare.py:120-174).
+__device__ void prepare_group(const PrepareArgs& a, int q, int w, int j) {
+  if (q < 0 || q >= a.num_requests) return;
+  const int qs = a.query_start_loc[q];
+  const int qe = a.query_start_loc[q + 1];
+  const int qlen = qe - qs;
+  if (qlen <= 0 || qs < 0 || qe > a.num_tokens) return;
+  const int64_t chunk_end = a.logical_positions[qe - 1];
+  const int64_t chunk_start = chunk_end - qlen + 1;
+  if (chunk_start < 0) return;
+  const int R = a.ratio;
+  const int64_t num_groups = (chunk_end + 1) / R - chunk_start / R;
+  const int key_off = a.num_heads * a.dim;
+  const int sblock = a.state_table[(int64_t)q * a.state_table_stride];
+  const bool ring_ok = sblock >= 0 && sblock < a.num_state_blocks;
+  const uint16_t* ring = a.state + (int64_t)(ring_ok ? sblock : 0) * a.state_block_stride;
+
+  if (w < num_groups) {
+    const int64_t first_boundary = ((chunk_start + R) / R) * R - 1;
+    const int64_t end_pos = first_boundary + (int64_t)w * R;
+    const int64_t boundary_token = qs + end_pos - chunk_start;
+    if (boundary_token >= qe) return;  // positions inconsistent with the chunk
+    const int64_t cslot = a.comp_slots[boundary_token];
+    float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    for (int m = 0; m < R; ++m) {
+      const int64_t src_pos = end_pos - (R - 1) + m;
+      const bool in_chunk = src_pos >= chunk_start;
+      const uint16_t* row =
+          in_chunk ? a.index_qk + (qs + src_pos - chunk_start) * a.index_token_stride + key_off
+                   : ring + (src_pos % a.state_size) * a.state_token_stride;
+      float v[8];
+      unpack8(load_row(row, j, a.dim, in_chunk || ring_ok), v);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) acc[i] += v[i];  // members in order, as the reference
+    }
+    float pooled[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) pooled[i] = round_bf16(__fdiv_rn(acc[i], (float)R));
+    const u32x4 out = norm_rope_row(a.k_nr, pack8(pooled), end_pos - (R - 1), j);
+    if (cslot >= 0 && cslot / a.comp_page < a.num_comp_blocks) {
+      uint16_t* dst = a.comp + (cslot / a.comp_page) * a.comp_block_stride +
+                      (cslot % a.comp_page) * a.comp_token_stride;
+      store_row(dst, j, a.dim, out);
+    }
+  }
+  if (w == 0) {
+    // Ring commit of the chunk's last raw keys, after this lane's ring reads
+    // above (the same lane reads and writes the same dims of a ring row).
+    const int suffix = min(qlen, a.state_size);
+    for (int off = 0; off < suffix; ++off) {
+      const int64_t token = qe - suffix + off;
+      const int64_t slot = a.state_slots[token];
+      if (slot < 0 || slot / a.state_size >= a.num_state_blocks) continue;
+      const u32x4 v = load_row(a.index_qk + token * a.index_token_stride + key_off, j, a.dim, true);
+      store_row(a.state + (slot / a.state_size) * a.state_block_stride +
+                    (slot % a.state_size) * a.state_token_stride,
+                j, a.dim, v);
+    }
+  }
+}
+
+__global__ __launch_bounds__(kPrepThreads) void prepare_kernel(const PrepareArgs a) {
+  const int j = threadIdx.x & (kGroupLanes - 1);
+  const int group = threadIdx.x / kGroupLanes;
+  int b = blockIdx.x;
+  if (b < a.k_blocks) {
+    const int item = b * kGroupsPerBlock + group;
+    const bool ok = item < a.num_k_work;
+    const int q = ok ? a.k_work[2 * item] : -1;
+    const int w = ok ? a.k_work[2 * item + 1] : 0;
+    prepare_group(a, q, w, j);
+    return;
+  }
+  b -= a.k_blocks;
+  if (b < a.q_blocks) {
+    const int64_t row = (int64_t)b * kGroupsPerBlock + group;  // token * heads + head
+    const bool ok = row < (int64_t)a.num_tokens * a.num_heads;
+    const int64_t token = ok ? row / a.num_heads : 0;
+    const int head = ok ? (int)(row % a.num_heads) : 0;
+    const u32x4 x =
+        load_row(a.index_qk + token * a.index_token_stride + (int64_t)head * a.dim, j, a.dim, ok);
+    const int64_t pos = a.positions[token * a.position_stride];
+    const u32x4 out = norm_rope_row(a.q_nr, x, pos, j);
+    if (ok) store_row(a.index_q_out + row * a.dim, j, a.dim, out);
+    return;
+  }
+  b -= a.q_blocks;
+  // Main K/V rows are already bf16 in their final coordinates (ops/prepare.py:74-95).
+  const int64_t item = (int64_t)b * kGroupsPerBlock + group;  // token * heads + head
+  if (item >= (int64_t)a.num_tokens * a.main_heads) return;
+  const int64_t token = item / a.main_heads;
+  const int head = (int)(item % a.main_heads);
+  const int64_t slot = a.main_slots[token];
+  if (slot < 0 || slot / a.main_page >= a.num_main_blocks) return;
+  const int64_t blk = slot / a.main_page, off = slot % a.main_page;
+  const u32x4 k = load_row(a.mk + token * a.mk_token + head * a.mk_head, j, a.main_dim, true);
+  const u32x4 v = load_row(a.mv + token * a.mv_token + head * a.mv_head, j, a.main_dim, true);
+  store_row(a.mkc + blk * a.mkc_block + off * a.mkc_token + head * a.mkc_head, j, a.main_dim, k);
+  store_row(a.mvc + blk * a.mvc_block + off * a.mvc_token + head * a.mvc_head, j, a.main_dim, v);
+}
+
+struct NormRopeArgs {
+  NormRope nr;
+  const uint16_t* values;
+  int64_t token_stride, head_stride;  // elements
+  int tokens, heads;
+  const int64_t* positions;
+  int64_t position_stride;
+  uint16_t* out;  // [tokens, heads, dim]
+};
+
+__global__ __launch_bounds__(kPrepThreads) void norm_rope_kernel(const NormRopeArgs a) {
+  const int j = threadIdx.x & (kGroupLanes - 1);
+  const int64_t row = (int64_t)blockIdx.x * kGroupsPerBlock + threadIdx.x / kGroupLanes;
+  const bool ok = row < (int64_t)a.tokens * a.heads;
+  const int64_t token = ok ? row / a.heads : 0;
+  const int head = ok ? (int)(row % a.heads) : 0;
+  const u32x4 x = load_row(a.values + token * a.token_stride + head * a.head_stride, j, a.nr.dim, ok);
+  const u32x4 out = norm_rope_row(a.nr, x, a.positions[token * a.position_stride], j);
+  if (ok) store_row(a.out + row * a.nr.dim, j, a.nr.dim, out);
+}
+
+int check_norm_rope(int dim, int rotary, int max_positions, const void* weight, const void* cos_sin,
+                    const char* name) {
+  if (dim != 64 && dim != 128)
+    return fail(QSA_ERR_UNSUPPORTED, std::string(name) + ": index head dim must be 64 or 128");
+  if (rotary < 0 || rotary > dim || rotary % 16)
+    return fail(QSA_ERR_UNSUPPORTED,
+                std::string(name) + ": rotary dim must be a multiple of 16 within the head dim");
+  if (!weight || (rotary > 0 && (!cos_sin || max_positions <= 0)))
+    return fail(QSA_ERR_INVALID, std::string(name) + ": null weight or rotary cache");
+  if (((uintptr_t)weight | (uintptr_t)cos_sin) & 15u)
+    return fail(QSA_ERR_INVALID, std::string(name) + ": weight and rotary cache must be 16-byte aligned");
+  return QSA_OK;
+}
+
+bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
+
+}  // namespace
+}  // namespace qsa
+
+using namespace qsa;
+
+extern "C" int qsa_indexer_prepare(
+    const void* index_qk, int64_t index_token_stride, int num_tokens, const int64_t* positions,
+    int64_t position_stride, const void* q_norm_weight, const void* k_norm_weight,
+    const void* cos_sin, int max_positions, float eps, void* index_q_out, void* state_cache,
+    int64_t state_block_stride, int64_t state_token_stride, int state_size, int num_state_blocks,
+    const int64_t* state_slots, const int32_t* state_table, int64_t state_table_stride,
+    const int32_t* query_start_loc, const int64_t* logical_positions, int num_requests,
+    void* compressed_cache, int64_t comp_block_stride, int64_t comp_token_stride,
+    int comp_page_size, int num_comp_blocks, const int64_t* compressed_slots,
+    const int32_t* k_work, int num_k_work, const void* main_key, int64_t main_key_token_stride,
+    int64_t main_key_head_stride, const void* main_value, int64_t main_value_token_stride,
+    int64_t main_value_head_stride, void* main_key_cache, int64_t main_key_cache_block_stride,
+    int64_t main_key_cache_token_stride, int64_t main_key_cache_head_stride,
+    void* main_value_cache, int64_t main_value_cache_block_stride,
+    int64_t main_value_cache_token_stride, int64_t main_value_cache_head_stride,
+    const int64_t* main_slots, int main_page_size, int num_main_blocks, int num_index_heads,
+    int index_head_dim, int rotary_dim, int compress_ratio, int main_kv_heads,
+    int main_head_dim, void* stream) {
+  const char* name = "qsa_indexer_prepare";
+  if (num_tokens < 0 || num_k_work < 0) return fail(QSA_ERR_INVALID, "qsa_indexer_prepare: negative size");
+  if (num_tokens == 0 && num_k_work == 0) return QSA_OK;
+  int st = check_norm_rope(index_head_dim, rotary_dim, max_positions, q_norm_weight, cos_sin, name);
+  if (st != QSA_OK) return st;
+  if (!k_norm_weight || !aligned16(k_norm_weight))
+    return fail(QSA_ERR_INVALID, "qsa_indexer_prepare: k_norm_weight must be a 16-byte aligned pointer");
+  if (num_index_heads <= 0 || compress_ratio <= 0 || state_size <= 0 || comp_page_size <= 0 ||
+      main_page_size <= 0 || main_kv_heads < 0)
+    return fail(QSA_ERR_INVALID, "qsa_indexer_prepare: bad head count, ratio or page size");
+  if (main_kv_heads > 0 && main_head_dim != 64 && main_head_dim != 128)
+    return fail(QSA_ERR_UNSUPPORTED, "qsa_indexer_prepare: main head dim must be 64 or 128");
+  if (!index_qk || !positions || !index_q_out ||
+      (num_k_work > 0 && (!state_cache || !state_slots || !state_table || !query_start_loc ||
+                          !logical_positions || !compressed_cache || !compressed_slots || !k_work)) ||
+      (main_kv_heads > 0 && num_tokens > 0 &&
+       (!main_key || !main_value || !main_key_cache || !main_value_cache || !main_slots)))
+    return fail(QSA_ERR_INVALID, "qsa_indexer_prepare: null tensor pointer");
+  if (!aligned16(index_qk) || !aligned16(index_q_out) || !aligned16(state_cache) ||
+      !aligned16(compressed_cache) || !aligned16(main_key) || !aligned16(main_value) ||
+      !aligned16(main_key_cache) || !aligned16(main_value_cache) ||
+      (index_token_stride | state_block_stride | state_token_stride | comp_block_stride |
+       comp_token_stride | main_key_token_stride | main_key_head_stride | main_value_token_stride |
+       main_value_head_stride | main_key_cache_block_stride | main_key_cache_token_stride |
+       main_key_cache_head_stride | main_value_cache_block_stride |
+       main_value_cache_token_stride | main_value_cache_head_stride) & 7)
+    return fail(QSA_ERR_INVALID,
+                "qsa_indexer_prepare: tensors must be 16-byte aligned with strides that are "
+                "multiples of 8 elements and unit dim stride");
+  PrepareArgs a = {};
+  a.q_nr = NormRope{static_cast<const uint16_t*>(q_norm_weight),
+                    static_cast<const uint16_t*>(cos_sin), max_positions, eps, index_head_dim,
+                    rotary_dim};
+  a.k_nr = a.q_nr;
+  a.k_nr.weight = static_cast<const uint16_t*>(k_norm_weight);
+  a.index_qk = static_cast<const uint16_t*>(index_qk);
+  a.index_token_stride = index_token_stride;
+  a.num_tokens = num_tokens;
+  a.positions = positions;
+  a.position_stride = position_stride;
+  a.index_q_out = static_cast<uint16_t*>(index_q_out);
+  a.num_heads = num_index_heads;
+  a.dim = index_head_dim;
+  a.state = static_cast<uint16_t*>(state_cache);
+  a.state_block_stride = state_block_stride;
+  a.state_token_stride = state_token_stride;
+  a.state_size = state_size;
+  a.num_state_blocks = num_state_blocks;
+  a.state_slots = state_slots;
+  a.state_table = state_table;
+  a.state_table_stride = state_table_stride;
+  a.query_start_loc = query_start_loc;
+  a.logical_positions = logical_positions;
+  a.num_requests = num_requests;
+  a.comp = static_cast<uint16_t*>(compressed_cache);
+  a.comp_block_stride = comp_block_stride;
+  a.comp_token_stride = comp_token_stride;
+  a.comp_page = comp_page_size;
+  a.num_comp_blocks = num_comp_blocks;
+  a.comp_slots = compressed_slots;
+  a.k_work = k_work;
+  a.num_k_work = num_k_work;
+  a.ratio = compress_ratio;
+  a.mk = static_cast<const uint16_t*>(main_key);
+  a.mk_token = main_key_token_stride;
+  a.mk_head = main_key_head_stride;
+  a.mv = static_cast<const uint16_t*>(main_value);
+  a.mv_token = main_value_token_stride;
+  a.mv_head = main_value_head_stride;
+  a.mkc = static_cast<uint16_t*>(main_key_cache);
+  a.mkc_block = main_key_cache_block_stride;
+  a.mkc_token = main_key_cache_token_stride;
+  a.mkc_head = main_key_cache_head_stride;
+  a.mvc = static_cast<uint16_t*>(main_value_cache);
+  a.mvc_block = main_value_cache_block_stride;
+  a.mvc_token = main_value_cache_token_stride;
+  a.mvc_head = main_value_cache_head_stride;
+  a.main_slots = main_slots;
+  a.main_page = main_page_size;
+  a.num_main_blocks = num_main_blocks;
+  a.main_heads = main_kv_heads;
+  a.main_dim = main_head_dim;
+  const int64_t k_blocks = ((int64_t)num_k_work + kGroupsPerBlock - 1) / kGroupsPerBlock;
+  const int64_t q_blocks = ((int64_t)num_tokens * num_index_heads + kGroupsPerBlock - 1) / kGroupsPerBlock;
+  const int64_t m_blocks = ((int64_t)num_tokens * main_kv_heads + kGroupsPerBlock - 1) / kGroupsPerBlock;
+  const int64_t blocks = k_blocks + q_blocks + m_blocks;
+  if (blocks > INT32_MAX) return fail(QSA_ERR_UNSUPPORTED, "qsa_indexer_prepare: grid too large");
+  if (num_tokens == 0 && num_k_work > 0)
+    return fail(QSA_ERR_INVALID, "qsa_indexer_prepare: compression work without tokens");
+  a.k_blocks = (int)k_blocks;
+  a.q_blocks = (int)q_blocks;
+  hipLaunchKernelGGL(prepare_kernel, dim3((unsigned)blocks), dim3(kPrepThreads), 0,
+                     static_cast<hipStream_t>(stream), a);
+  return check_launch("qsa_indexer_prepare launch");
+}
+
+extern "C" int qsa_indexer_norm_rope(const void* values, int64_t token_stride, int64_t head_stride,
+                                     int tokens, int heads, int dim, const void* weight,
+                                     const int64_t* positions, int64_t position_stride,
+                                     const void* cos_sin, int max_positions, float eps,
+                                     int rotary_dim, void* out, void* stream) {
+  const char* name = "qsa_indexer_norm_rope";
+  if (tokens < 0 || heads < 0) return fail(QSA_ERR_INVALID, "qsa_indexer_norm_rope: negative size");
+  if (tokens == 0 || heads == 0) return QSA_OK;
+  int st = check_norm_rope(dim, rotary_dim, max_positions, weight, cos_sin, name);
+  if (st != QSA_OK) return st;
+  if (!values || !positions || !out) return fail(QSA_ERR_INVALID, "qsa_indexer_norm_rope: null tensor pointer");
+  if (!aligned16(values) || !aligned16(out) || ((token_stride | head_stride) & 7))
+    return fail(QSA_ERR_INVALID,
+                "qsa_indexer_norm_rope: values and out must be 16-byte aligned with strides that "
+                "are multiples of 8 elements and unit dim stride");
+  const int64_t blocks = ((int64_t)tokens * heads + kGroupsPerBlock - 1) / kGroupsPerBlock;
+  if (blocks > INT32_MAX) return fail(QSA_ERR_UNSUPPORTED, "qsa_indexer_norm_rope: grid too large");
+  NormRopeArgs a;
+  a.nr = NormRope{static_cast<const uint16_t*>(weight), static_cast<const uint16_t*>(cos_sin),
+                  max_positions, eps, dim, rotary_dim};
+  a.values = static_cast<const uint16_t*>(values);
+  a.token_stride = token_stride;
+  a.head_stride = head_stride;
+  a.tokens = tokens;
+  a.heads = heads;
+  a.positions = positions;
+  a.position_stride = position_stride;
+  a.out = static_cast<uint16_t*>(out);
+  hipLaunchKernelGGL(norm_rope_kernel, dim3((unsigned)blocks), dim3(kPrepThreads), 0,
+                     static_cast<hipStream_t>(stream), a);
+  return check_launch("qsa_indexer_norm_rope launch");
+}

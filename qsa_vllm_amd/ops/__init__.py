@@ -1,14 +1,20 @@
 """gfx950 HIP operators of the QSA sparse-attention path (reference ``yulan_qsa_vllm/ops``)."""
 
 from .indexer import qsa_select_paged_decode, qsa_select_paged_prefill, select_paged_tokens
+from .normalization import IndexerRMSNorm, indexer_norm_rope, rotary_cache
+from .prepare import qsa_prepare
 from .qsa import qsa_select_paged_tokens, qsa_sparse_paged_attention
 from .topk import topk, topk_expand
 
 __all__ = [
+    "IndexerRMSNorm",
+    "indexer_norm_rope",
+    "qsa_prepare",
     "qsa_select_paged_decode",
     "qsa_select_paged_prefill",
     "qsa_select_paged_tokens",
     "qsa_sparse_paged_attention",
+    "rotary_cache",
     "select_paged_tokens",
     "topk",
     "topk_expand",

@@ -26,6 +26,17 @@ _SCHEMAS = {
         "Tensor token_to_req, Tensor table, Tensor(a!) output, Tensor(b!) counts, "
         "int ratio, int page_size, bool physical, bool store_counts) -> ()"),
     # New ops of this build.
+    "indexer_prepare": (
+        "indexer_prepare(Tensor index_qk, Tensor positions, Tensor q_norm_weight, "
+        "Tensor k_norm_weight, Tensor cos_sin, float eps, Tensor(a!) index_q_out, "
+        "Tensor(b!) state_cache, Tensor state_slots, Tensor state_table, Tensor query_start_loc, "
+        "Tensor logical_positions, Tensor(c!) compressed_cache, Tensor compressed_slots, "
+        "Tensor k_work, Tensor main_key, Tensor main_value, Tensor(d!) main_key_cache, "
+        "Tensor(e!) main_value_cache, Tensor main_slots, int num_index_heads, "
+        "int index_head_dim, int rotary_dim, int compress_ratio) -> ()"),
+    "indexer_norm_rope": (
+        "indexer_norm_rope(Tensor values, Tensor weight, Tensor positions, Tensor cos_sin, "
+        "float eps, int rotary_dim, Tensor(a!) out) -> ()"),
     "indexer_decode": (
         "indexer_decode(Tensor q, Tensor k_cache, Tensor page_table, Tensor visible, "
         "Tensor(a!) logits, int decode_query_len) -> ()"),
@@ -157,6 +168,127 @@ def _topk_expand_impl(scores, lengths, positions, sequence_lengths, token_to_req
 
 
 # --- indexer ----------------------------------------------------------------
+
+# --- indexer preparation ------------------------------------------------------
+
+def _bf16_vec(t, n, name):
+    _dtype(t, torch.bfloat16, name)
+    _require(t.dim() == 1 and t.numel() == n and (n <= 1 or t.stride(0) == 1),
+             f"{name} must be a contiguous [{n}] vector")
+
+
+def _rotary_cache(cos_sin, rotary_dim, name="cos_sin"):
+    _dtype(cos_sin, torch.bfloat16, name)
+    _require(cos_sin.dim() == 2 and cos_sin.size(1) == rotary_dim and cos_sin.is_contiguous(),
+             f"{name} must be a contiguous [positions, rotary_dim] tensor")
+
+
+def _positions(t, n, name):
+    _dtype(t, torch.int64, name)
+    _require(t.dim() == 1 and t.numel() >= n, f"{name} must be 1-D with at least {n} entries")
+
+
+def _unit_dim(t, name, dims):
+    _dtype(t, torch.bfloat16, name)
+    _require(t.dim() == dims and t.stride(-1) == 1, f"{name} must be {dims}-D with unit dim stride")
+
+
+def _indexer_prepare_impl(index_qk, positions, q_norm_weight, k_norm_weight, cos_sin, eps,
+                          index_q_out, state_cache, state_slots, state_table, query_start_loc,
+                          logical_positions, compressed_cache, compressed_slots, k_work,
+                          main_key, main_value, main_key_cache, main_value_cache, main_slots,
+                          num_index_heads, index_head_dim, rotary_dim, compress_ratio):
+    dev = _on_gpu(index_qk, positions, q_norm_weight, k_norm_weight, cos_sin, index_q_out,
+                  state_cache, state_slots, state_table, query_start_loc, logical_positions,
+                  compressed_cache, compressed_slots, k_work, main_key, main_value,
+                  main_key_cache, main_value_cache, main_slots)
+    tokens = index_qk.size(0)
+    heads, dim = int(num_index_heads), int(index_head_dim)
+    _unit_dim(index_qk, "index_qk", 2)
+    _require(index_qk.size(1) >= (heads + 1) * dim, "index_qk must hold (heads + 1) * dim columns")
+    _positions(positions, tokens, "positions")
+    _bf16_vec(q_norm_weight, dim, "q_norm_weight")
+    _bf16_vec(k_norm_weight, dim, "k_norm_weight")
+    _rotary_cache(cos_sin, rotary_dim)
+    _dtype(index_q_out, torch.bfloat16, "index_q_out")
+    _require(index_q_out.is_contiguous() and index_q_out.numel() == tokens * heads * dim,
+             "index_q_out must be a contiguous [tokens, heads, dim] tensor")
+    for t, name in ((state_cache, "state_cache"), (compressed_cache, "compressed_cache")):
+        _dtype(t, torch.bfloat16, name)
+        _require(t.dim() in (3, 4) and t.stride(-1) == 1 and t.size(-1) == dim
+                 and (t.dim() == 3 or t.size(2) == 1),
+                 f"{name} must be [blocks, page, (1,) dim] with unit dim stride")
+    for t, name in ((state_slots, "state_slots"), (compressed_slots, "compressed_slots"),
+                    (main_slots, "main_slots")):
+        _positions(t, tokens, name)
+        _require(t.numel() <= 1 or t.stride(0) == 1, f"{name} must be contiguous")
+    _positions(logical_positions, tokens, "logical_positions")
+    _require(logical_positions.numel() <= 1 or logical_positions.stride(0) == 1,
+             "logical_positions must be contiguous")
+    _dtype(state_table, torch.int32, "state_table")
+    _require(state_table.dim() == 2, "state_table must be [requests, width]")
+    _vector(query_start_loc, torch.int32, "query_start_loc")
+    num_requests = query_start_loc.numel() - 1
+    _require(state_table.size(0) >= num_requests, "state_table has fewer rows than requests")
+    _dtype(k_work, torch.int32, "k_work")
+    _require(k_work.dim() == 2 and k_work.size(1) == 2 and k_work.is_contiguous(),
+             "k_work must be a contiguous [items, 2] tensor")
+    _unit_dim(main_key, "main_key", 3)
+    _unit_dim(main_value, "main_value", 3)
+    _unit_dim(main_key_cache, "main_key_cache", 4)
+    _unit_dim(main_value_cache, "main_value_cache", 4)
+    kv_heads, main_dim = main_key.size(1), main_key.size(2)
+    _require(tuple(main_value.shape) == (tokens, kv_heads, main_dim) and main_key.size(0) == tokens,
+             "main_key / main_value must be [tokens, kv_heads, dim]")
+    _require(main_key_cache.shape == main_value_cache.shape
+             and main_key_cache.size(2) == kv_heads and main_key_cache.size(3) == main_dim,
+             "main caches must be [blocks, page, kv_heads, dim] matching main_key")
+    if tokens == 0 and k_work.size(0) == 0:
+        return
+    with torch.cuda.device(dev):
+        _lib.call("qsa_indexer_prepare",
+                  _ptr(index_qk), _stride(index_qk, 0), tokens,
+                  _ptr(positions), _stride(positions, 0),
+                  _ptr(q_norm_weight), _ptr(k_norm_weight),
+                  _ptr(cos_sin), cos_sin.size(0), ctypes.c_float(eps),
+                  _ptr(index_q_out),
+                  _ptr(state_cache), _stride(state_cache, 0),
+                  _stride(state_cache, 1), state_cache.size(1), state_cache.size(0),
+                  _ptr(state_slots), _ptr(state_table),
+                  _stride(state_table, 0), _ptr(query_start_loc),
+                  _ptr(logical_positions), num_requests,
+                  _ptr(compressed_cache), _stride(compressed_cache, 0),
+                  _stride(compressed_cache, 1), compressed_cache.size(1), compressed_cache.size(0),
+                  _ptr(compressed_slots), _ptr(k_work), k_work.size(0),
+                  _ptr(main_key), _stride(main_key, 0), _stride(main_key, 1),
+                  _ptr(main_value), _stride(main_value, 0), _stride(main_value, 1),
+                  _ptr(main_key_cache), _stride(main_key_cache, 0), _stride(main_key_cache, 1),
+                  _stride(main_key_cache, 2),
+                  _ptr(main_value_cache), _stride(main_value_cache, 0),
+                  _stride(main_value_cache, 1), _stride(main_value_cache, 2),
+                  _ptr(main_slots), main_key_cache.size(1), main_key_cache.size(0),
+                  heads, dim, int(rotary_dim), int(compress_ratio), kv_heads, main_dim,
+                  _stream(dev))
+
+
+def _indexer_norm_rope_impl(values, weight, positions, cos_sin, eps, rotary_dim, out):
+    dev = _on_gpu(values, weight, positions, cos_sin, out)
+    _unit_dim(values, "values", 3)
+    tokens, heads, dim = values.shape
+    _bf16_vec(weight, dim, "weight")
+    _positions(positions, tokens, "positions")
+    _rotary_cache(cos_sin, rotary_dim)
+    _dtype(out, torch.bfloat16, "out")
+    _require(out.is_contiguous() and tuple(out.shape) == (tokens, heads, dim),
+             "out must be a contiguous tensor shaped like values")
+    if tokens == 0 or heads == 0:
+        return
+    with torch.cuda.device(dev):
+        _lib.call("qsa_indexer_norm_rope", _ptr(values), _stride(values, 0), _stride(values, 1),
+                  tokens, heads, dim, _ptr(weight), _ptr(positions), _stride(positions, 0),
+                  _ptr(cos_sin), cos_sin.size(0), ctypes.c_float(eps), int(rotary_dim),
+                  _ptr(out), _stream(dev))
+
 
 def _cache_strides(k_cache, name):
     _dtype(k_cache, torch.bfloat16, name)
@@ -309,6 +441,8 @@ _IMPLS = {
     "indexer_prefill": _indexer_prefill_impl,
     "sparse_attention": _sparse_attention_impl,
     "sparse_attention_merge": _sparse_attention_merge_impl,
+    "indexer_prepare": _indexer_prepare_impl,
+    "indexer_norm_rope": _indexer_norm_rope_impl,
 }
 
 _library = None

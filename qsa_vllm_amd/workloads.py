@@ -264,3 +264,183 @@ def indexer_bytes(wl: QSAWorkload) -> int:
 def indexer_flops(wl: QSAWorkload) -> int:
     s = wl.shape
     return 2 * s.index_heads * s.index_dim * int(wl.visible.to(torch.int64).sum())
+
+
+# --- indexer preparation inputs ------------------------------------------------
+
+
+@dataclass
+class PrepareCase:
+    """Inputs of one qsa_prepare call (ops/prepare.py:177-225) with the metadata
+    its kernel reads (the upstream builder that makes it in serving is not part
+    of the plugin): a ring of ``state_size`` raw keys per request, compressed
+    cache pages, main K/V rows and their cache, ``k_work`` items."""
+
+    index_qk: torch.Tensor            # [tokens, (heads + 1) * dim] view, projection row stride
+    positions: torch.Tensor           # int64 [tokens]
+    q_norm_weight: torch.Tensor
+    k_norm_weight: torch.Tensor
+    cos_sin: torch.Tensor             # bf16 [max_positions, rotary]
+    eps: float
+    raw: object                       # slot_mapping, block_table, query_start_loc, logical_positions
+    comp: object                      # slot_mapping, k_work_metadata
+    state_cache: torch.Tensor         # [blocks, state_size, dim]
+    compressed_cache: torch.Tensor    # [blocks, comp_page, 1, dim]
+    main_key: torch.Tensor            # [tokens, kv_heads, main_dim] view
+    main_value: torch.Tensor
+    main_key_cache: torch.Tensor      # [blocks, page, kv_heads, main_dim] views of main_kv
+    main_value_cache: torch.Tensor
+    main_slots: torch.Tensor          # int64 [tokens]
+    num_index_heads: int
+    index_head_dim: int
+    rotary_dim: int
+    compress_ratio: int
+    num_groups: int                   # compression groups closed by this step
+    chunk_lens: list                  # new tokens per request
+    main_kv: torch.Tensor             # the K|V cache allocation [blocks, page, kv_heads, 2 * dim]
+
+    def call_args(self):
+        """Positional and keyword arguments of qsa_prepare (both signatures)."""
+        args = (self.index_qk, self.positions, self.q_norm_weight, self.k_norm_weight,
+                self.cos_sin, self.eps, self.raw, self.comp, self.state_cache,
+                self.compressed_cache, self.main_key, self.main_value, self.main_key_cache,
+                self.main_value_cache, self.main_slots)
+        kwargs = dict(num_index_heads=self.num_index_heads, index_head_dim=self.index_head_dim,
+                      rotary_dim=self.rotary_dim, compress_ratio=self.compress_ratio)
+        return args, kwargs
+
+    def clone_outputs(self):
+        """Copies of the tensors qsa_prepare writes (to run it twice from one state)."""
+        return {"state_cache": self.state_cache.clone(),
+                "compressed_cache": self.compressed_cache.clone(),
+                "main_kv": self.main_kv.clone()}
+
+    def prepare_bytes(self) -> int:
+        """Algorithmic HBM bytes of one call: every byte read and written once
+        (queries, raw keys of the closed groups and ring members, ring commits,
+        main K/V rows, the rotary rows of the tokens, gammas)."""
+        tokens = self.index_qk.shape[0]
+        h, d, r = self.num_index_heads, self.index_head_dim, self.compress_ratio
+        kvh, md = self.main_key.shape[1], self.main_key.shape[2]
+        row = d * 2
+        q = tokens * h * row * 2
+        groups = self.num_groups * (r * row + row)
+        ring = sum(min(c, self.state_cache.shape[1]) for c in self.chunk_lens) * row * 2
+        main = int((self.main_slots >= 0).sum()) * kvh * md * 2 * 2 * 2
+        rope = tokens * self.rotary_dim * 2
+        return q + groups + ring + main + rope + 2 * row
+
+
+def make_prepare_case(prefix_lens, chunk_lens, *, num_index_heads=32, index_head_dim=128,
+                      compress_ratio=16, state_size=None, comp_page=16, main_kv_heads=2,
+                      main_head_dim=128, main_page=16, rotary_dim=64, theta=1.0e7, eps=1.0e-6,
+                      projection_pad=64, work_pad=3, drop_slot_every=0, device="cpu",
+                      seed=0) -> PrepareCase:
+    """Request q has prefix_lens[q] cached tokens and appends chunk_lens[q]
+    tokens at positions prefix .. prefix + chunk - 1. index_qk, main_key and
+    main_value are column slices of one projection row (as the fused QKV +
+    indexer GEMM output), the ring of each request holds random raw keys of
+    its earlier positions, and every slot table is a seeded permutation.
+    drop_slot_every > 0 sets every n-th slot of each mapping to -1."""
+    from .ops.normalization import rotary_cache
+
+    gen = torch.Generator(device="cpu").manual_seed(seed)
+    R = compress_ratio
+    S = state_size or R
+    H, D = num_index_heads, index_head_dim
+    prefix = [int(p) for p in prefix_lens]
+    chunks = [int(c) for c in chunk_lens]
+    nreq = len(chunks)
+    tokens = sum(chunks)
+    qsl = [0]
+    for c in chunks:
+        qsl.append(qsl[-1] + c)
+    logical = torch.cat([torch.arange(p, p + c, dtype=torch.int64) for p, c in zip(prefix, chunks)]
+                        ) if tokens else torch.zeros(0, dtype=torch.int64)
+    req_of = torch.repeat_interleave(torch.arange(nreq), torch.tensor(chunks)) if tokens else \
+        torch.zeros(0, dtype=torch.int64)
+    max_pos = max((p + c for p, c in zip(prefix, chunks)), default=1) + 1
+
+    # One fused projection row: [main q | main k | main v | index q heads | index k | pad].
+    main_cols = main_kv_heads * main_head_dim
+    idx_cols = (H + 1) * D
+    cols = main_cols * 2 + idx_cols + projection_pad
+    proj = (torch.randn(tokens, cols, generator=gen) * 0.5).to(torch.bfloat16)
+    main_key = proj[:, :main_cols].view(tokens, main_kv_heads, main_head_dim)
+    main_value = proj[:, main_cols:2 * main_cols].view(tokens, main_kv_heads, main_head_dim)
+    index_qk = proj[:, 2 * main_cols:2 * main_cols + idx_cols]
+
+    def drop(mapping):
+        if drop_slot_every > 0:
+            mapping[::drop_slot_every] = -1
+        return mapping
+
+    # Ring: one block per request (permuted), random earlier raw keys.
+    ring_blocks = torch.randperm(nreq + 2, generator=gen)[:nreq].to(torch.int32)
+    state_cache = (torch.randn(nreq + 2, S, D, generator=gen) * 0.5).to(torch.bfloat16)
+    state_table = ring_blocks.view(nreq, 1).clone()
+    state_slots = (ring_blocks.to(torch.int64)[req_of] * S + logical % S) if tokens else \
+        torch.zeros(0, dtype=torch.int64)
+
+    # Compressed cache pages for every group up to the end of each chunk.
+    groups_total = [(p + c) // R for p, c in zip(prefix, chunks)]
+    pages = [max(1, (g + comp_page - 1) // comp_page) for g in groups_total]
+    comp_blocks = sum(pages) + 1
+    perm = torch.randperm(comp_blocks, generator=gen).to(torch.int32)
+    comp_table, at = [], 0
+    for n in pages:
+        comp_table.append(perm[at:at + n].tolist())
+        at += n
+    compressed_cache = torch.zeros(comp_blocks, comp_page, 1, D, dtype=torch.bfloat16)
+    comp_slots = torch.full((tokens,), -1, dtype=torch.int64)
+    items, closed = [], 0
+    for q in range(nreq):
+        chunk_start, chunk_end = prefix[q], prefix[q] + chunks[q] - 1
+        n_groups = (chunk_end + 1) // R - chunk_start // R if chunks[q] else 0
+        closed += max(n_groups, 0)
+        for t in range(qsl[q], qsl[q + 1]):
+            pos = int(logical[t])
+            if (pos + 1) % R == 0:
+                g = (pos + 1) // R - 1
+                comp_slots[t] = comp_table[q][g // comp_page] * comp_page + g % comp_page
+        if chunks[q]:
+            items += [(q, w) for w in range(max(n_groups, 1))]
+    perm_items = torch.randperm(len(items), generator=gen).tolist()
+    items = [items[i] for i in perm_items] + [(-1, 0)] * work_pad
+    k_work = torch.tensor(items, dtype=torch.int32).view(-1, 2)
+
+    # Main cache: K|V interleaved per (token, kv head) row, permuted pages.
+    main_blocks = max(1, (tokens + main_page - 1) // main_page) + 2
+    kv = torch.zeros(main_blocks, main_page, main_kv_heads, 2 * main_head_dim, dtype=torch.bfloat16)
+    main_key_cache, main_value_cache = kv[..., :main_head_dim], kv[..., main_head_dim:]
+    slot_perm = torch.randperm(main_blocks * main_page, generator=gen)[:tokens]
+    main_slots = slot_perm.to(torch.int64)
+
+    q_w = (1.0 + 0.25 * torch.randn(D, generator=gen)).to(torch.bfloat16)
+    k_w = (1.0 + 0.25 * torch.randn(D, generator=gen)).to(torch.bfloat16)
+    cos_sin = rotary_cache(max_pos, rotary_dim, float(theta), "cpu") if rotary_dim else \
+        torch.zeros(max_pos, 0, dtype=torch.bfloat16)
+
+    from types import SimpleNamespace
+    dev = torch.device(device)
+
+    def to(t):
+        return t.to(dev)
+
+    # Move whole allocations so the views keep their strides.
+    proj_d = to(proj)
+    kv_d = to(kv)
+    raw = SimpleNamespace(slot_mapping=to(drop(state_slots.clone())), block_table=to(state_table),
+                          query_start_loc=to(torch.tensor(qsl, dtype=torch.int32)),
+                          logical_positions=to(logical))
+    comp = SimpleNamespace(slot_mapping=to(drop(comp_slots.clone())), k_work_metadata=to(k_work))
+    return PrepareCase(
+        index_qk=proj_d[:, 2 * main_cols:2 * main_cols + idx_cols],
+        positions=to(logical.clone()), q_norm_weight=to(q_w), k_norm_weight=to(k_w),
+        cos_sin=to(cos_sin.contiguous()), eps=float(eps), raw=raw, comp=comp,
+        state_cache=to(state_cache), compressed_cache=to(compressed_cache),
+        main_key=proj_d[:, :main_cols].view(tokens, main_kv_heads, main_head_dim),
+        main_value=proj_d[:, main_cols:2 * main_cols].view(tokens, main_kv_heads, main_head_dim),
+        main_key_cache=kv_d[..., :main_head_dim], main_value_cache=kv_d[..., main_head_dim:],
+        main_slots=to(drop(main_slots.clone())), num_index_heads=H, index_head_dim=D,
+        rotary_dim=rotary_dim, compress_ratio=R, num_groups=closed, chunk_lens=chunks, main_kv=kv_d)

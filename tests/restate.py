@@ -90,3 +90,73 @@ def softmax_attend(q_vec, keys, values):
     w = [math.exp(s - m) for s in scores]
     z = sum(w)
     return [sum(w[t] * values[t][d] for t in range(len(keys))) / z for d in range(dim)]
+
+
+# --- indexer preparation (scalar statement with emulated fp32 / bf16 rounding) ---
+
+def f32(x):
+    """Nearest fp32 (ties to even) of a Python float."""
+    import struct
+    return struct.unpack("<f", struct.pack("<f", x))[0]
+
+
+def bf16(x):
+    """Nearest bf16 (ties to even) of an fp32 value, by bit arithmetic."""
+    import struct
+    bits = struct.unpack("<I", struct.pack("<f", x))[0]
+    bits = (bits + 0x7FFF + ((bits >> 16) & 1)) & 0xFFFF0000
+    return struct.unpack("<f", struct.pack("<I", bits))[0]
+
+
+def norm_rope_row(x, pos, gamma, table, eps, rotary):
+    """One row: x and gamma lists of bf16 values, table a list of [cos..., sin...]
+    rows (bf16 values). Every fp32 operation is one double operation on fp32
+    operands (exact at these sizes) rounded by f32."""
+    dim = len(x)
+    ss = math.fsum(v * v for v in x)
+    inv = f32(1.0 / math.sqrt(f32(f32(f32(ss) / dim) + f32(eps))))
+    scaled = [bf16(f32(bf16(f32(v * inv)) * g)) for v, g in zip(x, gamma)]
+    out = list(scaled)
+    if rotary:
+        half = rotary // 2
+        row = table[pos] if 0 <= pos < len(table) else [0.0] * rotary
+        for d in range(rotary):
+            c = d % half
+            if d < half:
+                rotated = -scaled[d + half]
+            else:
+                rotated = scaled[d - half]
+            a = bf16(f32(scaled[d] * row[c]))
+            b = bf16(f32(rotated * row[half + c]))
+            out[d] = bf16(f32(a + b))
+    return out
+
+
+def prepare_request(chunk_positions, chunk_keys, ring, ratio, state_size, k_gamma, table, eps,
+                    rotary):
+    """One request's compression groups and ring after a chunk.
+
+    chunk_positions: consecutive positions of the chunk's tokens; chunk_keys:
+    their raw keys; ring: {slot: key} of the ring before the chunk (slot =
+    position % state_size). Walks the chunk's positions and closes a group at
+    every position p with (p + 1) % ratio == 0; its members are positions
+    p - ratio + 1 .. p, read from the chunk or else from the ring. Returns
+    ({p: normalised pooled key}, ring after committing the chunk's last
+    min(len, state_size) keys)."""
+    raw = dict(zip(chunk_positions, chunk_keys))
+    groups = {}
+    for p in chunk_positions:
+        if (p + 1) % ratio:
+            continue
+        members = []
+        for q in range(p - ratio + 1, p + 1):
+            members.append(raw[q] if q in raw else ring.get(q % state_size, [0.0] * len(k_gamma)))
+        acc = [0.0] * len(k_gamma)
+        for key in members:
+            acc = [f32(a + v) for a, v in zip(acc, key)]
+        pooled = [bf16(f32(a / ratio)) for a in acc]
+        groups[p] = norm_rope_row(pooled, p - ratio + 1, k_gamma, table, eps, rotary)
+    after = dict(ring)
+    for p in chunk_positions[-state_size:]:
+        after[p % state_size] = raw[p]
+    return groups, after
