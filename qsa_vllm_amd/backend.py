@@ -13,11 +13,12 @@ them:
   (``backend.py:148-153``).
 * :class:`YuLanQSAImpl` — zero the output, then sparse attention with the
   decode flags taken from ``max_query_len`` (``backend.py:24-68``).
-* :class:`QSACompressedMetadata` and :func:`select_for_layer` — the indexer's
-  selection call with the main block table and counts passed only in uniform
-  decode (``attention.py:116-142``, ``:191-214``).
-* :func:`run_qsa` — ``_run_qsa`` minus the index-q/key preparation, which sits
-  before this path.
+* :class:`QSACompressedMetadata`, :class:`QSARawMetadata`,
+  :class:`YuLanQSAIndexer` and :func:`select_for_layer` — the indexer: index
+  query/key preparation and cache writes, then the selection call with the
+  main block table and counts passed only in uniform decode
+  (``attention.py:79-142``, ``:191-214``).
+* :func:`run_qsa` — ``_run_qsa`` from the prepared index query on.
 
 The compressed-cache metadata is produced upstream in vLLM's QSA cache
 builder, whose source is not part of the plugin; its fields here follow what
@@ -31,6 +32,8 @@ from dataclasses import dataclass
 import torch
 
 from .ops.indexer import select_paged_tokens as qsa_select_paged_tokens  # attention.py:21
+from .ops.normalization import IndexerRMSNorm, rotary_cache
+from .ops.prepare import qsa_prepare
 from .ops.qsa import qsa_sparse_paged_attention
 
 
@@ -59,6 +62,59 @@ class QSACompressedMetadata:
     num_decode_tokens: int
     decode_query_len: int = 1
     visible_blocks: torch.Tensor | None = None
+    slot_mapping: torch.Tensor | None = None      # qsa_prepare: compressed slot per token
+    k_work_metadata: torch.Tensor | None = None   # qsa_prepare: (request, group) items
+
+
+@dataclass
+class QSARawMetadata:
+    """Raw-key ring metadata ``qsa_prepare`` reads (``ops/prepare.py:208-209``)."""
+
+    slot_mapping: torch.Tensor
+    block_table: torch.Tensor
+    query_start_loc: torch.Tensor
+    logical_positions: torch.Tensor
+
+
+class YuLanQSAIndexer:
+    """The replicated indexer of a QSA layer (``attention.py:79-142``): index-q
+    and compressed-key RMSNorm gammas, the rotary table, the raw-key ring and
+    the compressed-key cache. ``forward`` prepares (norm + RoPE, compression
+    groups, ring commit, main K/V writes) and selects."""
+
+    def __init__(self, num_heads: int, head_dim: int, compress_ratio: int, token_topk: int,
+                 rotary_dim: int, rope_theta: float, eps: float, max_position: int,
+                 raw_key_cache: torch.Tensor, compressed_key_cache: torch.Tensor):
+        self.num_heads = num_heads
+        self.head_dim = head_dim
+        self.compress_ratio = compress_ratio
+        self.token_topk = token_topk
+        self.rotary_dim = rotary_dim
+        device = compressed_key_cache.device
+        self.q_layernorm = IndexerRMSNorm(head_dim, eps).to(device)
+        self.k_layernorm = IndexerRMSNorm(head_dim, eps).to(device)
+        self.cos_sin_cache = rotary_cache(max_position, rotary_dim, float(rope_theta), device)
+        self.raw_key_cache = raw_key_cache
+        self.compressed_key_cache = compressed_key_cache
+
+    @property
+    def output_width(self):
+        return self.token_topk + self.compress_ratio - 1
+
+    def forward(self, projected, positions, raw_metadata, compressed_metadata, out,
+                main_key, main_value, main_key_cache, main_value_cache, main_slots,
+                *, main_block_table=None, valid_counts_out=None):
+        query = qsa_prepare(
+            projected, positions, self.q_layernorm.weight, self.k_layernorm.weight,
+            self.cos_sin_cache, self.q_layernorm.variance_epsilon, raw_metadata,
+            compressed_metadata, self.raw_key_cache, self.compressed_key_cache, main_key,
+            main_value, main_key_cache, main_value_cache, main_slots,
+            num_index_heads=self.num_heads, index_head_dim=self.head_dim,
+            rotary_dim=self.rotary_dim, compress_ratio=self.compress_ratio)
+        return select_for_layer(query, self.compressed_key_cache, compressed_metadata, out,
+                                self.token_topk, self.compress_ratio, main_key_cache,
+                                main_block_table=main_block_table,
+                                valid_counts_out=valid_counts_out)
 
 
 def canonicalize_singleton_dim_strides(t: torch.Tensor) -> torch.Tensor:

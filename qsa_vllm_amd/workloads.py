@@ -298,6 +298,10 @@ class PrepareCase:
     num_groups: int                   # compression groups closed by this step
     chunk_lens: list                  # new tokens per request
     main_kv: torch.Tensor             # the K|V cache allocation [blocks, page, kv_heads, 2 * dim]
+    main_block_table: torch.Tensor    # int32 [requests, pages], -1 past each sequence
+    comp_table: torch.Tensor          # int32 [requests, pages] of the compressed cache
+    seq_lens: torch.Tensor            # int32 [requests]: prefix + chunk
+    token_to_req: torch.Tensor        # int32 [tokens]
 
     def call_args(self):
         """Positional and keyword arguments of qsa_prepare (both signatures)."""
@@ -339,9 +343,11 @@ def make_prepare_case(prefix_lens, chunk_lens, *, num_index_heads=32, index_head
     """Request q has prefix_lens[q] cached tokens and appends chunk_lens[q]
     tokens at positions prefix .. prefix + chunk - 1. index_qk, main_key and
     main_value are column slices of one projection row (as the fused QKV +
-    indexer GEMM output), the ring of each request holds random raw keys of
-    its earlier positions, and every slot table is a seeded permutation.
-    drop_slot_every > 0 sets every n-th slot of each mapping to -1."""
+    indexer GEMM output); the ring of each request holds random raw keys of
+    its earlier positions, the compressed cache random keys of its earlier
+    groups and the main cache random K/V of its earlier positions, all behind
+    seeded permuted page tables. drop_slot_every > 0 sets every n-th slot of
+    each mapping to -1."""
     from .ops.normalization import rotary_cache
 
     gen = torch.Generator(device="cpu").manual_seed(seed)
@@ -382,7 +388,8 @@ def make_prepare_case(prefix_lens, chunk_lens, *, num_index_heads=32, index_head
     state_slots = (ring_blocks.to(torch.int64)[req_of] * S + logical % S) if tokens else \
         torch.zeros(0, dtype=torch.int64)
 
-    # Compressed cache pages for every group up to the end of each chunk.
+    # Compressed cache pages for every group up to the end of each chunk; the
+    # groups closed before the chunk hold earlier normalised keys.
     groups_total = [(p + c) // R for p, c in zip(prefix, chunks)]
     pages = [max(1, (g + comp_page - 1) // comp_page) for g in groups_total]
     comp_blocks = sum(pages) + 1
@@ -392,6 +399,10 @@ def make_prepare_case(prefix_lens, chunk_lens, *, num_index_heads=32, index_head
         comp_table.append(perm[at:at + n].tolist())
         at += n
     compressed_cache = torch.zeros(comp_blocks, comp_page, 1, D, dtype=torch.bfloat16)
+    for q in range(nreq):
+        for g_ in range(prefix[q] // R):
+            compressed_cache[comp_table[q][g_ // comp_page], g_ % comp_page, 0] = (
+                torch.randn(D, generator=gen) * 0.5).to(torch.bfloat16)
     comp_slots = torch.full((tokens,), -1, dtype=torch.int64)
     items, closed = [], 0
     for q in range(nreq):
@@ -409,12 +420,26 @@ def make_prepare_case(prefix_lens, chunk_lens, *, num_index_heads=32, index_head
     items = [items[i] for i in perm_items] + [(-1, 0)] * work_pad
     k_work = torch.tensor(items, dtype=torch.int32).view(-1, 2)
 
-    # Main cache: K|V interleaved per (token, kv head) row, permuted pages.
-    main_blocks = max(1, (tokens + main_page - 1) // main_page) + 2
-    kv = torch.zeros(main_blocks, main_page, main_kv_heads, 2 * main_head_dim, dtype=torch.bfloat16)
-    main_key_cache, main_value_cache = kv[..., :main_head_dim], kv[..., main_head_dim:]
-    slot_perm = torch.randperm(main_blocks * main_page, generator=gen)[:tokens]
-    main_slots = slot_perm.to(torch.int64)
+    # Main cache: K|V interleaved per (token, kv head) row, permuted pages
+    # holding every position of each sequence (earlier ones random); this
+    # step's tokens go to their block-table slots.
+    main_pages = [max(1, (p + c + main_page - 1) // main_page) for p, c in zip(prefix, chunks)]
+    main_blocks = sum(main_pages) + 2
+    mperm = torch.randperm(main_blocks, generator=gen).to(torch.int32)
+    main_table = torch.full((nreq, max(main_pages)), -1, dtype=torch.int32)
+    at = 0
+    for q, n in enumerate(main_pages):
+        main_table[q, :n] = mperm[at:at + n]
+        at += n
+    kv = (torch.randn(main_blocks, main_page, main_kv_heads, 2 * main_head_dim, generator=gen)
+          * 0.5).to(torch.bfloat16)
+    main_slots = torch.zeros(tokens, dtype=torch.int64)
+    for t in range(tokens):
+        pos = int(logical[t])
+        main_slots[t] = int(main_table[int(req_of[t]), pos // main_page]) * main_page + pos % main_page
+    comp_table_t = torch.full((nreq, max(pages)), -1, dtype=torch.int32)
+    for q in range(nreq):
+        comp_table_t[q, :len(comp_table[q])] = torch.tensor(comp_table[q], dtype=torch.int32)
 
     q_w = (1.0 + 0.25 * torch.randn(D, generator=gen)).to(torch.bfloat16)
     k_w = (1.0 + 0.25 * torch.randn(D, generator=gen)).to(torch.bfloat16)
@@ -443,4 +468,7 @@ def make_prepare_case(prefix_lens, chunk_lens, *, num_index_heads=32, index_head
         main_value=proj_d[:, main_cols:2 * main_cols].view(tokens, main_kv_heads, main_head_dim),
         main_key_cache=kv_d[..., :main_head_dim], main_value_cache=kv_d[..., main_head_dim:],
         main_slots=to(drop(main_slots.clone())), num_index_heads=H, index_head_dim=D,
-        rotary_dim=rotary_dim, compress_ratio=R, num_groups=closed, chunk_lens=chunks, main_kv=kv_d)
+        rotary_dim=rotary_dim, compress_ratio=R, num_groups=closed, chunk_lens=chunks, main_kv=kv_d,
+        main_block_table=to(main_table), comp_table=to(comp_table_t),
+        seq_lens=to(torch.tensor([p + c for p, c in zip(prefix, chunks)], dtype=torch.int32)),
+        token_to_req=to(req_of.to(torch.int32)))

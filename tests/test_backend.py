@@ -175,3 +175,99 @@ def test_run_qsa_prefill_and_mixed(decode_requests):
                                    want_idx, wl.block_table.cpu(), wl.token_to_req.cpu())
     _check_attn(output[:rows], want, "prefill/mixed")
     assert (output[rows:].float() == 0).all()
+
+
+def _layer_step_case(prefix, chunk, seed):
+    from qsa_vllm_amd.workloads import make_prepare_case
+    return make_prepare_case(prefix, chunk, num_index_heads=8, index_head_dim=128,
+                             compress_ratio=16, rotary_dim=64, main_kv_heads=2, main_head_dim=128,
+                             main_page=16, device=DEV, seed=seed)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("prefix,chunk", [([300, 511, 700, 420], [1, 1, 1, 1]),
+                                          ([40, 300], [48, 33])])
+def test_layer_step_prepare_select_attend(prefix, chunk):
+    """YuLanQSAIndexer.forward (prepare, then select) and YuLanQSAImpl.forward on one
+    consistent state: the new tokens' keys and K/V written by prepare are what
+    selection and attention read."""
+    from types import SimpleNamespace
+    from qsa_vllm_amd.graph_dispatch import decode_logits_columns, prefill_logits_width
+    backend = _backend()
+    case = _layer_step_case(prefix, chunk, seed=sum(chunk))
+    topk, R, page, hq, d = 256, 16, 16, 16, 128
+    width = topk + R - 1
+    tokens = case.index_qk.shape[0]
+    decode = max(chunk) == 1
+    print(f"[backend] layer step prefix={prefix} chunk={chunk}", flush=True)
+    # oracle first, on CPU copies of the untouched state
+    cpu_args, kwargs = case.call_args()
+    start = {k: v.cpu() for k, v in case.clone_outputs().items()}
+    cpu_args = [a.cpu() if isinstance(a, torch.Tensor) else a for a in cpu_args]
+    cpu_args[6] = SimpleNamespace(**{k: v.cpu() for k, v in vars(case.raw).items()})
+    cpu_args[7] = SimpleNamespace(**{k: v.cpu() for k, v in vars(case.comp).items()})
+    cpu_args[8], cpu_args[9] = start["state_cache"], start["compressed_cache"]
+    cpu_args[12], cpu_args[13] = start["main_kv"][..., :d], start["main_kv"][..., d:]
+    query_o = oracle.prepare(*cpu_args, **kwargs)
+
+    indexer = backend.YuLanQSAIndexer(8, 128, R, topk, 64, 1.0e7, 1e-6, 8,
+                                      case.state_cache, case.compressed_cache)
+    indexer.q_layernorm.weight.data.copy_(case.q_norm_weight)
+    indexer.k_layernorm.weight.data.copy_(case.k_norm_weight)
+    indexer.cos_sin_cache = case.cos_sin
+    layer = backend.QSALayerState(case.main_kv.permute(0, 2, 1, 3), d, tokens + 2, width)
+    key_cache, value_cache = layer.main_kv_views()
+    qsl = case.raw.query_start_loc
+    comp_meta = backend.QSACompressedMetadata(
+        block_table=case.comp_table, token_to_req=case.token_to_req,
+        logical_positions=case.positions, seq_lens=case.seq_lens, query_start_loc=qsl,
+        max_query_len=max(chunk), max_seq_len=int(case.seq_lens.max()),
+        num_decodes=len(chunk) if decode else 0, num_decode_tokens=tokens if decode else 0,
+        slot_mapping=case.comp.slot_mapping, k_work_metadata=case.comp.k_work_metadata)
+    raw_meta = backend.QSARawMetadata(**vars(case.raw))
+    indexer.forward(case.index_qk, case.positions, raw_meta, comp_meta,
+                    layer.topk_indices_buffer[:tokens], case.main_key, case.main_value,
+                    key_cache, value_cache, case.main_slots,
+                    main_block_table=case.main_block_table if decode else None,
+                    valid_counts_out=layer.topk_counts_buffer[:tokens] if decode else None)
+    g = torch.Generator().manual_seed(5)
+    q = (torch.randn(tokens, hq, d, generator=g)).to(torch.bfloat16).to(DEV)
+    impl = backend.YuLanQSAImpl(hq, 2, d)
+    main = backend.YuLanQSAMetadata(num_actual_tokens=tokens, max_query_len=max(chunk),
+                                    block_table=case.main_block_table, slot_mapping=case.main_slots)
+    output = torch.full((tokens + 2, hq, d), float("nan"), dtype=torch.bfloat16, device=DEV)
+    impl.forward(layer, q, main, output, token_to_req=case.token_to_req)
+    torch.cuda.synchronize()
+
+    # caches written by prepare
+    assert torch.equal(case.compressed_cache.cpu(), start["compressed_cache"])
+    assert torch.equal(case.main_kv.cpu(), start["main_kv"])
+    # selection: GPU scores of the oracle's prepared query, then the oracle's top-k
+    visible = oracle.visible_blocks(case.positions.cpu(), case.seq_lens.cpu(),
+                                    case.token_to_req.cpu(), R)
+    cap = case.comp_table.shape[1] * case.compressed_cache.shape[1]
+    if decode:
+        cols = decode_logits_columns(int(case.seq_lens.max()), R, cap)
+        lg = torch.full((tokens, cols), float("nan"), device=DEV)
+        torch.ops.yulan_qsa_kernels.indexer_decode(query_o.to(DEV), case.compressed_cache,
+                                                   case.comp_table, visible.to(DEV), lg, 1)
+    else:
+        cols = prefill_logits_width(int(case.seq_lens.max()), R, cap)
+        lg = torch.full((tokens, cols), float("nan"), device=DEV)
+        torch.ops.yulan_qsa_kernels.indexer_prefill(query_o.to(DEV), case.compressed_cache,
+                                                    case.comp_table, qsl, visible.to(DEV), lg,
+                                                    0, tokens, max(chunk))
+    want_idx, want_cnt = oracle.topk_expand(lg.cpu(), visible, case.positions.cpu(),
+                                            case.seq_lens.cpu(), case.token_to_req.cpu(),
+                                            case.main_block_table.cpu() if decode else None,
+                                            width, R, page, decode)
+    assert torch.equal(layer.topk_indices_buffer[:tokens].cpu(), want_idx)
+    if decode:
+        assert torch.equal(layer.topk_counts_buffer[:tokens].cpu(), want_cnt)
+    kv = start["main_kv"]
+    want = oracle.sparse_attention(q.cpu(), kv[..., :d], kv[..., d:], want_idx,
+                                   case.main_block_table.cpu(), case.token_to_req.cpu(),
+                                   indices_are_physical=decode,
+                                   valid_counts=want_cnt if decode else None)
+    _check_attn(output[:tokens], want, "layer step")
+    assert (output[tokens:].float() == 0).all()

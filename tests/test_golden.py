@@ -143,3 +143,73 @@ def test_kernels_attention_golden():
                                          valid_counts=counts.to(DEV), decode_config=(32, splits, 4))
         err = (out.cpu().double() - want).abs()
         assert err.max() <= 2e-2 and err.mean() <= 2e-3, splits
+
+
+# --------------------------------------------------------------------------- preparation
+
+def _bf(rows):
+    return torch.tensor(rows, dtype=torch.float32).to(torch.bfloat16)
+
+
+def _prepare_inputs(device="cpu"):
+    from types import SimpleNamespace
+    g = GOLDEN["prepare"]
+    heads, dim, mdim = g["heads"], g["dim"], g["main_dim"]
+    tokens = len(g["positions"])
+    i64 = lambda v: torch.tensor(v, dtype=torch.int64, device=device)  # noqa: E731
+    i32 = lambda v: torch.tensor(v, dtype=torch.int32, device=device)  # noqa: E731
+    main = _bf(g["main_cache"]).view(len(g["main_cache"]), g["main_page"], 1, 2 * mdim).to(device)
+    raw = SimpleNamespace(slot_mapping=i64(g["state_slots"]), block_table=i32(g["state_table"]),
+                          query_start_loc=i32(g["query_start_loc"]),
+                          logical_positions=i64(g["positions"]))
+    comp = SimpleNamespace(slot_mapping=i64(g["comp_slots"]), k_work_metadata=i32(g["k_work"]))
+    args = (_bf(g["index_qk"]).to(device), i64(g["positions"]), _bf(g["q_gamma"]).to(device),
+            _bf(g["k_gamma"]).to(device), _bf(g["table"]).to(device), g["eps"], raw, comp,
+            _bf(g["state_cache"]).to(device), _bf(g["comp_cache"]).to(device),
+            _bf(g["main_key"]).view(tokens, 1, mdim).to(device),
+            _bf(g["main_value"]).view(tokens, 1, mdim).to(device),
+            main[..., :mdim], main[..., mdim:], i64(g["main_slots"]))
+    kwargs = dict(num_index_heads=heads, index_head_dim=dim, rotary_dim=g["rotary"],
+                  compress_ratio=g["ratio"])
+    return g, args, kwargs, main
+
+
+def _check_prepare(g, query, args, main):
+    assert query.float().cpu().tolist() == g["query"]
+    assert args[8].float().cpu().tolist() == g["state_after"]
+    assert args[9].float().cpu().tolist() == g["comp_after"]
+    assert main.float().cpu().view(len(g["main_after"]), g["main_page"], -1).tolist() == g["main_after"]
+
+
+def test_oracle_norm_rope_golden():
+    g = GOLDEN["norm_rope"]
+    got = oracle.norm_rope(_bf(g["x"]), torch.tensor(g["positions"]), _bf(g["gamma"]),
+                           _bf(g["table"]), g["eps"], g["rotary"])
+    assert got.float().tolist() == g["out"]
+
+
+def test_oracle_prepare_golden():
+    g, args, kwargs, main = _prepare_inputs()
+    query = oracle.prepare(*args, **kwargs)
+    _check_prepare(g, query, args, main)
+
+
+@pytest.mark.gpu
+def test_kernels_norm_rope_golden():
+    from qsa_vllm_amd.ops import IndexerRMSNorm, indexer_norm_rope
+    g = GOLDEN["norm_rope"]
+    norm = IndexerRMSNorm(g["dim"], g["eps"])
+    norm.weight.data = _bf(g["gamma"])
+    x = _bf(g["x"]).view(len(g["x"]), 1, g["dim"]).to(DEV)
+    got = indexer_norm_rope(x, norm.to(DEV), torch.tensor(g["positions"], device=DEV),
+                            _bf(g["table"]).to(DEV), g["rotary"])
+    assert got.view(len(g["x"]), g["dim"]).float().cpu().tolist() == g["out"]
+
+
+@pytest.mark.gpu
+def test_kernels_prepare_golden():
+    from qsa_vllm_amd.ops import qsa_prepare
+    g, args, kwargs, main = _prepare_inputs(DEV)
+    query = qsa_prepare(*args, **kwargs)
+    torch.cuda.synchronize()
+    _check_prepare(g, query, args, main)
