@@ -268,11 +268,61 @@ def main():
             "step": round(ms_step * 1e3, 3),
         },
         "indexer_gbps": round(idx_bytes / (index_us * 1e-6) / 1e9, 1),
+        "prepare": time_prepare(wl, stream),
     }
     if args.cpu_seconds > 0:
         result["cpu_baseline"] = cpu_baseline(wl, args)
     print(json.dumps(result), flush=True)
     return 0
+
+
+def time_prepare(wl, stream, rounds=20, reps=8):
+    """qsa_prepare (index-q norm + RoPE, compression groups, ring commit, main
+    K/V writes) for this step's tokens: decode rows append one token each,
+    chunked prefill appends the chunk. Timed from a graph of `reps` launches."""
+    import torch
+
+    from qsa_vllm_amd.ops import qsa_prepare
+    from qsa_vllm_amd.workloads import make_prepare_case
+
+    s = wl.shape
+    if wl.is_decode:
+        prefix, chunk = (wl.seq_lens.cpu() - 1).tolist(), [1] * wl.rows
+    else:
+        prefix, chunk = [s.prefix] * s.batch, [s.chunk] * s.batch
+    case = make_prepare_case(prefix, chunk, num_index_heads=s.index_heads,
+                             index_head_dim=s.index_dim, compress_ratio=s.compress_ratio,
+                             main_kv_heads=s.num_kv_heads, main_head_dim=s.head_dim,
+                             main_page=s.page_size, history=False, device=wl.q.device,
+                             seed=s.seed + 17)
+    args, kwargs = case.call_args()
+    qsa_prepare(*args, **kwargs)
+    torch.cuda.synchronize()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        qsa_prepare(*args, **kwargs)
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        for _ in range(reps):
+            qsa_prepare(*args, **kwargs)
+    graph.replay()
+    torch.cuda.synchronize()
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    a.record(stream)
+    for _ in range(rounds):
+        graph.replay()
+    b.record(stream)
+    torch.cuda.synchronize()
+    us = a.elapsed_time(b) * 1e3 / (rounds * reps)
+    nbytes = case.prepare_bytes()
+    gbps = nbytes / (us * 1e-6) / 1e9
+    return {"kernel": "prepare_kernel", "bound": "hbm", "tokens": case.index_qk.shape[0],
+            "compression_groups": case.num_groups, "us_per_launch": round(us, 3),
+            "algorithmic_bytes_per_launch": int(nbytes), "achieved": round(gbps, 1),
+            "peak": HBM_PEAK_GBPS, "unit": "GB/s", "frac": round(gbps / HBM_PEAK_GBPS, 4)}
 
 
 def describe(s):
@@ -397,6 +447,7 @@ def run_prefill(args, wl):
         },
         "attention_gathered_gbps": round(gathered / (attn_ms * 1e-3) / 1e9, 1),
         "attention_gathered_bytes": gathered,
+        "prepare": time_prepare(wl, stream, rounds=5, reps=4),
     }
     print(json.dumps(result), flush=True)
     return 0

@@ -72,10 +72,37 @@ __device__ __forceinline__ double group_sum(double v) {
   return v;
 }
 
+// What one lane needs to normalise and rotate any row at one position: its
+// gamma, cos and sin slices (raw bf16 pairs, zero outside the rotary dims or
+// the table) and its rotate-half partner lane. The loads are issued here and
+// consumed only when a row is rotated, so they overlap the row loads.
+struct RopeLane {
+  u32x4 gamma, cosr, sinr;
+  int src;          // partner lane: dims d < half pair with d + half, the rest with d - half
+  bool rot, first_half;
+};
+
+__device__ __forceinline__ RopeLane rope_lane(const NormRope& nr, int64_t pos, int j) {
+  RopeLane r;
+  const bool live = 8 * j < nr.dim;
+  r.gamma = *reinterpret_cast<const u32x4*>(live ? (const void*)(nr.weight + 8 * j)
+                                                 : (const void*)g_qsa_zero_rows);
+  const int half = nr.rotary / 2;
+  r.rot = 8 * j < nr.rotary;
+  r.first_half = 8 * j < half;
+  const int lane = threadIdx.x & 63;
+  r.src = r.rot ? (r.first_half ? lane + half / 8 : lane - half / 8) : lane;
+  const bool ok = r.rot && pos >= 0 && pos < nr.max_positions;
+  const uint16_t* cs = nr.cos_sin + (ok ? pos * nr.rotary + (8 * j) % half : 0);
+  r.cosr = *reinterpret_cast<const u32x4*>(ok ? (const void*)cs : (const void*)g_qsa_zero_rows);
+  r.sinr = *reinterpret_cast<const u32x4*>(ok ? (const void*)(cs + half) : (const void*)g_qsa_zero_rows);
+  return r;
+}
+
 // RMSNorm + partial RoPE of one row held by a 16-lane group; lane j holds
 // dims 8 j .. 8 j + 7 in x (zeros past the row). Every lane of the group
 // must call it (it shuffles within the group).
-__device__ __forceinline__ u32x4 norm_rope_row(const NormRope& nr, u32x4 x, int64_t pos, int j) {
+__device__ __forceinline__ u32x4 norm_rope_apply(const NormRope& nr, const RopeLane& rl, u32x4 x) {
   float f[8];
   unpack8(x, f);
   double ss = 0.0;
@@ -84,42 +111,23 @@ __device__ __forceinline__ u32x4 norm_rope_row(const NormRope& nr, u32x4 x, int6
   ss = group_sum(ss);
   const float mean = __fdiv_rn((float)ss, (float)nr.dim);
   const float inv = (float)__ddiv_rn(1.0, __dsqrt_rn((double)__fadd_rn(mean, nr.eps)));
-
-  const bool live = 8 * j < nr.dim;
-  const u32x4 graw = *reinterpret_cast<const u32x4*>(
-      live ? (const void*)(nr.weight + 8 * j) : (const void*)g_qsa_zero_rows);
   float gamma[8];
-  unpack8(graw, gamma);
+  unpack8(rl.gamma, gamma);
   float scaled[8];
 #pragma unroll
   for (int i = 0; i < 8; ++i) scaled[i] = round_bf16(round_bf16(f[i] * inv) * gamma[i]);
   const u32x4 sc = pack8(scaled);
-
-  // Rotate-half partner: dims d < half pair with d + half, the rest of the
-  // rotary dims with d - half, i.e. lane j +/- half / 8 of the same group.
-  const int half = nr.rotary / 2;
-  const bool rot = 8 * j < nr.rotary;
-  const bool first_half = 8 * j < half;
-  const int lane = threadIdx.x & 63;
-  const int src = rot ? (first_half ? lane + half / 8 : lane - half / 8) : lane;
   u32x4 pr;
 #pragma unroll
-  for (int i = 0; i < 4; ++i) pr[i] = __builtin_amdgcn_ds_bpermute(4 * src, sc[i]);
-  const bool pos_ok = pos >= 0 && pos < nr.max_positions;
-  const int channel = (8 * j) % max(half, 1);
-  const uint16_t* cs = nr.cos_sin + (pos_ok ? pos : 0) * nr.rotary + channel;
-  const bool cs_ok = rot && pos_ok;
-  const u32x4 craw = *reinterpret_cast<const u32x4*>(cs_ok ? (const void*)cs : (const void*)g_qsa_zero_rows);
-  const u32x4 sraw =
-      *reinterpret_cast<const u32x4*>(cs_ok ? (const void*)(cs + half) : (const void*)g_qsa_zero_rows);
-  if (!rot) return sc;
+  for (int i = 0; i < 4; ++i) pr[i] = __builtin_amdgcn_ds_bpermute(4 * rl.src, sc[i]);
+  if (!rl.rot) return sc;
   float partner[8], cosv[8], sinv[8], out[8];
   unpack8(pr, partner);
-  unpack8(craw, cosv);
-  unpack8(sraw, sinv);
+  unpack8(rl.cosr, cosv);
+  unpack8(rl.sinr, sinv);
 #pragma unroll
   for (int i = 0; i < 8; ++i) {
-    const float rotated = first_half ? -partner[i] : partner[i];
+    const float rotated = rl.first_half ? -partner[i] : partner[i];
     const float a = round_bf16(scaled[i] * cosv[i]);
     const float b = round_bf16(rotated * sinv[i]);
     out[i] = a + b;  // rounded to bf16 by pack8
@@ -185,11 +193,19 @@ struct PrepareArgs {
   int k_blocks, q_blocks;
 };
 
+// Rows a lane loads before it uses any: loads in a loop whose trip count is
+// only known at run time would otherwise each wait out a round trip.
+constexpr int kBatch = 16;
+// Query heads of one token per row group: they share the position's rotary
+// slices, and eight rows per group keep enough bytes in flight.
+constexpr int kQHeads = 8;
+
 // Compression group `w` of request q (ops/prepare.py:120-174).
 __device__ void prepare_group(const PrepareArgs& a, int q, int w, int j) {
   if (q < 0 || q >= a.num_requests) return;
   const int qs = a.query_start_loc[q];
   const int qe = a.query_start_loc[q + 1];
+  const int sblock = a.state_table[(int64_t)q * a.state_table_stride];
   const int qlen = qe - qs;
   if (qlen <= 0 || qs < 0 || qe > a.num_tokens) return;
   const int64_t chunk_end = a.logical_positions[qe - 1];
@@ -198,7 +214,6 @@ __device__ void prepare_group(const PrepareArgs& a, int q, int w, int j) {
   const int R = a.ratio;
   const int64_t num_groups = (chunk_end + 1) / R - chunk_start / R;
   const int key_off = a.num_heads * a.dim;
-  const int sblock = a.state_table[(int64_t)q * a.state_table_stride];
   const bool ring_ok = sblock >= 0 && sblock < a.num_state_blocks;
   const uint16_t* ring = a.state + (int64_t)(ring_ok ? sblock : 0) * a.state_block_stride;
 
@@ -207,23 +222,35 @@ __device__ void prepare_group(const PrepareArgs& a, int q, int w, int j) {
     const int64_t end_pos = first_boundary + (int64_t)w * R;
     const int64_t boundary_token = qs + end_pos - chunk_start;
     if (boundary_token >= qe) return;  // positions inconsistent with the chunk
+    const int64_t first = end_pos - (R - 1);
     const int64_t cslot = a.comp_slots[boundary_token];
+    const RopeLane rl = rope_lane(a.k_nr, first, j);
     float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-    for (int m = 0; m < R; ++m) {
-      const int64_t src_pos = end_pos - (R - 1) + m;
-      const bool in_chunk = src_pos >= chunk_start;
-      const uint16_t* row =
-          in_chunk ? a.index_qk + (qs + src_pos - chunk_start) * a.index_token_stride + key_off
-                   : ring + (src_pos % a.state_size) * a.state_token_stride;
-      float v[8];
-      unpack8(load_row(row, j, a.dim, in_chunk || ring_ok), v);
+    for (int m0 = 0; m0 < R; m0 += kBatch) {
+      u32x4 v[kBatch];
 #pragma unroll
-      for (int i = 0; i < 8; ++i) acc[i] += v[i];  // members in order, as the reference
+      for (int i = 0; i < kBatch; ++i) {
+        const int64_t src_pos = first + m0 + i;
+        const bool in_chunk = src_pos >= chunk_start;
+        const uint16_t* row =
+            in_chunk ? a.index_qk + (qs + src_pos - chunk_start) * a.index_token_stride + key_off
+                     : ring + (src_pos % a.state_size) * a.state_token_stride;
+        v[i] = load_row(row, j, a.dim, m0 + i < R && (in_chunk || ring_ok));
+      }
+#pragma unroll
+      for (int i = 0; i < kBatch; ++i) {
+        float f[8];
+        unpack8(v[i], f);
+        const bool member = m0 + i < R;
+#pragma unroll
+        for (int d = 0; d < 8; ++d)  // members in order, as the reference
+          acc[d] = member ? acc[d] + f[d] : acc[d];
+      }
     }
     float pooled[8];
 #pragma unroll
     for (int i = 0; i < 8; ++i) pooled[i] = round_bf16(__fdiv_rn(acc[i], (float)R));
-    const u32x4 out = norm_rope_row(a.k_nr, pack8(pooled), end_pos - (R - 1), j);
+    const u32x4 out = norm_rope_apply(a.k_nr, rl, pack8(pooled));
     if (cslot >= 0 && cslot / a.comp_page < a.num_comp_blocks) {
       uint16_t* dst = a.comp + (cslot / a.comp_page) * a.comp_block_stride +
                       (cslot % a.comp_page) * a.comp_token_stride;
@@ -234,15 +261,42 @@ __device__ void prepare_group(const PrepareArgs& a, int q, int w, int j) {
     // Ring commit of the chunk's last raw keys, after this lane's ring reads
     // above (the same lane reads and writes the same dims of a ring row).
     const int suffix = min(qlen, a.state_size);
-    for (int off = 0; off < suffix; ++off) {
-      const int64_t token = qe - suffix + off;
-      const int64_t slot = a.state_slots[token];
-      if (slot < 0 || slot / a.state_size >= a.num_state_blocks) continue;
-      const u32x4 v = load_row(a.index_qk + token * a.index_token_stride + key_off, j, a.dim, true);
-      store_row(a.state + (slot / a.state_size) * a.state_block_stride +
-                    (slot % a.state_size) * a.state_token_stride,
-                j, a.dim, v);
+    for (int o0 = 0; o0 < suffix; o0 += kBatch) {
+      u32x4 v[kBatch];
+      int64_t slot[kBatch];
+#pragma unroll
+      for (int i = 0; i < kBatch; ++i) {
+        const bool ok = o0 + i < suffix;
+        const int64_t token = ok ? qe - suffix + o0 + i : qe - 1;
+        const int64_t raw = a.state_slots[token];
+        slot[i] = ok ? raw : -1;
+        v[i] = load_row(a.index_qk + token * a.index_token_stride + key_off, j, a.dim, ok);
+      }
+#pragma unroll
+      for (int i = 0; i < kBatch; ++i) {
+        if (slot[i] >= 0 && slot[i] / a.state_size < a.num_state_blocks)
+          store_row(a.state + (slot[i] / a.state_size) * a.state_block_stride +
+                        (slot[i] % a.state_size) * a.state_token_stride,
+                    j, a.dim, v[i]);
+      }
     }
+  }
+}
+
+// kQHeads query heads of one token: every row load is issued before the
+// first row is normalised.
+__device__ __forceinline__ void norm_rope_heads(const NormRope& nr, const uint16_t* token_row,
+                                                int64_t head_stride, int h0, int heads,
+                                                int64_t pos, bool ok, uint16_t* out_row, int j) {
+  u32x4 x[kQHeads];
+#pragma unroll
+  for (int i = 0; i < kQHeads; ++i)
+    x[i] = load_row(token_row + (int64_t)(h0 + i) * head_stride, j, nr.dim, ok && h0 + i < heads);
+  const RopeLane rl = rope_lane(nr, pos, j);
+#pragma unroll
+  for (int i = 0; i < kQHeads; ++i) {
+    const u32x4 out = norm_rope_apply(nr, rl, x[i]);
+    if (ok && h0 + i < heads) store_row(out_row + (int64_t)(h0 + i) * nr.dim, j, nr.dim, out);
   }
 }
 
@@ -260,28 +314,27 @@ __global__ __launch_bounds__(kPrepThreads) void prepare_kernel(const PrepareArgs
   }
   b -= a.k_blocks;
   if (b < a.q_blocks) {
-    const int64_t row = (int64_t)b * kGroupsPerBlock + group;  // token * heads + head
-    const bool ok = row < (int64_t)a.num_tokens * a.num_heads;
-    const int64_t token = ok ? row / a.num_heads : 0;
-    const int head = ok ? (int)(row % a.num_heads) : 0;
-    const u32x4 x =
-        load_row(a.index_qk + token * a.index_token_stride + (int64_t)head * a.dim, j, a.dim, ok);
+    const int hblocks = (a.num_heads + kQHeads - 1) / kQHeads;
+    const int64_t item = (int64_t)b * kGroupsPerBlock + group;  // token * hblocks + head block
+    const bool ok = item < (int64_t)a.num_tokens * hblocks;
+    const int64_t token = ok ? item / hblocks : 0;
+    const int h0 = ok ? (int)(item % hblocks) * kQHeads : 0;
     const int64_t pos = a.positions[token * a.position_stride];
-    const u32x4 out = norm_rope_row(a.q_nr, x, pos, j);
-    if (ok) store_row(a.index_q_out + row * a.dim, j, a.dim, out);
+    norm_rope_heads(a.q_nr, a.index_qk + token * a.index_token_stride, a.dim, h0, a.num_heads,
+                    pos, ok, a.index_q_out + token * a.num_heads * a.dim, j);
     return;
   }
   b -= a.q_blocks;
   // Main K/V rows are already bf16 in their final coordinates (ops/prepare.py:74-95).
   const int64_t item = (int64_t)b * kGroupsPerBlock + group;  // token * heads + head
-  if (item >= (int64_t)a.num_tokens * a.main_heads) return;
-  const int64_t token = item / a.main_heads;
-  const int head = (int)(item % a.main_heads);
+  const bool ok = item < (int64_t)a.num_tokens * a.main_heads;
+  const int64_t token = ok ? item / a.main_heads : 0;
+  const int head = ok ? (int)(item % a.main_heads) : 0;
   const int64_t slot = a.main_slots[token];
-  if (slot < 0 || slot / a.main_page >= a.num_main_blocks) return;
+  const u32x4 k = load_row(a.mk + token * a.mk_token + head * a.mk_head, j, a.main_dim, ok);
+  const u32x4 v = load_row(a.mv + token * a.mv_token + head * a.mv_head, j, a.main_dim, ok);
+  if (!ok || slot < 0 || slot / a.main_page >= a.num_main_blocks) return;
   const int64_t blk = slot / a.main_page, off = slot % a.main_page;
-  const u32x4 k = load_row(a.mk + token * a.mk_token + head * a.mk_head, j, a.main_dim, true);
-  const u32x4 v = load_row(a.mv + token * a.mv_token + head * a.mv_head, j, a.main_dim, true);
   store_row(a.mkc + blk * a.mkc_block + off * a.mkc_token + head * a.mkc_head, j, a.main_dim, k);
   store_row(a.mvc + blk * a.mvc_block + off * a.mvc_token + head * a.mvc_head, j, a.main_dim, v);
 }
@@ -298,13 +351,14 @@ struct NormRopeArgs {
 
 __global__ __launch_bounds__(kPrepThreads) void norm_rope_kernel(const NormRopeArgs a) {
   const int j = threadIdx.x & (kGroupLanes - 1);
-  const int64_t row = (int64_t)blockIdx.x * kGroupsPerBlock + threadIdx.x / kGroupLanes;
-  const bool ok = row < (int64_t)a.tokens * a.heads;
-  const int64_t token = ok ? row / a.heads : 0;
-  const int head = ok ? (int)(row % a.heads) : 0;
-  const u32x4 x = load_row(a.values + token * a.token_stride + head * a.head_stride, j, a.nr.dim, ok);
-  const u32x4 out = norm_rope_row(a.nr, x, a.positions[token * a.position_stride], j);
-  if (ok) store_row(a.out + row * a.nr.dim, j, a.nr.dim, out);
+  const int hblocks = (a.heads + kQHeads - 1) / kQHeads;
+  const int64_t item = (int64_t)blockIdx.x * kGroupsPerBlock + threadIdx.x / kGroupLanes;
+  const bool ok = item < (int64_t)a.tokens * hblocks;
+  const int64_t token = ok ? item / hblocks : 0;
+  const int h0 = ok ? (int)(item % hblocks) * kQHeads : 0;
+  const int64_t pos = a.positions[token * a.position_stride];
+  norm_rope_heads(a.nr, a.values + token * a.token_stride, a.head_stride, h0, a.heads, pos, ok,
+                  a.out + token * a.heads * a.nr.dim, j);
 }
 
 int check_norm_rope(int dim, int rotary, int max_positions, const void* weight, const void* cos_sin,
@@ -429,7 +483,8 @@ extern "C" int qsa_indexer_prepare(
   a.main_heads = main_kv_heads;
   a.main_dim = main_head_dim;
   const int64_t k_blocks = ((int64_t)num_k_work + kGroupsPerBlock - 1) / kGroupsPerBlock;
-  const int64_t q_blocks = ((int64_t)num_tokens * num_index_heads + kGroupsPerBlock - 1) / kGroupsPerBlock;
+  const int64_t q_items = (int64_t)num_tokens * ((num_index_heads + kQHeads - 1) / kQHeads);
+  const int64_t q_blocks = (q_items + kGroupsPerBlock - 1) / kGroupsPerBlock;
   const int64_t m_blocks = ((int64_t)num_tokens * main_kv_heads + kGroupsPerBlock - 1) / kGroupsPerBlock;
   const int64_t blocks = k_blocks + q_blocks + m_blocks;
   if (blocks > INT32_MAX) return fail(QSA_ERR_UNSUPPORTED, "qsa_indexer_prepare: grid too large");
@@ -457,7 +512,8 @@ extern "C" int qsa_indexer_norm_rope(const void* values, int64_t token_stride, i
     return fail(QSA_ERR_INVALID,
                 "qsa_indexer_norm_rope: values and out must be 16-byte aligned with strides that "
                 "are multiples of 8 elements and unit dim stride");
-  const int64_t blocks = ((int64_t)tokens * heads + kGroupsPerBlock - 1) / kGroupsPerBlock;
+  const int64_t items = (int64_t)tokens * ((heads + kQHeads - 1) / kQHeads);
+  const int64_t blocks = (items + kGroupsPerBlock - 1) / kGroupsPerBlock;
   if (blocks > INT32_MAX) return fail(QSA_ERR_UNSUPPORTED, "qsa_indexer_norm_rope: grid too large");
   NormRopeArgs a;
   a.nr = NormRope{static_cast<const uint16_t*>(weight), static_cast<const uint16_t*>(cos_sin),

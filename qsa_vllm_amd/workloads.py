@@ -338,8 +338,8 @@ class PrepareCase:
 def make_prepare_case(prefix_lens, chunk_lens, *, num_index_heads=32, index_head_dim=128,
                       compress_ratio=16, state_size=None, comp_page=16, main_kv_heads=2,
                       main_head_dim=128, main_page=16, rotary_dim=64, theta=1.0e7, eps=1.0e-6,
-                      projection_pad=64, work_pad=3, drop_slot_every=0, device="cpu",
-                      seed=0) -> PrepareCase:
+                      projection_pad=64, work_pad=3, drop_slot_every=0, history=True,
+                      device="cpu", seed=0) -> PrepareCase:
     """Request q has prefix_lens[q] cached tokens and appends chunk_lens[q]
     tokens at positions prefix .. prefix + chunk - 1. index_qk, main_key and
     main_value are column slices of one projection row (as the fused QKV +
@@ -347,7 +347,9 @@ def make_prepare_case(prefix_lens, chunk_lens, *, num_index_heads=32, index_head
     its earlier positions, the compressed cache random keys of its earlier
     groups and the main cache random K/V of its earlier positions, all behind
     seeded permuted page tables. drop_slot_every > 0 sets every n-th slot of
-    each mapping to -1."""
+    each mapping to -1. history=False leaves the earlier compressed keys zero
+    and maps only the main pages this step writes (a timing case: the
+    kernel's work and slots are the same)."""
     from .ops.normalization import rotary_cache
 
     gen = torch.Generator(device="cpu").manual_seed(seed)
@@ -399,7 +401,7 @@ def make_prepare_case(prefix_lens, chunk_lens, *, num_index_heads=32, index_head
         comp_table.append(perm[at:at + n].tolist())
         at += n
     compressed_cache = torch.zeros(comp_blocks, comp_page, 1, D, dtype=torch.bfloat16)
-    for q in range(nreq):
+    for q in range(nreq if history else 0):
         for g_ in range(prefix[q] // R):
             compressed_cache[comp_table[q][g_ // comp_page], g_ % comp_page, 0] = (
                 torch.randn(D, generator=gen) * 0.5).to(torch.bfloat16)
@@ -424,15 +426,17 @@ def make_prepare_case(prefix_lens, chunk_lens, *, num_index_heads=32, index_head
     # holding every position of each sequence (earlier ones random); this
     # step's tokens go to their block-table slots.
     main_pages = [max(1, (p + c + main_page - 1) // main_page) for p, c in zip(prefix, chunks)]
-    main_blocks = sum(main_pages) + 2
+    first_page = [0 if history else p // main_page for p in prefix]
+    main_blocks = sum(n - f for n, f in zip(main_pages, first_page)) + 2
     mperm = torch.randperm(main_blocks, generator=gen).to(torch.int32)
     main_table = torch.full((nreq, max(main_pages)), -1, dtype=torch.int32)
     at = 0
     for q, n in enumerate(main_pages):
-        main_table[q, :n] = mperm[at:at + n]
-        at += n
-    kv = (torch.randn(main_blocks, main_page, main_kv_heads, 2 * main_head_dim, generator=gen)
-          * 0.5).to(torch.bfloat16)
+        main_table[q, first_page[q]:n] = mperm[at:at + n - first_page[q]]
+        at += n - first_page[q]
+    kv_shape = (main_blocks, main_page, main_kv_heads, 2 * main_head_dim)
+    kv = ((torch.randn(kv_shape, generator=gen) * 0.5).to(torch.bfloat16) if history
+          else torch.zeros(kv_shape, dtype=torch.bfloat16))
     main_slots = torch.zeros(tokens, dtype=torch.int64)
     for t in range(tokens):
         pos = int(logical[t])
