@@ -269,6 +269,7 @@ def main():
         },
         "indexer_gbps": round(idx_bytes / (index_us * 1e-6) / 1e9, 1),
         "prepare": time_prepare(wl, stream),
+        "layer_step": time_layer_step(wl, stream),
     }
     if args.cpu_seconds > 0:
         result["cpu_baseline"] = cpu_baseline(wl, args)
@@ -323,6 +324,73 @@ def time_prepare(wl, stream, rounds=20, reps=8):
             "compression_groups": case.num_groups, "us_per_launch": round(us, 3),
             "algorithmic_bytes_per_launch": int(nbytes), "achieved": round(gbps, 1),
             "peak": HBM_PEAK_GBPS, "unit": "GB/s", "frac": round(gbps / HBM_PEAK_GBPS, 4)}
+
+
+def time_layer_step(wl, stream, reps=8, rounds=10):
+    """The whole QSA decode layer step (prepare -> select -> attend) on the
+    workload's caches and page tables, metadata from QSAMetadataBuilder, timed
+    from a graph of `reps` back-to-back steps."""
+    import torch
+
+    from qsa_vllm_amd.backend import QSALayerState, YuLanQSAImpl, YuLanQSAIndexer
+    from qsa_vllm_amd.graph_dispatch import SHORT_DECODE_COLUMNS, capture_column_scope
+    from qsa_vllm_amd.layer_step import qsa_layer_step
+    from qsa_vllm_amd.metadata import QSAMetadataBuilder
+
+    s = wl.shape
+    dev = wl.q.device
+    rows = wl.rows
+    ring = torch.zeros(rows + 2, s.compress_ratio, s.index_dim, dtype=torch.bfloat16, device=dev)
+    indexer = YuLanQSAIndexer(s.index_heads, s.index_dim, s.compress_ratio, s.token_topk, 64,
+                              1.0e7, 1e-6, int(wl.seq_lens.max()) + 1, ring, wl.index_cache)
+    kv_view = wl.kv_cache.permute(0, 2, 1, 3) if s.kv_layout == "token_major" else wl.kv_cache
+    layer = QSALayerState(kv_view, s.head_dim, rows, s.width)
+    impl = YuLanQSAImpl(s.num_q_heads, s.num_kv_heads, s.head_dim)
+    builder = QSAMetadataBuilder(
+        compress_ratio=s.compress_ratio, main_page_size=s.page_size,
+        comp_page_size=wl.index_cache.shape[1], ring_size=s.compress_ratio,
+        max_num_requests=rows, max_num_tokens=rows, main_table_width=wl.block_table.shape[1],
+        comp_table_width=wl.index_table.shape[1], device=dev)
+    batch = builder.build((wl.seq_lens.cpu() - 1).tolist(), [1] * rows, wl.block_table,
+                          wl.index_table, torch.arange(rows, dtype=torch.int32))
+    idx_cols, kv_cols = (s.index_heads + 1) * s.index_dim, s.num_kv_heads * s.head_dim
+    gen = torch.Generator(device=dev).manual_seed(s.seed + 23)
+    projected = (torch.randn(rows, idx_cols + 2 * kv_cols, generator=gen, device=dev)
+                 * 0.5).to(torch.bfloat16)
+    index_qk = projected[:, :idx_cols]
+    main_key = projected[:, idx_cols:idx_cols + kv_cols].view(rows, s.num_kv_heads, s.head_dim)
+    main_value = projected[:, idx_cols + kv_cols:].view(rows, s.num_kv_heads, s.head_dim)
+    output = torch.empty_like(wl.q)
+
+    def step():
+        qsa_layer_step(indexer, impl, layer, batch, index_qk, main_key, main_value, wl.q, output)
+
+    with capture_column_scope(SHORT_DECODE_COLUMNS):
+        step()
+        torch.cuda.synchronize()
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            step()
+        torch.cuda.current_stream().wait_stream(side)
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            for _ in range(reps):
+                step()
+    graph.replay()
+    torch.cuda.synchronize()
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    a.record(stream)
+    for _ in range(rounds):
+        graph.replay()
+    b.record(stream)
+    torch.cuda.synchronize()
+    if not torch.isfinite(output.float()).all():
+        raise SystemExit("non-finite layer step output: results invalid")
+    us = a.elapsed_time(b) * 1e3 / (rounds * reps)
+    return {"ops": "qsa_prepare -> select_paged_tokens -> qsa_sparse_paged_attention",
+            "us_per_step": round(us, 3), "tokens_per_s": round(rows / (us * 1e-6), 1)}
 
 
 def describe(s):
