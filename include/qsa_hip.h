@@ -138,6 +138,42 @@ int qsa_indexer_norm_rope(const void* values, int64_t token_stride, int64_t head
                           const void* cos_sin, int max_positions, float eps, int rotary_dim,
                           void* out, void* stream);
 
+/*
+ * Replaces qsa_store_cache_rows and its kernel _store_qsa_rows_kernel
+ * (ops/qsa.py:366-401, 691-706): rows [num_rows, width] bf16 into
+ * cache[slot / page_size, slot % page_size, 0, :width] for
+ * 0 <= slot_mapping[r] < num_blocks * page_size (int64 slots).
+ */
+int qsa_store_cache_rows(void* cache, int64_t cache_block_stride, int64_t cache_token_stride,
+                         int num_blocks, int page_size, int width,
+                         const int64_t* slot_mapping, const void* rows, int64_t row_stride,
+                         int num_rows, void* stream);
+
+/*
+ * Replaces qsa_compress_groups_with_ratio and its kernel
+ * _compress_qsa_groups_kernel (ops/qsa.py:403-549, 709-750): for each row
+ * (token) that closes a group with a compressed slot, the bf16 mean of the
+ * compress_ratio raw keys ending at its position (this step's rows, or the
+ * request's ring before the chunk; fp32 sum in member order), else 0; and the
+ * group's first position in 3 int64 columns, read from raw_positions /
+ * rope_positions when rope_positions is given. Every row of pooled and
+ * first_positions is written.
+ */
+int qsa_compress_groups(const void* raw_keys, int64_t raw_row_stride,
+                        const int64_t* raw_positions, int64_t raw_pos_row_stride,
+                        int64_t raw_pos_dim_stride, const void* state_cache,
+                        int64_t state_block_stride, int64_t state_token_stride, int state_size,
+                        int num_state_blocks, const int64_t* rope_positions,
+                        int64_t rope_block_stride, int64_t rope_token_stride,
+                        int64_t rope_dim_stride, const int32_t* state_table,
+                        int64_t state_table_stride, const int32_t* token_to_req,
+                        const int32_t* query_start_loc, int num_requests,
+                        const int64_t* logical_positions, const int64_t* compressed_slots,
+                        int rows, int head_dim, int compress_ratio, void* pooled,
+                        int64_t pooled_row_stride, int64_t* first_positions,
+                        int64_t first_positions_row_stride, int64_t first_positions_col_stride,
+                        void* stream);
+
 /* ------------------------------------------------------------------------ */
 /* Kernel 1: indexer scoring                                                 */
 /* ------------------------------------------------------------------------ */
@@ -180,6 +216,22 @@ int qsa_indexer_prefill(const void* q, int64_t q_row_stride, int64_t q_head_stri
                         int max_query_len,
                         float* logits, int64_t logits_row_stride, int logits_cols,
                         void* stream);
+
+/*
+ * Replaces expand_qsa_block_indices_cuda and its kernel
+ * _expand_qsa_indices_kernel (ops/qsa.py:18-106, 552-591): the expansion of
+ * qsa_topk_expand applied to caller-chosen block ids (block_indices
+ * [rows, >= topk] int32, rank i = column i, -1 for none) instead of a top-k.
+ */
+int qsa_expand_block_indices(const int32_t* block_indices, int64_t block_row_stride,
+                             int64_t block_col_stride, int block_cols, int rows, int topk,
+                             const int64_t* positions, const int32_t* sequence_lengths,
+                             int num_requests, const int32_t* token_to_req,
+                             const int32_t* table, int64_t table_row_stride, int table_width,
+                             int32_t* output, int64_t output_row_stride,
+                             int64_t output_col_stride, int output_width, int32_t* counts,
+                             int ratio, int page_size, int physical, int store_counts,
+                             void* stream);
 
 /* ------------------------------------------------------------------------ */
 /* Kernel 3: bf16 paged sparse GQA attention                                 */

@@ -51,6 +51,9 @@ __all__ = [
     "uint32_keys",
     "topk_ids",
     "topk_expand",
+    "expand_blocks",
+    "store_cache_rows",
+    "compress_groups",
     "select_paged_tokens",
     "sparse_attention",
     "sparse_attention_partials",
@@ -194,8 +197,18 @@ def topk_expand(scores, lengths, positions, sequence_lengths, token_to_req, tabl
     Returns ``(out[rows, output_width] int32, counts[rows] int32)``.
     """
     k = output_width // ratio
-    ids = topk_ids(scores, lengths, k).long()
-    rows = scores.shape[0]
+    ids = topk_ids(scores, lengths, k)
+    return expand_blocks(ids, positions, sequence_lengths, token_to_req, table, output_width,
+                         ratio, page_size, physical, k)
+
+
+def expand_blocks(block_ids, positions, sequence_lengths, token_to_req, table, output_width,
+                  ratio, page_size, physical, k):
+    """Expansion of ranked block ids (rank i < k is ``block_ids[:, i]``, any order,
+    -1 for none) with the causal tail, mapping and counts: ``ops/csrc/topk.cu:97-180``
+    and its Triton twin ``ops/qsa.py:18-106``. Returns ``(out, counts)``."""
+    ids = block_ids[:, :k].long()
+    rows = ids.shape[0]
     num_requests = sequence_lengths.numel()
     req = token_to_req.long()
     mapped = (req >= 0) & (req < num_requests)
@@ -229,6 +242,63 @@ def topk_expand(scores, lengths, positions, sequence_lengths, token_to_req, tabl
     out = torch.where(valid, token, torch.full_like(token, -1)).to(torch.int32)
     counts = torch.minimum(expanded + tail_count, seq_len).to(torch.int32)
     return out, counts
+
+
+def store_cache_rows(cache, slot_mapping, rows):
+    """``qsa_store_cache_rows`` (ops/qsa.py:366-401, 691-706): row r into
+    cache[slot // page, slot % page, 0, :width] when 0 <= slot < blocks * page."""
+    rows = rows[:, 0] if rows.dim() == 3 else rows
+    page, width = cache.shape[1], cache.shape[3]
+    for r, slot in enumerate(slot_mapping.tolist()[:rows.shape[0]]):
+        if 0 <= slot < cache.shape[0] * page:
+            cache[slot // page, slot % page, 0, :width] = rows[r, :width]
+
+
+def compress_groups(raw_keys, raw_positions, state_cache, state_table, token_to_req,
+                    query_start_loc, logical_positions, compressed_slots, ratio, rope_cache=None):
+    """``qsa_compress_groups_with_ratio`` (ops/qsa.py:403-549, 709-750). Returns
+    ``(pooled [rows, 1, dim] bf16, first_positions [rows, 3] int64)``."""
+    rows, dim = token_to_req.numel(), raw_keys.shape[-1]
+    keys = raw_keys.reshape(raw_keys.shape[0], -1)[:, :dim].float()
+    ring = state_cache.reshape(state_cache.shape[0], state_cache.shape[1], -1)[..., :dim].float()
+    S = state_cache.shape[1]
+    qsl = query_start_loc.tolist()
+    nreq = len(qsl) - 1
+    pooled = torch.zeros(rows, 1, dim, dtype=torch.float32)
+    first_positions = torch.zeros(rows, 3, dtype=torch.int64)
+    for row in range(rows):
+        req = int(token_to_req[row])
+        end = int(logical_positions[row])
+        slot = int(compressed_slots[row])
+        req_ok = 0 <= req < nreq
+        qs, qe = (qsl[req], qsl[req + 1]) if req_ok else (0, 0)
+        block = int(state_table[req, 0]) if req_ok else -1
+        ring_ok = 0 <= block < ring.shape[0]
+        chunk_start = end - (row - qs)
+        valid = req_ok and qs <= row < qe and end >= ratio - 1 and slot >= 0
+        acc = torch.zeros(dim, dtype=torch.float32)
+        for m in range(ratio):
+            position = end - (ratio - 1) + m
+            if not valid:
+                continue
+            if position >= chunk_start:
+                raw_row = qs + position - chunk_start
+                if qs <= raw_row < qe and raw_row < rows:
+                    acc = acc + keys[raw_row]
+            elif ring_ok:
+                acc = acc + ring[block, position % S]
+        pooled[row, 0] = acc / torch.tensor(float(ratio), dtype=torch.float32)
+        first = end - ratio + 1
+        if rope_cache is None:
+            first_positions[row] = first if valid else 0
+        elif valid and first >= chunk_start:
+            raw_first = qs + first - chunk_start
+            if qs <= raw_first < qe and raw_first < rows:
+                first_positions[row] = raw_positions.reshape(raw_positions.shape[0], -1)[raw_first, :3]
+        elif valid and ring_ok:
+            first_positions[row] = rope_cache.reshape(rope_cache.shape[0], rope_cache.shape[1],
+                                                      -1)[block, first % S, :3]
+    return pooled.to(torch.bfloat16), first_positions
 
 
 def select_paged_tokens(q, k_cache, page_table, token_to_req, query_positions,

@@ -70,6 +70,33 @@ SIGNATURES = {
                                       c_ptr, c_i64,
                                       c_ptr, c_i32, ctypes.c_float, c_i32,
                                       c_ptr, c_ptr]),
+    "qsa_store_cache_rows": (c_i32, [c_ptr, c_i64, c_i64,
+                                     c_i32, c_i32, c_i32,
+                                     c_ptr, c_ptr, c_i64,
+                                     c_i32, c_ptr]),
+    "qsa_compress_groups": (c_i32, [c_ptr, c_i64,
+                                    c_ptr, c_i64,
+                                    c_i64, c_ptr,
+                                    c_i64, c_i64, c_i32,
+                                    c_i32, c_ptr,
+                                    c_i64, c_i64,
+                                    c_i64, c_ptr,
+                                    c_i64, c_ptr,
+                                    c_ptr, c_i32,
+                                    c_ptr, c_ptr,
+                                    c_i32, c_i32, c_i32, c_ptr,
+                                    c_i64, c_ptr,
+                                    c_i64, c_i64,
+                                    c_ptr]),
+    "qsa_expand_block_indices": (c_i32, [c_ptr, c_i64,
+                                         c_i64, c_i32, c_i32, c_i32,
+                                         c_ptr, c_ptr,
+                                         c_i32, c_ptr,
+                                         c_ptr, c_i64, c_i32,
+                                         c_ptr, c_i64,
+                                         c_i64, c_i32, c_ptr,
+                                         c_i32, c_i32, c_i32, c_i32,
+                                         c_ptr]),
     "qsa_indexer_decode": (c_i32, [c_ptr, c_i64, c_i64,
                                    c_i32, c_i32, c_i32, c_ptr,
                                    c_i64, c_i64,

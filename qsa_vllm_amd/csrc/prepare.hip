@@ -361,6 +361,125 @@ __global__ __launch_bounds__(kPrepThreads) void norm_rope_kernel(const NormRopeA
                   a.out + token * a.heads * a.nr.dim, j);
 }
 
+// Rows into paged cache slots (qsa_store_cache_rows, ops/qsa.py:366-401 and
+// 691-706): row r goes to slot_mapping[r] when 0 <= slot < blocks * page.
+// A group copies 128 dims per step.
+struct StoreRowsArgs {
+  uint16_t* cache;
+  int64_t block_stride, token_stride;  // elements
+  int num_blocks, page, width;
+  const int64_t* slots;
+  const uint16_t* rows;
+  int64_t row_stride;
+  int num_rows;
+};
+
+__global__ __launch_bounds__(kPrepThreads) void store_rows_kernel(const StoreRowsArgs a) {
+  const int j = threadIdx.x & (kGroupLanes - 1);
+  const int64_t r = (int64_t)blockIdx.x * kGroupsPerBlock + threadIdx.x / kGroupLanes;
+  if (r >= a.num_rows) return;
+  const int64_t slot = a.slots[r];
+  const bool ok = slot >= 0 && slot < (int64_t)a.num_blocks * a.page;
+  const uint16_t* src = a.rows + r * a.row_stride;
+  uint16_t* dst = a.cache + (ok ? (slot / a.page) * a.block_stride + (slot % a.page) * a.token_stride : 0);
+  for (int c = 0; c < a.width; c += 8 * kGroupLanes) {
+    const u32x4 v = load_row(src + c, j, a.width - c, ok);
+    if (ok) store_row(dst + c, j, a.width - c, v);
+  }
+}
+
+// Mean of the complete group ending at each row (qsa_compress_groups_with_ratio,
+// ops/qsa.py:403-549 and 709-750): members from this step's rows, or from the
+// request's ring before the chunk; fp32 sum in member order, divided by the
+// ratio, stored as bf16 (0 for rows that close no valid group). The group's
+// first position goes to 3 int64 columns: from the raw or ring position tables
+// when they are given, else the position itself (0 for invalid rows).
+struct CompressArgs {
+  const uint16_t* raw;
+  int64_t raw_row_stride;
+  const int64_t* raw_pos;
+  int64_t raw_pos_row_stride, raw_pos_dim_stride;
+  const uint16_t* state;
+  int64_t state_block_stride, state_token_stride;
+  int state_size, num_state_blocks;
+  const int64_t* rope;
+  int64_t rope_block_stride, rope_token_stride, rope_dim_stride;
+  const int32_t* state_table;
+  int64_t state_table_stride;
+  const int32_t* token_to_req;
+  const int32_t* query_start_loc;
+  int num_requests;
+  const int64_t* logical_positions;
+  const int64_t* compressed_slots;
+  int rows, dim, ratio;
+  uint16_t* pooled;
+  int64_t pooled_row_stride;
+  int64_t* first_positions;
+  int64_t fp_row_stride, fp_col_stride;
+};
+
+__global__ __launch_bounds__(kPrepThreads) void compress_groups_kernel(const CompressArgs a) {
+  const int j = threadIdx.x & (kGroupLanes - 1);
+  const int row = blockIdx.x * kGroupsPerBlock + threadIdx.x / kGroupLanes;
+  if (row >= a.rows) return;
+  const int request = a.token_to_req[row];
+  const bool req_ok = request >= 0 && request < a.num_requests;
+  const int safe = req_ok ? request : 0;
+  const int64_t end_pos = a.logical_positions[row];
+  const int64_t cslot = a.compressed_slots[row];
+  const int qs = req_ok ? a.query_start_loc[safe] : 0;
+  const int qe = req_ok ? a.query_start_loc[safe + 1] : 0;
+  const int sblock = req_ok ? a.state_table[(int64_t)safe * a.state_table_stride] : -1;
+  const int R = a.ratio;
+  const int64_t chunk_start = end_pos - (row - qs);
+  const bool valid = req_ok && row >= qs && row < qe && end_pos >= R - 1 && cslot >= 0;
+  const bool ring_ok = sblock >= 0 && sblock < a.num_state_blocks;
+  const uint16_t* ring = a.state + (int64_t)(ring_ok ? sblock : 0) * a.state_block_stride;
+  float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  for (int m0 = 0; m0 < R; m0 += kBatch) {
+    u32x4 v[kBatch];
+#pragma unroll
+    for (int i = 0; i < kBatch; ++i) {
+      const int64_t position = end_pos - (R - 1) + m0 + i;
+      const bool use_raw = position >= chunk_start;
+      const int64_t raw_row = qs + position - chunk_start;
+      const bool raw_ok = raw_row >= qs && raw_row < qe && raw_row < a.rows;
+      const uint16_t* src = use_raw ? a.raw + (raw_ok ? raw_row : 0) * a.raw_row_stride
+                                    : ring + (position >= 0 ? position % a.state_size : 0) *
+                                                 a.state_token_stride;
+      v[i] = load_row(src, j, a.dim, valid && m0 + i < R && (use_raw ? raw_ok : ring_ok));
+    }
+#pragma unroll
+    for (int i = 0; i < kBatch; ++i) {
+      float f[8];
+      unpack8(v[i], f);
+      const bool member = m0 + i < R;
+#pragma unroll
+      for (int d = 0; d < 8; ++d) acc[d] = member ? acc[d] + f[d] : acc[d];
+    }
+  }
+  float mean[8];
+#pragma unroll
+  for (int d = 0; d < 8; ++d) mean[d] = __fdiv_rn(acc[d], (float)R);
+  store_row(a.pooled + (int64_t)row * a.pooled_row_stride, j, a.dim, pack8(mean));
+  if (j < 3) {
+    const int64_t first = end_pos - R + 1;
+    int64_t value = valid ? first : 0;
+    if (a.rope) {
+      const bool from_raw = first >= chunk_start;
+      const int64_t raw_first = qs + first - chunk_start;
+      const bool raw_ok = valid && from_raw && raw_first >= qs && raw_first < qe && raw_first < a.rows;
+      const bool ring_pos_ok = valid && !from_raw && ring_ok;
+      value = raw_ok ? a.raw_pos[raw_first * a.raw_pos_row_stride + j * a.raw_pos_dim_stride]
+              : ring_pos_ok ? a.rope[(int64_t)sblock * a.rope_block_stride +
+                                     (first % a.state_size) * a.rope_token_stride +
+                                     j * a.rope_dim_stride]
+                            : 0;
+    }
+    a.first_positions[(int64_t)row * a.fp_row_stride + j * a.fp_col_stride] = value;
+  }
+}
+
 int check_norm_rope(int dim, int rotary, int max_positions, const void* weight, const void* cos_sin,
                     const char* name) {
   if (dim != 64 && dim != 128)
@@ -529,4 +648,63 @@ extern "C" int qsa_indexer_norm_rope(const void* values, int64_t token_stride, i
   hipLaunchKernelGGL(norm_rope_kernel, dim3((unsigned)blocks), dim3(kPrepThreads), 0,
                      static_cast<hipStream_t>(stream), a);
   return check_launch("qsa_indexer_norm_rope launch");
+}
+
+extern "C" int qsa_store_cache_rows(void* cache, int64_t cache_block_stride,
+                                    int64_t cache_token_stride, int num_blocks, int page_size,
+                                    int width, const int64_t* slot_mapping, const void* rows,
+                                    int64_t row_stride, int num_rows, void* stream) {
+  if (num_rows < 0) return fail(QSA_ERR_INVALID, "qsa_store_cache_rows: negative rows");
+  if (num_rows == 0) return QSA_OK;
+  if (!cache || !slot_mapping || !rows) return fail(QSA_ERR_INVALID, "qsa_store_cache_rows: null tensor pointer");
+  if (page_size <= 0 || num_blocks < 0 || width <= 0 || width % 8)
+    return fail(QSA_ERR_UNSUPPORTED, "qsa_store_cache_rows: width must be a positive multiple of 8");
+  if (!aligned16(cache) || !aligned16(rows) || ((cache_block_stride | cache_token_stride | row_stride) & 7))
+    return fail(QSA_ERR_INVALID,
+                "qsa_store_cache_rows: cache and rows must be 16-byte aligned with strides that "
+                "are multiples of 8 elements and unit dim stride");
+  StoreRowsArgs a{static_cast<uint16_t*>(cache), cache_block_stride, cache_token_stride, num_blocks,
+                  page_size, width, slot_mapping, static_cast<const uint16_t*>(rows), row_stride,
+                  num_rows};
+  hipLaunchKernelGGL(store_rows_kernel, dim3((num_rows + kGroupsPerBlock - 1) / kGroupsPerBlock),
+                     dim3(kPrepThreads), 0, static_cast<hipStream_t>(stream), a);
+  return check_launch("qsa_store_cache_rows launch");
+}
+
+extern "C" int qsa_compress_groups(
+    const void* raw_keys, int64_t raw_row_stride, const int64_t* raw_positions,
+    int64_t raw_pos_row_stride, int64_t raw_pos_dim_stride, const void* state_cache,
+    int64_t state_block_stride, int64_t state_token_stride, int state_size, int num_state_blocks,
+    const int64_t* rope_positions, int64_t rope_block_stride, int64_t rope_token_stride,
+    int64_t rope_dim_stride, const int32_t* state_table, int64_t state_table_stride,
+    const int32_t* token_to_req, const int32_t* query_start_loc, int num_requests,
+    const int64_t* logical_positions, const int64_t* compressed_slots, int rows, int head_dim,
+    int compress_ratio, void* pooled, int64_t pooled_row_stride, int64_t* first_positions,
+    int64_t first_positions_row_stride, int64_t first_positions_col_stride, void* stream) {
+  if (rows < 0) return fail(QSA_ERR_INVALID, "qsa_compress_groups: negative rows");
+  if (rows == 0) return QSA_OK;
+  if (head_dim != 64 && head_dim != 128)
+    return fail(QSA_ERR_UNSUPPORTED, "qsa_compress_groups: head dim must be 64 or 128");
+  if (compress_ratio <= 0 || state_size <= 0)
+    return fail(QSA_ERR_INVALID, "qsa_compress_groups: ratio and ring size must be positive");
+  if (!raw_keys || !state_cache || !state_table || !token_to_req || !query_start_loc ||
+      !logical_positions || !compressed_slots || !pooled || !first_positions ||
+      (rope_positions && !raw_positions))
+    return fail(QSA_ERR_INVALID, "qsa_compress_groups: null tensor pointer");
+  if (!aligned16(raw_keys) || !aligned16(state_cache) || !aligned16(pooled) ||
+      ((raw_row_stride | state_block_stride | state_token_stride | pooled_row_stride) & 7))
+    return fail(QSA_ERR_INVALID,
+                "qsa_compress_groups: keys, ring and output must be 16-byte aligned with strides "
+                "that are multiples of 8 elements and unit dim stride");
+  CompressArgs a{static_cast<const uint16_t*>(raw_keys), raw_row_stride, raw_positions,
+                 raw_pos_row_stride, raw_pos_dim_stride, static_cast<const uint16_t*>(state_cache),
+                 state_block_stride, state_token_stride, state_size, num_state_blocks,
+                 rope_positions, rope_block_stride, rope_token_stride, rope_dim_stride,
+                 state_table, state_table_stride, token_to_req, query_start_loc, num_requests,
+                 logical_positions, compressed_slots, rows, head_dim, compress_ratio,
+                 static_cast<uint16_t*>(pooled), pooled_row_stride, first_positions,
+                 first_positions_row_stride, first_positions_col_stride};
+  hipLaunchKernelGGL(compress_groups_kernel, dim3((rows + kGroupsPerBlock - 1) / kGroupsPerBlock),
+                     dim3(kPrepThreads), 0, static_cast<hipStream_t>(stream), a);
+  return check_launch("qsa_compress_groups launch");
 }

@@ -176,6 +176,39 @@ int launch_topk(TopkArgs a, int rows, int cols, void* workspace, size_t workspac
   return QSA_OK;
 }
 
+// Expansion of caller-chosen block ids (expand_qsa_block_indices_cuda,
+// ops/qsa.py:18-106, 552-591): rank i < topk is block_indices[row, i], in the
+// caller's order; everything else as in topk_expand's writer.
+struct ExpandBlocksArgs {
+  const int32_t* blocks;
+  int64_t block_row_stride, block_col_stride;
+  int32_t* out;
+  int64_t out_row_stride;
+  int topk;
+  ExpandMeta meta;
+};
+
+constexpr int kExpandThreads = 256;
+
+__global__ __launch_bounds__(kExpandThreads) void expand_blocks_kernel(const ExpandBlocksArgs a) {
+  __shared__ int tail_page[kTailSlots];
+  extern __shared__ int sel[];  // block ids, then their first tokens' slots
+  const int row = blockIdx.x;
+  const int tid = threadIdx.x;
+  const RowPrefetch f =
+      prefetch_tail<true>(a.meta, a.meta.token_to_req[row], (int)a.meta.positions[row]);
+  const int32_t* brow = a.blocks + (int64_t)row * a.block_row_stride;
+  for (int i = tid; i < a.topk; i += kExpandThreads) {
+    const int b = brow[(int64_t)i * a.block_col_stride];
+    sel[i] = b;
+    sel[a.topk + i] =
+        (a.meta.physical && b >= 0) ? first_slot(a.meta, block_page(a.meta, f.r, b, true), b) : -1;
+  }
+  if (tid < kTailSlots && tid < a.meta.ratio - 1) tail_page[tid] = f.tail_ok ? f.tail_pp : -1;
+  lds_barrier();
+  write_expanded(a.meta, f.r, row, a.topk, sel, tail_page, a.out + (int64_t)row * a.out_row_stride);
+}
+
 int check_common(const float* scores, int rows, int cols, const int32_t* lengths,
                  const int32_t* output, int topk, const char* name) {
   if (rows < 0 || cols < 0) return fail(QSA_ERR_INVALID, std::string(name) + ": negative shape");
@@ -261,4 +294,55 @@ extern "C" int qsa_topk_expand(const float* scores, int64_t score_row_stride, in
   a.meta.store_counts = store_counts ? 1 : 0;
   return launch_topk<true>(a, rows, cols, workspace, workspace_bytes,
                            static_cast<hipStream_t>(stream));
+}
+
+extern "C" int qsa_expand_block_indices(const int32_t* block_indices, int64_t block_row_stride,
+                                        int64_t block_col_stride, int block_cols, int rows,
+                                        int topk, const int64_t* positions,
+                                        const int32_t* sequence_lengths, int num_requests,
+                                        const int32_t* token_to_req, const int32_t* table,
+                                        int64_t table_row_stride, int table_width,
+                                        int32_t* output, int64_t output_row_stride,
+                                        int64_t output_col_stride, int output_width,
+                                        int32_t* counts, int ratio, int page_size, int physical,
+                                        int store_counts, void* stream) {
+  if (rows < 0) return fail(QSA_ERR_INVALID, "qsa_expand_block_indices: negative rows");
+  if (rows == 0) return QSA_OK;
+  if (ratio <= 0 || topk <= 0 || topk > kMaxTopk)
+    return fail(QSA_ERR_INVALID, "qsa_expand_block_indices: ratio and topk must be positive "
+                                 "(topk at most 8192)");
+  if (block_cols < topk)
+    return fail(QSA_ERR_INVALID, "qsa_expand_block_indices: fewer block columns than topk");
+  if (!block_indices || !positions || !sequence_lengths || !token_to_req || !output)
+    return fail(QSA_ERR_INVALID, "qsa_expand_block_indices: null tensor pointer");
+  if (physical && (!table || page_size <= 0))
+    return fail(QSA_ERR_INVALID,
+                "qsa_expand_block_indices: physical mapping needs a table and page_size");
+  if (store_counts && !counts) return fail(QSA_ERR_INVALID, "qsa_expand_block_indices: null counts");
+  ExpandBlocksArgs a = {};
+  a.blocks = block_indices;
+  a.block_row_stride = block_row_stride;
+  a.block_col_stride = block_col_stride;
+  a.out = output;
+  a.out_row_stride = output_row_stride;
+  a.topk = topk;
+  a.meta.positions = positions;
+  a.meta.sequence_lengths = sequence_lengths;
+  a.meta.token_to_req = token_to_req;
+  a.meta.table = physical ? table : nullptr;
+  a.meta.counts = counts;
+  a.meta.table_row_stride = table_row_stride;
+  a.meta.out_col_stride = output_col_stride;
+  a.meta.num_requests = num_requests;
+  a.meta.table_width = physical ? table_width : 0;
+  a.meta.page_size = page_size > 0 ? page_size : 1;
+  a.meta.page_div = FastDiv::make(page_size > 0 ? page_size : 1);
+  a.meta.ratio = ratio;
+  a.meta.ratio_div = FastDiv::make(ratio);
+  a.meta.out_width = output_width;
+  a.meta.physical = physical ? 1 : 0;
+  a.meta.store_counts = store_counts ? 1 : 0;
+  hipLaunchKernelGGL(expand_blocks_kernel, dim3(rows), dim3(kExpandThreads),
+                     (size_t)2 * topk * sizeof(int), static_cast<hipStream_t>(stream), a);
+  return check_launch("qsa_expand_block_indices launch");
 }

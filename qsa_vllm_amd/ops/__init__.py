@@ -3,11 +3,15 @@
 from .indexer import qsa_select_paged_decode, qsa_select_paged_prefill, select_paged_tokens
 from .normalization import IndexerRMSNorm, indexer_norm_rope, rotary_cache
 from .prepare import qsa_prepare
-from .qsa import qsa_select_paged_tokens, qsa_sparse_paged_attention
+from .qsa import (expand_qsa_block_indices_cuda, qsa_compress_groups_with_ratio,
+                  qsa_select_paged_tokens, qsa_sparse_paged_attention, qsa_store_cache_rows)
 from .topk import topk, topk_expand
 
 __all__ = [
     "IndexerRMSNorm",
+    "expand_qsa_block_indices_cuda",
+    "qsa_compress_groups_with_ratio",
+    "qsa_store_cache_rows",
     "indexer_norm_rope",
     "qsa_prepare",
     "qsa_select_paged_decode",

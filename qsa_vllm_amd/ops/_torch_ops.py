@@ -34,6 +34,16 @@ _SCHEMAS = {
         "Tensor k_work, Tensor main_key, Tensor main_value, Tensor(d!) main_key_cache, "
         "Tensor(e!) main_value_cache, Tensor main_slots, int num_index_heads, "
         "int index_head_dim, int rotary_dim, int compress_ratio) -> ()"),
+    "store_cache_rows": "store_cache_rows(Tensor(a!) cache, Tensor slot_mapping, Tensor rows) -> ()",
+    "compress_groups": (
+        "compress_groups(Tensor raw_keys, Tensor? raw_positions, Tensor state_cache, "
+        "Tensor? rope_cache, Tensor state_table, Tensor token_to_req, Tensor query_start_loc, "
+        "Tensor logical_positions, Tensor compressed_slots, int ratio, Tensor(a!) pooled, "
+        "Tensor(b!) first_positions) -> ()"),
+    "expand_block_indices": (
+        "expand_block_indices(Tensor block_indices, Tensor positions, Tensor sequence_lengths, "
+        "Tensor token_to_req, Tensor table, Tensor(a!) output, Tensor(b!) counts, int ratio, "
+        "int topk, int page_size, bool physical, bool store_counts) -> ()"),
     "indexer_norm_rope": (
         "indexer_norm_rope(Tensor values, Tensor weight, Tensor positions, Tensor cos_sin, "
         "float eps, int rotary_dim, Tensor(a!) out) -> ()"),
@@ -290,6 +300,111 @@ def _indexer_norm_rope_impl(values, weight, positions, cos_sin, eps, rotary_dim,
                   _ptr(out), _stream(dev))
 
 
+def _store_cache_rows_impl(cache, slot_mapping, rows):
+    dev = _on_gpu(cache, slot_mapping, rows)
+    _dtype(cache, torch.bfloat16, "cache")
+    _require(cache.dim() == 4 and cache.stride(3) == 1, "cache must be [blocks, page, heads, width] "
+             "with unit width stride")
+    if rows.dim() == 3:
+        rows = rows[:, 0]
+    _dtype(rows, torch.bfloat16, "rows")
+    _require(rows.dim() == 2 and rows.stride(1) == 1 and rows.size(1) >= cache.size(3),
+             "rows must be [rows, >= width] with unit dim stride")
+    _positions(slot_mapping, rows.size(0), "slot_mapping")
+    _require(slot_mapping.numel() <= 1 or slot_mapping.stride(0) == 1, "slot_mapping must be contiguous")
+    if rows.size(0) == 0:
+        return
+    with torch.cuda.device(dev):
+        _lib.call("qsa_store_cache_rows", _ptr(cache), _stride(cache, 0), _stride(cache, 1),
+                  cache.size(0), cache.size(1), cache.size(3), _ptr(slot_mapping), _ptr(rows),
+                  _stride(rows, 0), rows.size(0), _stream(dev))
+
+
+def _compress_groups_impl(raw_keys, raw_positions, state_cache, rope_cache, state_table,
+                          token_to_req, query_start_loc, logical_positions, compressed_slots,
+                          ratio, pooled, first_positions):
+    dev = _on_gpu(raw_keys, raw_positions, state_cache, rope_cache, state_table, token_to_req,
+                  query_start_loc, logical_positions, compressed_slots, pooled, first_positions)
+    _dtype(raw_keys, torch.bfloat16, "raw_keys")
+    _require(raw_keys.dim() == 3 and raw_keys.size(1) == 1 and raw_keys.stride(2) == 1,
+             "raw_keys must be [rows, 1, dim] with unit dim stride")
+    dim = raw_keys.size(2)
+    _dtype(state_cache, torch.bfloat16, "compressor_state_cache")
+    _require(state_cache.dim() == 4 and state_cache.size(2) == 1 and state_cache.stride(3) == 1
+             and state_cache.size(3) >= dim,
+             "compressor_state_cache must be [blocks, ring, 1, >= dim] with unit dim stride")
+    _vector(token_to_req, torch.int32, "token_to_req")
+    rows = token_to_req.numel()
+    _vector(query_start_loc, torch.int32, "query_start_loc")
+    _dtype(state_table, torch.int32, "compressor_state_block_table")
+    _require(state_table.dim() == 2 and state_table.size(0) >= query_start_loc.numel() - 1,
+             "compressor_state_block_table must be [requests, width]")
+    for t, name in ((logical_positions, "logical_positions"), (compressed_slots, "compressed_slots")):
+        _positions(t, rows, name)
+        _require(t.numel() <= 1 or t.stride(0) == 1, f"{name} must be contiguous")
+    _require(raw_keys.size(0) >= rows, "raw_keys has fewer rows than token_to_req")
+    _dtype(pooled, torch.bfloat16, "pooled")
+    _require(pooled.dim() == 3 and pooled.size(0) >= rows and pooled.size(2) == dim
+             and pooled.stride(2) == 1, "pooled must be [rows, 1, dim]")
+    _dtype(first_positions, torch.int64, "first_positions")
+    _require(first_positions.dim() == 2 and first_positions.size(1) >= 3,
+             "first_positions must be [rows, 3]")
+    rp = (0, 0)
+    if rope_cache is not None:
+        _dtype(rope_cache, torch.int64, "rope_cache")
+        _require(rope_cache.dim() == 4 and rope_cache.size(3) >= 3, "rope_cache must be "
+                 "[blocks, ring, 1, >= 3] int64")
+        _dtype(raw_positions, torch.int64, "raw_positions")
+        _require(raw_positions.dim() == 3 and raw_positions.size(2) >= 3,
+                 "raw_positions must be [rows, 1, >= 3] int64")
+        rp = (_stride(raw_positions, 0), _stride(raw_positions, 2))
+    if rows == 0:
+        return
+    with torch.cuda.device(dev):
+        _lib.call("qsa_compress_groups", _ptr(raw_keys), _stride(raw_keys, 0),
+                  _ptr(raw_positions if rope_cache is not None else None), rp[0], rp[1],
+                  _ptr(state_cache), _stride(state_cache, 0), _stride(state_cache, 1),
+                  state_cache.size(1), state_cache.size(0),
+                  _ptr(rope_cache), _stride(rope_cache, 0) if rope_cache is not None else 0,
+                  _stride(rope_cache, 1) if rope_cache is not None else 0,
+                  _stride(rope_cache, 3) if rope_cache is not None else 0,
+                  _ptr(state_table), _stride(state_table, 0), _ptr(token_to_req),
+                  _ptr(query_start_loc), query_start_loc.numel() - 1, _ptr(logical_positions),
+                  _ptr(compressed_slots), rows, dim, int(ratio), _ptr(pooled),
+                  _stride(pooled, 0), _ptr(first_positions), _stride(first_positions, 0),
+                  first_positions.stride(1), _stream(dev))
+
+
+def _expand_block_indices_impl(block_indices, positions, sequence_lengths, token_to_req, table,
+                               output, counts, ratio, topk, page_size, physical, store_counts):
+    dev = _on_gpu(block_indices, positions, sequence_lengths, token_to_req, table, output, counts)
+    _dtype(block_indices, torch.int32, "block_indices")
+    _require(block_indices.dim() == 2, "block_indices must be [rows, blocks]")
+    rows = block_indices.size(0)
+    _positions(positions, rows, "query_positions")
+    _vector(sequence_lengths, torch.int32, "sequence_lengths")
+    _vector(token_to_req, torch.int32, "token_to_req", rows)
+    _dtype(output, torch.int32, "output")
+    _require(output.dim() == 2 and output.size(0) >= rows, "output must be [rows, width]")
+    if physical:
+        _dtype(table, torch.int32, "main_block_table")
+        _require(table.dim() == 2 and (table.size(1) <= 1 or table.stride(1) == 1),
+                 "main_block_table must be [requests, width] with unit column stride")
+    if store_counts:
+        _vector(counts, torch.int32, "valid_counts_out", rows)
+    if rows == 0:
+        return
+    with torch.cuda.device(dev):
+        _lib.call("qsa_expand_block_indices", _ptr(block_indices), _stride(block_indices, 0),
+                  _stride(block_indices, 1), block_indices.size(1), rows, int(topk),
+                  _ptr(positions), _ptr(sequence_lengths), sequence_lengths.numel(),
+                  _ptr(token_to_req), _ptr(table if physical else None),
+                  table.stride(0) if physical else 0, table.size(1) if physical else 0,
+                  _ptr(output), _stride(output, 0), output.stride(1), output.size(1),
+                  _ptr(counts if store_counts else None), int(ratio), int(page_size),
+                  1 if physical else 0, 1 if store_counts else 0, _stream(dev))
+
+
 def _cache_strides(k_cache, name):
     _dtype(k_cache, torch.bfloat16, name)
     _require(k_cache.dim() in (3, 4), f"{name} must be [blocks, page, (1,) dim]")
@@ -443,6 +558,9 @@ _IMPLS = {
     "sparse_attention_merge": _sparse_attention_merge_impl,
     "indexer_prepare": _indexer_prepare_impl,
     "indexer_norm_rope": _indexer_norm_rope_impl,
+    "store_cache_rows": _store_cache_rows_impl,
+    "compress_groups": _compress_groups_impl,
+    "expand_block_indices": _expand_block_indices_impl,
 }
 
 _library = None

@@ -2,8 +2,12 @@
 
 Same entry points and signatures as the reference ``yulan_qsa_vllm/ops/qsa.py``:
 ``qsa_sparse_paged_attention`` (:594-688) and ``qsa_select_paged_tokens``
-(:753-782). The split-K kernel and the LSE merge run in ``libqsa_hip.so``
-behind ``torch.ops.yulan_qsa_kernels.sparse_attention``.
+(:753-782), plus the module's helpers that nothing in the plugin calls:
+``expand_qsa_block_indices_cuda`` (:552-591), ``qsa_store_cache_rows``
+(:691-706) and ``qsa_compress_groups_with_ratio`` (:709-750). The split-K
+kernel and the LSE merge run in ``libqsa_hip.so`` behind
+``torch.ops.yulan_qsa_kernels.sparse_attention``; the helpers behind
+``expand_block_indices``, ``store_cache_rows`` and ``compress_groups``.
 
 ``decode_config`` keeps the reference's ``(block_n, target_splits, warps)``
 tuple; only ``target_splits`` is meaningful here (the HIP kernel walks fixed
@@ -96,3 +100,74 @@ def qsa_select_paged_tokens(
         num_decode_tokens=num_decode_tokens, decode_query_len=decode_query_len,
         visible_blocks=visible_blocks,
     )
+
+
+def expand_qsa_block_indices_cuda(
+    block_indices: torch.Tensor,
+    query_positions: torch.Tensor,
+    sequence_lengths: torch.Tensor,
+    token_to_req: torch.Tensor,
+    compress_ratio: int,
+    token_topk: int,
+    out: torch.Tensor | None = None,
+    *,
+    main_block_table: torch.Tensor | None = None,
+    main_page_size: int = 1,
+    valid_counts_out: torch.Tensor | None = None,
+) -> torch.Tensor:
+    """Expand caller-chosen complete blocks (rank i = column i of
+    ``block_indices``) plus the visible causal tail into token ids or, with
+    ``main_block_table``, physical slots (ops/qsa.py:552-591)."""
+    output_width = token_topk + compress_ratio - 1
+    if out is None:
+        out = torch.empty((block_indices.shape[0], output_width), dtype=torch.int32,
+                          device=block_indices.device)
+    if not block_indices.shape[0]:
+        return out
+    physical = main_block_table is not None
+    torch.ops.yulan_qsa_kernels.expand_block_indices(
+        block_indices, query_positions, sequence_lengths, token_to_req,
+        main_block_table if physical else out, out,
+        valid_counts_out if valid_counts_out is not None else out,
+        int(compress_ratio), int(token_topk // compress_ratio), int(main_page_size), physical,
+        valid_counts_out is not None)
+    return out
+
+
+def qsa_store_cache_rows(cache: torch.Tensor, slot_mapping: torch.Tensor,
+                         rows: torch.Tensor) -> None:
+    """Write bf16 raw or compressed key rows into cache pages at their slots
+    (ops/qsa.py:691-706)."""
+    if rows.ndim == 3:
+        rows = rows[:, 0]
+    if not rows.shape[0]:
+        return
+    torch.ops.yulan_qsa_kernels.store_cache_rows(cache, slot_mapping, rows)
+
+
+def qsa_compress_groups_with_ratio(
+    raw_keys: torch.Tensor,
+    raw_positions: torch.Tensor,
+    compressor_state_cache: torch.Tensor,
+    compressor_state_block_table: torch.Tensor,
+    token_to_req: torch.Tensor,
+    query_start_loc: torch.Tensor,
+    logical_positions: torch.Tensor,
+    compressed_slots: torch.Tensor,
+    compress_ratio: int,
+    rope_cache: torch.Tensor | None = None,
+) -> tuple[torch.Tensor, torch.Tensor]:
+    """fp32 mean of each complete group across the prior ring and the current
+    chunk, and the group's first position (ops/qsa.py:709-750). Returns
+    ``(pooled [rows, 1, dim], first_positions [rows, 3] int64)``."""
+    rows = token_to_req.numel()
+    pooled = torch.empty((rows, 1, raw_keys.shape[2]), dtype=raw_keys.dtype,
+                         device=raw_keys.device)
+    first_positions = torch.empty((rows, 3), dtype=torch.int64, device=raw_keys.device)
+    if not rows:
+        return pooled, first_positions
+    torch.ops.yulan_qsa_kernels.compress_groups(
+        raw_keys, raw_positions if rope_cache is not None else None, compressor_state_cache,
+        rope_cache, compressor_state_block_table, token_to_req, query_start_loc,
+        logical_positions, compressed_slots, int(compress_ratio), pooled, first_positions)
+    return pooled, first_positions

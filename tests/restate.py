@@ -160,3 +160,49 @@ def prepare_request(chunk_positions, chunk_keys, ring, ratio, state_size, k_gamm
     for p in chunk_positions[-state_size:]:
         after[p % state_size] = raw[p]
     return groups, after
+
+
+def pool_rows(rows_req, rows_pos, rows_slot, qsl, ring_blocks, ring, raw, ratio, ring_size,
+              raw_pos=None, ring_pos=None):
+    """Per row: the mean of the group ending at its position, walking member
+    positions and looking each up among the request's chunk rows (by position)
+    or its ring (by position mod ring size); 0 for rows that close no valid
+    group. Also the group's first position (3 columns). fp32 sums in member
+    order via f32, the mean rounded to bf16."""
+    out, firsts = [], []
+    dim = len(raw[0])
+    nreq = len(qsl) - 1
+    for row, (q, end, slot) in enumerate(zip(rows_req, rows_pos, rows_slot)):
+        if not (0 <= q < nreq):
+            out.append([0.0] * dim)
+            firsts.append([0, 0, 0])
+            continue
+        chunk = {}
+        for r in range(qsl[q], qsl[q + 1]):
+            chunk[end - (row - r)] = r        # positions run with the rows inside a chunk
+        block = ring_blocks[q]
+        ok = qsl[q] <= row < qsl[q + 1] and end >= ratio - 1 and slot >= 0
+        if not ok:
+            out.append([0.0] * dim)
+            firsts.append([0, 0, 0])
+            continue
+        acc = [0.0] * dim
+        for p in range(end - ratio + 1, end + 1):
+            if p in chunk:
+                key = raw[chunk[p]]
+            elif p < min(chunk) and 0 <= block < len(ring):
+                key = ring[block][p % ring_size]
+            else:
+                key = [0.0] * dim
+            acc = [f32(a + v) for a, v in zip(acc, key)]
+        out.append([bf16(f32(a / ratio)) for a in acc])
+        first = end - ratio + 1
+        if raw_pos is None:
+            firsts.append([first] * 3)
+        elif first in chunk:
+            firsts.append(list(raw_pos[chunk[first]][:3]))
+        elif 0 <= block < len(ring):
+            firsts.append(list(ring_pos[block][first % ring_size][:3]))
+        else:
+            firsts.append([0, 0, 0])
+    return out, firsts
