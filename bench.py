@@ -30,7 +30,7 @@ import time
 METRIC = "QSA decode tokens/s + sparse-attn HBM GB/s (% of peak), 32k ctx, 1 MI355X"
 HBM_PEAK_GBPS = 8000.0
 BF16_PEAK_TFLOPS = 2500.0
-WORKLOADS = ("decode_32k", "decode_long_skew", "prefill_8k_on_16k")
+WORKLOADS = ("decode_32k", "decode_long_skew", "prefill_8k_on_16k", "hybrid_decoder_step")
 
 
 def parse_args():
@@ -99,6 +99,8 @@ def main():
 
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
+    if args.workload == "hybrid_decoder_step":
+        return run_hybrid(args, dev)
     t0 = time.time()
     wl = make_workload(args.workload, device=dev)
     s = wl.shape
@@ -516,6 +518,164 @@ def run_prefill(args, wl):
         "attention_gathered_gbps": round(gathered / (attn_ms * 1e-3) / 1e9, 1),
         "attention_gathered_bytes": gathered,
         "prepare": time_prepare(wl, stream, rounds=5, reps=4),
+    }
+    print(json.dumps(result), flush=True)
+    return 0
+
+
+HYBRID_DECODES, HYBRID_CHUNKS, HYBRID_CHUNK = 112, 16, 512
+
+
+def hybrid_workload(dev, seed=11):
+    """The hybrid decoder's mixed continuous batch: 112 decode requests at
+    contexts U[4096, 32768], then 16 prefill chunks of 512 tokens on prefixes
+    512 * U{0..31}."""
+    import numpy as np
+
+    from qsa_vllm_amd.hybrid import HybridConfig, make_hybrid_workload
+
+    rng = np.random.default_rng(seed)
+    decode_lens = rng.integers(4096, 32768, HYBRID_DECODES, endpoint=True).tolist()
+    prefixes = (512 * rng.integers(0, 32, HYBRID_CHUNKS)).tolist()
+    return make_hybrid_workload(HybridConfig(), decode_lens=decode_lens, chunk_prefixes=prefixes,
+                                chunk=HYBRID_CHUNK, device=dev, seed=seed)
+
+
+def hybrid_flops(wl):
+    """Projection/MLP GEMM FLOPs of one step (2 per weight per token) plus the
+    LM head rows."""
+    cfg, m = wl.cfg, wl.model
+    tokens = wl.num_tokens
+    per_token = 0
+    for layer in m.layers:
+        mx = layer.mixer
+        mats = [layer.mlp.gate_up_proj, layer.mlp.down_proj]
+        for norm in (layer.input_layernorm, layer.post_attention_layernorm):
+            mats += [norm.gate_down, norm.gate_up]
+        if layer.kind == "full_attention":
+            mats += [mx.qkv_weight, mx.o_proj]
+        else:
+            mats += [mx.in_proj_qkvz, mx.in_proj_ba, mx.out_proj]
+        per_token += sum(w.numel() for w in mats)
+    per_token += m.norm.gate_down.numel() + m.norm.gate_up.numel()
+    return 2 * per_token * tokens + 2 * m.lm_head.numel() * len(wl.scheduled)
+
+
+def run_hybrid(args, dev):
+    """Whole decoder step of the hybrid model on the mixed batch: metadata
+    build, embedding, 32 layers (24 GDN, 8 QSA on the path's kernels), final
+    norm and the LM head rows. Eager launches (a mixed batch is not captured)."""
+    import torch
+
+    t0 = time.time()
+    wl = hybrid_workload(dev)
+    model = wl.model
+    torch.cuda.synchronize()
+    log(f"hybrid workload built in {time.time() - t0:.1f}s: tokens={wl.num_tokens} "
+        f"requests={len(wl.scheduled)} memory={torch.cuda.memory_allocated() / 2**30:.1f} GiB")
+
+    def step():
+        return model.forward(wl.build())
+
+    if args.pmc_run:
+        for _ in range(2):
+            step()
+        torch.cuda.synchronize()
+        log("pmc run: 2 eager hybrid steps")
+        return 0
+    warmup = max(1, min(args.warmup, 3))
+    steps = max(1, min(args.steps, 10))
+    for _ in range(warmup):
+        step()
+    torch.cuda.synchronize()
+    log(f"hybrid warm-up done ({warmup} steps)")
+    stream = torch.cuda.current_stream()
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    wall = time.time()
+    a.record(stream)
+    for _ in range(steps):
+        logits = step()
+    b.record(stream)
+    torch.cuda.synchronize()
+    wall = (time.time() - wall) / steps * 1e3
+    ms_step = a.elapsed_time(b) / steps
+    if not torch.isfinite(logits).all():
+        raise SystemExit("non-finite logits: results invalid")
+
+    # Per-part times from one more step with events between the parts.
+    batch = wl.build()
+    marks = []
+
+    def mark(name):
+        e = torch.cuda.Event(enable_timing=True)
+        e.record(stream)
+        marks.append((name, e))
+
+    mark("start")
+    hidden, residual = model.embed(batch.token_ids), None
+    for layer in model.layers:
+        if residual is None:
+            residual = hidden
+            normalized = layer.input_layernorm(hidden)
+        else:
+            normalized, residual = layer.input_layernorm(hidden, residual)
+        mark("norms")
+        hidden = layer.mixer(normalized, batch)
+        mark("qsa_mixer" if layer.kind == "full_attention" else "gdn_mixer")
+        normalized, residual = layer.post_attention_layernorm(hidden, residual)
+        mark("norms")
+        hidden = layer.mlp(normalized)
+        mark("mlp")
+    model.logits(hidden, residual, batch)
+    mark("head")
+    torch.cuda.synchronize()
+    parts = {}
+    for (_, e0), (name, e1) in zip(marks, marks[1:]):
+        parts[name] = parts.get(name, 0.0) + e0.elapsed_time(e1)
+    flops = hybrid_flops(wl)
+    tflops = flops / (ms_step * 1e-3) / 1e12
+    cfg = wl.cfg
+    kinds = [layer.kind for layer in model.layers]
+    result = {
+        "metric": "hybrid decoder step tokens/s (32 layers, 3 GDN : 1 QSA, 112 decode + 16 x 512 "
+                  "prefill), 1 MI355X",
+        "value": round(wl.num_tokens / (ms_step * 1e-3), 1),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": steps,
+        "warmup": warmup,
+        "ms_per_step": round(ms_step, 3),
+        "wall_ms_per_step": round(wall, 3),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic: random-init bf16 weights N(0, 0.02), seeded token ids, random "
+                "cache and GDN-state history",
+        "config": {
+            "workload": f"hybrid decoder step: {cfg.num_layers} layers "
+                        f"({kinds.count('linear_attention')} GDN, {kinds.count('full_attention')} "
+                        f"QSA), hidden {cfg.hidden_size}, TP{cfg.tp_size} share: QSA "
+                        f"{cfg.heads}q/{cfg.kv_heads}kv x {cfg.head_dim}, GDN {cfg.key_heads}k/"
+                        f"{cfg.value_heads}v heads x {cfg.linear_key_head_dim}, MLP "
+                        f"{cfg.intermediate}, vocab shard {cfg.vocab_shard}; batch "
+                        f"{HYBRID_DECODES} decode (context U[4096,32768]) + {HYBRID_CHUNKS} "
+                        f"prefill chunks of {HYBRID_CHUNK}",
+            "tokens": wl.num_tokens,
+            "requests": len(wl.scheduled),
+            "graph": "eager",
+        },
+        "roofline": {
+            "kernel": "whole step (projection, MLP and LM head GEMMs)",
+            "bound": "mfma",
+            "achieved": round(tflops, 1),
+            "peak": BF16_PEAK_TFLOPS,
+            "unit": "TFLOP/s",
+            "frac": round(tflops / BF16_PEAK_TFLOPS, 4),
+            "traffic": None,
+            "algorithmic_flops_per_step": flops,
+        },
+        "breakdown_ms": {k: round(v, 3) for k, v in parts.items()},
     }
     print(json.dumps(result), flush=True)
     return 0

@@ -11,5 +11,6 @@ loudly when its HIP library is missing.
 from .qsa_oracle import *  # noqa: F401,F403
 from .qsa_oracle import __all__ as _path_all
 from .qsa_prepare_oracle import norm_rope, prepare, rotary_cache_table  # noqa: F401
+from . import hybrid_oracle as hybrid  # noqa: F401
 
-__all__ = list(_path_all) + ["norm_rope", "prepare", "rotary_cache_table"]
+__all__ = list(_path_all) + ["norm_rope", "prepare", "rotary_cache_table", "hybrid"]

@@ -1,0 +1,153 @@
+"""The hybrid decoder step on the GPU against the CPU oracle.
+
+A small model (GDN and QSA layers at the serving head shapes, small hidden
+size) steps one mixed batch: decode requests, then ragged prefill chunks.
+Contexts stay below the top-k budget, so every QSA row selects its whole
+causal context and the oracle's QSA layer is dense causal attention over the
+paged cache. Each layer is checked on the GPU layer's own inputs (so rounding
+does not accumulate across layers), then the final norm and LM head."""
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from oracle import hybrid as H
+from qsa_vllm_amd.hybrid import HybridConfig, make_hybrid_workload
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda:0"
+
+CFG = HybridConfig(num_layers=4, hidden_size=256, vocab_size=512, tp_size=2, num_heads=32,
+                   num_kv_heads=4, head_dim=128, intermediate_size=1024, linear_num_key_heads=4,
+                   linear_num_value_heads=8, indexer_heads=8, token_topk=2048, init_std=0.05)
+
+
+def _workload(seed):
+    return make_hybrid_workload(CFG, decode_lens=[700, 1500, 33, 260], chunk_prefixes=[0, 300, 1000],
+                                chunk=100, device=DEV, seed=seed, state_std=0.05)
+
+
+def _cpu(t):
+    return t.detach().cpu()
+
+
+def _norm_args(n):
+    return (_cpu(n.weight), _cpu(n.gate_down), _cpu(n.gate_up), _cpu(n.gate_up_bias), CFG.rms_norm_eps)
+
+
+def _close(got, want, what, rel_max=0.03, rel_mean=3e-3):
+    got, want = got.double().cpu(), want.double().cpu()
+    err = (got - want).abs()
+    scale = want.abs().max().item()
+    print(f"[hybrid] {what}: max_err={err.max().item():.3e} mean_err={err.mean().item():.3e} "
+          f"scale={scale:.3e}", flush=True)
+    assert err.max().item() <= rel_max * scale and err.mean().item() <= rel_mean * scale, what
+
+
+def _sequences(wl):
+    starts = np.concatenate(([0], np.cumsum(wl.scheduled)[:-1]))
+    return [(list(range(int(s), int(s) + n)), int(slot))
+            for s, n, slot in zip(starts, wl.scheduled, wl.state_slots)]
+
+
+def _oracle_qsa(mixer, x, batch, kv0):
+    """Projection, K/V writes, dense causal attention with the output gate, o_proj."""
+    qkv = H.bf16(x.double() @ _cpu(mixer.qkv_weight).double().T + _cpu(mixer.qkv_bias).double())
+    query, gate, key, value, _ = H.qsa_projection_split(qkv, mixer.heads, mixer.kv_heads,
+                                                        mixer.head_dim, mixer.index_size)
+    kv = kv0.clone()
+    page = kv.shape[1]
+    d = mixer.head_dim
+    for t, slot in enumerate(_cpu(batch.qsa.main.slot_mapping).tolist()):
+        kv[slot // page, slot % page, :, :d] = key[t]
+        kv[slot // page, slot % page, :, d:] = value[t]
+    positions = _cpu(batch.qsa.positions)
+    width = CFG.output_width
+    indices = torch.full((x.shape[0], width), -1, dtype=torch.int32)
+    for t, p in enumerate(positions.tolist()):
+        indices[t, :p + 1] = torch.arange(p + 1, dtype=torch.int32)
+    core = oracle.sparse_attention(query.contiguous(), kv[..., :d], kv[..., d:], indices,
+                                   _cpu(batch.qsa.main.block_table), _cpu(batch.qsa.token_to_req),
+                                   output_gate=gate.contiguous())
+    return H.bf16(H.bf16(core).reshape(x.shape[0], -1).double() @ _cpu(mixer.o_proj).double().T), kv
+
+
+def _gdn_params(m):
+    return {"in_proj_qkvz": _cpu(m.in_proj_qkvz), "in_proj_ba": _cpu(m.in_proj_ba),
+            "conv_weight": _cpu(m.conv_weight), "A_log": _cpu(m.A_log),
+            "dt_bias": _cpu(m.dt_bias), "norm_weight": _cpu(m.norm_weight),
+            "out_proj": _cpu(m.out_proj)}
+
+
+def test_hybrid_step_layers_against_oracle():
+    wl = _workload(seed=5)
+    model = wl.model
+    batch = wl.build()
+    torch.cuda.synchronize()
+    print(f"[hybrid] tokens={wl.num_tokens} decodes={batch.num_decode_tokens} "
+          f"layers={[l.kind for l in model.layers]}", flush=True)
+    hidden, residual = model.embed(batch.token_ids), None
+    assert torch.equal(_cpu(hidden), _cpu(model.embed_tokens)[torch.as_tensor(wl.token_ids)])
+    for i, layer in enumerate(model.layers):
+        x_in = _cpu(hidden)
+        r_in = None if residual is None else _cpu(residual)
+        mixer = layer.mixer
+        if layer.kind == "linear_attention":
+            conv0, ssm0 = _cpu(mixer.conv_state).clone(), _cpu(mixer.ssm_state).clone()
+        else:
+            kv0 = _cpu(mixer.layer.kv_cache.permute(0, 2, 1, 3))
+        hidden, residual = layer(hidden, residual, batch)
+        torch.cuda.synchronize()
+        # oracle on the same inputs
+        if r_in is None:
+            n, res = H.gated_norm(x_in, None, *_norm_args(layer.input_layernorm))
+            res = x_in
+        else:
+            n, res = H.gated_norm(x_in, r_in, *_norm_args(layer.input_layernorm))
+        if layer.kind == "linear_attention":
+            mixed = H.gdn_mixer(n, _gdn_params(mixer), conv0, ssm0, _sequences(wl),
+                                key_heads=mixer.hk, value_heads=mixer.hv, key_dim=mixer.dk,
+                                value_dim=mixer.dv, eps=CFG.rms_norm_eps)
+            # the conv state holds projection outputs: rounding-level differences
+            _close(_cpu(mixer.conv_state), conv0, f"layer {i} conv state", 1e-2, 1e-4)
+            _close(_cpu(mixer.ssm_state), ssm0, f"layer {i} gdn state", 1e-2, 1e-3)
+        else:
+            mixed, kv = _oracle_qsa(mixer, n, batch, kv0)
+            # every row attended over its whole causal context
+            counts = (_cpu(mixer.layer.topk_indices_buffer[:wl.num_tokens]) >= 0).sum(1)
+            assert torch.equal(counts, _cpu(batch.qsa.positions) + 1), f"layer {i} selection"
+            slots = _cpu(batch.qsa.main.slot_mapping).long()
+            page = kv.shape[1]
+            got_kv = _cpu(mixer.layer.kv_cache.permute(0, 2, 1, 3))
+            _close(got_kv[slots // page, slots % page], kv[slots // page, slots % page],
+                   f"layer {i} written K/V rows", 1e-2, 1e-3)
+            got_kv[slots // page, slots % page] = kv[slots // page, slots % page]
+            assert torch.equal(got_kv, kv), f"layer {i} K/V rows outside the batch's slots"
+        n2, res2 = H.gated_norm(mixed, res, *_norm_args(layer.post_attention_layernorm))
+        out = H.swiglu(n2, _cpu(layer.mlp.gate_up_proj), _cpu(layer.mlp.down_proj))
+        _close(_cpu(residual), res2, f"layer {i} ({layer.kind}) residual")
+        _close(_cpu(hidden), out, f"layer {i} ({layer.kind}) output")
+    logits = model.logits(hidden, residual, batch)
+    final, _ = H.gated_norm(_cpu(hidden), _cpu(residual), *_norm_args(model.norm))
+    rows = _cpu(batch.logits_rows)
+    want = H.bf16(final[rows].double() @ _cpu(model.lm_head).double().T)
+    _close(_cpu(logits), want, "logits")
+
+
+def test_hybrid_forward_matches_layerwise_run():
+    a, b = _workload(seed=6), _workload(seed=6)
+    batch_a, batch_b = a.build(), b.build()
+    logits_a = a.model.forward(batch_a)
+    hidden, residual = b.model.embed(batch_b.token_ids), None
+    for layer in b.model.layers:
+        hidden, residual = layer(hidden, residual, batch_b)
+    logits_b = b.model.logits(hidden, residual, batch_b)
+    torch.cuda.synchronize()
+    assert torch.equal(logits_a, logits_b)
+    for la, lb in zip(a.model.layers, b.model.layers):
+        if la.kind == "linear_attention":
+            assert torch.equal(la.mixer.ssm_state, lb.mixer.ssm_state)
+            assert torch.equal(la.mixer.conv_state, lb.mixer.conv_state)
+        else:
+            assert torch.equal(la.mixer.layer.kv_cache, lb.mixer.layer.kv_cache)
