@@ -290,6 +290,77 @@ int qsa_sparse_attention_merge(const float* partial_out, const float* partial_ls
                                int64_t gate_head_stride, int64_t gate_dim_stride,
                                void* stream);
 
+/* ------------------------------------------------------------------------ */
+/* Hybrid decoder layers around the path (the model's other token mixers)    */
+/* ------------------------------------------------------------------------ */
+
+/*
+ * Replaces YuLanGatedNorm.forward (model.py:85-98) with vLLM's fused
+ * residual-add RMSNorm inside: when residual_in is given, residual_out =
+ * bf16(x + residual_in) (may alias residual_in) and the norm runs on it;
+ * out = n * bf16(sigmoid(gate_up(silu(gate_down(n))) + bias)) with
+ * n = bf16(bf16(x * rsqrt(mean(x^2) + eps)) * weight). gate_down [rank, hidden],
+ * gate_up [hidden, rank], rank 16, hidden a multiple of 512 up to 4096.
+ */
+int qsa_gated_norm(const void* x, int64_t x_stride, const void* residual_in,
+                   int64_t residual_in_stride, void* residual_out, int64_t residual_out_stride,
+                   const void* weight, const void* gate_down, const void* gate_up,
+                   const void* gate_up_bias, void* out, int64_t out_stride, int rows,
+                   int hidden, int rank, float eps, void* stream);
+
+/*
+ * Replaces the SiluAndMul activation of Qwen2MoeMLP (model.py:211-217, vLLM):
+ * out[t, i] = bf16(silu(gu[t, i]) * gu[t, intermediate + i]) in fp32.
+ */
+int qsa_silu_mul(const void* gate_up, int64_t gate_up_stride, void* out, int64_t out_stride,
+                 int rows, int intermediate, void* stream);
+
+/*
+ * The GDN token mixer of the linear-attention layers (model.py:205-212:
+ * vLLM's QwenGatedDeltaNetAttention). Sequences are consecutive token ranges
+ * [query_start_loc[s], query_start_loc[s+1]) with state slot slots[s]
+ * (slots outside [0, num_slots) have no state: zero initial state, nothing
+ * stored). Projection rows are grouped per key head [q, k, v (r heads),
+ * z (r heads)] (qkvz) and [b (r), a (r)] (ba); head dims 128.
+ *
+ * qsa_gdn_prep: causal depthwise conv (width conv_kernel, weights
+ * [channels, K]) over each sequence's inputs, the conv state [slots, K-1,
+ * channels] supplying the inputs before the chunk, SiLU, bf16; q_out/k_out
+ * [tokens, key_heads, 128] fp32 l2-normalised (q times 128^-1/2); v_out
+ * [tokens, value_heads, 128] bf16; g_out = -exp(A_log) softplus(a + dt_bias),
+ * beta_out = sigmoid(b), [tokens, value_heads] fp32.
+ */
+int qsa_gdn_prep(const void* qkvz, int64_t qkvz_stride, const void* ba, int64_t ba_stride,
+                 const void* conv_weight, const void* conv_state, int num_slots,
+                 const int32_t* query_start_loc, const int32_t* token_to_seq,
+                 const int64_t* slots, int num_seqs, const float* A_log, const float* dt_bias,
+                 int key_heads, int value_heads, int head_dim, int conv_kernel, int tokens,
+                 float* q_out, float* k_out, void* v_out, float* g_out, float* beta_out,
+                 void* stream);
+
+/* The conv state after the step: each sequence's last K-1 inputs. Run after
+ * qsa_gdn_prep of the same step (which reads the old state). Sequences whose
+ * range leaves [0, tokens) are skipped (also by qsa_gdn_recurrence). */
+int qsa_gdn_conv_state(const void* qkvz, int64_t qkvz_stride, int tokens, void* conv_state,
+                       int num_slots, const int32_t* query_start_loc, const int64_t* slots,
+                       int num_seqs, int key_heads, int value_heads, int head_dim,
+                       int conv_kernel, void* stream);
+
+/* Gated delta rule over each sequence's tokens in order, the state [slots,
+ * value_heads, 128, 128] fp32 updated in place: S <- e^g S,
+ * u = beta (v - S^T k), S <- S + k u^T, o = S^T q; o [tokens, value_heads, 128]
+ * bf16. Value head h reads key head h / (value_heads / key_heads). */
+int qsa_gdn_recurrence(const float* q, const float* k, const void* v, const float* g,
+                       const float* beta, int tokens, float* state, int num_slots,
+                       const int32_t* query_start_loc, const int64_t* slots, int num_seqs,
+                       int key_heads, int value_heads, int head_dim, void* o, void* stream);
+
+/* Gated RMSNorm of the GDN output: y = bf16(rmsnorm(o) * weight * silu(z)) per
+ * (token, value head), z read from the qkvz projection rows. */
+int qsa_gdn_gated_norm(const void* o, const void* qkvz, int64_t qkvz_stride, const void* weight,
+                       float eps, int tokens, int key_heads, int value_heads, int head_dim,
+                       void* y, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

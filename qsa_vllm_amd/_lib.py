@@ -130,6 +130,20 @@ SIGNATURES = {
                                            c_ptr, c_i64, c_i64,
                                            c_ptr, c_i64, c_i64, c_i64,
                                            c_ptr]),
+    "qsa_gated_norm": (c_i32, [c_ptr, c_i64, c_ptr, c_i64, c_ptr, c_i64,
+                               c_ptr, c_ptr, c_ptr, c_ptr, c_ptr, c_i64,
+                               c_i32, c_i32, c_i32, ctypes.c_float, c_ptr]),
+    "qsa_silu_mul": (c_i32, [c_ptr, c_i64, c_ptr, c_i64, c_i32, c_i32, c_ptr]),
+    "qsa_gdn_prep": (c_i32, [c_ptr, c_i64, c_ptr, c_i64, c_ptr, c_ptr, c_i32,
+                             c_ptr, c_ptr, c_ptr, c_i32, c_ptr, c_ptr,
+                             c_i32, c_i32, c_i32, c_i32, c_i32,
+                             c_ptr, c_ptr, c_ptr, c_ptr, c_ptr, c_ptr]),
+    "qsa_gdn_conv_state": (c_i32, [c_ptr, c_i64, c_i32, c_ptr, c_i32, c_ptr, c_ptr, c_i32,
+                                   c_i32, c_i32, c_i32, c_i32, c_ptr]),
+    "qsa_gdn_recurrence": (c_i32, [c_ptr, c_ptr, c_ptr, c_ptr, c_ptr, c_i32, c_ptr, c_i32,
+                                   c_ptr, c_ptr, c_i32, c_i32, c_i32, c_i32, c_ptr, c_ptr]),
+    "qsa_gdn_gated_norm": (c_i32, [c_ptr, c_ptr, c_i64, c_ptr, ctypes.c_float, c_i32, c_i32,
+                                   c_i32, c_i32, c_ptr, c_ptr]),
 }
 
 

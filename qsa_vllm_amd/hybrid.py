@@ -8,8 +8,9 @@ SwiGLU MLP, a final gated norm and the LM head. Layer ``i`` is QSA when
 
 What runs where: the QSA layers call the path's HIP kernels through
 :func:`qsa_vllm_amd.layer_step.qsa_layer_step` (prepare, select, attend); the
-projections are hipBLASLt GEMMs through ``torch.nn.functional.linear``; GDN,
-norms and the MLP activation are PyTorch (:mod:`qsa_vllm_amd.gdn`).
+projections are hipBLASLt GEMMs through ``torch.nn.functional.linear``; the
+gated norms, the MLP activation and the GDN mixer between its projections are
+the HIP kernels of :mod:`qsa_vllm_amd.ops.hybrid_layers`.
 
 Tensor parallelism: the weights held are one rank's share of a TP
 ``tp_size`` model - attention, GDN and MLP heads/intermediate divided by
@@ -46,13 +47,13 @@ import torch
 import torch.nn.functional as F
 
 from .backend import QSALayerState, YuLanQSAImpl, YuLanQSAIndexer
-from .gdn import (conv_decode, conv_prefill, gated_rmsnorm, gdn_chunked, gdn_decode, gdn_gates,
-                  l2norm)
 from .layer_step import qsa_layer_step
 from .metadata import QSABatch, QSAMetadataBuilder
+from .ops.hybrid_layers import (gated_norm, gdn_conv_state, gdn_gated_norm, gdn_prep,
+                                gdn_recurrence, silu_mul)
 
 __all__ = ["HybridConfig", "HybridBatch", "HybridBatchBuilder", "HybridDecoder",
-           "HybridWorkload", "make_hybrid_workload", "rms_norm"]
+           "HybridWorkload", "make_hybrid_workload"]
 
 
 @dataclass(frozen=True)
@@ -84,7 +85,6 @@ class HybridConfig:
     page_size: int = 16
     comp_page_size: int = 16
     init_std: float = 0.02
-    gdn_chunk: int = 64
 
     def layer_types(self) -> list[str]:
         return ["full_attention" if (i + 1) % self.full_attention_every == 0
@@ -145,15 +145,9 @@ class _Init:
         return torch.rand(shape, generator=self.gen, device=self.device) * (high - low) + low
 
 
-def rms_norm(x: torch.Tensor, weight: torch.Tensor, eps: float) -> torch.Tensor:
-    """``bf16(bf16(x * rsqrt(mean(x^2) + eps)) * weight)``, statistics in fp32."""
-    xf = x.float()
-    inv = torch.rsqrt(xf.pow(2).mean(-1, keepdim=True) + eps)
-    return (xf * inv).to(torch.bfloat16) * weight
-
-
 class GatedNorm:
-    """``YuLanGatedNorm`` (``model.py:60-98``)."""
+    """``YuLanGatedNorm`` (``model.py:60-98``) with vLLM's fused residual add:
+    ``norm(x, residual)`` adds ``x`` into ``residual`` in place."""
 
     def __init__(self, cfg: HybridConfig, init: _Init):
         h, r = cfg.hidden_size, cfg.gated_norm_rank
@@ -164,30 +158,20 @@ class GatedNorm:
         self.gate_up_bias = init.normal(h)
 
     def __call__(self, x, residual=None):
-        if residual is not None:
-            x = x + residual
-            residual = x
-        normalized = rms_norm(x, self.weight, self.eps)
-        up = F.linear(F.silu(F.linear(normalized, self.gate_down)), self.gate_up, self.gate_up_bias)
-        gated = normalized * torch.sigmoid(up)
-        return gated if residual is None else (gated, residual)
+        gated, res = gated_norm(x, residual, self.weight, self.gate_down, self.gate_up,
+                                self.gate_up_bias, self.eps)
+        return gated if residual is None else (gated, res)
 
 
 class SwiGLU:
-    """``Qwen2MoeMLP`` with ``hidden_act="silu"``: ``down(silu(gate) * up)``,
-    the activation product in fp32 (vLLM's ``SiluAndMul``)."""
+    """``Qwen2MoeMLP`` with ``hidden_act="silu"``: ``down(silu(gate) * up)``."""
 
     def __init__(self, cfg: HybridConfig, init: _Init):
-        i = cfg.intermediate
-        self.intermediate = i
-        self.gate_up_proj = init.normal(2 * i, cfg.hidden_size)
-        self.down_proj = init.normal(cfg.hidden_size, i)
+        self.gate_up_proj = init.normal(2 * cfg.intermediate, cfg.hidden_size)
+        self.down_proj = init.normal(cfg.hidden_size, cfg.intermediate)
 
     def __call__(self, x):
-        gu = F.linear(x, self.gate_up_proj)
-        i = self.intermediate
-        act = (F.silu(gu[:, :i].float()) * gu[:, i:].float()).to(torch.bfloat16)
-        return F.linear(act, self.down_proj)
+        return F.linear(silu_mul(F.linear(x, self.gate_up_proj)), self.down_proj)
 
 
 class QSAAttention:
@@ -240,7 +224,6 @@ class GatedDeltaNet:
         dk, dv = cfg.linear_key_head_dim, cfg.linear_value_head_dim
         self.hk, self.hv, self.dk, self.dv, self.r = hk, hv, dk, dv, hv // hk
         self.eps = cfg.rms_norm_eps
-        self.chunk = cfg.gdn_chunk
         self.in_proj_qkvz = init.normal(hk * (2 * dk + 2 * self.r * dv), cfg.hidden_size)
         self.in_proj_ba = init.normal(2 * hv, cfg.hidden_size)
         self.conv_weight = init.normal(cfg.conv_dim, cfg.conv_kernel, std=0.5)
@@ -251,55 +234,18 @@ class GatedDeltaNet:
         self.conv_state = init.normal(num_slots, cfg.conv_kernel - 1, cfg.conv_dim, std=1.0)
         self.ssm_state = init.normal(num_slots, hv, dk, dv, std=state_std, dtype=torch.float32)
 
-    def split(self, qkvz, ba):
-        """(q [t, hk, dk], k, v [t, hv, dv], z, b [t, hv], a) views/copies."""
-        t, hk, dk, dv, r = qkvz.shape[0], self.hk, self.dk, self.dv, self.r
-        grp = qkvz.view(t, hk, 2 * dk + 2 * r * dv)
-        q, k = grp[..., :dk], grp[..., dk:2 * dk]
-        v = grp[..., 2 * dk:2 * dk + r * dv].reshape(t, self.hv, dv)
-        z = grp[..., 2 * dk + r * dv:].reshape(t, self.hv, dv)
-        bag = ba.view(t, hk, 2 * r)
-        return q, k, v, z, bag[..., :r].reshape(t, self.hv), bag[..., r:].reshape(t, self.hv)
-
-    def _heads(self, conv):
-        """Normalised, scaled q and k expanded to the value heads, v; fp32."""
-        t, hk, dk = conv.shape[0], self.hk, self.dk
-        q = l2norm(conv[..., :hk * dk].unflatten(-1, (hk, dk))) * dk ** -0.5
-        k = l2norm(conv[..., hk * dk:2 * hk * dk].unflatten(-1, (hk, dk)))
-        v = conv[..., 2 * hk * dk:].unflatten(-1, (self.hv, self.dv)).float()
-        return q.repeat_interleave(self.r, dim=-2), k.repeat_interleave(self.r, dim=-2), v
-
     def __call__(self, x, batch: "HybridBatch"):
         t = x.shape[0]
-        q, k, v, z, b, a = self.split(F.linear(x, self.in_proj_qkvz), F.linear(x, self.in_proj_ba))
-        mixed = torch.cat((q.reshape(t, -1), k.reshape(t, -1), v.reshape(t, -1)), dim=-1)
-        g, beta = gdn_gates(a, b, self.A_log, self.dt_bias)
-        core = torch.empty(t, self.hv, self.dv, dtype=torch.bfloat16, device=x.device)
-        nd = batch.num_decode_tokens
-        if nd:
-            conv = conv_decode(mixed[:nd], self.conv_weight, self.conv_state, batch.decode_slots)
-            qd, kd, vd = self._heads(conv)
-            core[:nd] = gdn_decode(qd, kd, vd, g[:nd], beta[:nd], self.ssm_state,
-                                   batch.decode_slots).to(torch.bfloat16)
-        if t > nd:
-            gather, valid = batch.prefill_gather, batch.prefill_valid
-            conv = conv_prefill(mixed[nd:], self.conv_weight, self.conv_state, batch.prefill_slots,
-                                gather, batch.prefill_tail)                       # [S, L, C]
-            qp, kp, vp = self._heads(conv)                                        # [S, L, H, *]
-            m = valid[..., None, None]
-            zero = torch.zeros((), device=x.device)
-            qp, kp, vp = (torch.where(m, u, zero).transpose(1, 2) for u in (qp, kp, vp))
-            rows = torch.where(valid, gather, torch.zeros_like(gather))
-            gp = torch.where(valid[..., None], g[nd:][rows], zero).transpose(1, 2)
-            bp = torch.where(valid[..., None], beta[nd:][rows], zero).transpose(1, 2)
-            slots = batch.prefill_slots
-            o, final = gdn_chunked(qp.contiguous(), kp.contiguous(), vp.contiguous(),
-                                   gp.contiguous(), bp.contiguous(), self.ssm_state[slots],
-                                   self.chunk)
-            self.ssm_state[slots] = final
-            o = o.transpose(1, 2)[valid].to(torch.bfloat16)                       # [tokens, H, dv]
-            core[nd:][gather[valid]] = o
-        y = gated_rmsnorm(core, z, self.norm_weight, self.eps)
+        qkvz = F.linear(x, self.in_proj_qkvz)
+        ba = F.linear(x, self.in_proj_ba)
+        q, k, v, g, beta = gdn_prep(qkvz, ba, self.conv_weight, self.conv_state,
+                                    batch.query_start_loc, batch.token_to_seq, batch.state_slots,
+                                    self.A_log, self.dt_bias, self.hk, self.hv)
+        gdn_conv_state(qkvz, self.conv_state, batch.query_start_loc, batch.state_slots, self.hk,
+                       self.hv)
+        o = gdn_recurrence(q, k, v, g, beta, self.ssm_state, batch.query_start_loc,
+                           batch.state_slots, self.hk, self.hv)
+        y = gdn_gated_norm(o, qkvz, self.norm_weight, self.eps, self.hk, self.hv)
         return F.linear(y.view(t, -1), self.out_proj)
 
 
@@ -327,21 +273,25 @@ class DecoderLayer:
 @dataclass
 class HybridBatch:
     """One step's inputs: token ids, the QSA metadata (shared by every QSA
-    layer) and the GDN state slots and chunk layout."""
+    layer; its request ranges are the GDN sequences) and the GDN state slots."""
 
     token_ids: torch.Tensor            # int64 [tokens]
     qsa: QSABatch
     num_decode_tokens: int             # leading one-token requests
-    decode_slots: torch.Tensor         # int64 [decodes]
-    prefill_slots: torch.Tensor        # int64 [chunks]
-    prefill_gather: torch.Tensor       # int64 [chunks, L]: row in the prefill part or -1
-    prefill_valid: torch.Tensor        # bool [chunks, L]
-    prefill_tail: torch.Tensor         # int64 [chunks, K-1]: padded rows forming the new conv state
+    state_slots: torch.Tensor          # int64 [requests]
     logits_rows: torch.Tensor          # int64 [requests]: each request's last token
 
     @property
     def num_tokens(self) -> int:
         return self.qsa.num_tokens
+
+    @property
+    def query_start_loc(self) -> torch.Tensor:
+        return self.qsa.raw.query_start_loc
+
+    @property
+    def token_to_seq(self) -> torch.Tensor:
+        return self.qsa.token_to_req
 
 
 class HybridBatchBuilder:
@@ -368,23 +318,10 @@ class HybridBatchBuilder:
               state_slots) -> HybridBatch:
         qsa = self.qsa.build(computed, scheduled, main_table, comp_table, ring_blocks)
         sched = np.asarray(scheduled, dtype=np.int64)
-        slots = np.asarray(state_slots, dtype=np.int64)
-        nd = qsa.compressed.num_decodes
-        lens = sched[nd:]
-        chunk = self.cfg.gdn_chunk
-        width = max(chunk, int(math.ceil(lens.max() / chunk)) * chunk) if lens.size else chunk
-        gather = np.full((lens.size, width), -1, dtype=np.int64)
-        starts = np.concatenate(([0], np.cumsum(lens)[:-1])) if lens.size else np.zeros(0, np.int64)
-        for i, (s, n) in enumerate(zip(starts, lens)):
-            gather[i, :n] = s + np.arange(n)
-        k1 = self.cfg.conv_kernel - 1
-        tail = lens[:, None] + np.arange(k1)[None, :]
-        ends = np.cumsum(sched) - 1
-        return HybridBatch(
-            token_ids=self._dev(token_ids), qsa=qsa, num_decode_tokens=nd,
-            decode_slots=self._dev(slots[:nd]), prefill_slots=self._dev(slots[nd:]),
-            prefill_gather=self._dev(gather), prefill_valid=self._dev(gather >= 0, torch.bool),
-            prefill_tail=self._dev(tail), logits_rows=self._dev(ends))
+        return HybridBatch(token_ids=self._dev(token_ids), qsa=qsa,
+                           num_decode_tokens=qsa.compressed.num_decodes,
+                           state_slots=self._dev(np.asarray(state_slots, dtype=np.int64)),
+                           logits_rows=self._dev(np.cumsum(sched) - 1))
 
 
 class HybridDecoder:

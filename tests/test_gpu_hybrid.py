@@ -13,12 +13,13 @@ import torch
 
 import oracle
 from oracle import hybrid as H
-from qsa_vllm_amd.hybrid import HybridConfig, make_hybrid_workload
+from qsa_vllm_amd.hybrid import GatedDeltaNet, HybridBatchBuilder, HybridConfig, _Init, make_hybrid_workload
+from qsa_vllm_amd.ops import hybrid_layers as L
 
 pytestmark = pytest.mark.gpu
 DEV = "cuda:0"
 
-CFG = HybridConfig(num_layers=4, hidden_size=256, vocab_size=512, tp_size=2, num_heads=32,
+CFG = HybridConfig(num_layers=4, hidden_size=512, vocab_size=512, tp_size=2, num_heads=32,
                    num_kv_heads=4, head_dim=128, intermediate_size=1024, linear_num_key_heads=4,
                    linear_num_value_heads=8, indexer_heads=8, token_topk=2048, init_std=0.05)
 
@@ -128,8 +129,9 @@ def test_hybrid_step_layers_against_oracle():
         out = H.swiglu(n2, _cpu(layer.mlp.gate_up_proj), _cpu(layer.mlp.down_proj))
         _close(_cpu(residual), res2, f"layer {i} ({layer.kind}) residual")
         _close(_cpu(hidden), out, f"layer {i} ({layer.kind}) output")
+    h_in, r_in = _cpu(hidden), _cpu(residual)   # the final norm adds into residual in place
     logits = model.logits(hidden, residual, batch)
-    final, _ = H.gated_norm(_cpu(hidden), _cpu(residual), *_norm_args(model.norm))
+    final, _ = H.gated_norm(h_in, r_in, *_norm_args(model.norm))
     rows = _cpu(batch.logits_rows)
     want = H.bf16(final[rows].double() @ _cpu(model.lm_head).double().T)
     _close(_cpu(logits), want, "logits")
@@ -151,3 +153,106 @@ def test_hybrid_forward_matches_layerwise_run():
             assert torch.equal(la.mixer.conv_state, lb.mixer.conv_state)
         else:
             assert torch.equal(la.mixer.layer.kv_cache, lb.mixer.layer.kv_cache)
+
+
+def _bf16(shape, seed, scale=1.0):
+    g = torch.Generator().manual_seed(seed)
+    return (torch.randn(*shape, generator=g) * scale).to(torch.bfloat16)
+
+
+@pytest.mark.parametrize("rows,hidden,residual", [(37, 512, False), (37, 512, True),
+                                                   (5, 4096, True), (130, 2048, True)])
+def test_gated_norm_kernel_against_oracle(rows, hidden, residual):
+    x = _bf16((rows, hidden), 1, 2.0)
+    res = _bf16((rows, hidden), 2) if residual else None
+    w = (1 + 0.3 * _bf16((hidden,), 3).float()).to(torch.bfloat16)
+    down, up, bias = _bf16((16, hidden), 4, 0.05), _bf16((hidden, 16), 5, 0.3), _bf16((hidden,), 6, 0.5)
+    print(f"[hybrid] gated_norm rows={rows} hidden={hidden} residual={residual}", flush=True)
+    res_dev = res.to(DEV) if residual else None
+    out, res_out = L.gated_norm(x.to(DEV), res_dev, w.to(DEV), down.to(DEV), up.to(DEV),
+                                bias.to(DEV), 1e-6)
+    torch.cuda.synchronize()
+    want, want_res = H.gated_norm(x, res, w, down, up, bias, 1e-6)
+    if residual:
+        assert torch.equal(res_out.cpu(), want_res)      # bf16(x + r) is exact
+        assert res_out.data_ptr() == res_dev.data_ptr()  # in place
+    _close(out.cpu(), want, "gated_norm", 0.02, 2e-3)
+
+
+def test_silu_mul_kernel_against_oracle():
+    gu = _bf16((33, 2 * 5632), 7, 2.0)
+    got = L.silu_mul(gu.to(DEV)).cpu()
+    i = 5632
+    want = H.bf16(torch.nn.functional.silu(gu[:, :i].double()) * gu[:, i:].double())
+    diff = (got.float() - want.float()).abs()
+    # fp32 arithmetic vs float64: at most one bf16 unit apart
+    assert (diff <= want.float().abs() * 2 ** -7 + 1e-30).all()
+    assert (got == want).float().mean() > 0.99
+
+
+def _gdn_setup(seed, slots):
+    cfg = HybridConfig(num_layers=1, hidden_size=512, tp_size=1, vocab_size=64,
+                       linear_num_key_heads=2, linear_num_value_heads=4)
+    init = _Init(DEV, seed, 0.05)
+    mixer = GatedDeltaNet(cfg, init, num_slots=slots, state_std=0.05)
+    mixer.norm_weight = (1 + 0.2 * _bf16((128,), seed).float()).to(torch.bfloat16).to(DEV)
+    builder = HybridBatchBuilder(cfg, max_requests=8, max_tokens=256, main_table_width=64,
+                                 comp_table_width=8, device=DEV)
+    return cfg, mixer, builder
+
+
+def _gdn_step(mixer, builder, computed, scheduled, slots, seed):
+    n = len(scheduled)
+    tables = (torch.zeros(n, 64, dtype=torch.int32, device=DEV),
+              torch.zeros(n, 8, dtype=torch.int32, device=DEV))
+    batch = builder.build(computed, scheduled, [0] * sum(scheduled), *tables,
+                          torch.arange(n, dtype=torch.int32), slots)
+    x = _bf16((sum(scheduled), 512), seed)
+    conv0, ssm0 = _cpu(mixer.conv_state).clone(), _cpu(mixer.ssm_state).clone()
+    got = mixer(x.to(DEV), batch)
+    torch.cuda.synchronize()
+    starts = np.concatenate(([0], np.cumsum(scheduled)[:-1]))
+    seqs = [(list(range(int(st), int(st) + k)), int(sl))
+            for st, k, sl in zip(starts, scheduled, slots) if 0 <= sl < conv0.shape[0]]
+    want = H.gdn_mixer(x, _gdn_params(mixer), conv0, ssm0, seqs, key_heads=mixer.hk,
+                       value_heads=mixer.hv, key_dim=128, value_dim=128, eps=1e-6)
+    return got, want, conv0, ssm0
+
+
+def test_gdn_mixer_prefill_then_decode_against_oracle():
+    _, mixer, builder = _gdn_setup(seed=21, slots=6)
+    # step 1: ragged prefill chunks (one shorter than the conv width) + decodes
+    print("[hybrid] gdn step 1", flush=True)
+    got, want, conv, ssm = _gdn_step(mixer, builder, [9, 0, 40, 5, 2], [1, 1, 70, 2, 33],
+                                     [4, 0, 2, 5, 1], seed=22)
+    _close(got.cpu(), want, "gdn step 1 output")
+    _close(_cpu(mixer.conv_state), conv, "gdn step 1 conv state", 1e-2, 1e-4)
+    _close(_cpu(mixer.ssm_state), ssm, "gdn step 1 state", 1e-2, 1e-3)
+    # step 2: every sequence decodes one token from the states just written
+    print("[hybrid] gdn step 2", flush=True)
+    got, want, conv, ssm = _gdn_step(mixer, builder, [10, 1, 110, 7, 35], [1, 1, 1, 1, 1],
+                                     [4, 0, 2, 5, 1], seed=23)
+    _close(got.cpu(), want, "gdn step 2 output")
+    _close(_cpu(mixer.ssm_state), ssm, "gdn step 2 state", 1e-2, 1e-3)
+
+
+def test_gdn_sequence_without_slot_has_no_state():
+    _, mixer, builder = _gdn_setup(seed=31, slots=3)
+    before = _cpu(mixer.ssm_state).clone()
+    conv_before = _cpu(mixer.conv_state).clone()
+    n = 2
+    tables = (torch.zeros(n, 64, dtype=torch.int32, device=DEV),
+              torch.zeros(n, 8, dtype=torch.int32, device=DEV))
+    batch = builder.build([0, 4], [5, 3], [0] * 8, *tables, torch.arange(n, dtype=torch.int32),
+                          [-1, 7])   # no slot, slot past the pool
+    x = _bf16((8, 512), 32)
+    got = mixer(x.to(DEV), batch)
+    torch.cuda.synchronize()
+    assert torch.equal(_cpu(mixer.ssm_state), before)
+    assert torch.equal(_cpu(mixer.conv_state), conv_before)
+    zeros_ssm = torch.zeros(2, 4, 128, 128)
+    zeros_conv = torch.zeros(2, 3, mixer.conv_state.shape[2], dtype=torch.bfloat16)
+    want = H.gdn_mixer(x, _gdn_params(mixer), zeros_conv, zeros_ssm,
+                       [(list(range(5)), 0), (list(range(5, 8)), 1)], key_heads=2,
+                       value_heads=4, key_dim=128, value_dim=128, eps=1e-6)
+    _close(got.cpu(), want, "gdn without state")

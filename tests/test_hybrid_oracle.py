@@ -1,15 +1,13 @@
-"""CPU pins of the hybrid decoder oracle (oracle/hybrid_oracle.py) and the
-PyTorch GDN pieces (qsa_vllm_amd/gdn.py, the GDN mixer of qsa_vllm_amd/hybrid.py)
-checked against it."""
+"""CPU pins of the hybrid decoder oracle (oracle/hybrid_oracle.py), and the
+host-side checks of the hybrid layer ops (no GPU needed)."""
 
-import numpy as np
 import pytest
 import torch
 import torch.nn.functional as F
 
 from oracle import hybrid as H
-from qsa_vllm_amd import gdn
-from qsa_vllm_amd.hybrid import GatedDeltaNet, HybridBatchBuilder, HybridConfig, _Init
+from qsa_vllm_amd.hybrid import HybridBatchBuilder, HybridConfig
+from qsa_vllm_amd.ops import hybrid_layers
 
 
 def _gen(seed):
@@ -97,114 +95,25 @@ def test_rms_norm_closed_forms():
     assert torch.equal(H.rms_norm(x, w, 0.0), H.rms_norm(scaled, w, 0.0))
 
 
-@pytest.mark.parametrize("lengths,chunk", [([64], 16), ([37, 5, 16], 16), ([3], 8)])
-def test_chunked_product_matches_recurrence(lengths, chunk):
-    heads, dk, dv = 2, 8, 6
-    B = len(lengths)
-    L = -(-max(lengths) // chunk) * chunk
-    q = torch.zeros(B, heads, L, dk)
-    k, v = torch.zeros_like(q), torch.zeros(B, heads, L, dv)
-    g, beta = torch.zeros(B, heads, L), torch.zeros(B, heads, L)
-    s0 = torch.zeros(B, heads, dk, dv)
-    want_o, want_s = [], []
-    for b, n in enumerate(lengths):
-        qq, kk, vv, gg, bb, ss = _inputs(n, heads, dk, dv, seed=10 + b)
-        q[b, :, :n], k[b, :, :n], v[b, :, :n] = (u.transpose(0, 1).float() for u in (qq, kk, vv))
-        g[b, :, :n], beta[b, :, :n] = gg.T.float(), bb.T.float()
-        s0[b] = ss.float()
-        o, S = H.gated_delta_rule(qq, kk, vv, gg, bb, ss)
-        want_o.append(o)
-        want_s.append(S)
-    o, S = gdn.gdn_chunked(q, k, v, g, beta, s0, chunk=chunk)
-    for b, n in enumerate(lengths):
-        assert torch.allclose(o[b, :, :n].transpose(0, 1).double(), want_o[b], atol=2e-5)
-        assert torch.allclose(S[b].double(), want_s[b], atol=2e-5)
+def test_layer_ops_reject_host_tensors():
+    x = torch.zeros(4, 512, dtype=torch.bfloat16)
+    w = torch.ones(512, dtype=torch.bfloat16)
+    with pytest.raises(RuntimeError, match="GPU tensor"):
+        hybrid_layers.gated_norm(x, None, w, torch.zeros(16, 512, dtype=torch.bfloat16),
+                                 torch.zeros(512, 16, dtype=torch.bfloat16), w, 1e-6)
+    with pytest.raises(RuntimeError, match="GPU tensor"):
+        hybrid_layers.silu_mul(torch.zeros(4, 64, dtype=torch.bfloat16))
 
 
-def test_decode_product_matches_one_recurrence_step():
-    heads, dk, dv = 3, 8, 5
-    q, k, v, g, beta, _ = _inputs(4, heads, dk, dv, seed=20)
-    state = torch.randn(6, heads, dk, dv, generator=_gen(21)) * 0.3
-    slots = torch.tensor([4, 0, 5, 2])
-    want = [H.gated_delta_rule(q[i:i + 1], k[i:i + 1], v[i:i + 1], g[i:i + 1], beta[i:i + 1],
-                               state[int(s)]) for i, s in enumerate(slots)]
-    before = state.clone()
-    o = gdn.gdn_decode(q.float(), k.float(), v.float(), g.float(), beta.float(), state, slots)
-    for i, s in enumerate(slots.tolist()):
-        assert torch.allclose(o[i].double(), want[i][0][0], atol=1e-5)
-        assert torch.allclose(state[s].double(), want[i][1], atol=1e-5)
-    for s in (1, 3):
-        assert torch.equal(state[s], before[s])
-
-
-def test_conv_product_matches_oracle():
-    C, K = 12, 4
-    g = _gen(30)
-    w = torch.randn(C, K, generator=g).to(torch.bfloat16)
-    state = torch.randn(5, K - 1, C, generator=g).to(torch.bfloat16)
-    lengths, slots = [6, 1, 2], torch.tensor([3, 0, 4])
-    rows = torch.randn(sum(lengths), C, generator=g).to(torch.bfloat16)
-    width = 8
-    gather = torch.full((3, width), -1, dtype=torch.int64)
-    at = 0
-    for i, n in enumerate(lengths):
-        gather[i, :n] = torch.arange(at, at + n)
-        at += n
-    tail = torch.tensor(lengths)[:, None] + torch.arange(K - 1)[None, :]
-    ref_state = state.clone()
-    out = gdn.conv_prefill(rows, w, state, slots, gather, tail)
-    at = 0
-    for i, n in enumerate(lengths):
-        s = int(slots[i])
-        want, new = H.causal_conv(rows[at:at + n], w, ref_state[s])
-        assert torch.equal(out[i, :n], H.bf16(want))
-        assert torch.equal(state[s], H.bf16(new))
-        at += n
-    # one decode token per sequence on the states just written
-    x = torch.randn(3, C, generator=g).to(torch.bfloat16)
-    ref_state = state.clone()
-    out = gdn.conv_decode(x, w, state, slots)
-    for i, s in enumerate(slots.tolist()):
-        want, new = H.causal_conv(x[i:i + 1], w, ref_state[s])
-        assert torch.equal(out[i], H.bf16(want[0]))
-        assert torch.equal(state[s], H.bf16(new))
-
-
-def _small_cfg(**kw):
-    base = dict(num_layers=1, hidden_size=64, tp_size=1, linear_num_key_heads=2,
-                linear_num_value_heads=4, linear_key_head_dim=16, linear_value_head_dim=16,
-                gdn_chunk=8, vocab_size=97)
-    base.update(kw)
-    return HybridConfig(**base)
-
-
-def _mixer_params(m):
-    return {"in_proj_qkvz": m.in_proj_qkvz, "in_proj_ba": m.in_proj_ba,
-            "conv_weight": m.conv_weight, "A_log": m.A_log, "dt_bias": m.dt_bias,
-            "norm_weight": m.norm_weight, "out_proj": m.out_proj}
-
-
-def test_gdn_mixer_cpu_matches_oracle():
-    cfg = _small_cfg()
-    init = _Init("cpu", 7, 0.1)
-    mixer = GatedDeltaNet(cfg, init, num_slots=6, state_std=0.1)
-    mixer.norm_weight = (1 + 0.2 * torch.randn(16, generator=_gen(8))).to(torch.bfloat16)
-    computed, scheduled = [40, 3, 0, 21], [1, 1, 19, 9]
-    slots = np.array([5, 1, 0, 3])
-    builder = HybridBatchBuilder(cfg, max_requests=4, max_tokens=32, main_table_width=8,
+def test_batch_builder_rows_and_sequences():
+    cfg = HybridConfig(num_layers=4, hidden_size=512, tp_size=1, vocab_size=64)
+    builder = HybridBatchBuilder(cfg, max_requests=4, max_tokens=40, main_table_width=8,
                                  comp_table_width=2, device="cpu")
     tables = torch.zeros(4, 8, dtype=torch.int32), torch.zeros(4, 2, dtype=torch.int32)
-    batch = builder.build(computed, scheduled, np.zeros(30, dtype=np.int64), *tables,
-                          torch.arange(4, dtype=torch.int32), slots)
-    x = (torch.randn(30, 64, generator=_gen(9))).to(torch.bfloat16)
-    conv0, ssm0 = mixer.conv_state.clone(), mixer.ssm_state.clone()
-    got = mixer(x, batch)
-    starts = np.concatenate(([0], np.cumsum(scheduled)[:-1]))
-    seqs = [(list(range(s, s + n)), int(slot)) for s, n, slot in zip(starts, scheduled, slots)]
-    want = H.gdn_mixer(x, _mixer_params(mixer), conv0, ssm0, seqs, key_heads=2, value_heads=4,
-                       key_dim=16, value_dim=16, eps=cfg.rms_norm_eps)
-    err = (got.double() - want.double()).abs()
-    scale = want.double().abs().max()
-    assert err.max() <= 0.02 * scale and err.mean() <= 2e-3 * scale, (err.max(), scale)
-    assert torch.equal(mixer.conv_state, conv0)
-    assert torch.allclose(mixer.ssm_state.double(), ssm0.double(), atol=1e-4)
+    b = builder.build([40, 3, 0, 21], [1, 1, 19, 9], list(range(30)), *tables,
+                      torch.arange(4, dtype=torch.int32), [5, 1, 0, 3])
+    assert b.num_tokens == 30 and b.num_decode_tokens == 2
+    assert b.logits_rows.tolist() == [0, 1, 20, 29]
+    assert b.query_start_loc.tolist() == [0, 1, 2, 21, 30]
+    assert b.token_to_seq.tolist() == [0, 1] + [2] * 19 + [3] * 9
+    assert b.state_slots.tolist() == [5, 1, 0, 3]
