@@ -66,7 +66,7 @@ __device__ __forceinline__ float wave_sum(float v) {
 // ---------------------------------------------------------------------------
 // Gated RMSNorm.
 //
-// A workgroup (4 or 8 waves) takes 16 tokens. With the v_mfma_f32_16x16x32_bf16
+// A workgroup (4 to 16 waves) takes 16 tokens. With the v_mfma_f32_16x16x32_bf16
 // operand layout (lane (m, g) = (lane & 15, lane >> 4) holds A[m][8 g .. +7]
 // and B[8 g .. +7][m] of each 32-deep slice; the accumulator gives lane (n, g)
 // rows 4 g .. 4 g + 3 of column n), lane (m, g) of wave w holds token m's
@@ -115,6 +115,8 @@ __global__ __launch_bounds__(64 * W) void gated_norm_kernel(const GatedNormArgs 
   float ss = 0.0f;
 #pragma unroll
   for (int s = 0; s < S; ++s) {
+    // Loads in batches of 4 groups: bounds the registers held by loads in flight.
+    if (s % 4 == 0 && s > 0) __builtin_amdgcn_sched_barrier(0);
     const int col = col0 + 32 * s;
     u32x4 xv = {0, 0, 0, 0};
     if (ok) xv = load_u32x4(a.x + t * a.x_stride + col);
@@ -145,6 +147,7 @@ __global__ __launch_bounds__(64 * W) void gated_norm_kernel(const GatedNormArgs 
   f32x4 down = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
   for (int s = 0; s < S; ++s) {
+    if (s % 4 == 0 && s > 0) __builtin_amdgcn_sched_barrier(0);
     const int col = col0 + 32 * s;
     float f[8], w[8];
     unpack8(n[s], f);
@@ -179,6 +182,7 @@ __global__ __launch_bounds__(64 * W) void gated_norm_kernel(const GatedNormArgs 
   const u32x4 zero4 = {0, 0, 0, 0};
 #pragma unroll
   for (int s = 0; s < S; ++s) {
+    if (s % 4 == 0 && s > 0) __builtin_amdgcn_sched_barrier(0);
     const int col = col0 + 32 * s;
     f32x4 up[2];
 #pragma unroll
@@ -607,7 +611,7 @@ extern "C" int qsa_gated_norm(const void* x, int64_t x_stride, const void* resid
     case 1: hipLaunchKernelGGL((gated_norm_kernel<4, 4>), grid, dim3(256), 0, s, a); break;
     case 2: hipLaunchKernelGGL((gated_norm_kernel<8, 4>), grid, dim3(256), 0, s, a); break;
     case 4: hipLaunchKernelGGL((gated_norm_kernel<8, 8>), grid, dim3(512), 0, s, a); break;
-    case 8: hipLaunchKernelGGL((gated_norm_kernel<16, 8>), grid, dim3(512), 0, s, a); break;
+    case 8: hipLaunchKernelGGL((gated_norm_kernel<8, 16>), grid, dim3(1024), 0, s, a); break;
     default: return fail(QSA_ERR_UNSUPPORTED, "qsa_gated_norm: hidden size must be 512, 1024, 2048 or 4096");
   }
   return check_launch("qsa_gated_norm");
