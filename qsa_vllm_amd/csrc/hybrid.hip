@@ -407,6 +407,7 @@ __global__ __launch_bounds__(256) void gdn_conv_state_kernel(const GdnConvStateA
 }
 
 constexpr int kRecTokens = 16;  // tokens staged in LDS per block
+constexpr int kChunkMin = 16;   // sequences this long take gdn_chunk_kernel
 
 struct GdnRecurArgs {
   const float* q;  // [tokens, key_heads, 128]
@@ -433,7 +434,7 @@ __global__ __launch_bounds__(256) void gdn_recurrence_kernel(const GdnRecurArgs 
   const int j = 32 * wave + (lane & 31);
   const int half = lane >> 5;
   const int start = a.seq_start[seq], len = a.seq_start[seq + 1] - start;
-  if (len <= 0 || start < 0 || start + len > a.tokens) return;
+  if (len <= 0 || len >= kChunkMin || start < 0 || start + len > a.tokens) return;
   const int64_t slot = a.slots[seq];
   const bool slot_ok = slot >= 0 && slot < a.num_slots;
   float* sp = a.state + ((slot_ok ? slot : 0) * a.value_heads + h) * (int64_t)(kHeadDim * kHeadDim) +
@@ -509,6 +510,284 @@ __global__ __launch_bounds__(256) void gdn_recurrence_kernel(const GdnRecurArgs 
   if (slot_ok) {
 #pragma unroll
     for (int i = 0; i < 64; ++i) sp[(int64_t)i * kHeadDim] = S[i];
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Chunked gated delta rule (sequences of kChunkMin tokens or more).
+//
+// The recurrence over a chunk of C = 64 tokens in its WY form. With G the
+// in-chunk cumulative log decay, gamma = e^G and S the state at the chunk
+// start:
+//   A[t][s] = beta_t e^{G_t - G_s} k_t.k_s (s < t),  (I + A) U = beta V - beta gamma (K S)
+//   O = gamma (Q S) + (e^{G_t - G_s} q_t.k_s)_{s <= t} U
+//   S <- gamma_C S + (e^{G_C - G_s} k_s)^T U
+// One workgroup (4 waves) per (sequence, value head). The state stays in
+// registers as 16x16 MFMA accumulator tiles (wave w: value columns 32 w ..
+// 32 w + 31, all 128 key rows) and feeds the K S / Q S products directly as
+// the B operand: a 32-deep slice pairs key-row tiles 2 ks and 2 ks + 1, slice
+// index 8 g + j being row 16 (2 ks + (j >> 2)) + 4 g + (j & 3) - exactly the
+// accumulator elements lane (n, g) holds - and the A operand reads K with the
+// same row order. Products run in bf16 with fp32 accumulation (the precision
+// of the reference's chunk kernels); the state, gates and the triangular
+// solve are fp32. The solve runs per value column: lanes l and l ^ 32 own the
+// column's first and second 32 rows of U and add their partial sums with one
+// cross-half exchange per row.
+// ---------------------------------------------------------------------------
+constexpr int kChunk = 64;
+
+struct ChunkLds {
+  uint16_t q[kChunk][136];        // bf16 q (normalised, scaled)
+  uint16_t k[kChunk][136];        // bf16 k
+  uint16_t v[kChunk][136];        // bf16 v
+  uint16_t kgt[kHeadDim][72];     // bf16 (e^{G_C - G_s} k_s)^T
+  uint16_t p[kChunk][72];         // bf16 (e^{G_t - G_s} q_t.k_s), s <= t
+  uint16_t ut[kHeadDim][72];      // bf16 U^T
+  float a[kChunk][68];            // fp32 A (strict lower)
+  float r[kChunk][132];           // fp32 right-hand side of the solve
+  float G[kChunk], gam[kChunk], beta[kChunk];
+};
+
+__device__ __forceinline__ uint16_t bf16_bits(float x) {
+  const __bf16 b = (__bf16)x;
+  return __builtin_bit_cast(uint16_t, b);
+}
+
+__device__ __forceinline__ bf16x8 lds_bf16x8(const uint16_t* p) {
+  return __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4*>(p));
+}
+
+// Two 4-element halves (8-byte aligned) as one 8-element operand.
+__device__ __forceinline__ bf16x8 lds_bf16x4x2(const uint16_t* lo, const uint16_t* hi) {
+  const u32x2 a = *reinterpret_cast<const u32x2*>(lo);
+  const u32x2 b = *reinterpret_cast<const u32x2*>(hi);
+  const u32x4 v = {a[0], a[1], b[0], b[1]};
+  return __builtin_bit_cast(bf16x8, v);
+}
+
+__global__ __launch_bounds__(256) void gdn_chunk_kernel(const GdnRecurArgs a) {
+  extern __shared__ __attribute__((aligned(16))) unsigned char chunk_lds_raw[];
+  ChunkLds& L = *reinterpret_cast<ChunkLds*>(chunk_lds_raw);
+  const int h = blockIdx.x % a.value_heads;
+  const int seq = a.num_seqs - 1 - (int)(blockIdx.x / a.value_heads);
+  const int mk = h / (a.value_heads / a.key_heads);
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int m = lane & 15, g = lane >> 4;
+  const int start = a.seq_start[seq], len = a.seq_start[seq + 1] - start;
+  if (len < kChunkMin || start < 0 || start + len > a.tokens) return;
+  const int64_t slot = a.slots[seq];
+  const bool slot_ok = slot >= 0 && slot < a.num_slots;
+  float* state = a.state + ((slot_ok ? slot : 0) * a.value_heads + h) * (int64_t)(kHeadDim * kHeadDim);
+
+  // S tiles: S[rt][nl] = rows 16 rt + 4 g + i, column 32 w + 16 nl + m.
+  f32x4 S[8][2];
+#pragma unroll
+  for (int rt = 0; rt < 8; ++rt)
+#pragma unroll
+    for (int nl = 0; nl < 2; ++nl)
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        S[rt][nl][i] = slot_ok ? state[(16 * rt + 4 * g + i) * kHeadDim + 32 * w + 16 * nl + m] : 0.0f;
+
+  for (int c0 = 0; c0 < len; c0 += kChunk) {
+    const int nc = min(kChunk, len - c0);
+    // 1. Stage the chunk: thread -> (row tid / 4, dims 32 (tid % 4) .. + 31).
+    const int row = tid >> 2, d0 = 32 * (tid & 3);
+    const bool live = row < nc;
+    const int64_t t = start + c0 + row;
+    float kf[32];
+    {
+      const float* qp = a.q + (t * a.key_heads + mk) * kHeadDim + d0;
+      const float* kp = a.k + (t * a.key_heads + mk) * kHeadDim + d0;
+#pragma unroll
+      for (int e = 0; e < 32; e += 4) {
+        f32x4 qv = {0.f, 0.f, 0.f, 0.f}, kv = {0.f, 0.f, 0.f, 0.f};
+        if (live) {
+          qv = *reinterpret_cast<const f32x4*>(qp + e);
+          kv = *reinterpret_cast<const f32x4*>(kp + e);
+        }
+        *reinterpret_cast<u32x2*>(&L.q[row][d0 + e]) = u32x2{pack_bf16x2(qv[0], qv[1]), pack_bf16x2(qv[2], qv[3])};
+        *reinterpret_cast<u32x2*>(&L.k[row][d0 + e]) = u32x2{pack_bf16x2(kv[0], kv[1]), pack_bf16x2(kv[2], kv[3])};
+#pragma unroll
+        for (int j = 0; j < 4; ++j) kf[e + j] = rbf(kv[j]);
+      }
+      const uint16_t* vp = a.v + (t * a.value_heads + h) * kHeadDim + d0;
+#pragma unroll
+      for (int e = 0; e < 32; e += 8) {
+        u32x4 vv = {0, 0, 0, 0};
+        if (live) vv = load_u32x4(vp + e);
+        *reinterpret_cast<u32x4*>(&L.v[row][d0 + e]) = vv;
+      }
+    }
+    if (w == 0) {  // gates of row `lane`, inclusive prefix sum of g
+      const bool ok = lane < nc;
+      float gv = ok ? a.g[(start + c0 + lane) * (int64_t)a.value_heads + h] : 0.0f;
+      const float bv = ok ? a.beta[(start + c0 + lane) * (int64_t)a.value_heads + h] : 0.0f;
+#pragma unroll
+      for (int d = 1; d < 64; d <<= 1) {
+        const float o = __shfl_up(gv, d, 64);
+        if (lane >= d) gv += o;
+      }
+      L.G[lane] = gv;
+      L.gam[lane] = expf(gv);
+      L.beta[lane] = bv;
+    }
+    __syncthreads();
+    {
+      const float scale = expf(L.G[kChunk - 1] - L.G[row]);
+#pragma unroll
+      for (int e = 0; e < 32; ++e) L.kgt[d0 + e][row] = bf16_bits(kf[e] * scale);
+    }
+    // 2. K S and Q S: tiles (ct, nl), rows 16 ct + 4 g + i, columns 32 w + 16 nl + m.
+    bf16x8 sb[4][2];
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks)
+#pragma unroll
+      for (int nl = 0; nl < 2; ++nl) {
+        const u32x4 v = {pack_bf16x2(S[2 * ks][nl][0], S[2 * ks][nl][1]),
+                         pack_bf16x2(S[2 * ks][nl][2], S[2 * ks][nl][3]),
+                         pack_bf16x2(S[2 * ks + 1][nl][0], S[2 * ks + 1][nl][1]),
+                         pack_bf16x2(S[2 * ks + 1][nl][2], S[2 * ks + 1][nl][3])};
+        sb[ks][nl] = __builtin_bit_cast(bf16x8, v);
+      }
+    f32x4 KS[4][2], QS[4][2];
+#pragma unroll
+    for (int ct = 0; ct < 4; ++ct)
+#pragma unroll
+      for (int nl = 0; nl < 2; ++nl) {
+        KS[ct][nl] = f32x4{0.f, 0.f, 0.f, 0.f};
+        QS[ct][nl] = f32x4{0.f, 0.f, 0.f, 0.f};
+      }
+#pragma unroll
+    for (int ct = 0; ct < 4; ++ct)
+#pragma unroll
+      for (int ks = 0; ks < 4; ++ks) {
+        const int r = 16 * ct + m;
+        const bf16x8 ak = lds_bf16x4x2(&L.k[r][32 * ks + 4 * g], &L.k[r][32 * ks + 16 + 4 * g]);
+        const bf16x8 aq = lds_bf16x4x2(&L.q[r][32 * ks + 4 * g], &L.q[r][32 * ks + 16 + 4 * g]);
+#pragma unroll
+        for (int nl = 0; nl < 2; ++nl) {
+          KS[ct][nl] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ak, sb[ks][nl], KS[ct][nl], 0, 0, 0);
+          QS[ct][nl] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(aq, sb[ks][nl], QS[ct][nl], 0, 0, 0);
+        }
+      }
+    // 3. K K^T and Q K^T for row tile w: rows 16 w + 4 g + i, columns 16 ct + m.
+#pragma unroll
+    for (int ct = 0; ct < 4; ++ct) {
+      f32x4 kk = {0.f, 0.f, 0.f, 0.f}, qk = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int ks = 0; ks < 4; ++ks) {
+        const bf16x8 bk = lds_bf16x8(&L.k[16 * ct + m][32 * ks + 8 * g]);
+        kk = __builtin_amdgcn_mfma_f32_16x16x32_bf16(lds_bf16x8(&L.k[16 * w + m][32 * ks + 8 * g]), bk, kk, 0, 0, 0);
+        qk = __builtin_amdgcn_mfma_f32_16x16x32_bf16(lds_bf16x8(&L.q[16 * w + m][32 * ks + 8 * g]), bk, qk, 0, 0, 0);
+      }
+      const int sc = 16 * ct + m;
+      const float Gs = L.G[sc];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int tr = 16 * w + 4 * g + i;
+        const float d = L.G[tr] - Gs;
+        const float e = sc <= tr ? expf(d) : 0.0f;
+        L.a[tr][sc] = sc < tr ? L.beta[tr] * e * kk[i] : 0.0f;
+        L.p[tr][sc] = bf16_bits(e * qk[i]);
+      }
+    }
+    // 4. Right-hand side beta (V - gamma K S).
+#pragma unroll
+    for (int ct = 0; ct < 4; ++ct)
+#pragma unroll
+      for (int nl = 0; nl < 2; ++nl)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int tr = 16 * ct + 4 * g + i, col = 32 * w + 16 * nl + m;
+          const float vv = __builtin_bit_cast(float, (uint32_t)L.v[tr][col] << 16);
+          L.r[tr][col] = L.beta[tr] * (vv - L.gam[tr] * KS[ct][nl][i]);
+        }
+    __syncthreads();
+    // 5. Forward substitution (I + A) U = R, column j = 32 w + (lane & 31).
+    {
+      const int j = 32 * w + (lane & 31), half = lane >> 5;
+      float u[32];
+#pragma unroll
+      for (int rr = 0; rr < 32; ++rr) u[rr] = 0.0f;
+#pragma unroll
+      for (int i = 0; i < kChunk; ++i) {
+        // Four independent chains keep the per-row dependency short.
+        float p0 = 0.0f, p1 = 0.0f, p2 = 0.0f, p3 = 0.0f;
+        if (i > 0) {
+          const float* arow = &L.a[i][32 * half];
+#pragma unroll
+          for (int rr = 0; rr < 32; rr += 4) {
+            if (rr < i) {  // rows past i contribute 0: A is strictly lower and u is still 0 there
+              const f32x4 av = *reinterpret_cast<const f32x4*>(arow + rr);
+              p0 += av[0] * u[rr];
+              p1 += av[1] * u[rr + 1];
+              p2 += av[2] * u[rr + 2];
+              p3 += av[3] * u[rr + 3];
+            }
+          }
+        }
+        const float ui = L.r[i][j] - sum_wave_halves((p0 + p1) + (p2 + p3));
+        if (i < 32) {
+          if (half == 0) u[i] = ui;
+        } else {
+          if (half == 1) u[i - 32] = ui;
+        }
+        if (half == (i >> 5)) L.ut[j][i] = bf16_bits(ui);
+      }
+    }
+    __syncthreads();
+    // 6. O = gamma (Q S) + P U.
+#pragma unroll
+    for (int ct = 0; ct < 4; ++ct) {
+      f32x4 o[2];
+#pragma unroll
+      for (int nl = 0; nl < 2; ++nl) o[nl] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks) {
+        const bf16x8 ap = lds_bf16x8(&L.p[16 * ct + m][32 * ks + 8 * g]);
+#pragma unroll
+        for (int nl = 0; nl < 2; ++nl)
+          o[nl] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+              ap, lds_bf16x8(&L.ut[32 * w + 16 * nl + m][32 * ks + 8 * g]), o[nl], 0, 0, 0);
+      }
+#pragma unroll
+      for (int nl = 0; nl < 2; ++nl)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int tr = 16 * ct + 4 * g + i;
+          if (tr < nc) {
+            const float val = L.gam[tr] * QS[ct][nl][i] + o[nl][i];
+            a.o[((start + c0 + tr) * (int64_t)a.value_heads + h) * kHeadDim + 32 * w + 16 * nl + m] =
+                bf16_bits(val);
+          }
+        }
+    }
+    // 7. S <- gamma_C S + Kg^T U.
+    const float gc = L.gam[kChunk - 1];
+#pragma unroll
+    for (int rt = 0; rt < 8; ++rt) {
+#pragma unroll
+      for (int nl = 0; nl < 2; ++nl) S[rt][nl] = S[rt][nl] * gc;
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks) {
+        const bf16x8 ak = lds_bf16x8(&L.kgt[16 * rt + m][32 * ks + 8 * g]);
+#pragma unroll
+        for (int nl = 0; nl < 2; ++nl)
+          S[rt][nl] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+              ak, lds_bf16x8(&L.ut[32 * w + 16 * nl + m][32 * ks + 8 * g]), S[rt][nl], 0, 0, 0);
+      }
+    }
+    __syncthreads();
+  }
+  if (slot_ok) {
+#pragma unroll
+    for (int rt = 0; rt < 8; ++rt)
+#pragma unroll
+      for (int nl = 0; nl < 2; ++nl)
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          state[(16 * rt + 4 * g + i) * kHeadDim + 32 * w + 16 * nl + m] = S[rt][nl][i];
   }
 }
 
@@ -709,6 +988,11 @@ extern "C" int qsa_gdn_recurrence(const float* q, const float* k, const void* v,
     return fail(QSA_ERR_UNSUPPORTED, "qsa_gdn_recurrence: too many (sequence, head) pairs");
   GdnRecurArgs a{q, k, static_cast<const uint16_t*>(v), g, beta, state, query_start_loc, slots,
                  num_seqs, key_heads, value_heads, num_slots, tokens, static_cast<uint16_t*>(o)};
+  // Long sequences (chunks) first on the stream: their workgroups are the long ones.
+  hipLaunchKernelGGL(gdn_chunk_kernel, dim3(num_seqs * value_heads), dim3(256), sizeof(ChunkLds),
+                     static_cast<hipStream_t>(stream), a);
+  const int st = check_launch("qsa_gdn_recurrence (chunks)");
+  if (st != QSA_OK) return st;
   hipLaunchKernelGGL(gdn_recurrence_kernel, dim3(num_seqs * value_heads), dim3(256), 0,
                      static_cast<hipStream_t>(stream), a);
   return check_launch("qsa_gdn_recurrence");
