@@ -44,6 +44,8 @@ def parse_args():
     p.add_argument("--cpu-seconds", type=float, default=10.0,
                    help="CPU work budget for the oracle baseline (0 disables it)")
     p.add_argument("--cpu-threads", type=int, default=0, help="0: min(16, cpu_count)")
+    p.add_argument("--no-hybrid", action="store_true",
+                   help="decode_32k: skip the hybrid decoder step figures added to the line")
     p.add_argument("--traffic", default=os.path.join(os.path.dirname(os.path.abspath(__file__)),
                                                      "profiles", "sparse_attn_decode_32k_traffic.txt"),
                    help="committed rocprofv3 PMC summary giving HBM bytes per attention launch")
@@ -275,6 +277,14 @@ def main():
     }
     if args.cpu_seconds > 0:
         result["cpu_baseline"] = cpu_baseline(wl, args)
+    if args.workload == "decode_32k" and not args.no_hybrid:
+        # The whole hybrid decoder step beside the headline (its own line:
+        # --workload hybrid_decoder_step). A failure here is recorded, not raised,
+        # so it cannot take the headline figures with it.
+        try:
+            result["hybrid_step"] = hybrid_summary(dev)
+        except Exception as exc:  # noqa: BLE001
+            result["hybrid_step"] = {"error": f"{type(exc).__name__}: {exc}"}
     print(json.dumps(result), flush=True)
     return 0
 
@@ -561,10 +571,10 @@ def hybrid_flops(wl):
     return 2 * per_token * tokens + 2 * m.lm_head.numel() * len(wl.scheduled)
 
 
-def run_hybrid(args, dev):
-    """Whole decoder step of the hybrid model on the mixed batch: metadata
-    build, embedding, 32 layers (24 GDN, 8 QSA on the path's kernels), final
-    norm and the LM head rows. Eager launches (a mixed batch is not captured)."""
+def measure_hybrid(dev, steps, warmup, breakdown=True):
+    """Times whole hybrid decoder steps (metadata build, embedding, 32 layers,
+    final norm, LM-head rows) on the mixed batch; eager launches (a mixed batch
+    is not captured). Returns the figures as a dict."""
     import torch
 
     t0 = time.time()
@@ -577,18 +587,9 @@ def run_hybrid(args, dev):
     def step():
         return model.forward(wl.build())
 
-    if args.pmc_run:
-        for _ in range(2):
-            step()
-        torch.cuda.synchronize()
-        log("pmc run: 2 eager hybrid steps")
-        return 0
-    warmup = max(1, min(args.warmup, 3))
-    steps = max(1, min(args.steps, 10))
     for _ in range(warmup):
         step()
     torch.cuda.synchronize()
-    log(f"hybrid warm-up done ({warmup} steps)")
     stream = torch.cuda.current_stream()
     a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     wall = time.time()
@@ -601,41 +602,84 @@ def run_hybrid(args, dev):
     ms_step = a.elapsed_time(b) / steps
     if not torch.isfinite(logits).all():
         raise SystemExit("non-finite logits: results invalid")
-
-    # Per-part times from one more step with events between the parts.
-    batch = wl.build()
-    marks = []
-
-    def mark(name):
-        e = torch.cuda.Event(enable_timing=True)
-        e.record(stream)
-        marks.append((name, e))
-
-    mark("start")
-    hidden, residual = model.embed(batch.token_ids), None
-    for layer in model.layers:
-        if residual is None:
-            residual = hidden
-            normalized = layer.input_layernorm(hidden)
-        else:
-            normalized, residual = layer.input_layernorm(hidden, residual)
-        mark("norms")
-        hidden = layer.mixer(normalized, batch)
-        mark("qsa_mixer" if layer.kind == "full_attention" else "gdn_mixer")
-        normalized, residual = layer.post_attention_layernorm(hidden, residual)
-        mark("norms")
-        hidden = layer.mlp(normalized)
-        mark("mlp")
-    model.logits(hidden, residual, batch)
-    mark("head")
-    torch.cuda.synchronize()
     parts = {}
-    for (_, e0), (name, e1) in zip(marks, marks[1:]):
-        parts[name] = parts.get(name, 0.0) + e0.elapsed_time(e1)
+    if breakdown:
+        # Per-part times from one more step with events between the parts.
+        batch = wl.build()
+        marks = []
+
+        def mark(name):
+            e = torch.cuda.Event(enable_timing=True)
+            e.record(stream)
+            marks.append((name, e))
+
+        mark("start")
+        hidden, residual = model.embed(batch.token_ids), None
+        for layer in model.layers:
+            if residual is None:
+                residual = hidden
+                normalized = layer.input_layernorm(hidden)
+            else:
+                normalized, residual = layer.input_layernorm(hidden, residual)
+            mark("norms")
+            hidden = layer.mixer(normalized, batch)
+            mark("qsa_mixer" if layer.kind == "full_attention" else "gdn_mixer")
+            normalized, residual = layer.post_attention_layernorm(hidden, residual)
+            mark("norms")
+            hidden = layer.mlp(normalized)
+            mark("mlp")
+        model.logits(hidden, residual, batch)
+        mark("head")
+        torch.cuda.synchronize()
+        for (_, e0), (name, e1) in zip(marks, marks[1:]):
+            parts[name] = parts.get(name, 0.0) + e0.elapsed_time(e1)
     flops = hybrid_flops(wl)
-    tflops = flops / (ms_step * 1e-3) / 1e12
+    out = {"wl": wl, "ms_per_step": ms_step, "wall_ms_per_step": wall, "flops": flops,
+           "breakdown_ms": {k: round(v, 3) for k, v in parts.items()}}
+    return out
+
+
+def hybrid_description(wl):
     cfg = wl.cfg
-    kinds = [layer.kind for layer in model.layers]
+    kinds = [layer.kind for layer in wl.model.layers]
+    return (f"hybrid decoder step: {cfg.num_layers} layers ({kinds.count('linear_attention')} GDN, "
+            f"{kinds.count('full_attention')} QSA), hidden {cfg.hidden_size}, TP{cfg.tp_size} share: "
+            f"QSA {cfg.heads}q/{cfg.kv_heads}kv x {cfg.head_dim}, GDN {cfg.key_heads}k/"
+            f"{cfg.value_heads}v heads x {cfg.linear_key_head_dim}, MLP {cfg.intermediate}, vocab "
+            f"shard {cfg.vocab_shard}; batch {HYBRID_DECODES} decode (context U[4096,32768]) + "
+            f"{HYBRID_CHUNKS} prefill chunks of {HYBRID_CHUNK}")
+
+
+def hybrid_summary(dev):
+    """Compact hybrid-step figures for the default benchmark line."""
+    m = measure_hybrid(dev, steps=3, warmup=2)
+    wl = m.pop("wl")
+    out = {"workload": hybrid_description(wl), "tokens": wl.num_tokens,
+           "ms_per_step": round(m["ms_per_step"], 3),
+           "tokens_per_s": round(wl.num_tokens / (m["ms_per_step"] * 1e-3), 1),
+           "gemm_tflops": round(m["flops"] / (m["ms_per_step"] * 1e-3) / 1e12, 1),
+           "breakdown_ms": m["breakdown_ms"]}
+    del wl
+    return out
+
+
+def run_hybrid(args, dev):
+    """The hybrid decoder step as the benchmark's own line."""
+    import torch
+
+    if args.pmc_run:
+        wl = hybrid_workload(dev)
+        for _ in range(2):
+            wl.model.forward(wl.build())
+        torch.cuda.synchronize()
+        log("pmc run: 2 eager hybrid steps")
+        return 0
+    warmup = max(1, min(args.warmup, 3))
+    steps = max(1, min(args.steps, 10))
+    m = measure_hybrid(dev, steps, warmup)
+    wl = m["wl"]
+    ms_step = m["ms_per_step"]
+    tflops = m["flops"] / (ms_step * 1e-3) / 1e12
     result = {
         "metric": "hybrid decoder step tokens/s (32 layers, 3 GDN : 1 QSA, 112 decode + 16 x 512 "
                   "prefill), 1 MI355X",
@@ -645,26 +689,15 @@ def run_hybrid(args, dev):
         "steps": steps,
         "warmup": warmup,
         "ms_per_step": round(ms_step, 3),
-        "wall_ms_per_step": round(wall, 3),
+        "wall_ms_per_step": round(m["wall_ms_per_step"], 3),
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "bf16",
         "data": "synthetic: random-init bf16 weights N(0, 0.02), seeded token ids, random "
                 "cache and GDN-state history",
-        "config": {
-            "workload": f"hybrid decoder step: {cfg.num_layers} layers "
-                        f"({kinds.count('linear_attention')} GDN, {kinds.count('full_attention')} "
-                        f"QSA), hidden {cfg.hidden_size}, TP{cfg.tp_size} share: QSA "
-                        f"{cfg.heads}q/{cfg.kv_heads}kv x {cfg.head_dim}, GDN {cfg.key_heads}k/"
-                        f"{cfg.value_heads}v heads x {cfg.linear_key_head_dim}, MLP "
-                        f"{cfg.intermediate}, vocab shard {cfg.vocab_shard}; batch "
-                        f"{HYBRID_DECODES} decode (context U[4096,32768]) + {HYBRID_CHUNKS} "
-                        f"prefill chunks of {HYBRID_CHUNK}",
-            "tokens": wl.num_tokens,
-            "requests": len(wl.scheduled),
-            "graph": "eager",
-        },
+        "config": {"workload": hybrid_description(wl), "tokens": wl.num_tokens,
+                   "requests": len(wl.scheduled), "graph": "eager"},
         "roofline": {
             "kernel": "whole step (projection, MLP and LM head GEMMs)",
             "bound": "mfma",
@@ -673,9 +706,9 @@ def run_hybrid(args, dev):
             "unit": "TFLOP/s",
             "frac": round(tflops / BF16_PEAK_TFLOPS, 4),
             "traffic": None,
-            "algorithmic_flops_per_step": flops,
+            "algorithmic_flops_per_step": m["flops"],
         },
-        "breakdown_ms": {k: round(v, 3) for k, v in parts.items()},
+        "breakdown_ms": m["breakdown_ms"],
     }
     print(json.dumps(result), flush=True)
     return 0
