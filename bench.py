@@ -96,7 +96,7 @@ def main():
     import torch
 
     from qsa_vllm_amd.ops import qsa_sparse_paged_attention, select_paged_tokens, topk_expand
-    from qsa_vllm_amd.workloads import (SHAPES, attention_bytes, fresh_queries, indexer_bytes,
+    from qsa_vllm_amd.workloads import (attention_bytes, fresh_queries, indexer_bytes,
                                         make_workload)
 
     dev = torch.device("cuda:0")

@@ -39,7 +39,6 @@ GDN projection layout: ``in_proj_qkvz`` grouped per key head as
 
 from __future__ import annotations
 
-import math
 from dataclasses import dataclass, field
 
 import numpy as np
