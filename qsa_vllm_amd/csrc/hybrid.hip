@@ -530,9 +530,8 @@ __global__ __launch_bounds__(256) void gdn_recurrence_kernel(const GdnRecurArgs 
 // accumulator elements lane (n, g) holds - and the A operand reads K with the
 // same row order. Products run in bf16 with fp32 accumulation (the precision
 // of the reference's chunk kernels); the state, gates and the triangular
-// solve are fp32. The solve runs per value column: lanes l and l ^ 32 own the
-// column's first and second 32 rows of U and add their partial sums with one
-// cross-half exchange per row.
+// solve are fp32: 16-row blocks, each taking the earlier blocks' contribution
+// as fp32 MFMA work and solving its diagonal block per value column.
 // ---------------------------------------------------------------------------
 constexpr int kChunk = 64;
 
@@ -704,39 +703,50 @@ __global__ __launch_bounds__(256) void gdn_chunk_kernel(const GdnRecurArgs a) {
           L.r[tr][col] = L.beta[tr] * (vv - L.gam[tr] * KS[ct][nl][i]);
         }
     __syncthreads();
-    // 5. Forward substitution (I + A) U = R, column j = 32 w + (lane & 31).
-    {
-      const int j = 32 * w + (lane & 31), half = lane >> 5;
-      float u[32];
+    // 5. Forward substitution (I + A) U = R in 16-row blocks. Block b first
+    // takes the earlier blocks' contribution, A[b rows][0 : 16 b] U[0 : 16 b]
+    // (v_mfma_f32_16x16x4f32, fp32 products: lane (m, kk) holds A[m][kk] and
+    // B[kk][m] of each 4-deep slice), then solves its 16x16 diagonal block
+    // per value column in registers. U overwrites R (fp32) and goes to U^T
+    // (bf16) for the products below.
 #pragma unroll
-      for (int rr = 0; rr < 32; ++rr) u[rr] = 0.0f;
+    for (int blk = 0; blk < 4; ++blk) {
+      if (blk > 0) {
+        const int kk = lane >> 4;
+        f32x4 acc[2] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
 #pragma unroll
-      for (int i = 0; i < kChunk; ++i) {
-        // Four independent chains keep the per-row dependency short.
-        float p0 = 0.0f, p1 = 0.0f, p2 = 0.0f, p3 = 0.0f;
-        if (i > 0) {
-          const float* arow = &L.a[i][32 * half];
+        for (int ks = 0; ks < 4 * blk; ++ks) {
+          const float av = L.a[16 * blk + m][4 * ks + kk];
 #pragma unroll
-          for (int rr = 0; rr < 32; rr += 4) {
-            if (rr < i) {  // rows past i contribute 0: A is strictly lower and u is still 0 there
-              const f32x4 av = *reinterpret_cast<const f32x4*>(arow + rr);
-              p0 += av[0] * u[rr];
-              p1 += av[1] * u[rr + 1];
-              p2 += av[2] * u[rr + 2];
-              p3 += av[3] * u[rr + 3];
-            }
-          }
+          for (int nl = 0; nl < 2; ++nl)
+            acc[nl] = __builtin_amdgcn_mfma_f32_16x16x4f32(
+                av, L.r[4 * ks + kk][32 * w + 16 * nl + m], acc[nl], 0, 0, 0);
         }
-        const float ui = L.r[i][j] - sum_wave_halves((p0 + p1) + (p2 + p3));
-        if (i < 32) {
-          if (half == 0) u[i] = ui;
-        } else {
-          if (half == 1) u[i - 32] = ui;
-        }
-        if (half == (i >> 5)) L.ut[j][i] = bf16_bits(ui);
+#pragma unroll
+        for (int nl = 0; nl < 2; ++nl)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) L.r[16 * blk + 4 * g + i][32 * w + 16 * nl + m] -= acc[nl][i];
+        __syncthreads();
       }
+      if (tid < kHeadDim) {
+        const int j = tid;
+        float u[16];
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+          const float* arow = &L.a[16 * blk + i][16 * blk];
+          float p0 = 0.0f, p1 = 0.0f;
+#pragma unroll
+          for (int s2 = 0; s2 < i; ++s2) {
+            if (s2 & 1) p1 += arow[s2] * u[s2];
+            else p0 += arow[s2] * u[s2];
+          }
+          u[i] = L.r[16 * blk + i][j] - (p0 + p1);
+          L.r[16 * blk + i][j] = u[i];
+          L.ut[j][16 * blk + i] = bf16_bits(u[i]);
+        }
+      }
+      __syncthreads();
     }
-    __syncthreads();
     // 6. O = gamma (Q S) + P U.
 #pragma unroll
     for (int ct = 0; ct < 4; ++ct) {
