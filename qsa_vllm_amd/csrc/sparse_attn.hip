@@ -600,14 +600,19 @@ bool plan_heads(int num_q_heads, int num_kv_heads, HeadPlan* plan) {
   return true;
 }
 
-// Waves per workgroup: 8 once (row, head group) pairs alone reach 64, so a
-// few splits give every CU one 8-wave workgroup; 4 below that, where more and
-// smaller workgroups spread a small batch wider. On the 64-row, 16-head decode
-// shape 8 waves x 4 splits measured faster than 4 waves x 8 splits. D = 128
-// with 4 kv heads per group needs more than the 256 registers a lane gets at
-// two waves per SIMD, so it always runs 4 waves (one per SIMD).
+// Waves per workgroup. Physical (decode) rows: 8 once (row, head group)
+// pairs alone reach 64, so a few splits give every CU one 8-wave workgroup; 4
+// below that, where more and smaller workgroups spread a small batch wider. On
+// the 64-row, 16-head decode shape 8 waves x 4 splits measured faster than 4
+// waves x 8 splits. Logical (prefill) rows always take 4 waves: at 256
+// registers a lane two such workgroups share a CU, so one row's start (index ->
+// table -> K round trips) overlaps the other's streaming; measured 5.11 ms
+// against 5.58 ms with 8 waves on the 32768-row chunked prefill. D = 128 with
+// 4 kv heads per group needs more than the 256 registers a lane gets at two
+// waves per SIMD, so it always runs 4 waves (one per SIMD).
 bool fits_8_waves(int head_dim, int nkv) { return !(head_dim == 128 && nkv == 4); }
-int waves_for(int rows, const HeadPlan& plan, int head_dim) {
+int waves_for(int rows, const HeadPlan& plan, int head_dim, bool physical) {
+  if (!physical) return 4;
   return (int64_t)rows * plan.groups >= 64 && fits_8_waves(head_dim, plan.nkv) ? 8 : 4;
 }
 
@@ -649,14 +654,15 @@ using namespace qsa;
 
 extern "C" int qsa_sparse_attention_splits(int rows, int num_q_heads, int num_kv_heads,
                                            int head_dim, int width, int use_decode_kernel) {
-  (void)use_decode_kernel;
   HeadPlan plan;
   if (rows <= 0 || !plan_heads(num_q_heads, num_kv_heads, &plan)) return 1;
   const int tiles = (width + kTile - 1) / kTile;
   const int64_t base = (int64_t)rows * plan.groups;
   // One 8-wave workgroup per CU, or two 4-wave ones, and at least two tiles
   // per split (a one-tile split pays for a partial and its merge for nothing).
-  const int64_t target = waves_for(rows, plan, head_dim) == 8 ? kCUs : 2 * kCUs;
+  // The decode kernel takes physical slots; prefill rows take logical ids.
+  const int64_t target =
+      waves_for(rows, plan, head_dim, use_decode_kernel != 0) == 8 ? kCUs : 2 * kCUs;
   int splits = 1;
   while (splits * 2 * base <= target && splits * 2 <= std::max(1, tiles / 2) && splits < 64)
     splits *= 2;
@@ -759,7 +765,7 @@ extern "C" int qsa_sparse_attention(
   if (plan.groups > 65535 || num_splits > 65535)
     return fail(QSA_ERR_UNSUPPORTED, "qsa_sparse_attention: grid too large");
   const dim3 grid(rows, num_splits, plan.groups);
-  const int waves = waves_for(rows, plan, head_dim);
+  const int waves = waves_for(rows, plan, head_dim, indices_are_physical != 0);
   hipStream_t s = static_cast<hipStream_t>(stream);
   hipError_t err = hipSuccess;
   if (head_dim == 128) {
