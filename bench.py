@@ -635,8 +635,41 @@ def measure_hybrid(dev, steps, warmup, breakdown=True):
             parts[name] = parts.get(name, 0.0) + e0.elapsed_time(e1)
     flops = hybrid_flops(wl)
     out = {"wl": wl, "ms_per_step": ms_step, "wall_ms_per_step": wall, "flops": flops,
-           "breakdown_ms": {k: round(v, 3) for k, v in parts.items()}}
+           "breakdown_ms": {k: round(v, 3) for k, v in parts.items()},
+           "decode_graph": measure_hybrid_decode_graph(wl, steps=max(steps, 5))}
     return out
+
+
+def measure_hybrid_decode_graph(wl, steps):
+    """The model's uniform decode step over the workload's decode requests
+    (one token each), replayed from a HIP graph: per step, a metadata build
+    (host inputs to the persistent buffers) and one replay."""
+    import torch
+
+    from qsa_vllm_amd.hybrid import HybridDecodeGraph
+
+    graph = HybridDecodeGraph(wl.model, wl.build_decode())
+    for _ in range(2):
+        graph.replay(wl.build_decode())
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream()
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    a.record(stream)
+    for _ in range(steps):
+        graph.replay(wl.build_decode())
+    b.record(stream)
+    torch.cuda.synchronize()
+    ms = a.elapsed_time(b) / steps
+    a.record(stream)
+    for _ in range(steps):
+        graph.replay()
+    b.record(stream)
+    torch.cuda.synchronize()
+    replay_ms = a.elapsed_time(b) / steps
+    n = graph.num_tokens
+    del graph
+    return {"requests": n, "ms_per_step": round(ms, 3), "replay_only_ms": round(replay_ms, 3),
+            "tokens_per_s": round(n / (ms * 1e-3), 1)}
 
 
 def hybrid_description(wl):
@@ -658,7 +691,7 @@ def hybrid_summary(dev):
            "ms_per_step": round(m["ms_per_step"], 3),
            "tokens_per_s": round(wl.num_tokens / (m["ms_per_step"] * 1e-3), 1),
            "gemm_tflops": round(m["flops"] / (m["ms_per_step"] * 1e-3) / 1e12, 1),
-           "breakdown_ms": m["breakdown_ms"]}
+           "breakdown_ms": m["breakdown_ms"], "decode_graph": m["decode_graph"]}
     del wl
     return out
 
@@ -709,6 +742,7 @@ def run_hybrid(args, dev):
             "algorithmic_flops_per_step": m["flops"],
         },
         "breakdown_ms": m["breakdown_ms"],
+        "decode_graph": m["decode_graph"],
     }
     print(json.dumps(result), flush=True)
     return 0

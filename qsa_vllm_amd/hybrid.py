@@ -46,13 +46,14 @@ import torch
 import torch.nn.functional as F
 
 from .backend import QSALayerState, YuLanQSAImpl, YuLanQSAIndexer
+from .graph_dispatch import capture_column_scope
 from .layer_step import qsa_layer_step
 from .metadata import QSABatch, QSAMetadataBuilder
 from .ops.hybrid_layers import (gated_norm, gdn_conv_state, gdn_gated_norm, gdn_prep,
                                 gdn_recurrence, silu_mul)
 
 __all__ = ["HybridConfig", "HybridBatch", "HybridBatchBuilder", "HybridDecoder",
-           "HybridWorkload", "make_hybrid_workload"]
+           "HybridDecodeGraph", "HybridWorkload", "make_hybrid_workload"]
 
 
 @dataclass(frozen=True)
@@ -295,7 +296,9 @@ class HybridBatch:
 
 class HybridBatchBuilder:
     """Builds :class:`HybridBatch` from scheduler-level inputs (tokens already
-    computed and scheduled per request, decode requests first)."""
+    computed and scheduled per request, decode requests first). Every tensor
+    of a batch is a view of a persistent device buffer refreshed by ``build``,
+    so a graph captured on one batch reads the next batch's values on replay."""
 
     def __init__(self, cfg: HybridConfig, *, max_requests: int, max_tokens: int,
                  main_table_width: int, comp_table_width: int, device):
@@ -306,21 +309,25 @@ class HybridBatchBuilder:
             comp_page_size=cfg.comp_page_size, ring_size=cfg.compress_ratio,
             max_num_requests=max_requests, max_num_tokens=max_tokens,
             main_table_width=main_table_width, comp_table_width=comp_table_width, device=device)
+        self.token_ids = torch.zeros(max_tokens, dtype=torch.int64, device=self.device)
+        self.state_slots = torch.full((max_requests,), -1, dtype=torch.int64, device=self.device)
+        self.logits_rows = torch.zeros(max_requests, dtype=torch.int64, device=self.device)
 
-    def _dev(self, a, dtype=torch.int64):
-        t = torch.as_tensor(np.ascontiguousarray(a), dtype=dtype)
+    def _fill(self, dst, a):
+        t = torch.as_tensor(np.ascontiguousarray(a), dtype=dst.dtype)
         if self.device.type == "cuda":
             t = t.pin_memory()
-        return t.to(self.device, non_blocking=True)
+        dst[:t.numel()].copy_(t, non_blocking=True)
+        return dst[:t.numel()]
 
     def build(self, computed, scheduled, token_ids, main_table, comp_table, ring_blocks,
               state_slots) -> HybridBatch:
         qsa = self.qsa.build(computed, scheduled, main_table, comp_table, ring_blocks)
         sched = np.asarray(scheduled, dtype=np.int64)
-        return HybridBatch(token_ids=self._dev(token_ids), qsa=qsa,
+        return HybridBatch(token_ids=self._fill(self.token_ids, token_ids), qsa=qsa,
                            num_decode_tokens=qsa.compressed.num_decodes,
-                           state_slots=self._dev(np.asarray(state_slots, dtype=np.int64)),
-                           logits_rows=self._dev(np.cumsum(sched) - 1))
+                           state_slots=self._fill(self.state_slots, np.asarray(state_slots)),
+                           logits_rows=self._fill(self.logits_rows, np.cumsum(sched) - 1))
 
 
 class HybridDecoder:
@@ -362,6 +369,36 @@ class HybridDecoder:
         return self.logits(hidden, residual, batch)
 
 
+class HybridDecodeGraph:
+    """``HybridDecoder.forward`` captured for a uniform decode batch (one token
+    per request) of one size, replayed after the builder refreshes its
+    buffers. ``columns`` pins the decode logits-width class during capture (0:
+    the compressed page table's capacity). Capture runs the step once as a
+    warm-up, which advances the caches and states like any step."""
+
+    def __init__(self, model: "HybridDecoder", batch: HybridBatch, columns: int = 0):
+        if batch.qsa.main.max_query_len != 1:
+            raise ValueError("graphs are captured for uniform decode batches only")
+        self.num_tokens = batch.num_tokens
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with capture_column_scope(columns), torch.cuda.stream(side):
+            model.forward(batch)
+        torch.cuda.current_stream().wait_stream(side)
+        torch.cuda.synchronize()
+        self.graph = torch.cuda.CUDAGraph()
+        with capture_column_scope(columns), torch.cuda.graph(self.graph):
+            self.logits = model.forward(batch)
+
+    def replay(self, batch: HybridBatch | None = None) -> torch.Tensor:
+        """Replay on the builder's current buffers; returns the logits buffer."""
+        if batch is not None and (batch.num_tokens != self.num_tokens
+                                  or batch.qsa.main.max_query_len != 1):
+            raise ValueError("batch is not a uniform decode batch of the captured size")
+        self.graph.replay()
+        return self.logits
+
+
 @dataclass
 class HybridWorkload:
     """A seeded mixed batch: requests, page tables, GDN slots and the model."""
@@ -385,6 +422,30 @@ class HybridWorkload:
     def build(self) -> HybridBatch:
         return self.builder.build(self.computed, self.scheduled, self.token_ids, self.main_table,
                                   self.comp_table, self.ring_blocks, self.state_slots)
+
+    def build_decode(self) -> HybridBatch:
+        """A uniform decode batch of the workload's decode requests (the
+        leading one-token requests), one more token each."""
+        n = 0
+        while n < len(self.scheduled) and self.scheduled[n] == 1:
+            n += 1
+        if n == 0:
+            raise ValueError("the workload has no decode requests")
+        return self.builder.build(self.computed[:n], [1] * n, self.token_ids[:n],
+                                  self.main_table[:n], self.comp_table[:n], self.ring_blocks[:n],
+                                  self.state_slots[:n])
+
+    def layer_states(self) -> list[torch.Tensor]:
+        """Every tensor a step writes (caches and recurrent states), for tests
+        that restore a starting point."""
+        out = []
+        for layer in self.model.layers:
+            mx = layer.mixer
+            if layer.kind == "full_attention":
+                out += [mx.layer.kv_cache, mx.indexer.raw_key_cache, mx.indexer.compressed_key_cache]
+            else:
+                out += [mx.conv_state, mx.ssm_state]
+        return out
 
 
 def make_hybrid_workload(cfg: HybridConfig, *, decode_lens, chunk_prefixes, chunk: int, device,

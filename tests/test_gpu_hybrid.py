@@ -13,7 +13,8 @@ import torch
 
 import oracle
 from oracle import hybrid as H
-from qsa_vllm_amd.hybrid import GatedDeltaNet, HybridBatchBuilder, HybridConfig, _Init, make_hybrid_workload
+from qsa_vllm_amd.hybrid import (GatedDeltaNet, HybridBatchBuilder, HybridConfig, HybridDecodeGraph,
+                                 _Init, make_hybrid_workload)
 from qsa_vllm_amd.ops import hybrid_layers as L
 
 pytestmark = pytest.mark.gpu
@@ -256,3 +257,31 @@ def test_gdn_sequence_without_slot_has_no_state():
                        [(list(range(5)), 0), (list(range(5, 8)), 1)], key_heads=2,
                        value_heads=4, key_dim=128, value_dim=128, eps=1e-6)
     _close(got.cpu(), want, "gdn without state")
+
+
+def test_decode_graph_replay_equals_eager():
+    """The whole model's uniform decode step from a HIP graph equals eager, for
+    a batch other than the captured one (new tokens and positions)."""
+    wl = _workload(seed=7)
+    start = [t.clone() for t in wl.layer_states()]
+
+    def restore():
+        for t, s0 in zip(wl.layer_states(), start):
+            t.copy_(s0)
+
+    graph = HybridDecodeGraph(wl.model, wl.build_decode())
+    base = list(wl.computed)
+    for trial in (1, 2):
+        wl.computed[:4] = [c + trial for c in base[:4]]
+        wl.token_ids[:4] = (wl.token_ids[:4] + 17 * trial) % CFG.vocab_size
+        restore()
+        eager = wl.model.forward(wl.build_decode()).clone()
+        eager_states = [t.clone() for t in wl.layer_states()]
+        restore()
+        got = graph.replay(wl.build_decode()).clone()
+        torch.cuda.synchronize()
+        print(f"[hybrid] decode graph trial {trial}: max diff "
+              f"{(got - eager).abs().max().item():.3e}", flush=True)
+        assert torch.equal(got, eager)
+        for a, b in zip(wl.layer_states(), eager_states):
+            assert torch.equal(a, b)
