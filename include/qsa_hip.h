@@ -306,7 +306,13 @@ int qsa_gated_norm(const void* x, int64_t x_stride, const void* residual_in,
                    int64_t residual_in_stride, void* residual_out, int64_t residual_out_stride,
                    const void* weight, const void* gate_down, const void* gate_up,
                    const void* gate_up_bias, void* out, int64_t out_stride, int rows,
-                   int hidden, int rank, float eps, void* stream);
+                   int hidden, int rank, float eps, void* workspace, size_t workspace_bytes,
+                   void* stream);
+
+/* Workspace qsa_gated_norm needs for `rows` tokens: non-zero for small
+ * batches (under 1024 tokens), which run as three launches over (16-token
+ * tile, 256-column slice) workgroups with fp32 partials in the workspace. */
+size_t qsa_gated_norm_workspace_bytes(int rows, int hidden);
 
 /*
  * Replaces the SiluAndMul activation of Qwen2MoeMLP (model.py:211-217, vLLM):

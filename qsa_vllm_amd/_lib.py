@@ -132,7 +132,8 @@ SIGNATURES = {
                                            c_ptr]),
     "qsa_gated_norm": (c_i32, [c_ptr, c_i64, c_ptr, c_i64, c_ptr, c_i64,
                                c_ptr, c_ptr, c_ptr, c_ptr, c_ptr, c_i64,
-                               c_i32, c_i32, c_i32, ctypes.c_float, c_ptr]),
+                               c_i32, c_i32, c_i32, ctypes.c_float, c_ptr, c_size, c_ptr]),
+    "qsa_gated_norm_workspace_bytes": (c_size, [c_i32, c_i32]),
     "qsa_silu_mul": (c_i32, [c_ptr, c_i64, c_ptr, c_i64, c_i32, c_i32, c_ptr]),
     "qsa_gdn_prep": (c_i32, [c_ptr, c_i64, c_ptr, c_i64, c_ptr, c_ptr, c_i32,
                              c_ptr, c_ptr, c_ptr, c_i32, c_ptr, c_ptr,

@@ -207,6 +207,158 @@ __global__ __launch_bounds__(64 * W) void gated_norm_kernel(const GatedNormArgs 
 }
 
 // ---------------------------------------------------------------------------
+// Gated RMSNorm for small batches (fewer than kSplitTiles 16-token tiles): the
+// fused kernel would run one workgroup per tile on a handful of CUs. Three
+// launches over (tile, 256-column slice) workgroups of one wave instead, with
+// fp32 partials in a workspace between them:
+//   1. residual add (stored) and per-slice sums of squares;
+//   2. inv from the slice sums (added in slice order), the normalised slice
+//      (stored into out) and its partial down projection (one MFMA per
+//      32-column group, as in the fused kernel);
+//   3. the slice partials of the down projection summed, SiLU, the slice's up
+//      projection, sigmoid and the product with the normalised slice.
+// ---------------------------------------------------------------------------
+constexpr int kSplitTiles = 64;
+constexpr int kSliceCols = 256;
+constexpr int kSliceGroups = kSliceCols / 32;
+
+struct SplitNormArgs {
+  GatedNormArgs n;
+  float* ssq;   // [rows, slices]
+  float* down;  // [rows, slices, 16]
+  int slices;
+};
+
+__global__ __launch_bounds__(64) void split_norm_stats_kernel(const SplitNormArgs a) {
+  const int lane = threadIdx.x, m = lane & 15, g = lane >> 4;
+  const int64_t t = (int64_t)blockIdx.x * kNormTokens + m;
+  const bool ok = t < a.n.rows;
+  const int64_t tl = ok ? t : 0;
+  const int col0 = kSliceCols * blockIdx.y + 8 * g;
+  u32x4 xv[kSliceGroups], rv[kSliceGroups];
+#pragma unroll
+  for (int s = 0; s < kSliceGroups; ++s) xv[s] = load_u32x4(a.n.x + tl * a.n.x_stride + col0 + 32 * s);
+  if (a.n.res_in) {
+#pragma unroll
+    for (int s = 0; s < kSliceGroups; ++s)
+      rv[s] = load_u32x4(a.n.res_in + tl * a.n.res_in_stride + col0 + 32 * s);
+  }
+  float ss = 0.0f;
+#pragma unroll
+  for (int s = 0; s < kSliceGroups; ++s) {
+    float f[8];
+    unpack8(xv[s], f);
+    if (a.n.res_in) {
+      float r[8];
+      unpack8(rv[s], r);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) f[e] = rbf(f[e] + r[e]);
+      if (ok) *reinterpret_cast<u32x4*>(a.n.res_out + t * a.n.res_out_stride + col0 + 32 * s) = pack8(f);
+    }
+#pragma unroll
+    for (int e = 0; e < 8; ++e) ss += f[e] * f[e];
+  }
+  ss += __shfl_xor(ss, 16, 64);
+  ss += __shfl_xor(ss, 32, 64);
+  if (ok && g == 0) a.ssq[t * a.slices + blockIdx.y] = ss;
+}
+
+__global__ __launch_bounds__(64) void split_norm_down_kernel(const SplitNormArgs a) {
+  const int lane = threadIdx.x, m = lane & 15, g = lane >> 4;
+  const int64_t t = (int64_t)blockIdx.x * kNormTokens + m;
+  const bool ok = t < a.n.rows;
+  const int64_t tl = ok ? t : 0;
+  const int col0 = kSliceCols * blockIdx.y + 8 * g;
+  // The normalised input is the residual sum when there is a residual.
+  const uint16_t* src = a.n.res_in ? a.n.res_out + tl * a.n.res_out_stride : a.n.x + tl * a.n.x_stride;
+  u32x4 xv[kSliceGroups];
+#pragma unroll
+  for (int s = 0; s < kSliceGroups; ++s) xv[s] = load_u32x4(src + col0 + 32 * s);
+  float sq = 0.0f;
+  for (int c = 0; c < a.slices; ++c) sq += a.ssq[tl * a.slices + c];
+  const float inv = rsqrtf(sq / (float)a.n.hidden + a.n.eps);
+  f32x4 down = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int s = 0; s < kSliceGroups; ++s) {
+    const int col = col0 + 32 * s;
+    float f[8], w[8];
+    unpack8(xv[s], f);
+    unpack8(load_u32x4(a.n.weight + col), w);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) f[e] = rbf(rbf(f[e] * inv) * w[e]);
+    xv[s] = pack8(f);
+    if (ok) *reinterpret_cast<u32x4*>(a.n.out + t * a.n.out_stride + col) = xv[s];
+    const u32x4 wd = load_u32x4(a.n.gate_down + (int64_t)m * a.n.hidden + col);
+    down = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, xv[s]),
+                                                   __builtin_bit_cast(bf16x8, wd), down, 0, 0, 0);
+  }
+  // down[token 4 g + i][rank m] of this slice
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int64_t tt = (int64_t)blockIdx.x * kNormTokens + 4 * g + i;
+    if (tt < a.n.rows) a.down[(tt * a.slices + blockIdx.y) * kRank + m] = down[i];
+  }
+}
+
+__global__ __launch_bounds__(64) void split_norm_gate_kernel(const SplitNormArgs a) {
+  const int lane = threadIdx.x, m = lane & 15, g = lane >> 4;
+  const int64_t t = (int64_t)blockIdx.x * kNormTokens + m;
+  const bool ok = t < a.n.rows;
+  const int64_t tl = ok ? t : 0;
+  const int col0 = kSliceCols * blockIdx.y + 8 * g;
+  // B operand s^T: lane (m, g < 2) = token m, ranks 8 g .. +7.
+  u32x4 sb = {0, 0, 0, 0};
+  if (g < 2) {
+    float d[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) d[e] = 0.0f;
+    for (int c = 0; c < a.slices; ++c) {
+      const float* dp = a.down + (tl * a.slices + c) * kRank + 8 * g;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) d[e] += dp[e];
+    }
+#pragma unroll
+    for (int e = 0; e < 8; ++e) d[e] = rbf(silu_f(rbf(d[e])));
+    sb = pack8(d);
+  }
+  const uint16_t* zero16 = reinterpret_cast<const uint16_t*>(g_qsa_zero_rows);
+  u32x4 nv[kSliceGroups];
+#pragma unroll
+  for (int s = 0; s < kSliceGroups; ++s) nv[s] = load_u32x4(a.n.out + tl * a.n.out_stride + col0 + 32 * s);
+#pragma unroll
+  for (int s = 0; s < kSliceGroups; ++s) {
+    const int col = col0 + 32 * s;
+    f32x4 up[2];
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const int arow = kSliceCols * blockIdx.y + 32 * s + 8 * (m >> 2) + 4 * h + (m & 3);
+      const u32x4 wu = load_u32x4(g < 2 ? a.n.gate_up + (int64_t)arow * kRank + 8 * g : zero16);
+      const f32x4 z = {0.f, 0.f, 0.f, 0.f};
+      up[h] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, wu),
+                                                      __builtin_bit_cast(bf16x8, sb), z, 0, 0, 0);
+    }
+    float b[8], f[8];
+    unpack8(load_u32x4(a.n.bias + col), b);
+    unpack8(nv[s], f);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) f[e] = rbf(f[e] * rbf(sigmoid_f(rbf(up[e >> 2][e & 3] + b[e]))));
+    nv[s] = pack8(f);
+  }
+  if (ok) {
+#pragma unroll
+    for (int s = 0; s < kSliceGroups; ++s)
+      *reinterpret_cast<u32x4*>(a.n.out + t * a.n.out_stride + col0 + 32 * s) = nv[s];
+  }
+}
+
+size_t split_norm_bytes(int rows, int hidden) {
+  const int tiles = (rows + kNormTokens - 1) / kNormTokens;
+  if (rows <= 0 || tiles >= kSplitTiles || hidden % kSliceCols) return 0;
+  const size_t slices = hidden / kSliceCols;
+  return (size_t)rows * slices * (1 + kRank) * sizeof(float);
+}
+
+// ---------------------------------------------------------------------------
 // SwiGLU activation.
 // ---------------------------------------------------------------------------
 struct SiluMulArgs {
@@ -869,12 +1021,16 @@ bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 
 
 using namespace qsa;
 
+extern "C" size_t qsa_gated_norm_workspace_bytes(int rows, int hidden) {
+  return split_norm_bytes(rows, hidden);
+}
+
 extern "C" int qsa_gated_norm(const void* x, int64_t x_stride, const void* residual_in,
                               int64_t residual_in_stride, void* residual_out,
                               int64_t residual_out_stride, const void* weight,
                               const void* gate_down, const void* gate_up, const void* gate_up_bias,
                               void* out, int64_t out_stride, int rows, int hidden, int rank,
-                              float eps, void* stream) {
+                              float eps, void* workspace, size_t workspace_bytes, void* stream) {
   if (rows < 0) return fail(QSA_ERR_INVALID, "qsa_gated_norm: negative rows");
   if (rows == 0) return QSA_OK;
   if (!x || !weight || !gate_down || !gate_up || !gate_up_bias || !out ||
@@ -894,8 +1050,21 @@ extern "C" int qsa_gated_norm(const void* x, int64_t x_stride, const void* resid
                   static_cast<const uint16_t*>(weight), static_cast<const uint16_t*>(gate_down),
                   static_cast<const uint16_t*>(gate_up), static_cast<const uint16_t*>(gate_up_bias),
                   static_cast<uint16_t*>(out), out_stride, rows, hidden, eps};
-  const dim3 grid((rows + kNormTokens - 1) / kNormTokens);
   hipStream_t s = static_cast<hipStream_t>(stream);
+  const size_t split_bytes = split_norm_bytes(rows, hidden);
+  if (split_bytes) {
+    if (!workspace || workspace_bytes < split_bytes || !aligned16(workspace))
+      return fail(QSA_ERR_WORKSPACE, "qsa_gated_norm: small batches need the workspace of "
+                                     "qsa_gated_norm_workspace_bytes (16-byte aligned)");
+    SplitNormArgs sa{a, static_cast<float*>(workspace), nullptr, hidden / kSliceCols};
+    sa.down = sa.ssq + (size_t)rows * sa.slices;
+    const dim3 sgrid((rows + kNormTokens - 1) / kNormTokens, sa.slices);
+    hipLaunchKernelGGL(split_norm_stats_kernel, sgrid, dim3(64), 0, s, sa);
+    hipLaunchKernelGGL(split_norm_down_kernel, sgrid, dim3(64), 0, s, sa);
+    hipLaunchKernelGGL(split_norm_gate_kernel, sgrid, dim3(64), 0, s, sa);
+    return check_launch("qsa_gated_norm (small batch)");
+  }
+  const dim3 grid((rows + kNormTokens - 1) / kNormTokens);
   switch (hidden / 512) {
     case 1: hipLaunchKernelGGL((gated_norm_kernel<4, 4>), grid, dim3(256), 0, s, a); break;
     case 2: hipLaunchKernelGGL((gated_norm_kernel<8, 4>), grid, dim3(256), 0, s, a); break;

@@ -49,11 +49,14 @@ def gated_norm(x, residual, weight, gate_down, gate_up, gate_up_bias, eps, *, ou
         out = torch.empty(rows, hidden, dtype=torch.bfloat16, device=dev)
     _rows2d(out, "out", hidden)
     res_stride = residual.stride(0) if residual is not None else 0
+    lib = _lib.load()
+    nbytes = lib.qsa_gated_norm_workspace_bytes(rows, hidden)
+    ws = torch.empty(nbytes, dtype=torch.uint8, device=dev) if nbytes else None
     with torch.cuda.device(dev):
         _lib.call("qsa_gated_norm", _ptr(x), x.stride(0), _ptr(residual), res_stride,
                   _ptr(residual), res_stride, _ptr(weight), _ptr(gate_down), _ptr(gate_up),
                   _ptr(gate_up_bias), _ptr(out), out.stride(0), rows, hidden, rank, float(eps),
-                  _stream(dev))
+                  _ptr(ws), nbytes, _stream(dev))
     return out, (residual if residual is not None else x)
 
 

@@ -161,8 +161,11 @@ def _bf16(shape, seed, scale=1.0):
     return (torch.randn(*shape, generator=g) * scale).to(torch.bfloat16)
 
 
+# Under 1024 rows the library takes its small-batch path (three launches over
+# column slices); from 1024 rows the fused 16-token-tile kernel.
 @pytest.mark.parametrize("rows,hidden,residual", [(37, 512, False), (37, 512, True),
-                                                   (5, 4096, True), (130, 2048, True)])
+                                                   (5, 4096, True), (130, 2048, True),
+                                                   (1030, 512, False), (1100, 4096, True)])
 def test_gated_norm_kernel_against_oracle(rows, hidden, residual):
     x = _bf16((rows, hidden), 1, 2.0)
     res = _bf16((rows, hidden), 2) if residual else None
