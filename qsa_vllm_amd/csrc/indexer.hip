@@ -64,6 +64,7 @@ constexpr int kPfWaves = 8;
 constexpr int kPfThreads = 64 * kPfWaves;
 constexpr int kPfRows = kPfRowsPerWave * kPfWaves;
 constexpr int kPfTileKeys = 64;
+constexpr int kPfHeads = 32;  // index-head slots of the A operand (M of the MFMA)
 
 // Per-lane sink for logits a lane must not write (columns past its row's
 // visible count): keeps the store unconditional.
@@ -77,6 +78,8 @@ __global__ __launch_bounds__(kPfThreads) void indexer_prefill_kernel(const Index
   constexpr int PER_THREAD = kPfTileKeys * CH / kPfThreads;
   static_assert(PER_THREAD * kPfThreads == kPfTileKeys * CH, "tile must split evenly");
   __shared__ __attribute__((aligned(16))) char s_keys[2][kPfTileKeys * ROW_BYTES];
+  // One padded 32-head Q row per wave, for the Q layout change (below).
+  __shared__ __attribute__((aligned(16))) char s_q[kPfWaves][kPfHeads * ROW_BYTES];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -84,17 +87,39 @@ __global__ __launch_bounds__(kPfThreads) void indexer_prefill_kernel(const Index
   const int kk = lane & 31;
   const int half = lane >> 5;
   const int req = blockIdx.x;
-  const int base = p.query_start_loc[0];
-  const int query_end = p.query_offset + p.num_rows;
-  const int req_start = max(p.query_start_loc[req] - base, p.query_offset);
-  const int req_end = min(p.query_start_loc[req + 1] - base, query_end);
-  const int tile_row0 = req_start + blockIdx.y * kPfRows;
-  if (tile_row0 >= req_end) return;
-
+  const int t_begin = blockIdx.z * p.key_tiles_per_wg;
   const int num_columns = p.table_width * p.cache_page;
   const int32_t* trow = p.table + (int64_t)req * p.table_row;
   const int32_t* zero_i = reinterpret_cast<const int32_t*>(g_qsa_zero_rows);
   const char* zero = reinterpret_cast<const char*>(g_qsa_zero_rows);
+
+  // Page-table entries of this thread's staging keys (tid + kPfThreads j) /
+  // CH of a tile, for every key inside the table: visibility is applied when
+  // the keys are loaded, so the entries depend on the request alone.
+  auto page_of = [&](int tile, int j) {
+    const int c = tile * kPfTileKeys + (tid + kPfThreads * j) / CH;
+    return *(c < num_columns ? trow + p.page_div.div(c) : zero_i);
+  };
+
+  // Prologue, in issue order: the page entries of the first two tiles, the
+  // request bounds (scalar loads), the visible counts, then the first tile's
+  // keys and Q. A wave's vector loads complete in issue order, so each step
+  // waits for one round trip, and Q streams in behind the keys.
+  int pg_cur[PER_THREAD], pg_next[PER_THREAD];
+#pragma unroll
+  for (int j = 0; j < PER_THREAD; ++j) pg_cur[j] = page_of(t_begin, j);
+#pragma unroll
+  for (int j = 0; j < PER_THREAD; ++j) pg_next[j] = page_of(t_begin + 1, j);
+
+  const int base = load_uniform(p.query_start_loc);
+  const int query_end = p.query_offset + p.num_rows;
+  const int req_start = max(load_uniform(p.query_start_loc + req) - base, p.query_offset);
+  const int req_end = min(load_uniform(p.query_start_loc + req + 1) - base, query_end);
+  // Later rows of a request see more keys: row tiles go out in descending
+  // order so the heaviest workgroups start first and the short ones fill
+  // the end of the launch.
+  const int tile_row0 = req_start + (int)(gridDim.y - 1 - blockIdx.y) * kPfRows;
+  if (tile_row0 >= req_end) return;
 
   // Visible keys of the workgroup's 32 rows: lane l of every wave reads row
   // l % 32, so each wave finds the workgroup maximum on its own.
@@ -105,15 +130,9 @@ __global__ __launch_bounds__(kPfThreads) void indexer_prefill_kernel(const Index
 #pragma unroll
   for (int i = 0; i < kPfRowsPerWave; ++i)
     rvis[i] = __builtin_amdgcn_readlane(my_vis, wave * kPfRowsPerWave + i);
-  const int t_begin = blockIdx.z * p.key_tiles_per_wg;
   const int t_end = min(t_begin + p.key_tiles_per_wg, (wg_vis + kPfTileKeys - 1) / kPfTileKeys);
   if (t_begin >= t_end) return;
 
-  // This thread's staging chunks: key (tid + kPfThreads j) / CH, chunk % CH.
-  auto page_of = [&](int tile, int j) {
-    const int c = tile * kPfTileKeys + (tid + kPfThreads * j) / CH;
-    return *(c < wg_vis ? trow + p.page_div.div(c) : zero_i);
-  };
   auto load_keys = [&](int tile, const int (&pg)[PER_THREAD], u32x4 (&st)[PER_THREAD]) {
 #pragma unroll
     for (int j = 0; j < PER_THREAD; ++j) {
@@ -134,27 +153,54 @@ __global__ __launch_bounds__(kPfThreads) void indexer_prefill_kernel(const Index
     }
   };
 
-  // Prologue: pages of the first two tiles, keys of the first, Q.
-  int pg_cur[PER_THREAD], pg_next[PER_THREAD];
-#pragma unroll
-  for (int j = 0; j < PER_THREAD; ++j) pg_cur[j] = page_of(t_begin, j);
-#pragma unroll
-  for (int j = 0; j < PER_THREAD; ++j) pg_next[j] = page_of(t_begin + 1, j);
   u32x4 st[PER_THREAD];
   load_keys(t_begin, pg_cur, st);
 
+  // Q of the wave's 4 rows. The A operand wants lane (kk, half) to hold head
+  // kk, dims 16 s + 8 half .. +7: loaded directly, every load instruction
+  // would touch 32 head rows for 32 bytes each, which measured ~13 us per
+  // workgroup. Instead each 16-lane group (8 for D = 64) loads one head's
+  // contiguous row, the wave writes the row into its padded LDS slot, and
+  // reads it back in the A layout (the same conflict-free pattern as the
+  // keys). Heads past num_heads and rows past the request are zeros.
+  constexpr int HPL = 64 / CH;         // heads per load instruction
+  constexpr int QLOADS = kPfHeads / HPL;
+  static_assert(QLOADS == KS, "one Q load per K step of the A operand");
   bf16x8 qa[kPfRowsPerWave][KS];
+  {
+    const int qh0 = lane / CH;  // head of this lane in load n: n * HPL + qh0
+    const int qc = lane % CH;   // 16 B chunk of that head's row
 #pragma unroll
-  for (int i = 0; i < kPfRowsPerWave; ++i) {
-    const int r = tile_row0 + wave * kPfRowsPerWave + i;
-    const bool ok = r < req_end && kk < p.num_heads;
-    const uint16_t* qrow = p.q + (int64_t)r * p.q_row + (int64_t)kk * p.q_head;
+    for (int i = 0; i < kPfRowsPerWave; ++i) {
+      const int r = tile_row0 + wave * kPfRowsPerWave + i;
+      const uint16_t* qrow = p.q + (int64_t)r * p.q_row + qc * 8;
 #pragma unroll
-    for (int s = 0; s < KS; ++s)
-      qa[i][s] = __builtin_bit_cast(
-          bf16x8, load_u32x4(ok ? (const void*)(qrow + 16 * s + 8 * half) : (const void*)zero));
+      for (int n = 0; n < QLOADS; ++n) {
+        const int h = n * HPL + qh0;
+        const bool ok = r < req_end && h < p.num_heads;
+        qa[i][n] = __builtin_bit_cast(
+            bf16x8, load_u32x4(ok ? (const void*)(qrow + (int64_t)h * p.q_head) : (const void*)zero));
+      }
+    }
   }
   store_keys(0, st);
+  {
+    char* slot = s_q[wave];
+    const int qh0 = lane / CH;
+    const int qc = lane % CH;
+#pragma unroll
+    for (int i = 0; i < kPfRowsPerWave; ++i) {
+#pragma unroll
+      for (int n = 0; n < QLOADS; ++n)
+        *reinterpret_cast<u32x4*>(slot + (n * HPL + qh0) * ROW_BYTES + qc * 16) =
+            __builtin_bit_cast(u32x4, qa[i][n]);
+      // A wave's LDS accesses complete in order: the reads see the row.
+#pragma unroll
+      for (int s2 = 0; s2 < KS; ++s2)
+        qa[i][s2] = __builtin_bit_cast(
+            bf16x8, *reinterpret_cast<const u32x4*>(slot + kk * ROW_BYTES + (16 * s2 + 8 * half) * 2));
+    }
+  }
   lds_barrier();
 
   float* discard = g_qsa_discard + tid;
@@ -166,29 +212,64 @@ __global__ __launch_bounds__(kPfThreads) void indexer_prefill_kernel(const Index
     for (int j = 0; j < PER_THREAD; ++j) pg_next[j] = page_of(tile + 2, j);
     __builtin_amdgcn_sched_barrier(0);
 
-#pragma unroll
-    for (int kb_i = 0; kb_i < kPfTileKeys / 32; ++kb_i) {
-      const char* krow = &s_keys[buf][(kb_i * 32 + kk) * ROW_BYTES];
-      bf16x8 kb[KS];
-#pragma unroll
-      for (int s = 0; s < KS; ++s)
-        kb[s] = __builtin_bit_cast(bf16x8,
-                                   *reinterpret_cast<const u32x4*>(krow + (16 * s + 8 * half) * 2));
+    // The tile's (key block, row) products in order; the ReLU head-sum of
+    // product j - 1 is interleaved with the MFMAs of product j (one MFMA, then
+    // a few VALU ops), so each wave keeps the matrix pipe busy through its own
+    // epilogues. Without that the per-tile barrier keeps the two waves of a
+    // SIMD in step, and both leave the pipe idle during their epilogues.
+    constexpr int kBlocks = kPfTileKeys / 32;
+    constexpr int kProducts = kBlocks * kPfRowsPerWave;
+    bf16x8 kbf[2][KS];  // B operands of the current and previous key block
+    f32x16 acc[2];
+    // Rows are paired: lanes keep the ReLU head-sum of their 16 heads per
+    // product, and one v_permlane32_swap of the pair's two partials gives
+    // (partial_a, partial_b) = (a lo, b lo) and (a hi, b hi), whose sum holds
+    // row i's 32 logits in lanes 0..31 and row i + 1's in lanes 32..63: one
+    // swap, add and store per two products, every lane storing a logit.
+    static_assert(kPfRowsPerWave % 2 == 0, "rows are paired");
+    float part[2];
+    auto emit = [&](int j, const f32x16& a) {
+      part[j & 1] = relu_head_sum(a);
+      if ((j & 1) == 0) return;
+      const int kb_i = j / kPfRowsPerWave;
+      const int i = (j % kPfRowsPerWave) - 1 + half;  // this lane's row of the pair
+      const auto sw = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(uint32_t, part[0]),
+                                                       __builtin_bit_cast(uint32_t, part[1]),
+                                                       false, false);
+      const float sum = __builtin_bit_cast(float, (uint32_t)sw[0]) +
+                        __builtin_bit_cast(float, (uint32_t)sw[1]);
       const int c = tile * kPfTileKeys + kb_i * 32 + kk;
+      const int r = tile_row0 + wave * kPfRowsPerWave + i;
+      const int vis = half ? rvis[(j % kPfRowsPerWave)] : rvis[(j % kPfRowsPerWave) - 1];
+      float* dst = c < vis ? p.logits + (int64_t)(r - p.query_offset) * p.logits_row + c : discard;
+      *dst = sum * p.scale;
+    };
 #pragma unroll
-      for (int i = 0; i < kPfRowsPerWave; ++i) {
-        f32x16 acc = {};
+    for (int j = 0; j < kProducts; ++j) {
+      const int kb_i = j / kPfRowsPerWave;
+      const int i = j % kPfRowsPerWave;
+      if (i == 0) {
+        const char* krow = &s_keys[buf][(kb_i * 32 + kk) * ROW_BYTES];
 #pragma unroll
         for (int s = 0; s < KS; ++s)
-          acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(qa[i][s], kb[s], acc, 0, 0, 0);
-        const float sum = sum_wave_halves(relu_head_sum(acc));
-        const int r = tile_row0 + wave * kPfRowsPerWave + i;
-        float* dst = (half == 0 && c < rvis[i])
-                         ? p.logits + (int64_t)(r - p.query_offset) * p.logits_row + c
-                         : discard;
-        *dst = sum * p.scale;
+          kbf[kb_i & 1][s] = __builtin_bit_cast(
+              bf16x8, *reinterpret_cast<const u32x4*>(krow + (16 * s + 8 * half) * 2));
       }
+      f32x16 a = {};
+#pragma unroll
+      for (int s = 0; s < KS; ++s)
+        a = __builtin_amdgcn_mfma_f32_32x32x16_bf16(qa[i][s], kbf[kb_i & 1][s], a, 0, 0, 0);
+      acc[j & 1] = a;
+      if (j > 0) emit(j - 1, acc[(j - 1) & 1]);
+      if (i == 0) __builtin_amdgcn_sched_group_barrier(0x100, KS, 0);  // LDS reads first
+#pragma unroll
+      for (int s = 0; s < KS; ++s) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA
+        __builtin_amdgcn_sched_group_barrier(0x002, 5, 0);  // then VALU of the epilogue
+      }
+      __builtin_amdgcn_sched_barrier(0);
     }
+    emit(kProducts - 1, acc[(kProducts - 1) & 1]);
     __builtin_amdgcn_sched_barrier(0);
     store_keys(buf ^ 1, st);
     lds_barrier();

@@ -49,11 +49,25 @@ __device__ __forceinline__ const char* key_ptr(const IndexerParams& p, const int
   return p.k + (int64_t)page * p.kb + (int64_t)off * p.kt;
 }
 
+// max(x, 0) as a signed-integer max of the fp32 bits: equal to the float
+// ReLU for every non-NaN x (negative floats, -0.0 included, are negative
+// integers) in one v_max_i32, where fmaxf first quiets its operand (a second
+// VALU op under IEEE mode).
+__device__ __forceinline__ float relu_f32(float x) {
+  return __int_as_float(max(__float_as_int(x), 0));
+}
+
+// Sum of the ReLU of a lane's 16 accumulator heads, as a pairwise tree (four
+// dependent adds instead of sixteen).
 __device__ __forceinline__ float relu_head_sum(const f32x16& acc) {
-  float s = 0.0f;
+  float r[16];
 #pragma unroll
-  for (int i = 0; i < 16; ++i) s += fmaxf(acc[i], 0.0f);
-  return s;
+  for (int i = 0; i < 16; ++i) r[i] = relu_f32(acc[i]);
+#pragma unroll
+  for (int w = 8; w >= 1; w >>= 1)
+#pragma unroll
+    for (int i = 0; i < w; ++i) r[i] += r[i + w];
+  return r[0];
 }
 
 // ---------------------------------------------------------------------------
@@ -118,7 +132,7 @@ __device__ __forceinline__ float tile_logit(const IndexerParams& p, const bf16x8
 #pragma unroll
     for (int s = 0; s < D / 32; ++s)
       acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(qa[hb][s], kb[s], acc, 0, 0, 0);
-    sum += fmaxf(acc[0], 0.0f) + fmaxf(acc[1], 0.0f) + fmaxf(acc[2], 0.0f) + fmaxf(acc[3], 0.0f);
+    sum += (relu_f32(acc[0]) + relu_f32(acc[1])) + (relu_f32(acc[2]) + relu_f32(acc[3]));
   }
   sum += shfl_xor_f(sum, 16);
   return sum_wave_halves(sum) * p.scale;

@@ -65,15 +65,22 @@ __device__ __forceinline__ float shfl_xor_f(float v, int mask) { return __shfl_x
 // v_permlane32_swap a, b exchanges the upper half of a with the lower half of
 // b; with a and b both holding v, a becomes (v[0..31], v[0..31]) and b
 // (v[32..63], v[32..63]), so a + b adds each lane to its partner (lower half
-// first in every lane, so both halves get the same bits). Written as inline
-// asm with both operands read-write so they get distinct registers (a swap of
-// a register with itself is a rotation); the nops cover the VALU-write ->
-// cross-lane-read hazard on either side.
+// first in every lane, so both halves get the same bits). The builtin ties
+// both operands to its results, so they get distinct registers (a swap of a
+// register with itself would be a rotation), and the compiler places the
+// hazard nops and may schedule it like any other VALU op.
 __device__ __forceinline__ float sum_wave_halves(float v) {
-  uint32_t a = __builtin_bit_cast(uint32_t, v);
-  uint32_t b = a;
-  asm volatile("s_nop 1\n\tv_permlane32_swap_b32 %0, %1\n\ts_nop 1" : "+v"(a), "+v"(b));
-  return __builtin_bit_cast(float, a) + __builtin_bit_cast(float, b);
+  const uint32_t a = __builtin_bit_cast(uint32_t, v);
+  const auto r = __builtin_amdgcn_permlane32_swap(a, a, false, false);
+  return __builtin_bit_cast(float, (uint32_t)r[0]) + __builtin_bit_cast(float, (uint32_t)r[1]);
+}
+
+// Load of a wave-uniform address through the scalar memory path (the
+// constant address space: the data must not change during the kernel). Its
+// wait is on the scalar counter, so it never queues behind vector loads.
+template <typename T>
+__device__ __forceinline__ T load_uniform(const T* p) {
+  return *(const __attribute__((address_space(4))) T*)p;
 }
 
 __device__ __forceinline__ u32x4 load_u32x4(const void* p) {
