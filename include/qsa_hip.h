@@ -199,6 +199,16 @@ int qsa_indexer_decode(const void* q, int64_t q_row_stride, int64_t q_head_strid
                        void* stream);
 
 /*
+ * Rows per logits span of the prefill selection (ops/indexer.py:324-329
+ * chunks rows by QSA_INDEXER_WORKSPACE_MB): the largest count within
+ * cap_bytes of fp32 logits of logits_cols columns, rounded down to whole
+ * launch rounds (one 32-row workgroup per compute unit) when the cap allows
+ * one. Only the launch count differs from the reference's chunking; every
+ * row's selection is the same.
+ */
+int qsa_indexer_prefill_span_rows(int logits_cols, int64_t cap_bytes);
+
+/*
  * Replaces _prefill_logits (ops/indexer.py:117-223, launch :282-302).
  *
  * q / visible are indexed by the prefill-relative absolute row; logits rows by

@@ -113,6 +113,7 @@ SIGNATURES = {
                                     c_i32, c_i32, c_i32,
                                     c_ptr, c_i64, c_i32,
                                     c_ptr]),
+    "qsa_indexer_prefill_span_rows": (c_i32, [c_i32, c_i64]),
     "qsa_sparse_attention_splits": (c_i32, [c_i32, c_i32, c_i32, c_i32, c_i32, c_i32]),
     "qsa_sparse_attention_workspace_bytes": (c_size, [c_i32, c_i32, c_i32, c_i32]),
     "qsa_sparse_attention": (c_i32, [c_ptr, c_i64, c_i64, c_i32, c_i32, c_i32,

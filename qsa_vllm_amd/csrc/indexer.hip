@@ -47,7 +47,11 @@ __global__ __launch_bounds__(64) void indexer_decode_kernel(const IndexerParams 
 }
 
 // ---------------------------------------------------------------------------
-// Prefill: grid (requests, row tiles of 32, key chunks), 8 waves x 4 rows.
+// Prefill: grid (32-row tiles of the call's rows, key chunks), 8 waves x 4
+// rows. A tile's rows need not share a request: the workgroup makes one pass
+// over the keys per request in the tile (a tile crossing a request boundary
+// makes two). The grid depends only on the call's row count, so every
+// launched workgroup has rows.
 //
 // Per 64-key tile, the workgroup stages the keys once in LDS (double
 // buffered) and every wave multiplies them against its 4 rows' Q (held in
@@ -65,10 +69,12 @@ constexpr int kPfThreads = 64 * kPfWaves;
 constexpr int kPfRows = kPfRowsPerWave * kPfWaves;
 constexpr int kPfTileKeys = 64;
 constexpr int kPfHeads = 32;  // index-head slots of the A operand (M of the MFMA)
+constexpr int kCUs = 256;     // compute units of an MI355X
 
-// Per-lane sink for logits a lane must not write (columns past its row's
-// visible count): keeps the store unconditional.
-static __device__ float g_qsa_discard[kPfThreads];
+// Sink for logits a lane must not write (columns past its row's visible
+// count), shared by all lanes: keeps the store unconditional without a
+// per-lane address register.
+static __device__ float g_qsa_discard[1];
 
 template <int D>
 __global__ __launch_bounds__(kPfThreads) void indexer_prefill_kernel(const IndexerParams p) {
@@ -86,13 +92,41 @@ __global__ __launch_bounds__(kPfThreads) void indexer_prefill_kernel(const Index
   const int wave = tid >> 6;
   const int kk = lane & 31;
   const int half = lane >> 5;
-  const int req = blockIdx.x;
-  const int t_begin = blockIdx.z * p.key_tiles_per_wg;
   const int num_columns = p.table_width * p.cache_page;
-  const int32_t* trow = p.table + (int64_t)req * p.table_row;
   const int32_t* zero_i = reinterpret_cast<const int32_t*>(g_qsa_zero_rows);
   const char* zero = reinterpret_cast<const char*>(g_qsa_zero_rows);
 
+  // The workgroup's 32 consecutive rows of this call's span. Later rows of a
+  // request see more keys, so tiles go out last-first: the heaviest start
+  // first and the short ones fill the end of the launch.
+  const int row0 = p.query_offset + (int)(gridDim.x - 1 - blockIdx.x) * kPfRows;
+  const int row_end = min(row0 + kPfRows, p.query_offset + p.num_rows);
+  const int t_begin = blockIdx.y * p.key_tiles_per_wg;
+  const int base = load_uniform(p.query_start_loc);
+
+  // Request of row0: the last r with query_start_loc[r] - base <= row0 (the
+  // last of any empty requests starting there is the one holding the row).
+  int req = -1;
+  for (int r0 = 0; r0 < p.num_requests; r0 += 64) {
+    const int r = r0 + lane;
+    const bool le = r < p.num_requests && p.query_start_loc[r] - base <= row0;
+    const int n = __builtin_popcountll(__ballot(le));
+    req += n;
+    if (n < 64) break;
+  }
+  // The 32 rows take one pass over the keys per request they belong to (one,
+  // unless the tile crosses a request boundary); in a pass, rows of other
+  // requests see no keys.
+  int seg_begin = row0;
+  int seg_end = min(load_uniform(p.query_start_loc + req + 1) - base, row_end);
+  if (seg_end <= seg_begin) return;
+
+  // Pass state: the request's page-table row, the page entries of the next
+  // two tiles to stage, the visible keys of the pass's rows and its tiles.
+  const int32_t* trow;
+  int pg_cur[PER_THREAD], pg_next[PER_THREAD];
+  int rvis[kPfRowsPerWave];
+  int wg_vis, t_end;
   // Page-table entries of this thread's staging keys (tid + kPfThreads j) /
   // CH of a tile, for every key inside the table: visibility is applied when
   // the keys are loaded, so the entries depend on the request alone.
@@ -100,39 +134,24 @@ __global__ __launch_bounds__(kPfThreads) void indexer_prefill_kernel(const Index
     const int c = tile * kPfTileKeys + (tid + kPfThreads * j) / CH;
     return *(c < num_columns ? trow + p.page_div.div(c) : zero_i);
   };
-
-  // Prologue, in issue order: the page entries of the first two tiles, the
-  // request bounds (scalar loads), the visible counts, then the first tile's
-  // keys and Q. A wave's vector loads complete in issue order, so each step
-  // waits for one round trip, and Q streams in behind the keys.
-  int pg_cur[PER_THREAD], pg_next[PER_THREAD];
+  // Issues the pass's page entries, then its visible counts (lane l of every
+  // wave reads row l % 32, so each wave finds the workgroup maximum itself).
+  auto setup_pass = [&]() {
+    trow = p.table + (int64_t)req * p.table_row;
 #pragma unroll
-  for (int j = 0; j < PER_THREAD; ++j) pg_cur[j] = page_of(t_begin, j);
+    for (int j = 0; j < PER_THREAD; ++j) pg_cur[j] = page_of(t_begin, j);
 #pragma unroll
-  for (int j = 0; j < PER_THREAD; ++j) pg_next[j] = page_of(t_begin + 1, j);
-
-  const int base = load_uniform(p.query_start_loc);
-  const int query_end = p.query_offset + p.num_rows;
-  const int req_start = max(load_uniform(p.query_start_loc + req) - base, p.query_offset);
-  const int req_end = min(load_uniform(p.query_start_loc + req + 1) - base, query_end);
-  // Later rows of a request see more keys: row tiles go out in descending
-  // order so the heaviest workgroups start first and the short ones fill
-  // the end of the launch.
-  const int tile_row0 = req_start + (int)(gridDim.y - 1 - blockIdx.y) * kPfRows;
-  if (tile_row0 >= req_end) return;
-
-  // Visible keys of the workgroup's 32 rows: lane l of every wave reads row
-  // l % 32, so each wave finds the workgroup maximum on its own.
-  const int vr = tile_row0 + kk;
-  const int my_vis = vr < req_end ? min(min(p.visible[vr], num_columns), p.logits_cols) : 0;
-  const int wg_vis = (int)__ockl_wfred_max_u32((uint32_t)my_vis);
-  int rvis[kPfRowsPerWave];
+    for (int j = 0; j < PER_THREAD; ++j) pg_next[j] = page_of(t_begin + 1, j);
+    const int vr = row0 + kk;
+    const int my_vis = vr >= seg_begin && vr < seg_end
+                           ? min(min(p.visible[vr], num_columns), p.logits_cols)
+                           : 0;
+    wg_vis = (int)__ockl_wfred_max_u32((uint32_t)my_vis);
 #pragma unroll
-  for (int i = 0; i < kPfRowsPerWave; ++i)
-    rvis[i] = __builtin_amdgcn_readlane(my_vis, wave * kPfRowsPerWave + i);
-  const int t_end = min(t_begin + p.key_tiles_per_wg, (wg_vis + kPfTileKeys - 1) / kPfTileKeys);
-  if (t_begin >= t_end) return;
-
+    for (int i = 0; i < kPfRowsPerWave; ++i)
+      rvis[i] = __builtin_amdgcn_readlane(my_vis, wave * kPfRowsPerWave + i);
+    t_end = min(t_begin + p.key_tiles_per_wg, (wg_vis + kPfTileKeys - 1) / kPfTileKeys);
+  };
   auto load_keys = [&](int tile, const int (&pg)[PER_THREAD], u32x4 (&st)[PER_THREAD]) {
 #pragma unroll
     for (int j = 0; j < PER_THREAD; ++j) {
@@ -153,8 +172,10 @@ __global__ __launch_bounds__(kPfThreads) void indexer_prefill_kernel(const Index
     }
   };
 
-  u32x4 st[PER_THREAD];
-  load_keys(t_begin, pg_cur, st);
+  // First pass prologue, in issue order: page entries, visible counts, Q,
+  // the first tile's keys. A wave's vector loads complete in issue order, so
+  // the visible counts wait for one round trip, and Q arrives with the keys.
+  setup_pass();
 
   // Q of the wave's 4 rows. The A operand wants lane (kk, half) to hold head
   // kk, dims 16 s + 8 half .. +7: loaded directly, every load instruction
@@ -162,32 +183,29 @@ __global__ __launch_bounds__(kPfThreads) void indexer_prefill_kernel(const Index
   // workgroup. Instead each 16-lane group (8 for D = 64) loads one head's
   // contiguous row, the wave writes the row into its padded LDS slot, and
   // reads it back in the A layout (the same conflict-free pattern as the
-  // keys). Heads past num_heads and rows past the request are zeros.
+  // keys). Heads past num_heads and rows past the span are zeros.
   constexpr int HPL = 64 / CH;         // heads per load instruction
   constexpr int QLOADS = kPfHeads / HPL;
   static_assert(QLOADS == KS, "one Q load per K step of the A operand");
+  const int qh0 = lane / CH;  // head of this lane in load n: n * HPL + qh0
+  const int qc = lane % CH;   // 16 B chunk of that head's row
   bf16x8 qa[kPfRowsPerWave][KS];
-  {
-    const int qh0 = lane / CH;  // head of this lane in load n: n * HPL + qh0
-    const int qc = lane % CH;   // 16 B chunk of that head's row
 #pragma unroll
-    for (int i = 0; i < kPfRowsPerWave; ++i) {
-      const int r = tile_row0 + wave * kPfRowsPerWave + i;
-      const uint16_t* qrow = p.q + (int64_t)r * p.q_row + qc * 8;
+  for (int i = 0; i < kPfRowsPerWave; ++i) {
+    const int r = row0 + wave * kPfRowsPerWave + i;
+    const uint16_t* qrow = p.q + (int64_t)r * p.q_row + qc * 8;
 #pragma unroll
-      for (int n = 0; n < QLOADS; ++n) {
-        const int h = n * HPL + qh0;
-        const bool ok = r < req_end && h < p.num_heads;
-        qa[i][n] = __builtin_bit_cast(
-            bf16x8, load_u32x4(ok ? (const void*)(qrow + (int64_t)h * p.q_head) : (const void*)zero));
-      }
+    for (int n = 0; n < QLOADS; ++n) {
+      const int h = n * HPL + qh0;
+      const bool ok = r < row_end && h < p.num_heads;
+      qa[i][n] = __builtin_bit_cast(
+          bf16x8, load_u32x4(ok ? (const void*)(qrow + (int64_t)h * p.q_head) : (const void*)zero));
     }
   }
-  store_keys(0, st);
+  u32x4 st[PER_THREAD];
+  load_keys(t_begin, pg_cur, st);
   {
     char* slot = s_q[wave];
-    const int qh0 = lane / CH;
-    const int qc = lane % CH;
 #pragma unroll
     for (int i = 0; i < kPfRowsPerWave; ++i) {
 #pragma unroll
@@ -201,79 +219,119 @@ __global__ __launch_bounds__(kPfThreads) void indexer_prefill_kernel(const Index
             bf16x8, *reinterpret_cast<const u32x4*>(slot + kk * ROW_BYTES + (16 * s2 + 8 * half) * 2));
     }
   }
-  lds_barrier();
 
-  float* discard = g_qsa_discard + tid;
-  for (int tile = t_begin; tile < t_end; ++tile) {
-    const int buf = (tile - t_begin) & 1;
-    // Next tile's keys and the page entries of the one after.
-    load_keys(tile + 1, pg_next, st);
+  float* discard = g_qsa_discard;
+  for (;;) {
+    if (t_begin < t_end) {  // uniform across the workgroup
+      store_keys(0, st);
+      // Makes stage 0 visible; a previous pass ended at a barrier after its
+      // last reads.
+      lds_barrier();
+      for (int tile = t_begin; tile < t_end; ++tile) {
+        const int buf = (tile - t_begin) & 1;
+        // Next tile's keys and the page entries of the one after.
+        load_keys(tile + 1, pg_next, st);
 #pragma unroll
-    for (int j = 0; j < PER_THREAD; ++j) pg_next[j] = page_of(tile + 2, j);
-    __builtin_amdgcn_sched_barrier(0);
+        for (int j = 0; j < PER_THREAD; ++j) pg_next[j] = page_of(tile + 2, j);
+        __builtin_amdgcn_sched_barrier(0);
 
-    // The tile's (key block, row) products in order; the ReLU head-sum of
-    // product j - 1 is interleaved with the MFMAs of product j (one MFMA, then
-    // a few VALU ops), so each wave keeps the matrix pipe busy through its own
-    // epilogues. Without that the per-tile barrier keeps the two waves of a
-    // SIMD in step, and both leave the pipe idle during their epilogues.
-    constexpr int kBlocks = kPfTileKeys / 32;
-    constexpr int kProducts = kBlocks * kPfRowsPerWave;
-    bf16x8 kbf[2][KS];  // B operands of the current and previous key block
-    f32x16 acc[2];
-    // Rows are paired: lanes keep the ReLU head-sum of their 16 heads per
-    // product, and one v_permlane32_swap of the pair's two partials gives
-    // (partial_a, partial_b) = (a lo, b lo) and (a hi, b hi), whose sum holds
-    // row i's 32 logits in lanes 0..31 and row i + 1's in lanes 32..63: one
-    // swap, add and store per two products, every lane storing a logit.
-    static_assert(kPfRowsPerWave % 2 == 0, "rows are paired");
-    float part[2];
-    auto emit = [&](int j, const f32x16& a) {
-      part[j & 1] = relu_head_sum(a);
-      if ((j & 1) == 0) return;
-      const int kb_i = j / kPfRowsPerWave;
-      const int i = (j % kPfRowsPerWave) - 1 + half;  // this lane's row of the pair
-      const auto sw = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(uint32_t, part[0]),
-                                                       __builtin_bit_cast(uint32_t, part[1]),
-                                                       false, false);
-      const float sum = __builtin_bit_cast(float, (uint32_t)sw[0]) +
-                        __builtin_bit_cast(float, (uint32_t)sw[1]);
-      const int c = tile * kPfTileKeys + kb_i * 32 + kk;
-      const int r = tile_row0 + wave * kPfRowsPerWave + i;
-      const int vis = half ? rvis[(j % kPfRowsPerWave)] : rvis[(j % kPfRowsPerWave) - 1];
-      float* dst = c < vis ? p.logits + (int64_t)(r - p.query_offset) * p.logits_row + c : discard;
-      *dst = sum * p.scale;
-    };
+        // The tile's (key block, row) products in order; the ReLU head-sum of
+        // product j - 1 is interleaved with the MFMAs of product j (one MFMA,
+        // then a few VALU ops), so each wave keeps the matrix pipe busy
+        // through its own epilogues. Without that the per-tile barrier keeps
+        // the two waves of a SIMD in step, and both leave the pipe idle
+        // during their epilogues.
+        constexpr int kBlocks = kPfTileKeys / 32;
+        constexpr int kProducts = kBlocks * kPfRowsPerWave;
+        bf16x8 kbf[2][KS];  // B operands of the current and previous key block
+        f32x16 acc[2];
+        // Rows are paired: lanes keep the ReLU head-sum of their 16 heads per
+        // product, and one v_permlane32_swap of the pair's two partials gives
+        // (partial_a, partial_b) = (a lo, b lo) and (a hi, b hi), whose sum
+        // holds row i's 32 logits in lanes 0..31 and row i + 1's in lanes
+        // 32..63: one swap, add and store per two products, every lane
+        // storing a logit.
+        static_assert(kPfRowsPerWave % 2 == 0, "rows are paired");
+        float part[2];
+        auto emit = [&](int j, const f32x16& a) {
+          part[j & 1] = relu_head_sum(a);
+          if ((j & 1) == 0) return;
+          const int kb_i = j / kPfRowsPerWave;
+          const int i = (j % kPfRowsPerWave) - 1 + half;  // this lane's row of the pair
+          const auto sw = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(uint32_t, part[0]),
+                                                           __builtin_bit_cast(uint32_t, part[1]),
+                                                           false, false);
+          const float sum = __builtin_bit_cast(float, (uint32_t)sw[0]) +
+                            __builtin_bit_cast(float, (uint32_t)sw[1]);
+          const int c = tile * kPfTileKeys + kb_i * 32 + kk;
+          const int r = row0 + wave * kPfRowsPerWave + i;
+          const int vis = half ? rvis[(j % kPfRowsPerWave)] : rvis[(j % kPfRowsPerWave) - 1];
+          float* dst =
+              c < vis ? p.logits + (int64_t)(r - p.query_offset) * p.logits_row + c : discard;
+          *dst = sum * p.scale;
+        };
 #pragma unroll
-    for (int j = 0; j < kProducts; ++j) {
-      const int kb_i = j / kPfRowsPerWave;
-      const int i = j % kPfRowsPerWave;
-      if (i == 0) {
-        const char* krow = &s_keys[buf][(kb_i * 32 + kk) * ROW_BYTES];
+        for (int j = 0; j < kProducts; ++j) {
+          const int kb_i = j / kPfRowsPerWave;
+          const int i = j % kPfRowsPerWave;
+          if (i == 0) {
+            const char* krow = &s_keys[buf][(kb_i * 32 + kk) * ROW_BYTES];
 #pragma unroll
-        for (int s = 0; s < KS; ++s)
-          kbf[kb_i & 1][s] = __builtin_bit_cast(
-              bf16x8, *reinterpret_cast<const u32x4*>(krow + (16 * s + 8 * half) * 2));
+            for (int s2 = 0; s2 < KS; ++s2)
+              kbf[kb_i & 1][s2] = __builtin_bit_cast(
+                  bf16x8, *reinterpret_cast<const u32x4*>(krow + (16 * s2 + 8 * half) * 2));
+          }
+          f32x16 a = {};
+#pragma unroll
+          for (int s2 = 0; s2 < KS; ++s2)
+            a = __builtin_amdgcn_mfma_f32_32x32x16_bf16(qa[i][s2], kbf[kb_i & 1][s2], a, 0, 0, 0);
+          acc[j & 1] = a;
+          if (j > 0) emit(j - 1, acc[(j - 1) & 1]);
+          if (i == 0) __builtin_amdgcn_sched_group_barrier(0x100, KS, 0);  // LDS reads first
+#pragma unroll
+          for (int s2 = 0; s2 < KS; ++s2) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA
+            __builtin_amdgcn_sched_group_barrier(0x002, 5, 0);  // then VALU of the epilogue
+          }
+          __builtin_amdgcn_sched_barrier(0);
+        }
+        emit(kProducts - 1, acc[(kProducts - 1) & 1]);
+        __builtin_amdgcn_sched_barrier(0);
+        store_keys(buf ^ 1, st);
+        lds_barrier();
       }
-      f32x16 a = {};
-#pragma unroll
-      for (int s = 0; s < KS; ++s)
-        a = __builtin_amdgcn_mfma_f32_32x32x16_bf16(qa[i][s], kbf[kb_i & 1][s], a, 0, 0, 0);
-      acc[j & 1] = a;
-      if (j > 0) emit(j - 1, acc[(j - 1) & 1]);
-      if (i == 0) __builtin_amdgcn_sched_group_barrier(0x100, KS, 0);  // LDS reads first
-#pragma unroll
-      for (int s = 0; s < KS; ++s) {
-        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA
-        __builtin_amdgcn_sched_group_barrier(0x002, 5, 0);  // then VALU of the epilogue
-      }
-      __builtin_amdgcn_sched_barrier(0);
     }
-    emit(kProducts - 1, acc[(kProducts - 1) & 1]);
-    __builtin_amdgcn_sched_barrier(0);
-    store_keys(buf ^ 1, st);
-    lds_barrier();
+    // The next request with rows in the tile, if any.
+    seg_begin = seg_end;
+    if (seg_begin >= row_end) break;
+    do {
+      ++req;
+      if (req >= p.num_requests) return;
+      seg_end = min(load_uniform(p.query_start_loc + req + 1) - base, row_end);
+    } while (seg_end <= seg_begin);
+    setup_pass();
+    if (t_begin < t_end) load_keys(t_begin, pg_cur, st);
   }
+}
+
+// Key chunks of a prefill launch: one 8-wave workgroup fills a CU, so a
+// launch of T row tiles runs in ceil(T * c / CUs) rounds of workgroups that
+// each cover 1/c of the key range plus a fixed start (Q and the first tiles,
+// ~12% of a whole-range workgroup). The count with the fewest such units
+// wins: a whole number of rounds keeps whole key ranges (Q loaded once), a
+// launch short of a round splits the keys to fill the chip.
+int prefill_key_chunks(int64_t row_tiles, int max_tiles) {
+  int best_c = 1;
+  double best = 1e300;
+  for (int c = 1; c <= std::min(8, std::max(1, max_tiles)); ++c) {
+    const int64_t rounds = (row_tiles * c + kCUs - 1) / kCUs;
+    const double cost = (double)rounds * (1.0 / c + 0.12);
+    if (cost < best - 1e-9) {
+      best = cost;
+      best_c = c;
+    }
+  }
+  return best_c;
 }
 
 int check_indexer(const void* q, int num_heads, int head_dim, const void* k_cache,
@@ -400,24 +458,28 @@ extern "C" int qsa_indexer_prefill(const void* q, int64_t q_row_stride, int64_t 
   p.num_requests = num_requests;
   p.query_offset = query_offset;
   p.num_rows = num_rows;
-  const int row_span = std::max(1, std::min(num_rows, max_query_len > 0 ? max_query_len : num_rows));
-  const int row_tiles = (row_span + kPfRows - 1) / kPfRows;
+  (void)max_query_len;  // the launch tiles this call's rows, whatever the requests' lengths
+  const int64_t row_tiles = ((int64_t)num_rows + kPfRows - 1) / kPfRows;
   const int max_tiles = (std::min(logits_cols, table_width * cache_page) + kPfTileKeys - 1) /
                         kPfTileKeys;
-  // Whole key ranges per workgroup (Q is loaded once) unless that leaves
-  // fewer than ~2 workgroups per CU; then split the keys into chunks.
-  const int64_t row_wgs = (int64_t)num_requests * row_tiles;
-  int chunks = (int)std::min<int64_t>(std::max<int64_t>(1, 512 / std::max<int64_t>(1, row_wgs)),
-                                      std::max(1, max_tiles));
-  p.key_tiles_per_wg = std::max(1, (max_tiles + chunks - 1) / chunks);
-  const int key_chunks = (std::max(1, max_tiles) + p.key_tiles_per_wg - 1) / p.key_tiles_per_wg;
-  if (row_tiles > 65535 || key_chunks > 65535)
+  const int key_chunks = prefill_key_chunks(row_tiles, max_tiles);
+  p.key_tiles_per_wg = std::max(1, (std::max(1, max_tiles) + key_chunks - 1) / key_chunks);
+  if (row_tiles > INT32_MAX)
     return fail(QSA_ERR_UNSUPPORTED, "qsa_indexer_prefill: grid too large");
-  const dim3 grid(num_requests, row_tiles, key_chunks);
+  const dim3 grid((unsigned)row_tiles, (unsigned)key_chunks);
   hipStream_t s = static_cast<hipStream_t>(stream);
   if (head_dim == 128)
     hipLaunchKernelGGL((indexer_prefill_kernel<128>), grid, dim3(kPfThreads), 0, s, p);
   else
     hipLaunchKernelGGL((indexer_prefill_kernel<64>), grid, dim3(kPfThreads), 0, s, p);
   return check_launch("qsa_indexer_prefill launch");
+}
+
+extern "C" int qsa_indexer_prefill_span_rows(int logits_cols, int64_t cap_bytes) {
+  if (logits_cols <= 0) return 1;
+  const int64_t cap_rows = std::max<int64_t>(1, cap_bytes / (4 * (int64_t)logits_cols));
+  // Whole rounds of one 32-row workgroup per CU when the cap allows one.
+  const int64_t round_rows = (int64_t)kCUs * kPfRows;
+  const int64_t rows = cap_rows >= round_rows ? cap_rows / round_rows * round_rows : cap_rows;
+  return (int)std::min<int64_t>(rows, INT32_MAX);
 }

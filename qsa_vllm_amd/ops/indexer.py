@@ -19,6 +19,7 @@ import os
 
 import torch
 
+from .. import _lib
 from ..graph_dispatch import decode_logits_columns, prefill_logits_width
 from .topk import topk_expand
 
@@ -94,7 +95,9 @@ def qsa_select_paged_prefill(
     rows_total = q.shape[0]
     width = prefill_logits_width(max_seq_len, compress_ratio,
                                  page_table.shape[1] * k_cache.shape[1])
-    rows_per_span = max(1, _LOGITS_CAP_BYTES // (4 * width))
+    # Spans stay within the cap; the library rounds them to whole launch
+    # rounds (only the launch count differs from the reference's chunks).
+    rows_per_span = max(1, int(_lib.load().qsa_indexer_prefill_span_rows(width, _LOGITS_CAP_BYTES)))
     buf = torch.empty(min(rows_total, rows_per_span), width, dtype=torch.float32,
                       device=q.device)
     for a, b in _spans(rows_total, rows_per_span):

@@ -88,6 +88,20 @@ def test_workspace_and_split_helpers():
     assert lib.qsa_sparse_attention_splits(32768, 16, 2, 128, 2063, 0) == 1
 
 
+def test_prefill_span_rows():
+    """Spans never exceed the logits cap, and are whole rounds of 256 x 32 rows
+    when the cap allows one."""
+    lib = _lib.load()
+    cap = 64 << 20
+    assert lib.qsa_indexer_prefill_span_rows(1536, cap) == 8192      # cap 10922 rows
+    assert lib.qsa_indexer_prefill_span_rows(64, cap) == 262144      # cap exactly whole rounds
+    assert lib.qsa_indexer_prefill_span_rows(6000, cap) == cap // (4 * 6000)  # under one round
+    assert lib.qsa_indexer_prefill_span_rows(1 << 30, cap) == 1
+    for cols in (64, 100, 1536, 2048, 4099, 32768):
+        rows = lib.qsa_indexer_prefill_span_rows(cols, cap)
+        assert 1 <= rows and rows * cols * 4 <= cap
+
+
 @pytest.mark.skipif(shutil.which("g++") is None, reason="needs g++")
 def test_fastdiv_exhaustive_host(tmp_path):
     src = tmp_path / "fd.cpp"

@@ -182,6 +182,40 @@ def test_indexer_prefill_parity():
         assert torch.allclose(got[written], want[written], rtol=2e-5, atol=2e-4)
 
 
+@pytest.mark.parametrize("dim,heads", [(128, 32), (64, 20)])
+def test_indexer_prefill_many_requests(dim, heads):
+    """More than 64 requests (the request search takes several ballots), empty
+    requests, 32-row tiles crossing several request boundaries, spans starting
+    inside a request, and key-range chunks."""
+    _note(f"indexer_prefill many requests dim={dim} heads={heads}")
+    g = torch.Generator().manual_seed(23)
+    cpage, width = 16, 16
+    lens = torch.randint(0, 40, (150,), generator=g)
+    lens[torch.rand(150, generator=g) < 0.15] = 0
+    lens[3] = 300  # one long request: tiles inside a single request
+    nreq = len(lens)
+    qsl = torch.zeros(nreq + 1, dtype=torch.int32)
+    qsl[1:] = torch.cumsum(lens, 0).to(torch.int32)
+    qsl += 7
+    rows = int(lens.sum())
+    q = torch.randn(rows, heads, dim, generator=g).to(torch.bfloat16)
+    blocks = nreq * width
+    cache = torch.randn(blocks, cpage, 1, dim, generator=g).to(torch.bfloat16)
+    table = torch.randperm(blocks, generator=g).view(nreq, width).to(torch.int32)
+    lw = width * cpage
+    vis = torch.randint(0, lw + 1, (rows,), generator=g, dtype=torch.int32)
+    for offset, n in [(0, rows), (45, 333), (rows - 70, 70), (1, 1)]:
+        want = oracle.indexer_scores_prefill(q, cache, table, qsl, vis, offset, n, lw)
+        logits = torch.full((n, lw), float("nan"), device=DEV)
+        torch.ops.yulan_qsa_kernels.indexer_prefill(q.to(DEV), cache.to(DEV), table.to(DEV),
+                                                    qsl.to(DEV), vis.to(DEV), logits, offset, n,
+                                                    int(lens.max()))
+        got = logits.cpu()
+        written = ~torch.isnan(want)
+        assert torch.equal(written, ~torch.isnan(got)), (offset, n)
+        assert torch.allclose(got[written], want[written], rtol=2e-5, atol=2e-4), (offset, n)
+
+
 def _attn_check(got, want, what):
     err = (got.float().cpu() - want).abs()
     _note(f"{what}: max_abs={err.max().item():.3e} mean_abs={err.mean().item():.3e}")
