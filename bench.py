@@ -436,7 +436,13 @@ def run_prefill(args, wl):
     out = torch.zeros_like(wl.q)
     width = prefill_logits_width(wl.max_seq_len, s.compress_ratio,
                                  wl.index_table.shape[1] * wl.index_cache.shape[1])
-    logits = torch.empty(rows, width, dtype=torch.float32, device=dev)
+    # The indexer and top-k figures cover the same logits spans as the step
+    # (select_paged_tokens caps the logits buffer and the library sizes spans).
+    from qsa_vllm_amd import _lib
+    from qsa_vllm_amd.ops.indexer import _LOGITS_CAP_BYTES
+    span = max(1, int(_lib.load().qsa_indexer_prefill_span_rows(width, _LOGITS_CAP_BYTES)))
+    spans = [(a, min(rows, a + span)) for a in range(0, rows, span)]
+    logits = torch.empty(min(rows, span), width, dtype=torch.float32, device=dev)
 
     def select():
         select_paged_tokens(wl.q_index, wl.index_cache, wl.index_table, wl.token_to_req,
@@ -449,13 +455,16 @@ def run_prefill(args, wl):
                                    wl.token_to_req, out)
 
     def index_only():
-        torch.ops.yulan_qsa_kernels.indexer_prefill(wl.q_index, wl.index_cache, wl.index_table,
-                                                    wl.query_start_loc, wl.visible, logits, 0,
-                                                    rows, wl.max_query_len)
+        for a, b in spans:
+            torch.ops.yulan_qsa_kernels.indexer_prefill(wl.q_index, wl.index_cache,
+                                                        wl.index_table, wl.query_start_loc,
+                                                        wl.visible, logits[:b - a], a, b - a,
+                                                        wl.max_query_len)
 
     def topk_only():
-        topk_expand(logits, wl.visible, wl.positions, wl.seq_lens, wl.token_to_req, idx,
-                    s.compress_ratio)
+        for a, b in spans:
+            topk_expand(logits[:b - a], wl.visible[a:b], wl.positions[a:b], wl.seq_lens,
+                        wl.token_to_req[a:b], idx[a:b], s.compress_ratio)
 
     def step():
         select()
@@ -516,8 +525,9 @@ def run_prefill(args, wl):
             "unit": "TFLOP/s",
             "frac": round(tflops / BF16_PEAK_TFLOPS, 4),
             "traffic": None,
-            "algorithmic_flops_per_launch": flops,
-            "ms_per_launch": round(idx_ms, 4),
+            "algorithmic_flops_per_step": flops,
+            "launches_per_step": len(spans),
+            "ms_per_step": round(idx_ms, 4),
         },
         "breakdown_ms": {
             "indexer_prefill": round(idx_ms, 4),
