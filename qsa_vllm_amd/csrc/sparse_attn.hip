@@ -787,7 +787,20 @@ struct HeadPlan {
   int groups;          // head groups per row
 };
 
-bool plan_heads(int num_q_heads, int num_kv_heads, HeadPlan* plan) {
+// Decode (physical) rows stream their K/V from HBM. Measured on MI355X (16 q /
+// 2 kv heads x 128, top-k 2048 tokens, four rotating query sets so the
+// selected K/V is not served by the Infinity Cache): a full round of 8-wave
+// workgroups (one per CU) streams fastest, and one kv head per workgroup is
+// the cheapest way to reach it (batch 128: 256 workgroups without a split 49.7
+// us, against 53.2 us for both kv heads per workgroup in 2 splits plus the
+// merge; batch 16: 8 splits 12.0 us against 16.2 us). A split pays for its
+// merge below ~160 workgroups (batch 64: 2 splits 27.5 us, none 29.4 us;
+// batch 96: none 38.0 us, 2 splits 43.8 us). So physical rows group kv heads
+// only while a full round remains, and split smaller batches up to a round.
+constexpr int kDecodeRoundWorkgroups = 256;
+constexpr int kDecodeNoSplitWorkgroups = 160;
+
+bool plan_heads(int num_q_heads, int num_kv_heads, int rows, bool physical, HeadPlan* plan) {
   if (num_kv_heads <= 0 || num_q_heads <= 0 || num_q_heads % num_kv_heads) return false;
   const int group = num_q_heads / num_kv_heads;
   if (group > 16) {
@@ -802,6 +815,9 @@ bool plan_heads(int num_q_heads, int num_kv_heads, HeadPlan* plan) {
         break;
       }
     }
+    if (physical)
+      while (nkv > 1 && (int64_t)rows * (num_q_heads / (nkv * group)) < kDecodeRoundWorkgroups)
+        nkv /= 2;
     plan->nkv = nkv;
     plan->heads_per_wave = nkv * group;
   }
@@ -889,17 +905,25 @@ using namespace qsa;
 extern "C" int qsa_sparse_attention_splits(int rows, int num_q_heads, int num_kv_heads,
                                            int head_dim, int width, int use_decode_kernel) {
   HeadPlan plan;
-  if (rows <= 0 || !plan_heads(num_q_heads, num_kv_heads, &plan)) return 1;
+  const bool physical = use_decode_kernel != 0;
+  if (rows <= 0 || !plan_heads(num_q_heads, num_kv_heads, rows, physical, &plan)) return 1;
   const int tiles = (width + kTile - 1) / kTile;
   const int64_t base = (int64_t)rows * plan.groups;
-  // One 8-wave workgroup per CU, or two 4-wave ones, and at least two tiles
-  // per split (a one-tile split pays for a partial and its merge for nothing).
-  // The decode kernel takes physical slots; prefill rows take logical ids.
-  const int64_t target =
-      waves_for(rows, plan, head_dim, use_decode_kernel != 0) == 8 ? kCUs : 2 * kCUs;
+  // At least two tiles per split (a one-tile split pays for a partial and its
+  // merge for nothing). The decode kernel takes physical slots (splits as
+  // measured, above); prefill rows (logical ids, 4-wave workgroups, two per
+  // CU) split up to two workgroups per CU.
   int splits = 1;
-  while (splits * 2 * base <= target && splits * 2 <= std::max(1, tiles / 2) && splits < 64)
-    splits *= 2;
+  if (physical) {
+    if (base < kDecodeNoSplitWorkgroups)
+      while (splits * base < kDecodeRoundWorkgroups && splits * 2 <= std::max(1, tiles / 2) &&
+             splits < 64)
+        splits *= 2;
+  } else {
+    const int64_t target = 2 * kCUs;
+    while (splits * 2 * base <= target && splits * 2 <= std::max(1, tiles / 2) && splits < 64)
+      splits *= 2;
+  }
   return splits;
 }
 
@@ -926,7 +950,7 @@ extern "C" int qsa_sparse_attention(
   if (head_dim != 64 && head_dim != 128)
     return fail(QSA_ERR_UNSUPPORTED, "qsa_sparse_attention: head_dim must be 64 or 128");
   HeadPlan plan;
-  if (!plan_heads(num_q_heads, num_kv_heads, &plan))
+  if (!plan_heads(num_q_heads, num_kv_heads, rows, indices_are_physical != 0, &plan))
     return fail(QSA_ERR_UNSUPPORTED,
                 "qsa_sparse_attention: query heads must be a multiple of kv heads with a GQA "
                 "group that divides 16 or is a multiple of 16");

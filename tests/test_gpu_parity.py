@@ -248,6 +248,15 @@ def test_attention_physical_parity_wide_batch(hq, hkv, dim, splits, layout):
     _physical_case(hq, hkv, dim, splits, layout, rows=72)
 
 
+@pytest.mark.parametrize("hq,hkv,dim", [(16, 2, 128), (4, 4, 128), (8, 8, 64), (16, 4, 64)])
+@pytest.mark.parametrize("splits", [1, 2])
+def test_attention_physical_parity_grouped_heads(hq, hkv, dim, splits):
+    """Batches of a full round of workgroups or more: decode rows then group
+    several kv heads per workgroup (at smaller batches each kv head gets its
+    own workgroup)."""
+    _physical_case(hq, hkv, dim, splits, "token_major", rows=264)
+
+
 def _physical_case(hq, hkv, dim, splits, layout, rows):
     _note(f"attention physical hq={hq} hkv={hkv} dim={dim} splits={splits} layout={layout} "
           f"rows={rows}")
