@@ -39,8 +39,15 @@ namespace {
 constexpr int kHeadDim = 128;
 
 __device__ __forceinline__ float rbf(float x) { return bf16_lo(pack_bf16x2(x, 0.0f)); }
-__device__ __forceinline__ float sigmoid_f(float x) { return 1.0f / (1.0f + expf(-x)); }
-__device__ __forceinline__ float silu_f(float x) { return x / (1.0f + expf(-x)); }
+// Sigmoid and SiLU through the hardware exp2 and reciprocal, each within a
+// couple of fp32 ulps before the results are rounded to bf16 (exp2 of a large
+// argument is +inf, whose reciprocal is 0). The IEEE expf and fp32 division
+// took ~25 VALU ops per element: the gate phase of the gated norm was
+// VALU-bound on them.
+__device__ __forceinline__ float sigmoid_f(float x) {
+  return __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(-x * 1.4426950408889634f));
+}
+__device__ __forceinline__ float silu_f(float x) { return x * sigmoid_f(x); }
 
 __device__ __forceinline__ void unpack8(const u32x4& v, float (&f)[8]) {
 #pragma unroll
