@@ -130,15 +130,20 @@ def _score_tol(q, keys, dim):
     return 2e-5 * mag + 1e-6
 
 
-@pytest.mark.parametrize("heads,dim,dql", [(32, 128, 1), (8, 64, 1), (4, 128, 2), (48, 128, 1)])
-def test_indexer_decode_parity(heads, dim, dql):
-    _note(f"indexer_decode heads={heads} dim={dim} dql={dql}")
-    g = torch.Generator().manual_seed(heads + dim + dql)
-    reqs, cpage, width = 9, 16, 13
+# The last two cases launch at least one wave per CU, which takes the
+# eight-tiles-per-wave split; the others take four.
+@pytest.mark.parametrize("heads,dim,dql,reqs,width", [
+    (32, 128, 1, 9, 13), (8, 64, 1, 9, 13), (4, 128, 2, 9, 13), (48, 128, 1, 9, 13),
+    (32, 128, 1, 36, 64), (16, 64, 2, 20, 64)])
+def test_indexer_decode_parity(heads, dim, dql, reqs, width):
+    _note(f"indexer_decode heads={heads} dim={dim} dql={dql} reqs={reqs} width={width}")
+    g = torch.Generator().manual_seed(heads + dim + dql + reqs)
+    cpage = 16
     rows = reqs * dql
+    pool = max(150, reqs * width + 7)
     q = torch.randn(rows, heads, dim, generator=g).to(torch.bfloat16)
-    cache = torch.randn(150, cpage, 1, dim, generator=g).to(torch.bfloat16)
-    table = torch.randperm(150, generator=g)[:reqs * width].view(reqs, width).to(torch.int32)
+    cache = torch.randn(pool, cpage, 1, dim, generator=g).to(torch.bfloat16)
+    table = torch.randperm(pool, generator=g)[:reqs * width].view(reqs, width).to(torch.int32)
     vis = torch.randint(0, width * cpage + 1, (rows,), generator=g, dtype=torch.int32)
     vis[0], vis[1] = width * cpage, 0
     cols = width * cpage
@@ -155,6 +160,13 @@ def test_indexer_decode_parity(heads, dim, dql):
             tol = _score_tol(q[r], keys, dim)
             assert ((got[r, :n] - want[r, :n]).abs() <= tol).all(), r
         assert torch.isnan(got[r, n:]).all(), "columns beyond visible must stay untouched"
+    if rows * ((cols + 127) // 128) >= 256:
+        # The first two requests alone take the four-tile split: same bits.
+        sub = 2 * dql
+        small = torch.full((sub, cols), float("nan"), device=DEV)
+        torch.ops.yulan_qsa_kernels.indexer_decode(q[:sub].to(DEV), cache.to(DEV), table[:2].to(DEV),
+                                                   vis[:sub].to(DEV), small, dql)
+        assert torch.equal(small.cpu().nan_to_num(-7.0), got[:sub].nan_to_num(-7.0))
 
 
 def test_indexer_prefill_parity():
