@@ -220,6 +220,17 @@ def main():
     index_us = time_graph(index_graph, n_sets * reps, rounds)
     topk_us = time_graph(topk_graph, n_sets * reps, rounds)
 
+    # The same steps launched eagerly (no graph): host launch overhead included.
+    eager_steps = max(n_sets, (args.steps // n_sets) * n_sets)
+    torch.cuda.synchronize()
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    a.record(stream)
+    for k in range(eager_steps):
+        step(k % n_sets)
+    b.record(stream)
+    torch.cuda.synchronize()
+    eager_us = a.elapsed_time(b) * 1e3 / eager_steps
+
     # Correctness gate on the timed data: counts follow the closed form.
     want_counts = s.token_topk + wl.seq_lens % s.compress_ratio
     for i in range(n_sets):
@@ -271,6 +282,8 @@ def main():
             "sparse_attention": round(attn_us, 3),
             "step": round(ms_step * 1e3, 3),
         },
+        "eager": {"us_per_step": round(eager_us, 3),
+                  "tokens_per_s": round(rows / (eager_us * 1e-6), 1)},
         "indexer_gbps": round(idx_bytes / (index_us * 1e-6) / 1e9, 1),
         "prepare": time_prepare(wl, stream),
         "layer_step": time_layer_step(wl, stream),
