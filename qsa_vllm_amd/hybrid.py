@@ -224,8 +224,16 @@ class GatedDeltaNet:
         dk, dv = cfg.linear_key_head_dim, cfg.linear_value_head_dim
         self.hk, self.hv, self.dk, self.dv, self.r = hk, hv, dk, dv, hv // hk
         self.eps = cfg.rms_norm_eps
-        self.in_proj_qkvz = init.normal(hk * (2 * dk + 2 * self.r * dv), cfg.hidden_size)
-        self.in_proj_ba = init.normal(2 * hv, cfg.hidden_size)
+        self.n_qkvz = hk * (2 * dk + 2 * self.r * dv)
+        qkvz_w = init.normal(self.n_qkvz, cfg.hidden_size)
+        ba_w = init.normal(2 * hv, cfg.hidden_size)
+        # One projection GEMM per call: in_proj_qkvz and in_proj_ba are row
+        # blocks of one weight, their outputs column blocks of one product
+        # (the GDN kernels take row strides).
+        self.in_proj = torch.cat([qkvz_w, ba_w])
+        del qkvz_w, ba_w
+        self.in_proj_qkvz = self.in_proj[:self.n_qkvz]
+        self.in_proj_ba = self.in_proj[self.n_qkvz:]
         self.conv_weight = init.normal(cfg.conv_dim, cfg.conv_kernel, std=0.5)
         self.A_log = init.uniform(hv, low=1.0, high=16.0).log()
         self.dt_bias = torch.ones(hv, dtype=torch.float32, device=init.device)
@@ -236,8 +244,8 @@ class GatedDeltaNet:
 
     def __call__(self, x, batch: "HybridBatch"):
         t = x.shape[0]
-        qkvz = F.linear(x, self.in_proj_qkvz)
-        ba = F.linear(x, self.in_proj_ba)
+        proj = F.linear(x, self.in_proj)
+        qkvz, ba = proj[:, :self.n_qkvz], proj[:, self.n_qkvz:]
         q, k, v, g, beta = gdn_prep(qkvz, ba, self.conv_weight, self.conv_state,
                                     batch.query_start_loc, batch.token_to_seq, batch.state_slots,
                                     self.A_log, self.dt_bias, self.hk, self.hv)
