@@ -556,22 +556,14 @@ def run_prefill(args, wl):
     return 0
 
 
-HYBRID_DECODES, HYBRID_CHUNKS, HYBRID_CHUNK = 112, 16, 512
 
 
 def hybrid_workload(dev, seed=11):
-    """The hybrid decoder's mixed continuous batch: 112 decode requests at
-    contexts U[4096, 32768], then 16 prefill chunks of 512 tokens on prefixes
-    512 * U{0..31}."""
-    import numpy as np
+    """The hybrid decoder's mixed continuous batch (112 decode requests at
+    contexts U[4096, 32768], 16 prefill chunks of 512 tokens)."""
+    from qsa_vllm_amd.hybrid import make_serving_hybrid_workload
 
-    from qsa_vllm_amd.hybrid import HybridConfig, make_hybrid_workload
-
-    rng = np.random.default_rng(seed)
-    decode_lens = rng.integers(4096, 32768, HYBRID_DECODES, endpoint=True).tolist()
-    prefixes = (512 * rng.integers(0, 32, HYBRID_CHUNKS)).tolist()
-    return make_hybrid_workload(HybridConfig(), decode_lens=decode_lens, chunk_prefixes=prefixes,
-                                chunk=HYBRID_CHUNK, device=dev, seed=seed)
+    return make_serving_hybrid_workload(dev, seed=seed)
 
 
 def hybrid_flops(wl):
@@ -696,14 +688,16 @@ def measure_hybrid_decode_graph(wl, steps):
 
 
 def hybrid_description(wl):
+    from qsa_vllm_amd.hybrid import SERVING_CHUNK, SERVING_CHUNKS, SERVING_DECODES
+
     cfg = wl.cfg
     kinds = [layer.kind for layer in wl.model.layers]
     return (f"hybrid decoder step: {cfg.num_layers} layers ({kinds.count('linear_attention')} GDN, "
             f"{kinds.count('full_attention')} QSA), hidden {cfg.hidden_size}, TP{cfg.tp_size} share: "
             f"QSA {cfg.heads}q/{cfg.kv_heads}kv x {cfg.head_dim}, GDN {cfg.key_heads}k/"
             f"{cfg.value_heads}v heads x {cfg.linear_key_head_dim}, MLP {cfg.intermediate}, vocab "
-            f"shard {cfg.vocab_shard}; batch {HYBRID_DECODES} decode (context U[4096,32768]) + "
-            f"{HYBRID_CHUNKS} prefill chunks of {HYBRID_CHUNK}")
+            f"shard {cfg.vocab_shard}; batch {SERVING_DECODES} decode (context U[4096,32768]) + "
+            f"{SERVING_CHUNKS} prefill chunks of {SERVING_CHUNK}")
 
 
 def hybrid_summary(dev):

@@ -1,7 +1,8 @@
 """CPU restatement of the hybrid decoder's layers around the QSA path.
 
-TEST INFRASTRUCTURE ONLY: the checker for ``qsa_vllm_amd.hybrid`` and
-``qsa_vllm_amd.gdn``. Nothing under ``qsa_vllm_amd`` imports it.
+TEST INFRASTRUCTURE ONLY: the checker for ``qsa_vllm_amd.hybrid`` and its
+layer kernels (``qsa_vllm_amd.ops.hybrid_layers``). Nothing under
+``qsa_vllm_amd`` imports it.
 
 Follows ``model.py:60-98`` (gated norm), ``:180-225`` (decoder layer),
 ``attention.py:145-234`` (QSA projection split, output gate, ``o_proj``) and

@@ -83,7 +83,7 @@ def visible_blocks(query_positions, sequence_lengths, token_to_req, compress_rat
 
 
 def decode_logits_columns(max_seq_len: int, compress_ratio: int, capacity: int) -> int:
-    """``graph_dispatch.py:323-331`` outside graph capture: 32768 short bucket or capacity."""
+    """``graph_dispatch.py:26-34`` outside graph capture: 32768 short bucket or capacity."""
     columns = 32768 if max_seq_len // compress_ratio <= 32768 else 0
     return min(columns, capacity) if columns else capacity
 

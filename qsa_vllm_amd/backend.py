@@ -211,7 +211,12 @@ def run_qsa(layer: QSALayerState, impl: YuLanQSAImpl, index_query: torch.Tensor,
             token_to_req: torch.Tensor) -> torch.Tensor:
     """``_run_qsa`` (``attention.py:191-214``) from the prepared index query on:
     select into the layer's top-k buffer (physical slots + counts in uniform
-    decode, logical token ids otherwise), then attend."""
+    decode, logical token ids otherwise), then attend. Without metadata (vLLM's
+    memory-profiling forward, ``attention.py:193-198``) the output is zeroed
+    and nothing else runs."""
+    if main is None or compressed is None:
+        output.zero_()
+        return output
     count = main.num_actual_tokens
     is_decode = main.max_query_len == 1
     key_cache, _ = layer.main_kv_views()

@@ -55,3 +55,17 @@ def capture_column_scope(columns: int):
         yield
     finally:
         _pinned_columns = saved
+
+
+def check_decode_graph_batch(batch, num_tokens: int, columns: int, compress_ratio: int) -> None:
+    """Raise ValueError unless ``batch`` (a ``QSABatch``) may replay a decode
+    graph captured for ``num_tokens`` one-token requests under width class
+    ``columns``: a batch whose longest compressed length exceeds the captured
+    class belongs to the other class's graph (``graph_dispatch.py:26-34``)."""
+    if batch.num_tokens != num_tokens or batch.main.max_query_len != 1:
+        raise ValueError("batch is not a uniform decode batch of the captured size")
+    if columns and batch.compressed.max_seq_len // compress_ratio > columns:
+        raise ValueError(
+            f"batch needs {batch.compressed.max_seq_len // compress_ratio} logits columns; the "
+            f"graph was captured for the {columns}-column width class")
+

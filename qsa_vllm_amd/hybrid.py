@@ -46,14 +46,15 @@ import torch
 import torch.nn.functional as F
 
 from .backend import QSALayerState, YuLanQSAImpl, YuLanQSAIndexer
-from .graph_dispatch import capture_column_scope
+from .graph_dispatch import capture_column_scope, check_decode_graph_batch
 from .layer_step import qsa_layer_step
 from .metadata import QSABatch, QSAMetadataBuilder
 from .ops.hybrid_layers import (gated_norm, gdn_conv_state, gdn_gated_norm, gdn_prep,
                                 gdn_recurrence, silu_mul)
 
 __all__ = ["HybridConfig", "HybridBatch", "HybridBatchBuilder", "HybridDecoder",
-           "HybridDecodeGraph", "HybridWorkload", "make_hybrid_workload"]
+           "HybridDecodeGraph", "HybridWorkload", "make_hybrid_workload",
+           "make_serving_hybrid_workload", "SERVING_DECODES", "SERVING_CHUNKS", "SERVING_CHUNK"]
 
 
 @dataclass(frozen=True)
@@ -229,11 +230,15 @@ class GatedDeltaNet:
         ba_w = init.normal(2 * hv, cfg.hidden_size)
         # One projection GEMM per call: in_proj_qkvz and in_proj_ba are row
         # blocks of one weight, their outputs column blocks of one product
-        # (the GDN kernels take row strides).
-        self.in_proj = torch.cat([qkvz_w, ba_w])
+        # (the GDN kernels take row strides, which must be multiples of 8
+        # elements: zero rows pad the weight to that, for any head count).
+        pad = -(self.n_qkvz + 2 * hv) % 8
+        self.in_proj = torch.cat([qkvz_w, ba_w, qkvz_w.new_zeros(pad, cfg.hidden_size)])
         del qkvz_w, ba_w
+        if self.in_proj.shape[0] % 8:
+            raise ValueError("GDN projection rows must pad to a multiple of 8")
         self.in_proj_qkvz = self.in_proj[:self.n_qkvz]
-        self.in_proj_ba = self.in_proj[self.n_qkvz:]
+        self.in_proj_ba = self.in_proj[self.n_qkvz:self.n_qkvz + 2 * hv]
         self.conv_weight = init.normal(cfg.conv_dim, cfg.conv_kernel, std=0.5)
         self.A_log = init.uniform(hv, low=1.0, high=16.0).log()
         self.dt_bias = torch.ones(hv, dtype=torch.float32, device=init.device)
@@ -245,7 +250,7 @@ class GatedDeltaNet:
     def __call__(self, x, batch: "HybridBatch"):
         t = x.shape[0]
         proj = F.linear(x, self.in_proj)
-        qkvz, ba = proj[:, :self.n_qkvz], proj[:, self.n_qkvz:]
+        qkvz, ba = proj[:, :self.n_qkvz], proj[:, self.n_qkvz:self.n_qkvz + 2 * self.hv]
         q, k, v, g, beta = gdn_prep(qkvz, ba, self.conv_weight, self.conv_state,
                                     batch.query_start_loc, batch.token_to_seq, batch.state_slots,
                                     self.A_log, self.dt_bias, self.hk, self.hv)
@@ -388,6 +393,8 @@ class HybridDecodeGraph:
         if batch.qsa.main.max_query_len != 1:
             raise ValueError("graphs are captured for uniform decode batches only")
         self.num_tokens = batch.num_tokens
+        self.columns = columns
+        self.compress_ratio = model.cfg.compress_ratio
         side = torch.cuda.Stream()
         side.wait_stream(torch.cuda.current_stream())
         with capture_column_scope(columns), torch.cuda.stream(side):
@@ -400,9 +407,9 @@ class HybridDecodeGraph:
 
     def replay(self, batch: HybridBatch | None = None) -> torch.Tensor:
         """Replay on the builder's current buffers; returns the logits buffer."""
-        if batch is not None and (batch.num_tokens != self.num_tokens
-                                  or batch.qsa.main.max_query_len != 1):
-            raise ValueError("batch is not a uniform decode batch of the captured size")
+        if batch is not None:
+            check_decode_graph_batch(batch.qsa, self.num_tokens, self.columns,
+                                     self.compress_ratio)
         self.graph.replay()
         return self.logits
 
@@ -500,3 +507,20 @@ def make_hybrid_workload(cfg: HybridConfig, *, decode_lens, chunk_prefixes, chun
                           scheduled=scheduled, token_ids=token_ids, main_table=main_table.to(dev),
                           comp_table=comp_table.to(dev), ring_blocks=ring_blocks,
                           state_slots=state_slots)
+
+
+# The serving batch of the hybrid step: 112 decode requests at contexts
+# U[4096, 32768], then 16 prefill chunks of 512 tokens on prefixes 512 * U{0..31}.
+SERVING_DECODES, SERVING_CHUNKS, SERVING_CHUNK = 112, 16, 512
+
+
+def make_serving_hybrid_workload(device, seed: int = 11,
+                                 cfg: HybridConfig | None = None) -> HybridWorkload:
+    """The full-size model (32 layers, hidden 4096, TP2 share) on the mixed
+    continuous batch of 112 decode requests and 16 prefill chunks (8304 tokens)."""
+    rng = np.random.default_rng(seed)
+    decode_lens = rng.integers(4096, 32768, SERVING_DECODES, endpoint=True).tolist()
+    prefixes = (SERVING_CHUNK * rng.integers(0, 32, SERVING_CHUNKS)).tolist()
+    return make_hybrid_workload(cfg or HybridConfig(), decode_lens=decode_lens,
+                                chunk_prefixes=prefixes, chunk=SERVING_CHUNK, device=device,
+                                seed=seed)

@@ -17,14 +17,19 @@ from __future__ import annotations
 
 import torch
 
-from .graph_dispatch import capture_column_scope
+from .graph_dispatch import capture_column_scope, check_decode_graph_batch
 
 
 def qsa_layer_step(indexer, impl, layer, batch, index_qk, main_key, main_value, query, output,
                    gate=None):
     """Prepare + select into the layer's top-k buffers (physical slots and
     counts in uniform decode, logical ids otherwise), then sparse attention
-    into ``output``. Returns ``output``."""
+    into ``output``. Returns ``output``. A step without metadata (``batch`` is
+    None: vLLM's memory-profiling forward, ``attention.py:193-198``) zeroes
+    ``output`` and writes nothing else."""
+    if batch is None:
+        output.zero_()
+        return output
     n = batch.num_tokens
     decode = batch.main.max_query_len == 1
     key_cache, value_cache = layer.main_kv_views()
@@ -52,6 +57,7 @@ class QSALayerStepGraph:
             raise ValueError("graphs are captured for uniform decode batches only")
         self.num_tokens = batch.num_tokens
         self.columns = columns
+        self.compress_ratio = indexer.compress_ratio
         args = (indexer, impl, layer, batch, index_qk, main_key, main_value, query, output, gate)
         side = torch.cuda.Stream()
         side.wait_stream(torch.cuda.current_stream())
@@ -65,8 +71,7 @@ class QSALayerStepGraph:
 
     def replay(self, batch=None):
         """Replay on the current metadata buffers; ``batch`` (from the same
-        builder) is checked against the captured shape."""
-        if batch is not None and (batch.num_tokens != self.num_tokens
-                                  or batch.main.max_query_len != 1):
-            raise ValueError("batch is not a uniform decode batch of the captured size")
+        builder) is checked against the captured size and width class."""
+        if batch is not None:
+            check_decode_graph_batch(batch, self.num_tokens, self.columns, self.compress_ratio)
         self.graph.replay()

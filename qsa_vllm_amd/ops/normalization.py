@@ -31,13 +31,33 @@ def rotary_cache(max_position, rotary_dim, theta, device):
     return torch.cat((angles.cos(), angles.sin()), dim=-1).to(torch.bfloat16)
 
 
+def _copy_weight_loader(param: torch.Tensor, loaded_weight: torch.Tensor) -> None:
+    """Checkpoint loader of the gamma: copy a tensor of the same shape into
+    the parameter (what vLLM's ``default_weight_loader`` does for it)."""
+    if param.shape != loaded_weight.shape:
+        raise ValueError(f"weight of shape {tuple(loaded_weight.shape)} does not fit a parameter "
+                         f"of shape {tuple(param.shape)}")
+    param.data.copy_(loaded_weight)
+
+
+def _default_weight_loader():
+    try:
+        from vllm.model_executor.model_loader.weight_utils import default_weight_loader
+    except ImportError:
+        return _copy_weight_loader
+    return default_weight_loader
+
+
 class IndexerRMSNorm(nn.Module):
     """Gamma (bf16, ones at init) and epsilon of an indexer RMSNorm
-    (ops/normalization.py:26-31)."""
+    (ops/normalization.py:26-31). The gamma carries the checkpoint loader
+    vLLM's model loader calls: vLLM's ``default_weight_loader`` when vLLM is
+    installed, else a shape-checked copy."""
 
     def __init__(self, width, epsilon):
         super().__init__()
         self.weight = nn.Parameter(torch.ones(width, dtype=torch.bfloat16))
+        self.weight.weight_loader = _default_weight_loader()
         self.variance_epsilon = epsilon
 
 

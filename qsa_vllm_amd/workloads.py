@@ -51,6 +51,7 @@ class QSAShape:
     chunk: int = 0                     # > 0: chunked prefill of `chunk` new tokens per sequence
     prefix: int = 0
     decode_requests: int = 0           # with chunk > 0: the first requests decode one token
+    table_tokens: int = 0              # > 0: page tables sized for this many tokens per request
     seed: int = 0
 
     @property
@@ -77,6 +78,13 @@ SHAPES = {
         page_size=16, compress_ratio=16, index_heads=32, index_dim=128, token_topk=2048,
         seq_len_min=24576, seq_len_max=24576, seq_len_dist="fixed", chunk=8192,
         prefix=16384, seed=3),
+    # decode_32k with page tables sized for the serving max-model-len of 524288 tokens:
+    # the compressed table holds 2048 pages of 16 keys, so decode scores into the
+    # 32768-column width class.
+    "decode_32k_serving_width": QSAShape(
+        "decode_32k_serving_width", batch=64, num_q_heads=16, num_kv_heads=2, head_dim=128,
+        page_size=16, compress_ratio=16, index_heads=32, index_dim=128, token_topk=2048,
+        seq_len_min=8192, seq_len_max=32768, table_tokens=524288, seed=2),
     # Long-context skewed decode: batch 8, lognormal(median 64k, sigma 0.5) in [16k, 128k].
     "decode_long_skew": QSAShape(
         "decode_long_skew", batch=8, num_q_heads=16, num_kv_heads=2, head_dim=128,
@@ -134,13 +142,15 @@ def _seq_lens(shape: QSAShape, gen: torch.Generator) -> torch.Tensor:
     raise ValueError(f"unknown seq_len_dist {shape.seq_len_dist}")
 
 
-def _paged_table(lengths: torch.Tensor, page: int, pool: int, gen: torch.Generator):
-    """Permuted page assignment: returns (table [B, max_pages] int32, num_blocks)."""
+def _paged_table(lengths: torch.Tensor, page: int, pool: int, gen: torch.Generator,
+                 min_width: int = 0):
+    """Permuted page assignment: returns (table [B, max(max_pages, min_width)]
+    int32, -1 past each sequence's pages; num_blocks)."""
     pages = [(int(n) + page - 1) // page for n in lengths]
     need = sum(pages)
     num_blocks = max(need, pool, 1)
     perm = torch.randperm(num_blocks, generator=gen)
-    width = max(max(pages, default=1), 1)
+    width = max(max(pages, default=1), 1, min_width)
     table = torch.full((len(pages), width), -1, dtype=torch.int32)
     at = 0
     for i, n in enumerate(pages):
@@ -193,9 +203,12 @@ def make_workload(shape: QSAShape | str, device="cpu", **overrides) -> QSAWorklo
     r = shape.compress_ratio
     visible = torch.minimum((positions + 1) // r, seq_lens[token_to_req.long()] // r).to(torch.int32)
 
-    block_table, num_blocks = _paged_table(seq_lens, shape.page_size, shape.pool_pages, cpu_gen)
+    block_table, num_blocks = _paged_table(seq_lens, shape.page_size, shape.pool_pages, cpu_gen,
+                                           -(-shape.table_tokens // shape.page_size))
     index_keys = seq_lens // r
-    index_table, index_blocks = _paged_table(index_keys, shape.index_cache_page, 0, cpu_gen)
+    index_table, index_blocks = _paged_table(
+        index_keys, shape.index_cache_page, 0, cpu_gen,
+        -(-(shape.table_tokens // r) // shape.index_cache_page))
 
     d, hkv = shape.head_dim, shape.num_kv_heads
     if shape.kv_layout == "token_major":

@@ -1,21 +1,33 @@
 """The hybrid decoder step on the GPU against the CPU oracle.
 
 A small model (GDN and QSA layers at the serving head shapes, small hidden
-size) steps one mixed batch: decode requests, then ragged prefill chunks.
-Contexts stay below the top-k budget, so every QSA row selects its whole
-causal context and the oracle's QSA layer is dense causal attention over the
-paged cache. Each layer is checked on the GPU layer's own inputs (so rounding
-does not accumulate across layers), then the final norm and LM head."""
+size) steps one mixed batch: decode requests, then ragged prefill chunks. It
+runs twice: with a top-k budget of 2048 tokens, which every context stays
+below (every QSA row attends over its whole causal context), and with a
+budget of 256 tokens, which most rows exceed (the QSA layers really select).
+Each layer is checked on the GPU layer's own inputs (so rounding does not
+accumulate across layers): the QSA selection bit-exact against the oracle's
+top-k on the indexer kernel's logits of the layer's prepared index queries,
+those logits against the oracle's scores, and the layer's output against the
+oracle's attention over the selection; then the final norm and LM head.
+
+The full-size model (32 layers, hidden 4096) on the serving batch of 8304
+tokens is checked by properties: finite logits, every QSA layer's selection
+against the closed-form counts and row invariants, top-k bit-exact on sampled
+rows of one QSA layer, and the decode graph's replay equal to eager."""
 
 import numpy as np
 import pytest
 import torch
 
 import oracle
+import qsa_vllm_amd.backend as backend_module
 from oracle import hybrid as H
+from qsa_vllm_amd.graph_dispatch import decode_logits_columns, prefill_logits_width
 from qsa_vllm_amd.hybrid import (GatedDeltaNet, HybridBatchBuilder, HybridConfig, HybridDecodeGraph,
-                                 _Init, make_hybrid_workload)
+                                 _Init, make_hybrid_workload, make_serving_hybrid_workload)
 from qsa_vllm_amd.ops import hybrid_layers as L
+from tests.selection_checks import logical_invariants
 
 pytestmark = pytest.mark.gpu
 DEV = "cuda:0"
@@ -23,10 +35,15 @@ DEV = "cuda:0"
 CFG = HybridConfig(num_layers=4, hidden_size=512, vocab_size=512, tp_size=2, num_heads=32,
                    num_kv_heads=4, head_dim=128, intermediate_size=1024, linear_num_key_heads=4,
                    linear_num_value_heads=8, indexer_heads=8, token_topk=2048, init_std=0.05)
+# Top-k 256 tokens = 16 blocks of 16: rows past position 271 select.
+CFG_SELECT = HybridConfig(num_layers=4, hidden_size=512, vocab_size=512, tp_size=2, num_heads=32,
+                          num_kv_heads=4, head_dim=128, intermediate_size=1024,
+                          linear_num_key_heads=4, linear_num_value_heads=8, indexer_heads=8,
+                          token_topk=256, init_std=0.05)
 
 
-def _workload(seed):
-    return make_hybrid_workload(CFG, decode_lens=[700, 1500, 33, 260], chunk_prefixes=[0, 300, 1000],
+def _workload(seed, cfg=CFG):
+    return make_hybrid_workload(cfg, decode_lens=[700, 1500, 33, 260], chunk_prefixes=[0, 300, 1000],
                                 chunk=100, device=DEV, seed=seed, state_std=0.05)
 
 
@@ -53,8 +70,9 @@ def _sequences(wl):
             for s, n, slot in zip(starts, wl.scheduled, wl.state_slots)]
 
 
-def _oracle_qsa(mixer, x, batch, kv0):
-    """Projection, K/V writes, dense causal attention with the output gate, o_proj."""
+def _oracle_qsa(mixer, x, batch, kv0, indices):
+    """Projection, K/V writes, attention over ``indices`` (logical token ids)
+    with the output gate, o_proj."""
     qkv = H.bf16(x.double() @ _cpu(mixer.qkv_weight).double().T + _cpu(mixer.qkv_bias).double())
     query, gate, key, value, _ = H.qsa_projection_split(qkv, mixer.heads, mixer.kv_heads,
                                                         mixer.head_dim, mixer.index_size)
@@ -64,15 +82,89 @@ def _oracle_qsa(mixer, x, batch, kv0):
     for t, slot in enumerate(_cpu(batch.qsa.main.slot_mapping).tolist()):
         kv[slot // page, slot % page, :, :d] = key[t]
         kv[slot // page, slot % page, :, d:] = value[t]
-    positions = _cpu(batch.qsa.positions)
-    width = CFG.output_width
-    indices = torch.full((x.shape[0], width), -1, dtype=torch.int32)
-    for t, p in enumerate(positions.tolist()):
-        indices[t, :p + 1] = torch.arange(p + 1, dtype=torch.int32)
     core = oracle.sparse_attention(query.contiguous(), kv[..., :d], kv[..., d:], indices,
                                    _cpu(batch.qsa.main.block_table), _cpu(batch.qsa.token_to_req),
                                    output_gate=gate.contiguous())
     return H.bf16(H.bf16(core).reshape(x.shape[0], -1).double() @ _cpu(mixer.o_proj).double().T), kv
+
+
+def _record_index_queries(monkeypatch):
+    """Keeps a copy of each QSA layer's prepared index queries (the input of
+    its selection) as the layer runs."""
+    seen = []
+    select = backend_module.select_for_layer
+
+    def recording(index_query, *args, **kwargs):
+        seen.append(index_query.clone())
+        return select(index_query, *args, **kwargs)
+
+    monkeypatch.setattr(backend_module, "select_for_layer", recording)
+    return seen
+
+
+def _kernel_logits(index_query, comp_cache, md, cfg):
+    """The indexer kernels' logits for a batch's rows, as select_paged_tokens
+    computes them: decode rows first (decode width class), then prefill rows
+    (prefill width). Returns [(rows, logits on the device)]."""
+    n = index_query.shape[0]
+    nd, nreq_d = md.num_decode_tokens, md.num_decodes
+    capacity = md.block_table.shape[1] * comp_cache.shape[1]
+    parts = []
+    if nd:
+        cols = decode_logits_columns(md.max_seq_len, cfg.compress_ratio, capacity)
+        lg = torch.full((nd, cols), float("nan"), device=DEV)
+        torch.ops.yulan_qsa_kernels.indexer_decode(index_query[:nd], comp_cache,
+                                                   md.block_table[:nreq_d],
+                                                   md.visible_blocks[:nd], lg, 1)
+        parts.append((slice(0, nd), lg))
+    if nd < n:
+        width = prefill_logits_width(md.max_seq_len, cfg.compress_ratio, capacity)
+        lg = torch.full((n - nd, width), float("nan"), device=DEV)
+        torch.ops.yulan_qsa_kernels.indexer_prefill(index_query[nd:], comp_cache,
+                                                    md.block_table[nreq_d:],
+                                                    md.query_start_loc[nreq_d:],
+                                                    md.visible_blocks[nd:], lg, 0, n - nd,
+                                                    md.max_query_len)
+        parts.append((slice(nd, n), lg))
+    return parts
+
+
+def _check_selection(i, mixer, batch, index_query, cfg, rows_checked=None):
+    """The layer's selection (logical ids in a mixed batch) bit-exact against
+    the oracle's top-k/expansion on the kernel's logits of the layer's own
+    index queries, and those logits against the oracle's scores, on
+    ``rows_checked`` (default: every row). Returns the selection (CPU)."""
+    md = batch.qsa.compressed
+    n = batch.num_tokens
+    comp = mixer.indexer.compressed_key_cache
+    got = _cpu(mixer.layer.topk_indices_buffer[:n])
+    vis, pos = _cpu(md.visible_blocks), _cpu(md.logical_positions)
+    seq, t2r = _cpu(md.seq_lens), _cpu(md.token_to_req)
+    table, qsl = _cpu(md.block_table), _cpu(md.query_start_loc)
+    comp_cpu, iq = _cpu(comp), _cpu(index_query)
+    nd, nreq_d = md.num_decode_tokens, md.num_decodes
+    for rows, lg in _kernel_logits(index_query, comp, md, cfg):
+        sel = torch.arange(rows.start, rows.stop)
+        if rows_checked is not None:
+            sel = sel[torch.isin(sel, rows_checked)]
+        logits = _cpu(lg)[sel - rows.start]
+        if rows.start == 0:   # decode row r belongs to request r
+            want = oracle.indexer_scores_decode(iq[sel], comp_cpu, table[sel], vis[sel], 1,
+                                                logits.shape[1])
+        else:
+            want = torch.cat([oracle.indexer_scores_prefill(iq[nd:], comp_cpu, table[nreq_d:],
+                                                            qsl[nreq_d:], vis[nd:], int(r) - nd,
+                                                            1, logits.shape[1])
+                              for r in sel])
+        written = ~torch.isnan(want)
+        assert torch.equal(written, ~torch.isnan(logits)), f"layer {i} logits written"
+        assert torch.allclose(logits[written], want[written], rtol=2e-5, atol=1e-4), \
+            f"layer {i} logits"
+        want_idx, _ = oracle.topk_expand(logits, vis[sel], pos[sel], seq, t2r[sel],
+                                         torch.zeros(1, 1, dtype=torch.int32), cfg.output_width,
+                                         cfg.compress_ratio, cfg.page_size, False)
+        assert torch.equal(got[sel], want_idx), f"layer {i} selection"
+    return got
 
 
 def _gdn_params(m):
@@ -82,15 +174,18 @@ def _gdn_params(m):
             "out_proj": _cpu(m.out_proj)}
 
 
-def test_hybrid_step_layers_against_oracle():
-    wl = _workload(seed=5)
+@pytest.mark.parametrize("cfg", [CFG, CFG_SELECT], ids=["dense", "selecting"])
+def test_hybrid_step_layers_against_oracle(cfg, monkeypatch):
+    wl = _workload(seed=5, cfg=cfg)
     model = wl.model
     batch = wl.build()
     torch.cuda.synchronize()
-    print(f"[hybrid] tokens={wl.num_tokens} decodes={batch.num_decode_tokens} "
-          f"layers={[l.kind for l in model.layers]}", flush=True)
+    print(f"[hybrid] token_topk={cfg.token_topk} tokens={wl.num_tokens} "
+          f"decodes={batch.num_decode_tokens} layers={[l.kind for l in model.layers]}", flush=True)
+    index_queries = _record_index_queries(monkeypatch)
     hidden, residual = model.embed(batch.token_ids), None
     assert torch.equal(_cpu(hidden), _cpu(model.embed_tokens)[torch.as_tensor(wl.token_ids)])
+    positions = _cpu(batch.qsa.positions)
     for i, layer in enumerate(model.layers):
         x_in = _cpu(hidden)
         r_in = None if residual is None else _cpu(residual)
@@ -115,10 +210,17 @@ def test_hybrid_step_layers_against_oracle():
             _close(_cpu(mixer.conv_state), conv0, f"layer {i} conv state", 1e-2, 1e-4)
             _close(_cpu(mixer.ssm_state), ssm0, f"layer {i} gdn state", 1e-2, 1e-3)
         else:
-            mixed, kv = _oracle_qsa(mixer, n, batch, kv0)
-            # every row attended over its whole causal context
-            counts = (_cpu(mixer.layer.topk_indices_buffer[:wl.num_tokens]) >= 0).sum(1)
-            assert torch.equal(counts, _cpu(batch.qsa.positions) + 1), f"layer {i} selection"
+            selection = _check_selection(i, mixer, batch, index_queries.pop(0), cfg)
+            counts = (selection >= 0).sum(1)
+            if cfg.token_topk >= 2048:
+                # every row attended over its whole causal context
+                assert torch.equal(counts, positions + 1), f"layer {i} selection"
+            else:
+                selecting = counts < positions + 1
+                print(f"[hybrid] layer {i}: {int(selecting.sum())} of {len(counts)} rows select",
+                      flush=True)
+                assert int(selecting.sum()) > len(counts) // 2, "most rows should select"
+            mixed, kv = _oracle_qsa(mixer, n, batch, kv0, selection)
             slots = _cpu(batch.qsa.main.slot_mapping).long()
             page = kv.shape[1]
             got_kv = _cpu(mixer.layer.kv_cache.permute(0, 2, 1, 3))
@@ -130,6 +232,7 @@ def test_hybrid_step_layers_against_oracle():
         out = H.swiglu(n2, _cpu(layer.mlp.gate_up_proj), _cpu(layer.mlp.down_proj))
         _close(_cpu(residual), res2, f"layer {i} ({layer.kind}) residual")
         _close(_cpu(hidden), out, f"layer {i} ({layer.kind}) output")
+    assert not index_queries
     h_in, r_in = _cpu(hidden), _cpu(residual)   # the final norm adds into residual in place
     logits = model.logits(hidden, residual, batch)
     final, _ = H.gated_norm(h_in, r_in, *_norm_args(model.norm))
@@ -194,9 +297,9 @@ def test_silu_mul_kernel_against_oracle():
     assert (got == want).float().mean() > 0.99
 
 
-def _gdn_setup(seed, slots):
+def _gdn_setup(seed, slots, key_heads=2, value_heads=4):
     cfg = HybridConfig(num_layers=1, hidden_size=512, tp_size=1, vocab_size=64,
-                       linear_num_key_heads=2, linear_num_value_heads=4)
+                       linear_num_key_heads=key_heads, linear_num_value_heads=value_heads)
     init = _Init(DEV, seed, 0.05)
     mixer = GatedDeltaNet(cfg, init, num_slots=slots, state_std=0.05)
     mixer.norm_weight = (1 + 0.2 * _bf16((128,), seed).float()).to(torch.bfloat16).to(DEV)
@@ -223,8 +326,13 @@ def _gdn_step(mixer, builder, computed, scheduled, slots, seed):
     return got, want, conv0, ssm0
 
 
-def test_gdn_mixer_prefill_then_decode_against_oracle():
-    _, mixer, builder = _gdn_setup(seed=21, slots=6)
+# 6 value heads: the projection's row count (qkvz + 2 * 6 gate rows) is not a
+# multiple of 8 without the weight's zero padding rows.
+@pytest.mark.parametrize("key_heads,value_heads", [(2, 4), (2, 6)])
+def test_gdn_mixer_prefill_then_decode_against_oracle(key_heads, value_heads):
+    _, mixer, builder = _gdn_setup(seed=21, slots=6, key_heads=key_heads,
+                                   value_heads=value_heads)
+    assert mixer.in_proj.stride(0) % 8 == 0 and mixer.in_proj.shape[0] % 8 == 0
     # step 1: ragged prefill chunks (one shorter than the conv width) + decodes
     print("[hybrid] gdn step 1", flush=True)
     got, want, conv, ssm = _gdn_step(mixer, builder, [9, 0, 40, 5, 2], [1, 1, 70, 2, 33],
@@ -288,3 +396,64 @@ def test_decode_graph_replay_equals_eager():
         assert torch.equal(got, eager)
         for a, b in zip(wl.layer_states(), eager_states):
             assert torch.equal(a, b)
+
+
+def test_hybrid_serving_batch_properties(monkeypatch):
+    """The full-size model (32 layers, hidden 4096, 8 QSA layers at 16q/2kv,
+    top-k 2048) on the serving batch: 112 decode requests at 4k-32k context
+    and 16 prefill chunks of 512 tokens."""
+    wl = make_serving_hybrid_workload(DEV, seed=11)
+    cfg = wl.cfg
+    batch = wl.build()
+    index_queries = _record_index_queries(monkeypatch)
+    logits = wl.model.forward(batch)
+    torch.cuda.synchronize()
+    print(f"[hybrid] serving batch: tokens={wl.num_tokens} logits {tuple(logits.shape)}",
+          flush=True)
+    assert torch.isfinite(logits).all()
+    md = batch.qsa.compressed
+    k = cfg.token_topk // cfg.compress_ratio
+    qsa_layers = [layer for layer in wl.model.layers if layer.kind == "full_attention"]
+    assert len(qsa_layers) == len(index_queries) == 8
+    for layer in qsa_layers:
+        logical_invariants(layer.mixer.layer.topk_indices_buffer[:wl.num_tokens],
+                           md.logical_positions, md.seq_lens, md.token_to_req, md.visible_blocks,
+                           cfg.compress_ratio, k)
+    # top-k bit-exact on the last QSA layer for every decode row and 512
+    # sampled prefill rows (the selection of most rows is active here)
+    g = torch.Generator().manual_seed(5)
+    nd = md.num_decode_tokens
+    sample = torch.cat([torch.arange(nd),
+                        nd + torch.randperm(wl.num_tokens - nd, generator=g)[:512]])
+    last = qsa_layers[-1]
+    _check_selection(len(wl.model.layers) - 1, last.mixer, batch, index_queries[-1], cfg,
+                     rows_checked=sample)
+
+
+def test_hybrid_serving_decode_graph_replay_equals_eager():
+    """The full-size model's uniform decode step (112 requests) from a HIP
+    graph equals eager launches, caches and states included."""
+    wl = make_serving_hybrid_workload(DEV, seed=12)
+    start = [t.clone() for t in wl.layer_states()]
+
+    def restore():
+        for t, s0 in zip(wl.layer_states(), start):
+            t.copy_(s0)
+
+    graph = HybridDecodeGraph(wl.model, wl.build_decode())
+    n = graph.num_tokens
+    base = list(wl.computed)
+    wl.computed[:n] = [c + 1 for c in base[:n]]
+    restore()
+    eager = wl.model.forward(wl.build_decode()).clone()
+    eager_states = [t.clone() for t in wl.layer_states()]
+    restore()
+    got = graph.replay(wl.build_decode()).clone()
+    torch.cuda.synchronize()
+    print(f"[hybrid] serving decode graph: requests={n} max diff "
+          f"{(got - eager).abs().max().item():.3e}", flush=True)
+    assert torch.isfinite(got).all()
+    assert torch.equal(got, eager)
+    for a, b in zip(wl.layer_states(), eager_states):
+        assert torch.equal(a, b)
+

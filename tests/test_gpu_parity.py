@@ -371,46 +371,6 @@ def test_decode_select_then_attend_small():
     _attn_check(out, want, "decode end-to-end")
 
 
-def test_decode_32k_full_size_properties():
-    """BASELINE decode shape at full size: exact checks on a row subset + global invariants."""
-    _note("decode_32k full size")
-    wl = make_workload("decode_32k", device=DEV)
-    s = wl.shape
-    rows = wl.rows
-    out_idx = torch.empty(rows, s.width, dtype=torch.int32, device=DEV)
-    counts = torch.empty(rows, dtype=torch.int32, device=DEV)
-    select_paged_tokens(wl.q_index, wl.index_cache, wl.index_table, wl.token_to_req, wl.positions,
-                        wl.seq_lens, s.token_topk, s.compress_ratio, out_idx,
-                        query_start_loc=wl.query_start_loc, max_query_len=1,
-                        max_seq_len=wl.max_seq_len, num_decodes=rows, num_decode_tokens=rows,
-                        visible_blocks=wl.visible, main_block_table=wl.block_table,
-                        main_page_size=s.page_size, valid_counts_out=counts)
-    out = torch.zeros_like(wl.q)
-    qsa_sparse_paged_attention(wl.q, wl.k_cache, wl.v_cache, out_idx, wl.block_table,
-                               wl.token_to_req, out, use_decode_kernel=True,
-                               indices_are_physical=True, valid_counts=counts)
-    torch.cuda.synchronize()
-    seq = wl.seq_lens.cpu()
-    assert torch.equal(counts.cpu(), s.token_topk + seq % s.compress_ratio)
-    assert torch.isfinite(out.float()).all()
-    idx = out_idx.cpu()
-    table = wl.block_table.cpu()
-    # every selected slot lies in a page of its own request and blocks are page-aligned runs
-    for r in range(0, rows, 9):
-        valid = idx[r, :int(counts[r])]
-        pages = set(table[r, :(int(seq[r]) + 15) // 16].tolist())
-        assert all(int(x) // 16 in pages for x in valid)
-        runs = valid[:s.token_topk].view(-1, 16)
-        assert torch.equal(runs - runs[:, :1], torch.arange(16).expand_as(runs))
-    # exact parity on a subset of rows (oracle on CPU, same indices)
-    sub = list(range(0, rows, 16))
-    kv_cpu = wl.kv_cache.cpu()
-    want = oracle.sparse_attention(
-        wl.q[sub].cpu(), kv_cpu[..., :s.head_dim], kv_cpu[..., s.head_dim:], idx[sub],
-        table, wl.token_to_req[sub].cpu(), indices_are_physical=True, valid_counts=counts[sub].cpu())
-    _attn_check(out[sub], want, "decode_32k rows subset")
-
-
 def test_graph_replay_matches_eager():
     _note("hip graph replay of the decode step")
     wl = make_workload("cpu_decode_4k", device=DEV, batch=16)

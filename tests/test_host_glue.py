@@ -1,0 +1,67 @@
+"""Host-side glue of the plugin surface that needs no GPU: the memory-profiling
+forward without metadata, the decode-graph replay guard, the indexer gamma's
+checkpoint loader (CPU)."""
+
+import pytest
+import torch
+
+from qsa_vllm_amd import backend
+from qsa_vllm_amd.graph_dispatch import SHORT_DECODE_COLUMNS, check_decode_graph_batch
+from qsa_vllm_amd.layer_step import qsa_layer_step
+from qsa_vllm_amd.metadata import QSAMetadataBuilder
+from qsa_vllm_amd.ops.normalization import IndexerRMSNorm
+
+
+class _Untouchable:
+    """Stands in for every layer object a step without metadata must not use."""
+
+    def __getattr__(self, name):
+        raise AssertionError(f"a step without metadata used .{name}")
+
+
+def test_run_qsa_without_metadata_zeroes_output():
+    """``attention.py:193-198``: the profile run has no metadata; the output is
+    zeroed and nothing else is touched."""
+    out = torch.full((3, 4, 8), 7.0, dtype=torch.bfloat16)
+    u = _Untouchable()
+    got = backend.run_qsa(u, u, u, u, u, u, out, None, None, 2048, 16, u)
+    assert got is out and (out == 0).all()
+
+
+def test_layer_step_without_metadata_zeroes_output():
+    out = torch.full((5, 2, 8), -3.0, dtype=torch.bfloat16)
+    u = _Untouchable()
+    got = qsa_layer_step(u, u, u, None, u, u, u, u, out, u)
+    assert got is out and (out == 0).all()
+
+
+def _decode_batch(seq_len, requests=2, ratio=16):
+    b = QSAMetadataBuilder(compress_ratio=ratio, main_page_size=16, comp_page_size=16,
+                           ring_size=ratio, max_num_requests=4, max_num_tokens=8,
+                           main_table_width=4, comp_table_width=4, device="cpu")
+    table = torch.zeros(requests, 4, dtype=torch.int32)
+    return b.build([seq_len - 1] * requests, [1] * requests, table, table, [0] * requests)
+
+
+def test_decode_graph_guard_width_class():
+    """A graph captured for the 32768-column class refuses a batch whose
+    longest compressed length needs more columns (the other class's graph);
+    the capacity class (0) takes any batch of its size."""
+    short = _decode_batch(SHORT_DECODE_COLUMNS * 16)
+    check_decode_graph_batch(short, 2, SHORT_DECODE_COLUMNS, 16)
+    long = _decode_batch(SHORT_DECODE_COLUMNS * 16 + 16)
+    with pytest.raises(ValueError, match="width class"):
+        check_decode_graph_batch(long, 2, SHORT_DECODE_COLUMNS, 16)
+    check_decode_graph_batch(long, 2, 0, 16)
+    with pytest.raises(ValueError, match="captured size"):
+        check_decode_graph_batch(short, 3, SHORT_DECODE_COLUMNS, 16)
+
+
+def test_indexer_gamma_weight_loader():
+    """``ops/normalization.py:29``: the gamma carries a checkpoint loader."""
+    norm = IndexerRMSNorm(16, 1e-6)
+    loaded = torch.arange(16, dtype=torch.bfloat16)
+    norm.weight.weight_loader(norm.weight, loaded)
+    assert torch.equal(norm.weight.data, loaded)
+    with pytest.raises(Exception):
+        norm.weight.weight_loader(norm.weight, torch.zeros(8, dtype=torch.bfloat16))
