@@ -288,6 +288,38 @@ int qsa_sparse_attention(const void* q, int64_t q_row_stride, int64_t q_head_str
                          int indices_are_physical, int num_splits,
                          void* workspace, size_t workspace_bytes, void* stream);
 
+/* Bytes of device scratch qsa_sparse_attention_noalloc holds per GPU. */
+#define QSA_SPARSE_ATTENTION_SCRATCH_BYTES ((size_t)32 << 20)
+
+/*
+ * No counterpart in the reference: qsa_sparse_attention for callers that
+ * cannot allocate device memory (code under HIP graph capture, tight serving
+ * loops, harnesses that forbid hipMalloc). Same arguments and results, minus
+ * the workspace: the split partials live in a device array of
+ * QSA_SPARSE_ATTENTION_SCRATCH_BYTES (32 MiB) that the library holds on each
+ * GPU it runs on until the process ends. Calls whose partials
+ * (qsa_sparse_attention_workspace_bytes) exceed it fail with
+ * QSA_ERR_WORKSPACE. The call allocates nothing. Every call on one GPU shares
+ * that GPU's array, so calls that overlap in time on one GPU (different
+ * streams without ordering between them) race. `stream` must belong to the
+ * current device.
+ */
+int qsa_sparse_attention_noalloc(const void* q, int64_t q_row_stride, int64_t q_head_stride,
+                                 int rows, int num_q_heads, int head_dim,
+                                 const void* k_cache, int64_t k_block_stride,
+                                 int64_t k_token_stride, int64_t k_head_stride,
+                                 const void* v_cache, int64_t v_block_stride,
+                                 int64_t v_token_stride, int64_t v_head_stride,
+                                 int num_blocks, int page_size, int num_kv_heads,
+                                 const int32_t* indices, int64_t indices_row_stride, int width,
+                                 const int32_t* block_table, int64_t table_row_stride,
+                                 int table_width, int num_requests,
+                                 const int32_t* token_to_req, const int32_t* valid_counts,
+                                 void* out, int64_t out_row_stride, int64_t out_head_stride,
+                                 const void* gate, int64_t gate_row_stride,
+                                 int64_t gate_head_stride, int64_t gate_dim_stride,
+                                 int indices_are_physical, int num_splits, void* stream);
+
 /*
  * Replaces _qsa_merge_splitk_kernel (ops/qsa.py:306-362) as a standalone call:
  * partial_out [num_splits, rows, Hq, D] fp32, partial_lse [num_splits, rows, Hq]

@@ -16,6 +16,8 @@ _lock = threading.Lock()
 _lib = None
 
 QSA_OK = 0
+QSA_ERR_WORKSPACE = -4
+SPARSE_ATTENTION_SCRATCH_BYTES = 32 << 20  # QSA_SPARSE_ATTENTION_SCRATCH_BYTES
 ABI_VERSION = 1
 
 c_i32 = ctypes.c_int
@@ -127,6 +129,16 @@ SIGNATURES = {
                                      c_ptr, c_i64, c_i64, c_i64,
                                      c_i32, c_i32,
                                      c_ptr, c_size, c_ptr]),
+    "qsa_sparse_attention_noalloc": (c_i32, [c_ptr, c_i64, c_i64, c_i32, c_i32, c_i32,
+                                             c_ptr, c_i64, c_i64, c_i64,
+                                             c_ptr, c_i64, c_i64, c_i64,
+                                             c_i32, c_i32, c_i32,
+                                             c_ptr, c_i64, c_i32,
+                                             c_ptr, c_i64, c_i32, c_i32,
+                                             c_ptr, c_ptr,
+                                             c_ptr, c_i64, c_i64,
+                                             c_ptr, c_i64, c_i64, c_i64,
+                                             c_i32, c_i32, c_ptr]),
     "qsa_sparse_attention_merge": (c_i32, [c_ptr, c_ptr, c_i32, c_i32, c_i32, c_i32,
                                            c_ptr, c_i64, c_i64,
                                            c_ptr, c_i64, c_i64, c_i64,

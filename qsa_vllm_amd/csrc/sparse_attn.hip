@@ -50,6 +50,7 @@
 #include "../../include/qsa_hip.h"
 
 #include <algorithm>
+#include <mutex>
 
 namespace qsa {
 namespace {
@@ -1068,3 +1069,92 @@ extern "C" int qsa_sparse_attention_merge(const float* partial_out, const float*
                       static_cast<const uint16_t*>(gate), gate_row_stride, gate_head_stride,
                       gate_dim_stride, static_cast<hipStream_t>(stream));
 }
+
+// ---------------------------------------------------------------------------
+// qsa_sparse_attention_noalloc: qsa_sparse_attention with the split partials
+// in `scratch`, a file-scope device array (each GPU the library runs on holds
+// its own copy until the process ends), for callers that cannot allocate.
+// Host code never passes `scratch` itself to a kernel (on the host its name
+// is a stand-in, not a device address): the address of this GPU's copy comes
+// from hipGetSymbolAddress, once per device, and is kept per device.
+// ---------------------------------------------------------------------------
+static __device__ __align__(256) float scratch[QSA_SPARSE_ATTENTION_SCRATCH_BYTES / sizeof(float)];
+
+namespace {
+constexpr int kScratchDevices = 64;
+std::mutex g_scratch_mutex;
+void* g_scratch_ptr[kScratchDevices] = {};
+
+// This GPU's copy of `scratch`. The stream must belong to the current device
+// (the one whose copy the address names).
+int scratch_address(hipStream_t stream, void** out) {
+  int current = -1;
+  hipError_t err = hipGetDevice(&current);
+  if (err != hipSuccess)
+    return fail(QSA_ERR_HIP, std::string("qsa_sparse_attention_noalloc: hipGetDevice: ") +
+                                 hipGetErrorString(err));
+  if (stream) {
+    hipDevice_t owner = -1;
+    err = hipStreamGetDevice(stream, &owner);
+    if (err != hipSuccess)
+      return fail(QSA_ERR_HIP, std::string("qsa_sparse_attention_noalloc: hipStreamGetDevice: ") +
+                                   hipGetErrorString(err));
+    if (owner != current)
+      return fail(QSA_ERR_INVALID,
+                  "qsa_sparse_attention_noalloc: the stream belongs to device " +
+                      std::to_string(owner) + " but device " + std::to_string(current) +
+                      " is current");
+  }
+  if (current < 0 || current >= kScratchDevices)
+    return fail(QSA_ERR_UNSUPPORTED, "qsa_sparse_attention_noalloc: device ordinal beyond 63");
+  std::lock_guard<std::mutex> lock(g_scratch_mutex);
+  if (!g_scratch_ptr[current]) {
+    void* ptr = nullptr;
+    err = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (err != hipSuccess || !ptr)
+      return fail(QSA_ERR_HIP, std::string("qsa_sparse_attention_noalloc: hipGetSymbolAddress: ") +
+                                   hipGetErrorString(err));
+    g_scratch_ptr[current] = ptr;
+  }
+  *out = g_scratch_ptr[current];
+  return QSA_OK;
+}
+}  // namespace
+
+extern "C" int qsa_sparse_attention_noalloc(
+    const void* q, int64_t q_row_stride, int64_t q_head_stride, int rows, int num_q_heads,
+    int head_dim, const void* k_cache, int64_t k_block_stride, int64_t k_token_stride,
+    int64_t k_head_stride, const void* v_cache, int64_t v_block_stride, int64_t v_token_stride,
+    int64_t v_head_stride, int num_blocks, int page_size, int num_kv_heads,
+    const int32_t* indices, int64_t indices_row_stride, int width, const int32_t* block_table,
+    int64_t table_row_stride, int table_width, int num_requests, const int32_t* token_to_req,
+    const int32_t* valid_counts, void* out, int64_t out_row_stride, int64_t out_head_stride,
+    const void* gate, int64_t gate_row_stride, int64_t gate_head_stride, int64_t gate_dim_stride,
+    int indices_are_physical, int num_splits, void* stream) {
+  if (rows < 0 || num_q_heads < 0 || head_dim < 0)
+    return fail(QSA_ERR_INVALID, "qsa_sparse_attention_noalloc: negative size");
+  if (num_splits < 1 || num_splits > 1024)
+    return fail(QSA_ERR_INVALID, "qsa_sparse_attention_noalloc: num_splits out of range");
+  const size_t need = qsa_sparse_attention_workspace_bytes(rows, num_q_heads, head_dim, num_splits);
+  if (need > QSA_SPARSE_ATTENTION_SCRATCH_BYTES)
+    return fail(QSA_ERR_WORKSPACE,
+                "qsa_sparse_attention_noalloc: split partials of " + std::to_string(need) +
+                    " bytes exceed the " + std::to_string(QSA_SPARSE_ATTENTION_SCRATCH_BYTES) +
+                    "-byte scratch (use fewer splits, or qsa_sparse_attention with a workspace)");
+  // Every partial the merge reads is written by this call's attention launch,
+  // so nothing in the scratch has to start at zero.
+  void* partials = nullptr;
+  if (need) {
+    const int status = scratch_address(static_cast<hipStream_t>(stream), &partials);
+    if (status != QSA_OK) return status;
+  }
+  return qsa_sparse_attention(
+      q, q_row_stride, q_head_stride, rows, num_q_heads, head_dim, k_cache, k_block_stride,
+      k_token_stride, k_head_stride, v_cache, v_block_stride, v_token_stride, v_head_stride,
+      num_blocks, page_size, num_kv_heads, indices, indices_row_stride, width, block_table,
+      table_row_stride, table_width, num_requests, token_to_req, valid_counts, out,
+      out_row_stride, out_head_stride, gate, gate_row_stride, gate_head_stride, gate_dim_stride,
+      indices_are_physical, num_splits, partials, need ? QSA_SPARSE_ATTENTION_SCRATCH_BYTES : 0,
+      stream);
+}
+
