@@ -30,7 +30,8 @@ import time
 METRIC = "QSA decode tokens/s + sparse-attn HBM GB/s (% of peak), 32k ctx, 1 MI355X"
 HBM_PEAK_GBPS = 8000.0
 BF16_PEAK_TFLOPS = 2500.0
-WORKLOADS = ("decode_32k", "decode_long_skew", "prefill_8k_on_16k", "hybrid_decoder_step")
+WORKLOADS = ("decode_32k", "decode_32k_serving_width", "decode_long_skew", "prefill_8k_on_16k",
+             "hybrid_decoder_step")
 
 
 def parse_args():

@@ -96,6 +96,70 @@ __global__ __launch_bounds__(THREADS) void topk_merge_kernel(const TopkArgs a) {
                                              a.out + (int64_t)row * a.out_row_stride, sh, st, sel);
 }
 
+// Few rows of a wide logits buffer (a decode batch in a wide width class):
+// one 1024-thread workgroup per row sizes its keys per thread by the row's
+// own length (2, 4, 8 or 16, and enough that the selection fits the dead key
+// stage), so a row costs what its length needs, whatever the buffer's width.
+// A row of 16385..32768 keys takes exact top-k of its two halves in turn
+// (winners kept in LDS), then exact top-k over the halves' winners in id
+// order. One static LDS region serves every shape: 16 keys per thread and
+// their pages, or the halves' keys and winners.
+constexpr int kAdaptiveThreads = 1024;
+constexpr int kAdaptiveHalf = kAdaptiveThreads * 16;
+constexpr int kAdaptiveMaxColumns = 2 * kAdaptiveHalf;
+
+template <bool EXPAND, bool PAGES>
+__global__ __launch_bounds__(kAdaptiveThreads) void topk_adaptive_kernel(const TopkArgs a) {
+  constexpr int T = kAdaptiveThreads;
+  __shared__ TopkShared<T> sh;
+  __shared__ __attribute__((aligned(16))) uint32_t stage_mem[T * 16 * 2];
+  const int row = blockIdx.x;
+  const int length = a.lengths[row];
+  const int n = min(max(length, 0), a.cols);
+  const float* srow = a.scores + (int64_t)row * a.score_row_stride;
+  int32_t* out = a.out + (int64_t)row * a.out_row_stride;
+  const int topk = a.topk;
+#define QSA_ADAPTIVE_ROW(ITEMS, LOAD, LIMIT, LENGTH, CLAMP)                                     \
+  {                                                                                             \
+    auto& st = *reinterpret_cast<TopkStage<T, ITEMS, PAGES>*>(stage_mem);                      \
+    static_assert(sizeof(TopkStage<T, ITEMS, PAGES>) <= sizeof(stage_mem), "stage too large");  \
+    process_row<T, ITEMS, EXPAND, PAGES>(LOAD, LIMIT, LENGTH, CLAMP, topk, a.meta, row, out, sh, \
+                                         st, reinterpret_cast<int*>(st.key));                   \
+  }
+  if (n <= kAdaptiveHalf) {
+    const DirectLoader load{srow, 0};
+    const int need = max(n, 2 * topk);  // keys, and room for the selection
+    if (need <= T * 2) QSA_ADAPTIVE_ROW(2, load, n, length, a.cols)
+    else if (need <= T * 4) QSA_ADAPTIVE_ROW(4, load, n, length, a.cols)
+    else if (need <= T * 8) QSA_ADAPTIVE_ROW(8, load, n, length, a.cols)
+    else QSA_ADAPTIVE_ROW(16, load, n, length, a.cols)
+    return;
+  }
+  // Halves: [0, 16384) and [16384, n), winners (ascending ids) to LDS past the
+  // halves' key stage; the second half's candidates follow the first's, so
+  // the merged list is in id order (ties go to the lower id, as in one pass).
+  int* winners = reinterpret_cast<int*>(stage_mem + T * 16);
+  auto& hst = *reinterpret_cast<TopkStage<T, 16, false>*>(stage_mem);
+  int* hsel = reinterpret_cast<int*>(hst.key);
+  process_row<T, 16, false, false>(DirectLoader{srow, 0}, kAdaptiveHalf, kAdaptiveHalf,
+                                   kAdaptiveHalf, topk, a.meta, row, winners, sh, hst, hsel);
+  __syncthreads();
+  const int rest = n - kAdaptiveHalf;
+  process_row<T, 16, false, false>(DirectLoader{srow, kAdaptiveHalf}, rest, rest, rest, topk,
+                                   a.meta, row, winners + topk, sh, hst, hsel);
+  __syncthreads();
+  const int count = topk + min(rest, topk);
+  const IndirectLoader merged{srow, winners};
+  // Each thread reads its candidates' ids before it overwrites the same LDS
+  // words with their pages (the page half of a 16-key stage is the winners).
+  const int need = max(count, 2 * topk);
+  if (need <= T * 2) QSA_ADAPTIVE_ROW(2, merged, count, count, count)
+  else if (need <= T * 4) QSA_ADAPTIVE_ROW(4, merged, count, count, count)
+  else if (need <= T * 8) QSA_ADAPTIVE_ROW(8, merged, count, count, count)
+  else QSA_ADAPTIVE_ROW(16, merged, count, count, count)
+#undef QSA_ADAPTIVE_ROW
+}
+
 template <int THREADS, int ITEMS>
 size_t dyn_lds(int topk) {
   return sel_in_stage<THREADS, ITEMS>(topk) ? 0 : (size_t)2 * topk * sizeof(int);
@@ -122,6 +186,23 @@ int launch_topk(TopkArgs a, int rows, int cols, void* workspace, size_t workspac
   if (a.topk > kMaxTopk)
     return fail(QSA_ERR_UNSUPPORTED, "qsa_topk: more than 8192 selected blocks per row");
   hipError_t err;
+  if (rows < kManyRows && cols > 2048 && cols <= kAdaptiveMaxColumns) {
+    // A decode batch (latency-bound: one workgroup per row) over a buffer
+    // wider than the 2048 columns the fixed shapes below are tuned for: the
+    // buffer's width is its width class, not its rows' lengths (a 32768-column
+    // class holds rows of 512-2048 keys at 8k-32k contexts), so each row sizes
+    // its own work.
+    const bool pages = EXPAND && a.meta.physical;
+    if (pages)
+      hipLaunchKernelGGL((topk_adaptive_kernel<true, true>), dim3(rows), dim3(kAdaptiveThreads), 0,
+                         s, a);
+    else
+      hipLaunchKernelGGL((topk_adaptive_kernel<EXPAND, false>), dim3(rows),
+                         dim3(kAdaptiveThreads), 0, s, a);
+    if ((err = hipGetLastError()) != hipSuccess)
+      return fail(QSA_ERR_HIP, std::string("qsa_topk launch: ") + hipGetErrorString(err));
+    return QSA_OK;
+  }
   if (cols <= kMaxDirectColumns) {
     // Few rows (a decode batch) leave most CUs idle and the time is one row's
     // latency: wider workgroups shorten the per-thread serial parts
@@ -226,6 +307,7 @@ using namespace qsa;
 
 extern "C" size_t qsa_topk_workspace_bytes(int rows, int cols, int topk) {
   if (rows <= 0 || cols <= kMaxDirectColumns || topk <= 0) return 0;
+  if (rows < kManyRows && cols <= kAdaptiveMaxColumns) return 0;  // one workgroup per row
   return (size_t)rows * partitions_for(cols) * topk * sizeof(int32_t);
 }
 

@@ -31,8 +31,11 @@
 // passes), derived row metadata is computed only when the row is written, and
 // reductions and scans are DPP sequences.
 //
-// Rows longer than the register-resident capacity use two passes: exact top-k
-// per 8192-column partition, then exact top-k over the partition winners.
+// A decode batch's rows (few, so latency counts) size the workgroup's keys
+// per thread by the row's own length, up to 16384 keys at once; a row of up
+// to 32768 keys takes its halves in turn and then the halves' winners, in one
+// workgroup. Longer rows use two launches: exact top-k per 8192-column
+// partition, then exact top-k over the partition winners.
 #pragma once
 
 #include "qsa_common.h"
@@ -250,7 +253,7 @@ __device__ __forceinline__ void block_scan2(int& a, int& b, TopkShared<THREADS>&
 // each one's first token (from page[e], the staged page of the element at
 // position e) to sel[topk..2 topk).
 template <int THREADS, int ITEMS, bool PAGES>
-__device__ void select_long(int length, int topk, const uint32_t (&key)[ITEMS],
+__device__ __forceinline__ void select_long(int length, int topk, const uint32_t (&key)[ITEMS],
                             const int (&id)[ITEMS], const int* page, const ExpandMeta& m,
                             TopkShared<THREADS>& sh, int* sel) {
   const int tid = threadIdx.x;
@@ -599,10 +602,11 @@ __device__ __forceinline__ RowPrefetch stage_row(const IndirectLoader& load, int
 // Select and write one row from staged keys. `sel` (2 * topk ints) may alias
 // the key stage, which is dead once the keys are in registers.
 template <int THREADS, int ITEMS, bool EXPAND, bool PAGES, typename Loader, typename Stage>
-__device__ void finish_row(const Loader& load, const uint32_t (&key)[ITEMS], const int (&id)[ITEMS],
-                           const RowPrefetch& f, const Stage& st, int staged,
-                           int length_raw, int clamp, int topk, const ExpandMeta& m, int row,
-                           int32_t* out, TopkShared<THREADS>& sh, int* sel) {
+__device__ __forceinline__ void finish_row(const Loader& load, const uint32_t (&key)[ITEMS],
+                                           const int (&id)[ITEMS], const RowPrefetch& f,
+                                           const Stage& st, int staged, int length_raw, int clamp,
+                                           int topk, const ExpandMeta& m, int row, int32_t* out,
+                                           TopkShared<THREADS>& sh, int* sel) {
   const int tid = threadIdx.x;
   const int length = length_raw > topk ? min(length_raw, clamp) : length_raw;
   if (length > topk) {
@@ -632,16 +636,21 @@ __device__ void finish_row(const Loader& load, const uint32_t (&key)[ITEMS], con
 // One row: stage the scores (and pages), select, write. PAGES stages the
 // physical page of every candidate (the expansion maps to physical slots); the
 // stage must then have room for them.
+//
+// Everything down to here is force-inlined: a kernel that instantiates several
+// row shapes would otherwise call them as functions, with their arguments
+// and arrays in scratch memory.
 template <int THREADS, int ITEMS, bool EXPAND, bool PAGES, typename Loader, typename Stage>
-__device__ void process_row(const Loader& load, int limit, int length_raw, int clamp, int topk,
-                            const ExpandMeta& m, int row, int32_t* out, TopkShared<THREADS>& sh,
-                            Stage& st, int* sel) {
+__device__ __forceinline__ void process_row(const Loader& load, int limit, int length_raw,
+                                            int clamp, int topk, const ExpandMeta& m, int row,
+                                            int32_t* out, TopkShared<THREADS>& sh, Stage& st,
+                                            int* sel) {
   uint32_t key[ITEMS];
   int id[ITEMS];
   const RowPrefetch f =
       stage_row<THREADS, ITEMS, EXPAND, PAGES>(load, limit, m, row, key, id, sh, st);
-  finish_row<THREADS, ITEMS, EXPAND, PAGES>(load, key, id, f, st, limit, length_raw, clamp, topk, m,
-                                            row, out, sh, sel);
+  finish_row<THREADS, ITEMS, EXPAND, PAGES>(load, key, id, f, st, limit, length_raw, clamp, topk,
+                                            m, row, out, sh, sel);
 }
 
 }  // namespace

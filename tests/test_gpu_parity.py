@@ -42,8 +42,13 @@ def _special_scores(rows, cols, g, mode):
     raise ValueError(mode)
 
 
+# Up to 1023 rows, widths past 2048 up to 32768 take the workgroup-per-row
+# shape sized by each row's own length (2-16 keys per thread; rows over 16384
+# keys in two halves and a merge of their winners); wider rows the partition +
+# merge launches.
 @pytest.mark.parametrize("cols,k", [(64, 16), (1000, 128), (2048, 128), (4096, 128), (8192, 128),
-                                    (16384, 512), (40000, 128), (70000, 512)])
+                                    (16384, 512), (20000, 128), (32768, 2048), (40000, 128),
+                                    (70000, 512)])
 @pytest.mark.parametrize("mode", ["random", "ties", "relu", "specials"])
 def test_topk_bit_exact(cols, k, mode):
     _note(f"topk cols={cols} k={k} mode={mode}")
@@ -52,6 +57,8 @@ def test_topk_bit_exact(cols, k, mode):
     scores = _special_scores(rows, cols, g, mode)
     lengths = torch.randint(0, cols + 1, (rows,), generator=g, dtype=torch.int32)
     lengths[0], lengths[1], lengths[2] = cols, k, min(cols, k + 1)
+    if rows > 5:  # lengths at the per-thread size boundaries of the row-sized shape
+        lengths[3], lengths[4], lengths[5] = min(cols, 2048), min(cols, 2049), min(cols, 16385)
     want = oracle.topk_ids(scores, lengths, k)
     out = torch.full((rows, k), -7, dtype=torch.int32, device=DEV)
     topk(scores.to(DEV), lengths.to(DEV), out)
@@ -103,12 +110,14 @@ def _expand_case(g, rows, cols, ratio, page, k, physical, reqs=5):
 
 @pytest.mark.parametrize("ratio,page,physical", [(16, 16, True), (4, 272, True), (4, 6, True),
                                                  (4, 16, False), (16, 16, False), (1, 16, True)])
-@pytest.mark.parametrize("cols,k", [(2048, 128), (9000, 64), (40000, 128)])
+@pytest.mark.parametrize("cols,k", [(2048, 128), (9000, 64), (32768, 128), (40000, 128)])
 def test_topk_expand_bit_exact(ratio, page, physical, cols, k):
     _note(f"topk_expand ratio={ratio} page={page} physical={physical} cols={cols} k={k}")
     g = torch.Generator().manual_seed(ratio * 1000 + page + cols + physical)
     rows = 8 if cols > 16384 else 40
     seq, t2r, pos, vis, table, scores = _expand_case(g, rows, cols, ratio, page, k, physical)
+    if cols == 32768:  # rows over 16384 keys: two halves, then their winners
+        vis[-2], vis[-3] = 16385, 30000
     width = k * ratio + ratio - 1
     want, want_counts = oracle.topk_expand(scores, vis, pos, seq, t2r, table, width, ratio, page,
                                            physical)
@@ -132,9 +141,11 @@ def _score_tol(q, keys, dim):
 
 # The last two cases launch at least one wave per CU, which takes the
 # eight-tiles-per-wave split; the others take four.
+# The last case's longest rows need two passes of their waves (rows stride
+# over their keys: the grid follows the batch, not the logits width).
 @pytest.mark.parametrize("heads,dim,dql,reqs,width", [
     (32, 128, 1, 9, 13), (8, 64, 1, 9, 13), (4, 128, 2, 9, 13), (48, 128, 1, 9, 13),
-    (32, 128, 1, 36, 64), (16, 64, 2, 20, 64)])
+    (32, 128, 1, 36, 64), (16, 64, 2, 20, 64), (32, 128, 1, 64, 400)])
 def test_indexer_decode_parity(heads, dim, dql, reqs, width):
     _note(f"indexer_decode heads={heads} dim={dim} dql={dql} reqs={reqs} width={width}")
     g = torch.Generator().manual_seed(heads + dim + dql + reqs)
@@ -154,8 +165,8 @@ def test_indexer_decode_parity(heads, dim, dql, reqs, width):
     got = logits.cpu()
     for r in range(rows):
         n = int(vis[r])
-        keys = torch.stack([cache[int(table[r // dql, c // cpage]), c % cpage, 0]
-                            for c in range(n)]) if n else torch.zeros(0, dim)
+        c = torch.arange(n)
+        keys = cache[table[r // dql, c // cpage].long(), c % cpage, 0]
         if n:
             tol = _score_tol(q[r], keys, dim)
             assert ((got[r, :n] - want[r, :n]).abs() <= tol).all(), r
