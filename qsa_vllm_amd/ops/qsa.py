@@ -61,7 +61,11 @@ def qsa_sparse_paged_attention(
         out = torch.empty_like(q)
     if not q.shape[0]:
         return out
-    num_splits = choose_num_splits(q, k_cache, logical_indices, use_decode_kernel, decode_config)
+    if decode_config is None and bool(use_decode_kernel) == bool(indices_are_physical):
+        num_splits = 0  # the library's choice for this shape, made inside the op
+    else:
+        num_splits = choose_num_splits(q, k_cache, logical_indices, use_decode_kernel,
+                                       decode_config)
     torch.ops.yulan_qsa_kernels.sparse_attention(
         q, k_cache, v_cache, logical_indices, block_table, token_to_req, out,
         output_gate, valid_counts, bool(indices_are_physical), int(num_splits))

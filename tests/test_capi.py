@@ -134,3 +134,52 @@ int main() {
                     str(src), "-o", str(exe)], check=True)
     out = subprocess.run([str(exe)], capture_output=True, text=True)
     assert out.returncode == 0 and "OK" in out.stdout, out.stdout
+
+
+TORCH_OPS = ("topk", "topk_expand", "indexer_prepare", "store_cache_rows", "compress_groups",
+             "expand_block_indices", "indexer_norm_rope", "indexer_decode", "indexer_prefill",
+             "select_decode", "select_prefill", "sparse_attention", "sparse_attention_merge")
+
+
+def test_torch_op_layer_defines_every_op():
+    import torch
+
+    import qsa_vllm_amd.ops  # noqa: F401  (loads libqsa_torch_ops.so)
+
+    ns = torch.ops.yulan_qsa_kernels
+    for name in TORCH_OPS:
+        assert getattr(ns, name).default._schema.name == f"yulan_qsa_kernels::{name}"
+    # the reference schemas, verbatim (ops/csrc/topk.cu:549-552)
+    assert str(ns.topk.default._schema) == (
+        "yulan_qsa_kernels::topk(Tensor scores, Tensor lengths, Tensor(a!) output) -> ()")
+    assert str(ns.topk_expand.default._schema) == (
+        "yulan_qsa_kernels::topk_expand(Tensor scores, Tensor lengths, Tensor positions, "
+        "Tensor sequence_lengths, Tensor token_to_req, Tensor table, Tensor(a!) output, "
+        "Tensor(b!) counts, int ratio, int page_size, bool physical, bool store_counts) -> ()")
+
+
+def test_torch_ops_reject_host_tensors():
+    """No CPU kernel is registered: host tensors are refused before any HIP call."""
+    import torch
+
+    import qsa_vllm_amd.ops  # noqa: F401
+
+    scores = torch.zeros(2, 8)
+    with pytest.raises((RuntimeError, NotImplementedError)):
+        torch.ops.yulan_qsa_kernels.topk(scores, torch.zeros(2, dtype=torch.int32),
+                                         torch.zeros(2, 4, dtype=torch.int32))
+
+
+def test_torch_ops_meta_kernels_trace_shapes():
+    import torch
+
+    import qsa_vllm_amd.ops  # noqa: F401
+
+    m = dict(device="meta")
+    torch.ops.yulan_qsa_kernels.sparse_attention(
+        torch.empty(4, 16, 128, dtype=torch.bfloat16, **m),
+        torch.empty(8, 16, 2, 128, dtype=torch.bfloat16, **m),
+        torch.empty(8, 16, 2, 128, dtype=torch.bfloat16, **m),
+        torch.empty(4, 64, dtype=torch.int32, **m), torch.empty(1, 1, dtype=torch.int32, **m),
+        torch.empty(4, dtype=torch.int32, **m), torch.empty(4, 16, 128, dtype=torch.bfloat16, **m),
+        None, None, True, 0)
