@@ -16,7 +16,15 @@ not timed; K steps are timed with HIP events between two synchronisations.
 The attention kernel's roofline figure comes from a separate timed loop of
 attention-only graphs on the same stream: achieved = algorithmic bytes per
 launch / mean launch time, against 8 TB/s. The CPU baseline times the eager
-PyTorch oracle of the same path on this host on a bounded sample.
+PyTorch oracle of the same path on this host on a bounded sample, for this
+batch and for the small eager decode step (batch 4, 8 q / 1 kv heads, 4096
+tokens).
+
+The default line also carries compact figures of the plan's other workloads
+(`workloads`: the same decode batch with page tables sized for a 524288-token
+max-model-len, the long-context skewed decode batch, the chunked prefill) and
+of the hybrid decoder step (`hybrid_step`); each has its own full line with
+--workload NAME.
 """
 
 from __future__ import annotations
@@ -45,6 +53,8 @@ def parse_args():
     p.add_argument("--cpu-seconds", type=float, default=10.0,
                    help="CPU work budget for the oracle baseline (0 disables it)")
     p.add_argument("--cpu-threads", type=int, default=0, help="0: min(16, cpu_count)")
+    p.add_argument("--no-extras", action="store_true",
+                   help="headline workload only (no summaries of the other workloads)")
     p.add_argument("--no-hybrid", action="store_true",
                    help="decode_32k: skip the hybrid decoder step figures added to the line")
     p.add_argument("--traffic", default=os.path.join(os.path.dirname(os.path.abspath(__file__)),
@@ -96,9 +106,7 @@ def main():
 
     import torch
 
-    from qsa_vllm_amd.ops import qsa_sparse_paged_attention, select_paged_tokens, topk_expand
-    from qsa_vllm_amd.workloads import (attention_bytes, fresh_queries, indexer_bytes,
-                                        make_workload)
+    from qsa_vllm_amd.workloads import make_workload
 
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
@@ -106,21 +114,138 @@ def main():
         return run_hybrid(args, dev)
     t0 = time.time()
     wl = make_workload(args.workload, device=dev)
-    s = wl.shape
-    rows = wl.rows
+    log(f"workload {args.workload} built in {time.time() - t0:.1f}s: rows={wl.rows} "
+        f"kv_cache={wl.kv_cache.numel() * 2 / 1e9:.2f} GB")
     if not wl.is_decode:
         return run_prefill(args, wl)
-    sets = [(wl.q, wl.q_index)] + [fresh_queries(wl, 100 + i) for i in range(args.sets - 1)]
+    if args.traffic_run or args.pmc_run:
+        return decode_counter_run(args, wl)
+    m = measure_decode(wl, args.steps, args.warmup, args.sets, eager=True)
+    s = wl.shape
+    stream = torch.cuda.current_stream()
+    # The committed counter summary covers the headline workload only.
+    traffic = read_traffic(args.traffic) if args.workload == "decode_32k" else None
+    result = {
+        "metric": METRIC,
+        "value": m["tokens_per_s"],
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(m["us_per_step"] * 1e-3, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic: seeded N(0,1) activations and caches, permuted block tables",
+        "config": {
+            "workload": describe(s),
+            "batch": s.batch,
+            "query_sets": m["query_sets"],
+            "kv_layout": s.kv_layout,
+            "graph": "HIP graph per block of steps",
+        },
+        "roofline": dict(m["roofline"], traffic=traffic),
+        "breakdown_us": m["breakdown_us"],
+        "eager": m["eager"],
+        "indexer_gbps": m["indexer_gbps"],
+        "prepare": time_prepare(wl, stream),
+        "layer_step": time_layer_step(wl, stream),
+    }
+    if args.cpu_seconds > 0:
+        result["cpu_baseline"] = cpu_baseline(wl, args)
+        # The eager CPU decode step the benchmark plan names first (batch 4,
+        # 8 q / 1 kv heads, 4096-token contexts), on the same cores.
+        small = make_workload("cpu_decode_4k", device="cpu")
+        result["cpu_baseline_cpu_decode_4k"] = cpu_baseline(small, args,
+                                                            seconds=args.cpu_seconds / 2)
+        del small
+    if args.workload == "decode_32k" and not args.no_extras:
+        # Every other workload of the plan beside the headline, compact (each
+        # also has its own line: --workload NAME). A failure is recorded, not
+        # raised, so it cannot take the headline figures with it.
+        del wl
+        result["workloads"] = {}
+        for name in ("decode_32k_serving_width", "decode_long_skew", "prefill_8k_on_16k"):
+            try:
+                result["workloads"][name] = workload_summary(name, dev)
+            except Exception as exc:  # noqa: BLE001
+                result["workloads"][name] = {"error": f"{type(exc).__name__}: {exc}"}
+            torch.cuda.empty_cache()
+        if not args.no_hybrid:
+            try:
+                result["hybrid_step"] = hybrid_summary(dev)
+            except Exception as exc:  # noqa: BLE001
+                result["hybrid_step"] = {"error": f"{type(exc).__name__}: {exc}"}
+    print(json.dumps(result), flush=True)
+    return 0
+
+
+def decode_queries(wl, n_sets):
+    """The workload's (q, q_index) and n_sets - 1 fresh sets of the same shapes."""
+    from qsa_vllm_amd.workloads import fresh_queries
+
+    return [(wl.q, wl.q_index)] + [fresh_queries(wl, 100 + i) for i in range(n_sets - 1)]
+
+
+def decode_counter_run(args, wl):
+    """Eager decode steps for a rocprofv3 counter pass (no timing)."""
+    import torch
+
+    from qsa_vllm_amd.ops import qsa_sparse_paged_attention, select_paged_tokens
+
+    s, rows, dev = wl.shape, wl.rows, wl.device
+    sets = decode_queries(wl, args.sets)
+    idx = [torch.empty(rows, s.width, dtype=torch.int32, device=dev) for _ in sets]
+    counts = [torch.empty(rows, dtype=torch.int32, device=dev) for _ in sets]
+    out = torch.zeros_like(wl.q)
+
+    def select(i):
+        select_paged_tokens(sets[i][1], wl.index_cache, wl.index_table, wl.token_to_req,
+                            wl.positions, wl.seq_lens, s.token_topk, s.compress_ratio, idx[i],
+                            query_start_loc=wl.query_start_loc, max_query_len=1,
+                            max_seq_len=wl.max_seq_len, num_decodes=rows, num_decode_tokens=rows,
+                            visible_blocks=wl.visible, main_block_table=wl.block_table,
+                            main_page_size=s.page_size, valid_counts_out=counts[i])
+
+    def attend(i):
+        qsa_sparse_paged_attention(sets[i][0], wl.k_cache, wl.v_cache, idx[i], wl.block_table,
+                                   wl.token_to_req, out, use_decode_kernel=True,
+                                   indices_are_physical=True, valid_counts=counts[i])
+
+    if args.traffic_run:
+        return traffic_run(select, attend, len(sets))
+    for _ in range(3):
+        for i in range(len(sets)):
+            select(i)
+            attend(i)
+    torch.cuda.synchronize()
+    log(f"pmc run: {3 * len(sets)} eager decode steps")
+    return 0
+
+
+def measure_decode(wl, steps, warmup, n_sets, eager=False):
+    """Decode steps of `wl` (indexer -> top-k/expand -> sparse attention +
+    merge) from HIP graphs over n_sets rotating query sets, then the same
+    kernels alone for the breakdown and the attention roofline. Returns the
+    figures as a dict (times in us)."""
+    import torch
+
+    from qsa_vllm_amd.graph_dispatch import decode_logits_columns
+    from qsa_vllm_amd.ops import qsa_sparse_paged_attention, select_paged_tokens, topk_expand
+    from qsa_vllm_amd.workloads import attention_bytes, indexer_bytes
+
+    s = wl.shape
+    rows = wl.rows
+    dev = wl.device
+    sets = decode_queries(wl, n_sets)
     n_sets = len(sets)
     idx = [torch.empty(rows, s.width, dtype=torch.int32, device=dev) for _ in sets]
     counts = [torch.empty(rows, dtype=torch.int32, device=dev) for _ in sets]
     outs = [torch.zeros_like(wl.q) for _ in sets]
-    cols = wl.index_table.shape[1] * wl.index_cache.shape[1]
-    from qsa_vllm_amd.graph_dispatch import decode_logits_columns
-    cols = decode_logits_columns(wl.max_seq_len, s.compress_ratio, cols)
+    cols = decode_logits_columns(wl.max_seq_len, s.compress_ratio,
+                                 wl.index_table.shape[1] * wl.index_cache.shape[1])
     logits = [torch.empty(rows, cols, dtype=torch.float32, device=dev) for _ in sets]
-    log(f"workload {args.workload} built in {time.time() - t0:.1f}s: rows={rows} "
-        f"kv_cache={wl.kv_cache.numel() * 2 / 1e9:.2f} GB")
 
     def select(i):
         select_paged_tokens(sets[i][1], wl.index_cache, wl.index_table, wl.token_to_req,
@@ -147,16 +272,6 @@ def main():
     def step(i):
         select(i)
         attend(i)
-
-    if args.traffic_run:
-        return traffic_run(select, attend, n_sets)
-    if args.pmc_run:
-        for _ in range(3):
-            for i in range(n_sets):
-                step(i)
-        torch.cuda.synchronize()
-        log(f"pmc run: {3 * n_sets} eager decode steps")
-        return 0
 
     # Eager pass (also initialises allocator pools), then capture.
     for i in range(n_sets):
@@ -193,17 +308,15 @@ def main():
         for i in range(rest):
             single[i].replay()
 
-    run_steps(args.warmup)
-    torch.cuda.synchronize()
-
     stream = torch.cuda.current_stream()
-    start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    run_steps(warmup)
     torch.cuda.synchronize()
+    start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     start.record(stream)
-    run_steps(args.steps)
+    run_steps(steps)
     stop.record(stream)
     torch.cuda.synchronize()
-    ms_step = start.elapsed_time(stop) / args.steps
+    us_step = start.elapsed_time(stop) * 1e3 / steps
 
     def time_graph(graph, launches, rounds):
         graph.replay()
@@ -216,21 +329,25 @@ def main():
         torch.cuda.synchronize()
         return a.elapsed_time(b) * 1e3 / (launches * rounds)  # us per launch
 
-    rounds = max(2, args.steps // (n_sets * reps))
+    rounds = max(2, steps // (n_sets * reps))
     attn_us = time_graph(attn_graph, n_sets * reps, rounds)
     index_us = time_graph(index_graph, n_sets * reps, rounds)
     topk_us = time_graph(topk_graph, n_sets * reps, rounds)
 
-    # The same steps launched eagerly (no graph): host launch overhead included.
-    eager_steps = max(n_sets, (args.steps // n_sets) * n_sets)
-    torch.cuda.synchronize()
-    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    a.record(stream)
-    for k in range(eager_steps):
-        step(k % n_sets)
-    b.record(stream)
-    torch.cuda.synchronize()
-    eager_us = a.elapsed_time(b) * 1e3 / eager_steps
+    out = {}
+    if eager:
+        # The same steps launched eagerly (no graph): host launch overhead included.
+        eager_steps = max(n_sets, (steps // n_sets) * n_sets)
+        torch.cuda.synchronize()
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record(stream)
+        for k in range(eager_steps):
+            step(k % n_sets)
+        b.record(stream)
+        torch.cuda.synchronize()
+        eager_us = a.elapsed_time(b) * 1e3 / eager_steps
+        out["eager"] = {"us_per_step": round(eager_us, 3),
+                        "tokens_per_s": round(rows / (eager_us * 1e-6), 1)}
 
     # Correctness gate on the timed data: counts follow the closed form.
     want_counts = s.token_topk + wl.seq_lens % s.compress_ratio
@@ -242,30 +359,10 @@ def main():
 
     attn_bytes = sum(attention_bytes(wl, counts[i]) for i in range(n_sets)) / n_sets
     attn_gbps = attn_bytes / (attn_us * 1e-6) / 1e9
-    idx_bytes = indexer_bytes(wl)
-    # The committed counter summary covers the headline workload only.
-    traffic = read_traffic(args.traffic) if args.workload == "decode_32k" else None
-
-    result = {
-        "metric": METRIC,
-        "value": round(rows / (ms_step * 1e-3), 1),
-        "unit": "tokens/s",
-        "n_gpus": 1,
-        "steps": args.steps,
-        "warmup": args.warmup,
-        "ms_per_step": round(ms_step, 5),
-        "higher_is_better": True,
-        "scaling": "weak",
-        "vs_baseline": None,
-        "dtype": "bf16",
-        "data": "synthetic: seeded N(0,1) activations and caches, permuted block tables",
-        "config": {
-            "workload": describe(s),
-            "batch": s.batch,
-            "query_sets": n_sets,
-            "kv_layout": s.kv_layout,
-            "graph": "HIP graph per block of steps",
-        },
+    out.update({
+        "query_sets": n_sets,
+        "us_per_step": us_step,
+        "tokens_per_s": round(rows / (us_step * 1e-6), 1),
         "roofline": {
             "kernel": "sparse_attn_kernel (+ split merge)",
             "bound": "hbm",
@@ -273,7 +370,6 @@ def main():
             "peak": HBM_PEAK_GBPS,
             "unit": "GB/s",
             "frac": round(attn_gbps / HBM_PEAK_GBPS, 4),
-            "traffic": traffic,
             "algorithmic_bytes_per_launch": int(attn_bytes),
             "us_per_launch": round(attn_us, 3),
         },
@@ -281,26 +377,36 @@ def main():
             "indexer_decode": round(index_us, 3),
             "topk_expand": round(topk_us, 3),
             "sparse_attention": round(attn_us, 3),
-            "step": round(ms_step * 1e3, 3),
+            "step": round(us_step, 3),
         },
-        "eager": {"us_per_step": round(eager_us, 3),
-                  "tokens_per_s": round(rows / (eager_us * 1e-6), 1)},
-        "indexer_gbps": round(idx_bytes / (index_us * 1e-6) / 1e9, 1),
-        "prepare": time_prepare(wl, stream),
-        "layer_step": time_layer_step(wl, stream),
-    }
-    if args.cpu_seconds > 0:
-        result["cpu_baseline"] = cpu_baseline(wl, args)
-    if args.workload == "decode_32k" and not args.no_hybrid:
-        # The whole hybrid decoder step beside the headline (its own line:
-        # --workload hybrid_decoder_step). A failure here is recorded, not raised,
-        # so it cannot take the headline figures with it.
-        try:
-            result["hybrid_step"] = hybrid_summary(dev)
-        except Exception as exc:  # noqa: BLE001
-            result["hybrid_step"] = {"error": f"{type(exc).__name__}: {exc}"}
-    print(json.dumps(result), flush=True)
-    return 0
+        "indexer_gbps": round(indexer_bytes(wl) / (index_us * 1e-6) / 1e9, 1),
+        "logits_columns": cols,
+    })
+    return out
+
+
+def workload_summary(name, dev, steps=40, warmup=8):
+    """Compact figures of one more workload for the default benchmark line."""
+    import torch
+
+    from qsa_vllm_amd.workloads import make_workload
+
+    wl = make_workload(name, device=dev)
+    if wl.is_decode:
+        m = measure_decode(wl, steps, warmup, 4)
+        out = {"workload": describe(wl.shape), "rows": wl.rows,
+               "tokens_per_s": m["tokens_per_s"], "us_per_step": round(m["us_per_step"], 3),
+               "breakdown_us": m["breakdown_us"], "logits_columns": m["logits_columns"],
+               "roofline": m["roofline"], "indexer_gbps": m["indexer_gbps"]}
+    else:
+        m = measure_prefill(wl, steps=5, warmup=2)
+        out = {"workload": describe(wl.shape), "rows": wl.rows,
+               "tokens_per_s": m["value"], "ms_per_step": m["ms_per_step"],
+               "breakdown_ms": m["breakdown_ms"], "roofline": m["roofline"],
+               "attention_gathered_gbps": m["attention_gathered_gbps"]}
+    del wl
+    torch.cuda.synchronize()
+    return out
 
 
 def time_prepare(wl, stream, rounds=20, reps=8):
@@ -437,6 +543,16 @@ def describe(s):
 def run_prefill(args, wl):
     """Chunked prefill step: prefill scoring (MFMA) -> logical top-k/expand ->
     sparse attention over logical ids. The step's rows are the new tokens."""
+    if args.pmc_run:
+        measure_prefill(wl, 3, 0, pmc_run=True)
+        return 0
+    result = measure_prefill(wl, max(1, min(args.steps, 20)), min(args.warmup, 3))
+    print(json.dumps(result), flush=True)
+    return 0
+
+
+def measure_prefill(wl, steps, warmup, pmc_run=False):
+    """The chunked-prefill step's figures (see run_prefill) as a dict."""
     import torch
 
     from qsa_vllm_amd.graph_dispatch import prefill_logits_width
@@ -484,12 +600,12 @@ def run_prefill(args, wl):
         select()
         attend()
 
-    if args.pmc_run:
-        for _ in range(3):
+    if pmc_run:
+        for _ in range(steps):
             step()
         torch.cuda.synchronize()
-        log("pmc run: 3 eager prefill steps")
-        return 0
+        log(f"pmc run: {steps} eager prefill steps")
+        return None
 
     stream = torch.cuda.current_stream()
 
@@ -504,8 +620,7 @@ def run_prefill(args, wl):
         torch.cuda.synchronize()
         return a.elapsed_time(b) / reps  # ms
 
-    steps = max(1, min(args.steps, 20))
-    for _ in range(min(args.warmup, 3)):
+    for _ in range(warmup):
         step()
     ms_step = timed(step, steps)
     idx_ms = timed(index_only, steps)
@@ -523,7 +638,7 @@ def run_prefill(args, wl):
         "unit": "tokens/s",
         "n_gpus": 1,
         "steps": steps,
-        "warmup": min(args.warmup, 3),
+        "warmup": warmup,
         "ms_per_step": round(ms_step, 4),
         "higher_is_better": True,
         "scaling": "weak",
@@ -553,8 +668,7 @@ def run_prefill(args, wl):
         "attention_gathered_bytes": gathered,
         "prepare": time_prepare(wl, stream, rounds=5, reps=4),
     }
-    print(json.dumps(result), flush=True)
-    return 0
+    return result
 
 
 
@@ -821,8 +935,8 @@ def _counter_means(root, counter):
 
 
 QSA_KERNELS = ("sparse_attn_kernel", "merge_kernel", "topk_direct_kernel",
-               "topk_partition_kernel", "topk_merge_kernel", "indexer_decode_kernel",
-               "indexer_prefill_kernel")
+               "topk_adaptive_kernel", "topk_partition_kernel", "topk_merge_kernel",
+               "indexer_decode_kernel", "indexer_prefill_kernel")
 
 
 def pmc_summary(root):
@@ -877,12 +991,13 @@ def traffic_summary(fetch_dir, write_dir):
     return "\n".join(lines)
 
 
-def cpu_baseline(wl, args):
+def cpu_baseline(wl, args, seconds=None):
     """Eager-PyTorch oracle of the same decode step on this host's cores."""
     import torch
 
     import oracle
 
+    seconds = args.cpu_seconds if seconds is None else seconds
     threads = args.cpu_threads or min(16, os.cpu_count() or 1)
     torch.set_num_threads(threads)
     cpu = {n: getattr(wl, n).cpu() for n in ("q", "q_index", "index_cache", "index_table",
@@ -898,7 +1013,7 @@ def cpu_baseline(wl, args):
                            cpu["seq_lens"], wl.shape.token_topk, wl.shape.compress_ratio)
         steps += 1
         elapsed = time.perf_counter() - t0
-        if elapsed >= args.cpu_seconds:
+        if elapsed >= seconds:
             break
     return {
         "value": round(steps * wl.rows / elapsed, 2),
