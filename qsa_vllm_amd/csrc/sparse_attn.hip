@@ -797,9 +797,13 @@ struct HeadPlan {
 // merge; batch 16: 8 splits 12.0 us against 16.2 us). A split pays for its
 // merge below ~160 workgroups (batch 64: 2 splits 27.5 us, none 29.4 us;
 // batch 96: none 38.0 us, 2 splits 43.8 us). So physical rows group kv heads
-// only while a full round remains, and split smaller batches up to a round.
+// only while a full round remains, and split smaller batches up to a round,
+// but not below 8 tiles (256 tokens) per split: shorter splits add partials to
+// merge faster than they shorten the launch (batch 8 of 2055 tokens: 4 splits
+// 11.9 us, 8 splits 10.3, 16 splits 10.9, 32 splits 12.7, merge included).
 constexpr int kDecodeRoundWorkgroups = 256;
 constexpr int kDecodeNoSplitWorkgroups = 160;
+constexpr int kDecodeMinSplitTiles = 8;
 
 bool plan_heads(int num_q_heads, int num_kv_heads, int rows, bool physical, HeadPlan* plan) {
   if (num_kv_heads <= 0 || num_q_heads <= 0 || num_q_heads % num_kv_heads) return false;
@@ -912,13 +916,14 @@ extern "C" int qsa_sparse_attention_splits(int rows, int num_q_heads, int num_kv
   const int64_t base = (int64_t)rows * plan.groups;
   // At least two tiles per split (a one-tile split pays for a partial and its
   // merge for nothing). The decode kernel takes physical slots (splits as
-  // measured, above); prefill rows (logical ids, 4-wave workgroups, two per
-  // CU) split up to two workgroups per CU.
+  // measured, above) and keeps at least kDecodeMinSplitTiles tiles per split;
+  // prefill rows (logical ids, 4-wave workgroups, two per CU) split up to two
+  // workgroups per CU.
   int splits = 1;
   if (physical) {
     if (base < kDecodeNoSplitWorkgroups)
-      while (splits * base < kDecodeRoundWorkgroups && splits * 2 <= std::max(1, tiles / 2) &&
-             splits < 64)
+      while (splits * base < kDecodeRoundWorkgroups &&
+             splits * 2 <= std::max(1, tiles / kDecodeMinSplitTiles) && splits < 64)
         splits *= 2;
   } else {
     const int64_t target = 2 * kCUs;

@@ -86,6 +86,14 @@ def test_workspace_and_split_helpers():
     s = lib.qsa_sparse_attention_splits(64, 16, 2, 128, 2063, 1)
     assert s >= 1 and s & (s - 1) == 0
     assert lib.qsa_sparse_attention_splits(32768, 16, 2, 128, 2063, 0) == 1
+    # Decode rows: 64 rows x 2 kv heads take 2 splits (a full round); small
+    # batches split up to a round but keep at least 8 tiles (256 tokens) each.
+    assert lib.qsa_sparse_attention_splits(64, 16, 2, 128, 2063, 1) == 2
+    assert lib.qsa_sparse_attention_splits(16, 16, 2, 128, 2063, 1) == 8
+    assert lib.qsa_sparse_attention_splits(8, 16, 2, 128, 2063, 1) == 8
+    assert lib.qsa_sparse_attention_splits(1, 16, 2, 128, 2063, 1) == 8
+    assert lib.qsa_sparse_attention_splits(8, 16, 2, 128, 511, 1) == 2   # 16 tiles
+    assert lib.qsa_sparse_attention_splits(8, 16, 2, 128, 480, 1) == 1   # 15 tiles
 
 
 def test_prefill_span_rows():
