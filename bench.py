@@ -707,6 +707,10 @@ def measure_hybrid(dev, steps, warmup, breakdown=True):
     is not captured). Returns the figures as a dict."""
     import torch
 
+    from qsa_vllm_amd.gemm_tuning import disable_tuned_gemms, enable_tuned_gemms
+
+    tuned = enable_tuned_gemms()
+    log(f"library GEMM choices from the recorded tuning file: {tuned}")
     t0 = time.time()
     wl = hybrid_workload(dev)
     model = wl.model
@@ -766,7 +770,9 @@ def measure_hybrid(dev, steps, warmup, breakdown=True):
     flops = hybrid_flops(wl)
     out = {"wl": wl, "ms_per_step": ms_step, "wall_ms_per_step": wall, "flops": flops,
            "breakdown_ms": {k: round(v, 3) for k, v in parts.items()},
-           "decode_graph": measure_hybrid_decode_graph(wl, steps=max(steps, 5))}
+           "decode_graph": measure_hybrid_decode_graph(wl, steps=max(steps, 5)),
+           "tuned_gemms": tuned}
+    disable_tuned_gemms()
     return out
 
 
@@ -823,7 +829,8 @@ def hybrid_summary(dev):
            "ms_per_step": round(m["ms_per_step"], 3),
            "tokens_per_s": round(wl.num_tokens / (m["ms_per_step"] * 1e-3), 1),
            "gemm_tflops": round(m["flops"] / (m["ms_per_step"] * 1e-3) / 1e12, 1),
-           "breakdown_ms": m["breakdown_ms"], "decode_graph": m["decode_graph"]}
+           "breakdown_ms": m["breakdown_ms"], "decode_graph": m["decode_graph"],
+           "library_gemm_choices": "recorded tuning file" if m["tuned_gemms"] else "library default"}
     del wl
     return out
 
@@ -862,7 +869,9 @@ def run_hybrid(args, dev):
         "data": "synthetic: random-init bf16 weights N(0, 0.02), seeded token ids, random "
                 "cache and GDN-state history",
         "config": {"workload": hybrid_description(wl), "tokens": wl.num_tokens,
-                   "requests": len(wl.scheduled), "graph": "eager"},
+                   "requests": len(wl.scheduled), "graph": "eager",
+                   "library_gemm_choices": ("recorded tuning file" if m["tuned_gemms"]
+                                            else "library default")},
         "roofline": {
             "kernel": "whole step (projection, MLP and LM head GEMMs)",
             "bound": "mfma",

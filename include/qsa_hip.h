@@ -351,9 +351,9 @@ int qsa_gated_norm(const void* x, int64_t x_stride, const void* residual_in,
                    int hidden, int rank, float eps, void* workspace, size_t workspace_bytes,
                    void* stream);
 
-/* Workspace qsa_gated_norm needs for `rows` tokens: non-zero for small
- * batches (under 1024 tokens), which run as three launches over (16-token
- * tile, 256-column slice) workgroups with fp32 partials in the workspace. */
+/* Workspace qsa_gated_norm needs for `rows` tokens: 0 for every shape (small
+ * batches, under 1024 tokens, run one workgroup per token; larger ones
+ * 16-token tiles). Kept so callers that size a workspace keep working. */
 size_t qsa_gated_norm_workspace_bytes(int rows, int hidden);
 
 /*

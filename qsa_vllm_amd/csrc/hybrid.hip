@@ -214,155 +214,128 @@ __global__ __launch_bounds__(64 * W) void gated_norm_kernel(const GatedNormArgs 
 }
 
 // ---------------------------------------------------------------------------
-// Gated RMSNorm for small batches (fewer than kSplitTiles 16-token tiles): the
-// fused kernel would run one workgroup per tile on a handful of CUs. Three
-// launches over (tile, 256-column slice) workgroups of one wave instead, with
-// fp32 partials in a workspace between them:
-//   1. residual add (stored) and per-slice sums of squares;
-//   2. inv from the slice sums (added in slice order), the normalised slice
-//      (stored into out) and its partial down projection (one MFMA per
-//      32-column group, as in the fused kernel);
-//   3. the slice partials of the down projection summed, SiLU, the slice's up
-//      projection, sigmoid and the product with the normalised slice.
+// Gated RMSNorm for small batches (fewer than kTokenNormRows tokens): the
+// 16-token tiles above would run on a handful of CUs. One workgroup per token
+// instead, hidden / 8 threads of 8 consecutive columns each, so a decode
+// batch spreads over as many CUs as it has tokens, in one launch. The rank-16
+// projections are per-thread dot products over the thread's columns:
+//  * down: 16 partial sums per thread, summed across the wave by a transpose
+//    reduction (each shuffle step halves the values a lane keeps: 17 shuffles
+//    for 16 sums), then across waves in LDS; every wave forms
+//    s = bf16(silu(bf16(down))) for the 16 ranks itself and broadcasts them
+//    from lanes 0..15 into scalar registers;
+//  * up: each of the thread's columns dots its 16 gate_up weights (32 B) with s.
+// Every load that does not depend on the token's statistics (the row, the
+// residual, gamma, the gate_down slices) is issued first; the gate_up slices
+// and the bias go out before the down reduction. The 2 x 16 x hidden gate
+// weights are read by every workgroup and come from L2 after the first ones.
 // ---------------------------------------------------------------------------
-constexpr int kSplitTiles = 64;
-constexpr int kSliceCols = 256;
-constexpr int kSliceGroups = kSliceCols / 32;
+constexpr int kTokenNormRows = 1024;
+constexpr int kTokenNormMaxWaves = 8;  // hidden up to 4096
 
-struct SplitNormArgs {
-  GatedNormArgs n;
-  float* ssq;   // [rows, slices]
-  float* down;  // [rows, slices, 16]
-  int slices;
-};
+// Sum over the wave of v[j] for each j < 16: returns the total of rank
+// j = (lane >> 2) & 15 (every lane holds one; lanes 4 j .. 4 j + 3 agree).
+__device__ __forceinline__ float wave_transpose_sum16(float (&v)[kRank]) {
+  const int lane = threadIdx.x & 63;
+#pragma unroll
+  for (int half = 8, bit = 32; half >= 1; half >>= 1, bit >>= 1) {
+    const bool upper = (lane & bit) != 0;
+#pragma unroll
+    for (int i = 0; i < half; ++i) {
+      const float keep = upper ? v[half + i] : v[i];
+      const float give = upper ? v[i] : v[half + i];
+      v[i] = keep + __shfl_xor(give, bit, 64);
+    }
+  }
+  float r = v[0];
+  r += __shfl_xor(r, 2, 64);
+  r += __shfl_xor(r, 1, 64);
+  return r;
+}
 
-__global__ __launch_bounds__(64) void split_norm_stats_kernel(const SplitNormArgs a) {
-  const int lane = threadIdx.x, m = lane & 15, g = lane >> 4;
-  const int64_t t = (int64_t)blockIdx.x * kNormTokens + m;
-  const bool ok = t < a.n.rows;
-  const int64_t tl = ok ? t : 0;
-  const int col0 = kSliceCols * blockIdx.y + 8 * g;
-  u32x4 xv[kSliceGroups], rv[kSliceGroups];
+__global__ __launch_bounds__(64 * kTokenNormMaxWaves) void token_norm_kernel(const GatedNormArgs a) {
+  __shared__ float wsq[kTokenNormMaxWaves];
+  __shared__ float wdown[kTokenNormMaxWaves][kRank];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int waves = blockDim.x >> 6;
+  const int64_t t = blockIdx.x;
+  const int col = 8 * tid;
+  const u32x4 xv = load_u32x4(a.x + t * a.x_stride + col);
+  u32x4 rv = {0, 0, 0, 0};
+  if (a.res_in) rv = load_u32x4(a.res_in + t * a.res_in_stride + col);
+  const u32x4 wv = load_u32x4(a.weight + col);
+  u32x4 wd[kRank];
 #pragma unroll
-  for (int s = 0; s < kSliceGroups; ++s) xv[s] = load_u32x4(a.n.x + tl * a.n.x_stride + col0 + 32 * s);
-  if (a.n.res_in) {
+  for (int j = 0; j < kRank; ++j) wd[j] = load_u32x4(a.gate_down + (int64_t)j * a.hidden + col);
+  float f[8];
+  unpack8(xv, f);
+  if (a.res_in) {
+    float r[8];
+    unpack8(rv, r);
 #pragma unroll
-    for (int s = 0; s < kSliceGroups; ++s)
-      rv[s] = load_u32x4(a.n.res_in + tl * a.n.res_in_stride + col0 + 32 * s);
+    for (int e = 0; e < 8; ++e) f[e] = rbf(f[e] + r[e]);
+    *reinterpret_cast<u32x4*>(a.res_out + t * a.res_out_stride + col) = pack8(f);
   }
   float ss = 0.0f;
 #pragma unroll
-  for (int s = 0; s < kSliceGroups; ++s) {
-    float f[8];
-    unpack8(xv[s], f);
-    if (a.n.res_in) {
-      float r[8];
-      unpack8(rv[s], r);
+  for (int e = 0; e < 8; ++e) ss += f[e] * f[e];
 #pragma unroll
-      for (int e = 0; e < 8; ++e) f[e] = rbf(f[e] + r[e]);
-      if (ok) *reinterpret_cast<u32x4*>(a.n.res_out + t * a.n.res_out_stride + col0 + 32 * s) = pack8(f);
-    }
-#pragma unroll
-    for (int e = 0; e < 8; ++e) ss += f[e] * f[e];
-  }
-  ss += __shfl_xor(ss, 16, 64);
-  ss += __shfl_xor(ss, 32, 64);
-  if (ok && g == 0) a.ssq[t * a.slices + blockIdx.y] = ss;
-}
-
-__global__ __launch_bounds__(64) void split_norm_down_kernel(const SplitNormArgs a) {
-  const int lane = threadIdx.x, m = lane & 15, g = lane >> 4;
-  const int64_t t = (int64_t)blockIdx.x * kNormTokens + m;
-  const bool ok = t < a.n.rows;
-  const int64_t tl = ok ? t : 0;
-  const int col0 = kSliceCols * blockIdx.y + 8 * g;
-  // The normalised input is the residual sum when there is a residual.
-  const uint16_t* src = a.n.res_in ? a.n.res_out + tl * a.n.res_out_stride : a.n.x + tl * a.n.x_stride;
-  u32x4 xv[kSliceGroups];
-#pragma unroll
-  for (int s = 0; s < kSliceGroups; ++s) xv[s] = load_u32x4(src + col0 + 32 * s);
+  for (int m = 32; m >= 1; m >>= 1) ss += __shfl_xor(ss, m, 64);
+  if (lane == 0) wsq[wave] = ss;
+  lds_barrier();
   float sq = 0.0f;
-  for (int c = 0; c < a.slices; ++c) sq += a.ssq[tl * a.slices + c];
-  const float inv = rsqrtf(sq / (float)a.n.hidden + a.n.eps);
-  f32x4 down = {0.f, 0.f, 0.f, 0.f};
+  for (int w = 0; w < waves; ++w) sq += wsq[w];
+  const float inv = rsqrtf(sq / (float)a.hidden + a.eps);
+  {
+    float g[8];
+    unpack8(wv, g);
 #pragma unroll
-  for (int s = 0; s < kSliceGroups; ++s) {
-    const int col = col0 + 32 * s;
-    float f[8], w[8];
-    unpack8(xv[s], f);
-    unpack8(load_u32x4(a.n.weight + col), w);
-#pragma unroll
-    for (int e = 0; e < 8; ++e) f[e] = rbf(rbf(f[e] * inv) * w[e]);
-    xv[s] = pack8(f);
-    if (ok) *reinterpret_cast<u32x4*>(a.n.out + t * a.n.out_stride + col) = xv[s];
-    const u32x4 wd = load_u32x4(a.n.gate_down + (int64_t)m * a.n.hidden + col);
-    down = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, xv[s]),
-                                                   __builtin_bit_cast(bf16x8, wd), down, 0, 0, 0);
+    for (int e = 0; e < 8; ++e) f[e] = rbf(rbf(f[e] * inv) * g[e]);
   }
-  // down[token 4 g + i][rank m] of this slice
+  u32x4 wu[2 * 8];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int64_t tt = (int64_t)blockIdx.x * kNormTokens + 4 * g + i;
-    if (tt < a.n.rows) a.down[(tt * a.slices + blockIdx.y) * kRank + m] = down[i];
+  for (int e = 0; e < 8; ++e) {
+    wu[2 * e] = load_u32x4(a.gate_up + (int64_t)(col + e) * kRank);
+    wu[2 * e + 1] = load_u32x4(a.gate_up + (int64_t)(col + e) * kRank + 8);
   }
-}
-
-__global__ __launch_bounds__(64) void split_norm_gate_kernel(const SplitNormArgs a) {
-  const int lane = threadIdx.x, m = lane & 15, g = lane >> 4;
-  const int64_t t = (int64_t)blockIdx.x * kNormTokens + m;
-  const bool ok = t < a.n.rows;
-  const int64_t tl = ok ? t : 0;
-  const int col0 = kSliceCols * blockIdx.y + 8 * g;
-  // B operand s^T: lane (m, g < 2) = token m, ranks 8 g .. +7.
-  u32x4 sb = {0, 0, 0, 0};
-  if (g < 2) {
-    float d[8];
+  const u32x4 bv = load_u32x4(a.bias + col);
+  float d[kRank];
 #pragma unroll
-    for (int e = 0; e < 8; ++e) d[e] = 0.0f;
-    for (int c = 0; c < a.slices; ++c) {
-      const float* dp = a.down + (tl * a.slices + c) * kRank + 8 * g;
+  for (int j = 0; j < kRank; ++j) {
+    float w[8];
+    unpack8(wd[j], w);
+    float acc = 0.0f;
 #pragma unroll
-      for (int e = 0; e < 8; ++e) d[e] += dp[e];
-    }
-#pragma unroll
-    for (int e = 0; e < 8; ++e) d[e] = rbf(silu_f(rbf(d[e])));
-    sb = pack8(d);
+    for (int e = 0; e < 8; ++e) acc += f[e] * w[e];
+    d[j] = acc;
   }
-  const uint16_t* zero16 = reinterpret_cast<const uint16_t*>(g_qsa_zero_rows);
-  u32x4 nv[kSliceGroups];
-#pragma unroll
-  for (int s = 0; s < kSliceGroups; ++s) nv[s] = load_u32x4(a.n.out + tl * a.n.out_stride + col0 + 32 * s);
-#pragma unroll
-  for (int s = 0; s < kSliceGroups; ++s) {
-    const int col = col0 + 32 * s;
-    f32x4 up[2];
-#pragma unroll
-    for (int h = 0; h < 2; ++h) {
-      const int arow = kSliceCols * blockIdx.y + 32 * s + 8 * (m >> 2) + 4 * h + (m & 3);
-      const u32x4 wu = load_u32x4(g < 2 ? a.n.gate_up + (int64_t)arow * kRank + 8 * g : zero16);
-      const f32x4 z = {0.f, 0.f, 0.f, 0.f};
-      up[h] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, wu),
-                                                      __builtin_bit_cast(bf16x8, sb), z, 0, 0, 0);
-    }
-    float b[8], f[8];
-    unpack8(load_u32x4(a.n.bias + col), b);
-    unpack8(nv[s], f);
-#pragma unroll
-    for (int e = 0; e < 8; ++e) f[e] = rbf(f[e] * rbf(sigmoid_f(rbf(up[e >> 2][e & 3] + b[e]))));
-    nv[s] = pack8(f);
+  const float dj = wave_transpose_sum16(d);
+  if ((lane & 3) == 0) wdown[wave][lane >> 2] = dj;
+  lds_barrier();
+  float sj = 0.0f;
+  if (lane < kRank) {
+    for (int w = 0; w < waves; ++w) sj += wdown[w][lane];
+    sj = rbf(silu_f(rbf(sj)));
   }
-  if (ok) {
+  float sr[kRank];
 #pragma unroll
-    for (int s = 0; s < kSliceGroups; ++s)
-      *reinterpret_cast<u32x4*>(a.n.out + t * a.n.out_stride + col0 + 32 * s) = nv[s];
+  for (int j = 0; j < kRank; ++j)
+    sr[j] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(sj), j));
+  float b[8];
+  unpack8(bv, b);
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    float u0[8], u1[8];
+    unpack8(wu[2 * e], u0);
+    unpack8(wu[2 * e + 1], u1);
+    float u = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) u += sr[j] * u0[j];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) u += sr[8 + j] * u1[j];
+    f[e] = rbf(f[e] * rbf(sigmoid_f(rbf(u + b[e]))));
   }
-}
-
-size_t split_norm_bytes(int rows, int hidden) {
-  const int tiles = (rows + kNormTokens - 1) / kNormTokens;
-  if (rows <= 0 || tiles >= kSplitTiles || hidden % kSliceCols) return 0;
-  const size_t slices = hidden / kSliceCols;
-  return (size_t)rows * slices * (1 + kRank) * sizeof(float);
+  *reinterpret_cast<u32x4*>(a.out + t * a.out_stride + col) = pack8(f);
 }
 
 // ---------------------------------------------------------------------------
@@ -1029,7 +1002,9 @@ bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 
 using namespace qsa;
 
 extern "C" size_t qsa_gated_norm_workspace_bytes(int rows, int hidden) {
-  return split_norm_bytes(rows, hidden);
+  (void)rows;
+  (void)hidden;
+  return 0;  // no launch shape needs one
 }
 
 extern "C" int qsa_gated_norm(const void* x, int64_t x_stride, const void* residual_in,
@@ -1058,18 +1033,11 @@ extern "C" int qsa_gated_norm(const void* x, int64_t x_stride, const void* resid
                   static_cast<const uint16_t*>(gate_up), static_cast<const uint16_t*>(gate_up_bias),
                   static_cast<uint16_t*>(out), out_stride, rows, hidden, eps};
   hipStream_t s = static_cast<hipStream_t>(stream);
-  const size_t split_bytes = split_norm_bytes(rows, hidden);
-  if (split_bytes) {
-    if (!workspace || workspace_bytes < split_bytes || !aligned16(workspace))
-      return fail(QSA_ERR_WORKSPACE, "qsa_gated_norm: small batches need the workspace of "
-                                     "qsa_gated_norm_workspace_bytes (16-byte aligned)");
-    SplitNormArgs sa{a, static_cast<float*>(workspace), nullptr, hidden / kSliceCols};
-    sa.down = sa.ssq + (size_t)rows * sa.slices;
-    const dim3 sgrid((rows + kNormTokens - 1) / kNormTokens, sa.slices);
-    hipLaunchKernelGGL(split_norm_stats_kernel, sgrid, dim3(64), 0, s, sa);
-    hipLaunchKernelGGL(split_norm_down_kernel, sgrid, dim3(64), 0, s, sa);
-    hipLaunchKernelGGL(split_norm_gate_kernel, sgrid, dim3(64), 0, s, sa);
-    return check_launch("qsa_gated_norm (small batch)");
+  (void)workspace;
+  (void)workspace_bytes;
+  if (rows < kTokenNormRows) {
+    hipLaunchKernelGGL(token_norm_kernel, dim3(rows), dim3(hidden / 8), 0, s, a);
+    return check_launch("qsa_gated_norm (one workgroup per token)");
   }
   const dim3 grid((rows + kNormTokens - 1) / kNormTokens);
   switch (hidden / 512) {

@@ -457,3 +457,41 @@ def test_hybrid_serving_decode_graph_replay_equals_eager():
     for a, b in zip(wl.layer_states(), eager_states):
         assert torch.equal(a, b)
 
+
+
+def test_recorded_gemm_choices_load_and_agree_with_library_default():
+    """The committed TunableOp records load on this software stack, and every
+    recorded solution computes what the library's default choice computes
+    (bf16 GEMMs at the recorded serving shapes, fp32 accumulation in both)."""
+    import torch.nn.functional as F
+
+    from qsa_vllm_amd.gemm_tuning import TUNING_FILE, disable_tuned_gemms, enable_tuned_gemms
+
+    shapes = []
+    for line in TUNING_FILE.read_text().splitlines():
+        op, params = line.split(",")[:2]
+        if op.startswith("Validator"):
+            continue
+        # column-major BLAS view of F.linear: m = out features, n = tokens
+        m, n, k = (int(v) for v in params.split("_")[1:4])
+        shapes.append((m, n, k, op.startswith("GemmAndBias")))
+    assert len(shapes) >= 10
+    g = torch.Generator(device=DEV).manual_seed(3)
+    cases = []
+    for m, n, k, bias in shapes:
+        x = torch.randn(n, k, device=DEV, dtype=torch.bfloat16, generator=g)
+        w = (0.02 * torch.randn(m, k, device=DEV, generator=g)).to(torch.bfloat16)
+        b = torch.randn(m, device=DEV, generator=g).to(torch.bfloat16) if bias else None
+        cases.append((x, w, b))
+    want = [F.linear(x, w, b) for x, w, b in cases]
+    assert enable_tuned_gemms()
+    try:
+        got = [F.linear(x, w, b) for x, w, b in cases]
+        torch.cuda.synchronize()
+    finally:
+        disable_tuned_gemms()
+    for (m, n, k, _), a, b in zip(shapes, got, want):
+        err = (a.float() - b.float()).abs().max().item()
+        scale = b.float().abs().max().item()
+        print(f"[hybrid] recorded GEMM {m}x{n}x{k}: max diff {err:.3e} of {scale:.3e}", flush=True)
+        assert err <= 0.02 * scale

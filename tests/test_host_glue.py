@@ -65,3 +65,20 @@ def test_indexer_gamma_weight_loader():
     assert torch.equal(norm.weight.data, loaded)
     with pytest.raises(Exception):
         norm.weight.weight_loader(norm.weight, torch.zeros(8, dtype=torch.bfloat16))
+
+
+def test_gemm_tuning_file_is_well_formed(tmp_path):
+    """The recorded library GEMM choices name their software stack (PyTorch
+    rejects the file on any other) and one solution per GEMM shape."""
+    from qsa_vllm_amd.gemm_tuning import TUNING_FILE, enable_tuned_gemms
+
+    lines = TUNING_FILE.read_text().splitlines()
+    validators = {line.split(",")[1]: line.split(",")[2] for line in lines
+                  if line.startswith("Validator,")}
+    assert {"PT_VERSION", "HIPBLASLT_VERSION", "ROCBLAS_VERSION", "GCN_ARCH_NAME"} <= set(validators)
+    assert validators["GCN_ARCH_NAME"].startswith("gfx950")
+    records = [line.split(",") for line in lines if not line.startswith("Validator,")]
+    assert len(records) >= 10
+    assert len({r[1] for r in records}) == len(records)  # one choice per shape
+    assert all(r[1].startswith("tn_") and r[2] for r in records)
+    assert enable_tuned_gemms(tmp_path / "missing.csv") is False
