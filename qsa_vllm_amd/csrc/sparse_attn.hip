@@ -9,10 +9,12 @@
 // G, NKV*G <= 16). Each wave walks 32-token tiles of the row's index list:
 //
 //   S^T[tok][head] = K_tile (A, 16 tokens x 32 dims) * Q^T (B, 32 dims x 16 heads)
-//       v_mfma_f32_16x16x32_bf16, K read straight from HBM into the A operand
-//       (16 B per lane, 64 B contiguous per token per instruction);
-//       one accumulator per kv head, each lane keeping the one its head
-//       attends with.
+//       v_mfma_f32_16x16x32_bf16; K rows are loaded whole, like V's, into the
+//       wave's LDS region (straight into LDS for logical rows with D = 128,
+//       through registers for physical rows) and read back in the A layout
+//       (D = 64 logical rows load the A layout straight from memory, 64 B
+//       contiguous per token per instruction); one accumulator per kv head,
+//       each lane keeping the one its head attends with.
 //   O^T[dim][head] += V_tile^T (A, 16 dims x 32 tokens) * P^T (B, 32 tok x 16 heads)
 //       each lane loads an 8 token x DPL dim block of V (one 16 B row load per
 //       token) and transposes it in registers with v_perm_b32; P^T is exactly
@@ -242,8 +244,10 @@ __device__ __forceinline__ void v_slots_from_k(const int (&ks)[2], int g, int (&
 
 // K in the MFMA A layout straight from memory (lane (n, g): dims 32 s + 8 g
 // .. + 7 of token 16 u + n; 16 tokens x 64 B per load instruction). Used for
-// logical (prefill) rows, where it measured faster than staging K through
-// LDS; physical (decode) rows load whole rows and stage them (stage_k).
+// logical (prefill) rows with D = 64, where it measured faster than staging K
+// through registers and LDS; D = 128 logical rows load whole rows straight
+// into LDS (dma_k), physical (decode) rows load whole rows and stage them
+// (stage_k).
 template <int D, int NKV>
 __device__ __forceinline__ void issue_k_direct(const AttnParams& p, const int (&slot)[2],
                                                const int64_t (&khead)[NKV], int g,
@@ -390,6 +394,56 @@ __device__ __forceinline__ void stage_k(char* lds, const KStageLanes<D>& l,
                                                         (v * kTile + 16 * u) * U * 16);
 }
 
+// K rows straight into the wave's LDS region (global_load_lds_dwordx4: lane l
+// of an instruction writes its 16 bytes at the destination + 16 l), for
+// logical (prefill) rows with D = 128. Instruction (v, i) covers the four
+// tokens 16 (i / 4) + 4 g + i % 4 of V's load pattern, one 256 B row per
+// 16-lane row g, into the 1 KB block v 8 KB + i KB; lane (n, g) loads the row's
+// 16-byte unit n ^ (token % 16), so unit c of token 16 u + m sits at position
+// c ^ m of its row and the A-layout reads (16 tokens per unit position) are
+// conflict-free. The data never passes through VGPRs; the wave waits for it
+// (vmcnt) only when it reads the block back.
+constexpr int kDmaKBlockBytes = 1024;
+
+// s_waitcnt immediate that waits for the vector-memory counter alone (gfx9
+// encoding: vmcnt in bits 3:0 and 15:14, expcnt and lgkmcnt at their maxima).
+constexpr int vmcnt_only(int n) { return (n & 15) | (7 << 4) | (15 << 8) | ((n >> 4) << 14); }
+
+template <int D, int NKV>
+__device__ __forceinline__ void dma_k(const AttnParams& p, const int (&slot)[8],
+                                      const int64_t (&khead)[NKV], int n, int g, char* region) {
+  static_assert(D == 128, "one 256 B row per 16 lanes");
+  const char* zero = reinterpret_cast<const char*>(g_qsa_zero_rows);
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const int64_t off = slot[i] >= 0 ? slot_offset(p, slot[i], p.kb, p.kt) : 0;
+    const int unit = 16 * (n ^ (4 * g + (i & 3)));
+#pragma unroll
+    for (int v = 0; v < NKV; ++v) {
+      const char* src = (slot[i] >= 0 ? p.k + off + khead[v] : zero) + unit;
+      __builtin_amdgcn_global_load_lds(
+          (const __attribute__((address_space(1))) void*)src,
+          (__attribute__((address_space(3))) void*)(region + (v * 8 + i) * kDmaKBlockBytes), 16,
+          0, 0);
+    }
+  }
+}
+
+// The A layout from a region dma_k filled: lane (n, g) reads unit 4 s + g of
+// token 16 u + n, written by instruction 4 u + n % 4 in row n / 4.
+template <int D, int NKV>
+__device__ __forceinline__ void read_k_dma(const char* region, int n, int g, TileK<D, NKV>& K) {
+  const char* lane_base = region + (n & 3) * kDmaKBlockBytes + (n >> 2) * 256;
+#pragma unroll
+  for (int v = 0; v < NKV; ++v)
+#pragma unroll
+    for (int u = 0; u < 2; ++u)
+#pragma unroll
+      for (int s = 0; s < D / 32; ++s)
+        K.r[v][u][s] = *reinterpret_cast<const u32x4*>(
+            lane_base + (v * 8 + 4 * u) * kDmaKBlockBytes + 16 * ((4 * s + g) ^ n));
+}
+
 template <int D, int NKV>
 __device__ __forceinline__ void issue_v(const AttnParams& p, const KVBuffers<NKV>& b,
                                         const int (&slot)[8], int n, TileV<D, NKV>& V) {
@@ -487,9 +541,11 @@ void sparse_attn_kernel(const AttnParams p) {
   constexpr int DPL = D / 16;  // V dims per lane = P.V MFMAs per kv slot
   constexpr int KS = D / 32;   // K steps of the Q.K MFMA
 
-  // Each wave's K staging region (physical rows), then (after the tile loop)
-  // the waves' partial outputs for the combine.
-  constexpr int kStageUnits = PHYSICAL ? NKV * kTile * (D / 8) : 0;
+  // Logical rows with D = 128 load K rows into LDS directly (dma_k).
+  constexpr bool DMA_K = !PHYSICAL && D == 128;
+  // Each wave's K staging region (physical rows, or the direct loads), then
+  // (after the tile loop) the waves' partial outputs for the combine.
+  constexpr int kStageUnits = (PHYSICAL || DMA_K) ? NKV * kTile * (D / 8) : 0;
   constexpr int kStageBytes = WAVES * kStageUnits * 16;
   constexpr int kCombineBytes = WAVES * 16 * (D + 4) * 4;
   __shared__ __attribute__((aligned(16))) char s_lds[kStageBytes > kCombineBytes ? kStageBytes
@@ -564,7 +620,68 @@ void sparse_attn_kernel(const AttnParams p) {
   for (int j = 0; j < DPL; ++j) oacc[j] = f32x4{0.f, 0.f, 0.f, 0.f};
 
   int t = t_begin + wave;
-  if (!PHYSICAL && t < t_end) {
+  if constexpr (DMA_K) {
+    if (t < t_end) {
+    // As the three-stage loop below, with K rows loaded into the wave's LDS
+    // region: per trip, K(t) is read back (waiting for its loads only), then
+    // K(t+W) is issued into the same region, table(t+2W), index(t+3W),
+    // V(t+W). The slots of K(t+W) come from lanes' ds_bpermute, which
+    // completes after the reads of K(t) (LDS operations complete in order),
+    // so the new rows never overwrite rows not yet read.
+    char* kregion = s_lds + wave * kStageUnits * 16;
+    TileIdx ia, ib;
+    int pa[2];
+    int ks[2], vs[8];
+    TileK<D, NKV> K;
+    TileV<D, NKV> V;
+    load_tile_idx(irow, t, t_end, n_valid, n, ia);
+#pragma unroll
+    for (int u = 0; u < 2; ++u) pa[u] = table_page(p, trow, req_ok, ia.key(u));
+#pragma unroll
+    for (int u = 0; u < 2; ++u) ks[u] = logical_slot(p, req_ok, ia.key(u), pa[u]);
+    v_slots_from_k(ks, g, vs);
+    load_tile_idx(irow, t + WAVES, t_end, n_valid, n, ia);
+    QSA_SCHED_FENCE();
+    dma_k<D, NKV>(p, vs, khead, n, g, kregion);
+    QSA_SCHED_FENCE();
+#pragma unroll
+    for (int u = 0; u < 2; ++u) pa[u] = table_page(p, trow, req_ok, ia.key(u));
+    QSA_SCHED_FENCE();
+    load_tile_idx(irow, t + 2 * WAVES, t_end, n_valid, n, ib);
+    QSA_SCHED_FENCE();
+    load_v(vs, V);
+    QSA_SCHED_FENCE();
+    for (; t < t_end; t += WAVES) {
+      // K(t) has landed once at most the loads issued after it (table 2,
+      // index 2, V 8 NKV) are outstanding; the compiler does not order LDS
+      // reads after direct loads into LDS by itself.
+      __builtin_amdgcn_s_waitcnt(vmcnt_only(4 + 8 * NKV));
+      read_k_dma<D, NKV>(kregion, n, g, K);
+      QSA_SCHED_FENCE();
+#pragma unroll
+      for (int u = 0; u < 2; ++u) ks[u] = logical_slot(p, req_ok, ia.key(u), pa[u]);
+      v_slots_from_k(ks, g, vs);
+      dma_k<D, NKV>(p, vs, khead, n, g, kregion);
+      QSA_SCHED_FENCE();
+      const u32x4 praw = qk_softmax<D, NKV>(p, K, bq, vslot, V.mask, m_run, l_run, oacc);
+      QSA_SCHED_FENCE();
+      pv_mfma<D, NKV>(V, praw, vslot, oacc);
+      QSA_SCHED_FENCE();
+#pragma unroll
+      for (int u = 0; u < 2; ++u) pa[u] = table_page(p, trow, req_ok, ib.key(u));
+      ia = ib;
+      QSA_SCHED_FENCE();
+      load_tile_idx(irow, t + 3 * WAVES, t_end, n_valid, n, ib);
+      QSA_SCHED_FENCE();
+      load_v(vs, V);
+      QSA_SCHED_FENCE();
+    }
+    // The last trip's K loads (of the tile past the split: the zero block)
+    // land in LDS that the combine reuses.
+    __builtin_amdgcn_s_waitcnt(0);
+    }
+  } else if constexpr (!PHYSICAL) {
+    if (t < t_end) {
     // Three stages: index entries of t+3W, table entries of t+2W, K/V of t+W
     // are in flight while tile t computes. Issue order per trip: K(t+W),
     // table(t+2W), index(t+3W), V(t+W); each wait is for the oldest group.
@@ -609,7 +726,9 @@ void sparse_attn_kernel(const AttnParams p) {
       load_v(vs, V);
       QSA_SCHED_FENCE();
     }
-  } else if (PHYSICAL && t < t_end) {
+    }
+  } else {
+    if (t < t_end) {
     TileIdx idx;
     int ks[2], vs[8];
     TileK<D, NKV> K;
@@ -646,6 +765,7 @@ void sparse_attn_kernel(const AttnParams p) {
       load_v(vs, V);
       QSA_SCHED_FENCE();
     }
+    }
   }
 
   // Row sums are lane-partial (each lane summed its own tokens).
@@ -653,7 +773,7 @@ void sparse_attn_kernel(const AttnParams p) {
   l_run += shfl_xor_f(l_run, 32);
 
   // s_o shares LDS with the other waves' K staging regions.
-  if constexpr (PHYSICAL) __syncthreads();
+  if constexpr (PHYSICAL || DMA_K) __syncthreads();
   // oacc[j][r] = O[head n][DPL * (4 g + r) + j].
 #pragma unroll
   for (int j = 0; j < DPL; ++j)
