@@ -76,6 +76,7 @@ void vec(const Tensor& t, at::ScalarType s, const char* name, int64_t min_len = 
 void positions(const Tensor& t, int64_t n, const char* name) {
   dtype(t, at::kLong, name);
   QSA_REQUIRE(t.dim() == 1 && t.numel() >= n, name, " must be 1-D with at least ", n, " entries");
+  QSA_REQUIRE(t.numel() <= 1 || t.stride(0) == 1, name, " must be contiguous");
 }
 
 void unit_dim(const Tensor& t, const char* name, int64_t dims) {
