@@ -248,45 +248,20 @@ __device__ __forceinline__ void block_scan2(int& a, int& b, TopkShared<THREADS>&
 
 // --- selection --------------------------------------------------------------
 
-// Exact top-k of `length` (> topk) keys in registers. Writes the selected ids
-// in ascending-id order to sel[0..topk) and, with PAGES, the physical slot of
-// each one's first token (from page[e], the staged page of the element at
-// position e) to sel[topk..2 topk).
+// Exact top-k among the candidate keys (bit j of `cand`: key[j] is one) of
+// a row whose candidates all lie in [lo, hi] and include every key that can
+// be selected. Writes the selected ids in ascending-id order to sel[0..topk)
+// and, with PAGES, the physical slot of each one's first token (from
+// page[pos[j]], the staged page of the element) to sel[topk..2 topk).
+// Candidates are in id order across threads (thread t's before thread t+1's).
 template <int THREADS, int ITEMS, bool PAGES>
-__device__ __forceinline__ void select_long(int length, int topk, const uint32_t (&key)[ITEMS],
-                            const int (&id)[ITEMS], const int* page, const ExpandMeta& m,
-                            TopkShared<THREADS>& sh, int* sel) {
+__device__ __forceinline__ void radix_rank(int topk, uint32_t lo, uint32_t hi, uint32_t cand,
+                                           const uint32_t (&key)[ITEMS], const int (&id)[ITEMS],
+                                           const int (&pos)[ITEMS], const int* page,
+                                           const ExpandMeta& m, TopkShared<THREADS>& sh, int* sel) {
   const int tid = threadIdx.x;
   const int lane = tid & 63;
-  const int base = tid * ITEMS;
-  uint32_t active = 0;
-  uint32_t lo = 0xffffffffu, hi = 0u;
-#pragma unroll
-  for (int j = 0; j < ITEMS; ++j) {
-    if (base + j < length) {
-      active |= 1u << j;
-      lo = min(lo, key[j]);
-      hi = max(hi, key[j]);
-    }
-  }
-  // Lower bound on the topk-th largest key. Active threads are a prefix, so
-  // waves [0, full) have 64 active lanes, each holding its thread maximum
-  // (`hi` here, a distinct element). If each of those waves bounds the m-th
-  // largest of its maxima from below, with m * full >= topk, at least topk
-  // distinct elements are >= the smallest of these floors: keys below it
-  // cannot be selected and never enter the histograms.
-  uint32_t floor = 0u;  // 0: no bound
-#if QSA_TOPK_PRUNE
-  {
-    const int threads_active = min(THREADS, (length + ITEMS - 1) / ITEMS);
-    const int full = threads_active / 64;
-    const int m = full > 0 ? (topk + full - 1) / full : 65;
-    if (m <= 64) floor = (tid >> 6) < full ? wave_floor_mth_largest(hi, m) : 0xffffffffu;
-  }
-#endif
-  block_bounds<THREADS>(lo, hi, floor, sh);
-  lo = max(lo, floor);  // smallest candidate bound; lo <= hi still holds
-
+  const uint32_t cand0 = cand;
   // Result: selected = {key > thr} + first `remaining` ids with key == thr
   // (tie mode), or {key >= thr} (ge mode).
   uint32_t thr = lo;
@@ -297,10 +272,6 @@ __device__ __forceinline__ void select_long(int length, int topk, const uint32_t
     const int high_bit = 31 - __builtin_clz(lo ^ hi);
     int shift = high_bit > kDigitBits - 1 ? high_bit - (kDigitBits - 1) : 0;
     uint32_t prefix = shift + kDigitBits >= 32 ? 0u : (lo & ~((1u << (shift + kDigitBits)) - 1u));
-    uint32_t cand = 0;
-#pragma unroll
-    for (int j = 0; j < ITEMS; ++j)
-      if (((active >> j) & 1u) && key[j] >= lo) cand |= 1u << j;
     // One barrier per pass: every wave reads the whole histogram and finds
     // the bin itself (identical results), and pass k counts into buffer
     // k % 3, so the buffer read in pass k - 1 can be cleared during pass k
@@ -384,7 +355,7 @@ __device__ __forceinline__ void select_long(int length, int topk, const uint32_t
   int n_sel = 0, n_tie = 0;
 #pragma unroll
   for (int j = 0; j < ITEMS; ++j) {
-    if ((active >> j) & 1u) {
+    if ((cand0 >> j) & 1u) {
       n_sel += ge ? key[j] >= thr : key[j] > thr;
       n_tie += !ge && key[j] == thr;
     }
@@ -392,7 +363,7 @@ __device__ __forceinline__ void select_long(int length, int topk, const uint32_t
   block_scan2<THREADS>(n_sel, n_tie, sh);
 #pragma unroll
   for (int j = 0; j < ITEMS; ++j) {
-    if (!((active >> j) & 1u)) continue;
+    if (!((cand0 >> j) & 1u)) continue;
     const bool strict = ge ? key[j] >= thr : key[j] > thr;
     int rank = -1;
     if (strict) {
@@ -404,9 +375,106 @@ __device__ __forceinline__ void select_long(int length, int topk, const uint32_t
     }
     if (rank >= 0) {
       sel[rank] = id[j];
-      sel[topk + rank] = PAGES ? first_slot(m, page[base + j], id[j]) : -1;
+      sel[topk + rank] = PAGES ? first_slot(m, page[pos[j]], id[j]) : -1;
     }
   }
+}
+
+// Exact top-k of `length` (> topk) keys in registers (thread t holds
+// elements t ITEMS .. t ITEMS + ITEMS - 1 of the row). Writes the selected ids
+// in ascending-id order to sel[0..topk) and, with PAGES, the physical slot of
+// each one's first token (from page[e], the staged page of the element at
+// position e) to sel[topk..2 topk). `scratch` (scratch_words 32-bit words of
+// LDS, dead until the selection is written) holds the compacted candidates.
+template <int THREADS, int ITEMS, bool PAGES>
+__device__ __forceinline__ void select_long(int length, int topk, const uint32_t (&key)[ITEMS],
+                            const int (&id)[ITEMS], const int* page, const ExpandMeta& m,
+                            TopkShared<THREADS>& sh, int* sel, uint32_t* scratch,
+                            int scratch_words) {
+  const int tid = threadIdx.x;
+  const int base = tid * ITEMS;
+  uint32_t active = 0;
+  uint32_t lo = 0xffffffffu, hi = 0u;
+#pragma unroll
+  for (int j = 0; j < ITEMS; ++j) {
+    if (base + j < length) {
+      active |= 1u << j;
+      lo = min(lo, key[j]);
+      hi = max(hi, key[j]);
+    }
+  }
+  // Lower bound on the topk-th largest key. Active threads are a prefix, so
+  // waves [0, full) have 64 active lanes, each holding its thread maximum
+  // (`hi` here, a distinct element). If each of those waves bounds the m-th
+  // largest of its maxima from below, with m * full >= topk, at least topk
+  // distinct elements are >= the smallest of these floors: keys below it
+  // cannot be selected and never enter the histograms.
+  uint32_t floor = 0u;  // 0: no bound
+#if QSA_TOPK_PRUNE
+  {
+    const int threads_active = min(THREADS, (length + ITEMS - 1) / ITEMS);
+    const int full = threads_active / 64;
+    const int mm = full > 0 ? (topk + full - 1) / full : 65;
+    if (mm <= 64) floor = (tid >> 6) < full ? wave_floor_mth_largest(hi, mm) : 0xffffffffu;
+  }
+#endif
+  block_bounds<THREADS>(lo, hi, floor, sh);
+  lo = max(lo, floor);  // smallest candidate bound; lo <= hi still holds
+  uint32_t cand = 0;
+#pragma unroll
+  for (int j = 0; j < ITEMS; ++j)
+    if (((active >> j) & 1u) && key[j] >= lo) cand |= 1u << j;
+
+  if constexpr (ITEMS >= 4) {
+    // Few candidates (the usual case once the bound has pruned): compact them,
+    // in id order, to kCompact per thread and select among those, so the
+    // radix passes and the ranking loop over kCompact keys per thread instead
+    // of ITEMS. Three arrays of kCompact x THREADS words: keys, ids, positions.
+    constexpr int kCompact = ITEMS >= 8 ? 2 : 1;
+    int off = __builtin_popcount(cand), unused = 0;
+    block_scan2<THREADS>(off, unused, sh);
+    int total = 0;
+#pragma unroll
+    for (int w = 0; w < THREADS / 64; ++w) total += sh.wsel[w];
+    if (total <= kCompact * THREADS && 3 * kCompact * THREADS <= scratch_words) {
+      uint32_t* ckey = scratch;
+      int* cid = reinterpret_cast<int*>(scratch + kCompact * THREADS);
+      int* cpos = cid + kCompact * THREADS;
+      int o = off;
+#pragma unroll
+      for (int j = 0; j < ITEMS; ++j) {
+        if ((cand >> j) & 1u) {
+          ckey[o] = key[j];
+          cid[o] = id[j];
+          cpos[o] = base + j;
+          ++o;
+        }
+      }
+      lds_barrier();
+      uint32_t ck[kCompact];
+      int ci[kCompact], cp[kCompact];
+      uint32_t ccand = 0;
+#pragma unroll
+      for (int j = 0; j < kCompact; ++j) {
+        const int e = kCompact * tid + j;
+        const bool ok = e < total;
+        ck[j] = ok ? ckey[e] : 0u;
+        ci[j] = ok ? cid[e] : 0;
+        cp[j] = ok ? cpos[e] : 0;
+        ccand |= (uint32_t)ok << j;
+      }
+      // Every wave has its candidates in registers before any selection is
+      // written (sel may share the scratch words).
+      lds_barrier();
+      radix_rank<THREADS, kCompact, PAGES>(topk, lo, hi, ccand, ck, ci, cp, page, m, sh, sel);
+      return;
+    }
+    lds_barrier();  // every wave has read the scan totals before they are reused
+  }
+  int pos[ITEMS];
+#pragma unroll
+  for (int j = 0; j < ITEMS; ++j) pos[j] = base + j;
+  radix_rank<THREADS, ITEMS, PAGES>(topk, lo, hi, cand, key, id, pos, page, m, sh, sel);
 }
 
 // Writes one expanded output row from ranked block ids in sel[0..topk) and
@@ -610,7 +678,9 @@ __device__ __forceinline__ void finish_row(const Loader& load, const uint32_t (&
   const int tid = threadIdx.x;
   const int length = length_raw > topk ? min(length_raw, clamp) : length_raw;
   if (length > topk) {
-    select_long<THREADS, ITEMS, PAGES>(length, topk, key, id, st.page, m, sh, sel);
+    select_long<THREADS, ITEMS, PAGES>(length, topk, key, id, st.page, m, sh, sel,
+                                       reinterpret_cast<uint32_t*>(const_cast<uint32_t*>(st.key)),
+                                       THREADS * ITEMS);
   } else {
     // At most topk entries: the loader's first `length` ids in order, then -1.
     lds_barrier();  // every wave has read its keys back before sel overwrites them
