@@ -128,9 +128,11 @@ __global__ __launch_bounds__(kAdaptiveThreads) void topk_adaptive_kernel(const T
   }
   if (n <= kAdaptiveHalf) {
     const DirectLoader load{srow, 0};
-    const int need = max(n, 2 * topk);  // keys, and room for the selection
-    if (need <= T * 2) QSA_ADAPTIVE_ROW(2, load, n, length, a.cols)
-    else if (need <= T * 4) QSA_ADAPTIVE_ROW(4, load, n, length, a.cols)
+    // Keys, and room for the selection. Rows of up to 4096 keys take four
+    // per thread (a row of 2048 keys fills the lower half of the threads),
+    // so the candidates the bound leaves are compacted to one per thread.
+    const int need = max(n, 2 * topk);
+    if (need <= T * 4) QSA_ADAPTIVE_ROW(4, load, n, length, a.cols)
     else if (need <= T * 8) QSA_ADAPTIVE_ROW(8, load, n, length, a.cols)
     else QSA_ADAPTIVE_ROW(16, load, n, length, a.cols)
     return;
