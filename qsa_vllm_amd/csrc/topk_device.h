@@ -103,7 +103,15 @@ struct RowMeta {
   const int32_t* table_row;  // null unless physical
 };
 
-__device__ __forceinline__ int tail_start_of(int pos, int ratio) { return ((pos + 1) / ratio) * ratio; }
+// x / ratio with C semantics: one multiply-high for x >= 0 (the integer
+// division sequence runs only for a negative x).
+__device__ __forceinline__ int div_ratio(const ExpandMeta& m, int x) {
+  return x >= 0 ? m.ratio_div.div(x) : x / m.ratio;
+}
+// First token of the causal tail (the incomplete block) of position pos.
+__device__ __forceinline__ int tail_start_of(const ExpandMeta& m, int pos) {
+  return div_ratio(m, pos + 1) * m.ratio;
+}
 
 // Logical page of token t, or -1 when t has no page-table entry to read.
 __device__ __forceinline__ int token_page(const ExpandMeta& m, int t) {
@@ -490,8 +498,8 @@ __device__ __forceinline__ void write_expanded(const ExpandMeta& m, const RowMet
                                                int topk, const int* sel, const int* tail_page,
                                                int32_t* out) {
   const int p1 = r.pos + 1;
-  const int complete = max(0, min(min(p1 / m.ratio, r.seq_len / m.ratio), topk));
-  const int tail_start = tail_start_of(r.pos, m.ratio);
+  const int complete = max(0, min(min(div_ratio(m, p1), div_ratio(m, r.seq_len)), topk));
+  const int tail_start = tail_start_of(m, r.pos);
   const int tail_count = p1 - tail_start;
   const int expanded = complete * m.ratio;
   const bool block_in_page = m.physical && (m.page_size % m.ratio == 0);
@@ -566,7 +574,7 @@ __device__ __forceinline__ RowPrefetch prefetch_tail(const ExpandMeta& m, int re
   f.r.seq_len = mapped ? m.sequence_lengths[req] : 0;
   f.r.table_row = m.physical ? m.table + (int64_t)(mapped ? req : 0) * m.table_row_stride : nullptr;
   const int tid = threadIdx.x;
-  const int lp = (tid < kTailSlots && tid < m.ratio - 1) ? token_page(m, tail_start_of(pos, m.ratio) + tid)
+  const int lp = (tid < kTailSlots && tid < m.ratio - 1) ? token_page(m, tail_start_of(m, pos) + tid)
                                                           : -1;
   f.tail_ok = f.r.table_row && lp >= 0;
   f.tail_pp = *(f.tail_ok ? f.r.table_row + lp : reinterpret_cast<const int32_t*>(g_qsa_zero_rows));

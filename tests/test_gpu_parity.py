@@ -132,6 +132,15 @@ def test_topk_expand_bit_exact(ratio, page, physical, cols, k):
     assert torch.equal(out.cpu(), want)
     assert torch.equal(counts.cpu(), want_counts)
     assert (big[:, 1::2] == -9).all()
+    # A contiguous output view starting 4 bytes past a 16-byte boundary, with
+    # nothing written outside it.
+    flat = torch.full((rows * width + 2,), -9, dtype=torch.int32, device=DEV)
+    out_c = flat[1:1 + rows * width].view(rows, width)
+    topk_expand(scores.to(DEV), vis.to(DEV), pos.to(DEV), seq.to(DEV), t2r.to(DEV), out_c, ratio,
+                main_block_table=table.to(DEV) if physical else None, main_page_size=page)
+    torch.cuda.synchronize()
+    assert torch.equal(out_c.cpu(), want)
+    assert flat[0].item() == -9 and flat[-1].item() == -9
 
 
 def _score_tol(q, keys, dim):
