@@ -471,9 +471,9 @@ __device__ __forceinline__ void select_long(int length, int topk, const uint32_t
         cp[j] = ok ? cpos[e] : 0;
         ccand |= (uint32_t)ok << j;
       }
-      // Every wave has its candidates in registers before any selection is
-      // written (sel may share the scratch words).
-      lds_barrier();
+      // sel may share the scratch words: radix_rank writes it only after the
+      // barrier of its rank scan, which every wave reaches with its
+      // candidates already in registers, so no barrier is needed here.
       radix_rank<THREADS, kCompact, PAGES>(topk, lo, hi, ccand, ck, ci, cp, page, m, sh, sel);
       return;
     }
