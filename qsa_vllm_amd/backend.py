@@ -175,7 +175,10 @@ class YuLanQSAImpl:
         num_tokens = attn_metadata.num_actual_tokens
         key_cache, value_cache = layer.main_kv_views()
         decode = attn_metadata.max_query_len == 1
-        output.zero_()
+        # The reference zero-fills the whole output first. The attention
+        # writes every element of output[:num_tokens] (a row without a valid
+        # slot gets zeros), so only the padded rows past it need the fill.
+        output[num_tokens:].zero_()
         qsa_sparse_paged_attention(
             query[:num_tokens], key_cache, value_cache,
             layer.topk_indices_buffer[:num_tokens], attn_metadata.block_table,
