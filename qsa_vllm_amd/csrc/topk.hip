@@ -108,10 +108,18 @@ constexpr int kAdaptiveThreads = 1024;
 constexpr int kAdaptiveHalf = kAdaptiveThreads * 16;
 constexpr int kAdaptiveMaxColumns = 2 * kAdaptiveHalf;
 
+// Rows of up to this many threads x 4 keys (2048) run on the lower waves
+// alone, in the 512 x 4 shape of the direct kernel for 2048 columns.
+constexpr int kAdaptiveNarrow = 512;
+
 template <bool EXPAND, bool PAGES>
 __global__ __launch_bounds__(kAdaptiveThreads) void topk_adaptive_kernel(const TopkArgs a) {
   constexpr int T = kAdaptiveThreads;
-  __shared__ TopkShared<T> sh;
+  __shared__ union {
+    TopkShared<T> full;
+    TopkShared<kAdaptiveNarrow> narrow;
+  } shu;
+  auto& sh = shu.full;
   __shared__ __attribute__((aligned(16))) uint32_t stage_mem[T * 16 * 2];
   const int row = blockIdx.x;
   const int length = a.lengths[row];
@@ -129,9 +137,21 @@ __global__ __launch_bounds__(kAdaptiveThreads) void topk_adaptive_kernel(const T
   if (n <= kAdaptiveHalf) {
     const DirectLoader load{srow, 0};
     // Keys, and room for the selection. Rows of up to 4096 keys take four
-    // per thread (a row of 2048 keys fills the lower half of the threads),
-    // so the candidates the bound leaves are compacted to one per thread.
+    // per thread, so the candidates the bound leaves are compacted to one per
+    // thread.
     const int need = max(n, 2 * topk);
+    if (need <= kAdaptiveNarrow * 4) {
+      // The upper waves end here. A barrier waits only for the waves of the
+      // workgroup that have not ended, so the lower half runs the 512-thread
+      // row with its own barriers; fewer waves per barrier and per block scan
+      // make each phase of a short row cheaper.
+      if (threadIdx.x >= kAdaptiveNarrow) return;
+      auto& st = *reinterpret_cast<TopkStage<kAdaptiveNarrow, 4, PAGES>*>(stage_mem);
+      process_row<kAdaptiveNarrow, 4, EXPAND, PAGES>(load, n, length, a.cols, topk, a.meta, row,
+                                                     out, shu.narrow, st,
+                                                     reinterpret_cast<int*>(st.key));
+      return;
+    }
     if (need <= T * 4) QSA_ADAPTIVE_ROW(4, load, n, length, a.cols)
     else if (need <= T * 8) QSA_ADAPTIVE_ROW(8, load, n, length, a.cols)
     else QSA_ADAPTIVE_ROW(16, load, n, length, a.cols)
@@ -289,7 +309,8 @@ __global__ __launch_bounds__(kExpandThreads) void expand_blocks_kernel(const Exp
   }
   if (tid < kTailSlots && tid < a.meta.ratio - 1) tail_page[tid] = f.tail_ok ? f.tail_pp : -1;
   lds_barrier();
-  write_expanded(a.meta, f.r, row, a.topk, sel, tail_page, a.out + (int64_t)row * a.out_row_stride);
+  write_expanded(a.meta, f.r, row, a.topk, sel, tail_page, a.out + (int64_t)row * a.out_row_stride,
+                 kExpandThreads);
 }
 
 int check_common(const float* scores, int rows, int cols, const int32_t* lengths,

@@ -496,7 +496,7 @@ __device__ __forceinline__ void select_long(int length, int topk, const uint32_t
 // anywhere in the loop would make every iteration wait for all earlier stores.
 __device__ __forceinline__ void write_expanded(const ExpandMeta& m, const RowMeta& r, int row,
                                                int topk, const int* sel, const int* tail_page,
-                                               int32_t* out) {
+                                               int32_t* out, int threads) {
   const int p1 = r.pos + 1;
   const int complete = max(0, min(min(div_ratio(m, p1), div_ratio(m, r.seq_len)), topk));
   const int tail_start = tail_start_of(m, r.pos);
@@ -506,7 +506,7 @@ __device__ __forceinline__ void write_expanded(const ExpandMeta& m, const RowMet
   const bool from_lds = !m.physical || (block_in_page && m.ratio - 1 <= kTailSlots);
   const int64_t cs = m.out_col_stride;
   if (from_lds) {
-    for (int c = threadIdx.x; c < m.out_width; c += blockDim.x) {
+    for (int c = threadIdx.x; c < m.out_width; c += threads) {
       int v = -1;
       if (c < expanded) {
         const int rank = m.ratio_div.div(c);
@@ -529,7 +529,7 @@ __device__ __forceinline__ void write_expanded(const ExpandMeta& m, const RowMet
       out[(int64_t)c * cs] = v;
     }
   } else {
-    for (int c = threadIdx.x; c < m.out_width; c += blockDim.x) {
+    for (int c = threadIdx.x; c < m.out_width; c += threads) {
       int v = -1;
       if (c < expanded) {
         const int rank = m.ratio_div.div(c);
@@ -705,7 +705,7 @@ __device__ __forceinline__ void finish_row(const Loader& load, const uint32_t (&
   if (EXPAND && tid < kTailSlots && tid < m.ratio - 1) sh.tail_page[tid] = f.tail_ok ? f.tail_pp : -1;
   lds_barrier();
   if (EXPAND) {
-    write_expanded(m, f.r, row, topk, sel, sh.tail_page, out);
+    write_expanded(m, f.r, row, topk, sel, sh.tail_page, out, THREADS);
   } else {
     for (int c = tid; c < topk; c += THREADS) out[c] = sel[c];
   }
