@@ -841,7 +841,12 @@ void sparse_attn_kernel(const AttnParams p) {
 
 // LSE merge of split partials (ops/qsa.py:306-362). One thread per (row, head,
 // 4 dims); a thread issues the loads of up to kMergeChunk splits at once so a
-// merge costs one memory round trip per chunk.
+// merge costs one memory round trip per chunk. The grid is (rows, parts of a
+// row): workgroups are dispatched round-robin over the XCDs in linear order,
+// so with a row count that is a multiple of 8 every workgroup of row r runs on
+// XCD r mod 8, the XCD whose attention workgroups (grid (rows, splits, head
+// groups)) wrote that row's partials, and the partials are read from that
+// XCD's L2 instead of from another's write-back.
 __global__ __launch_bounds__(256) void merge_kernel(const float* __restrict__ part_out,
                                                     const float* __restrict__ part_lse,
                                                     int num_splits, int rows, int num_q_heads,
@@ -849,12 +854,12 @@ __global__ __launch_bounds__(256) void merge_kernel(const float* __restrict__ pa
                                                     int64_t out_head, const uint16_t* gate,
                                                     int64_t g_row, int64_t g_head, int64_t g_dim) {
   const int chunks = head_dim / 4;
-  const int64_t item = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (item >= (int64_t)rows * num_q_heads * chunks) return;
-  const int d0 = (int)(item % chunks) * 4;
-  const int64_t rh = item / chunks;  // row * num_q_heads + head
-  const int row = (int)(rh / num_q_heads);
-  const int head = (int)(rh % num_q_heads);
+  const int item = (int)blockIdx.y * (int)blockDim.x + (int)threadIdx.x;  // within the row
+  if (item >= num_q_heads * chunks) return;
+  const int row = blockIdx.x;
+  const int head = item / chunks;
+  const int d0 = (item % chunks) * 4;
+  const int64_t rh = (int64_t)row * num_q_heads + head;
   const int64_t split_stride = (int64_t)rows * num_q_heads;
   float lmax = -INFINITY, den = 0.0f;
   float acc[4] = {0.f, 0.f, 0.f, 0.f};
@@ -1015,8 +1020,9 @@ int launch_merge(const float* part_out, const float* part_lse, int num_splits, i
                  int num_q_heads, int head_dim, uint16_t* out, int64_t out_row, int64_t out_head,
                  const uint16_t* gate, int64_t g_row, int64_t g_head, int64_t g_dim,
                  hipStream_t s) {
-  const int64_t items = (int64_t)rows * num_q_heads * (head_dim / 4);
-  const dim3 grid((unsigned)((items + 255) / 256));
+  const int64_t parts = ((int64_t)num_q_heads * (head_dim / 4) + 255) / 256;
+  if (parts > 65535) return fail(QSA_ERR_UNSUPPORTED, "qsa_sparse_attention merge: too many heads");
+  const dim3 grid((unsigned)rows, (unsigned)parts);
   hipLaunchKernelGGL(merge_kernel, grid, dim3(256), 0, s, part_out, part_lse, num_splits, rows,
                      num_q_heads, head_dim, out, out_row, out_head, gate, g_row, g_head, g_dim);
   return check_launch("qsa_sparse_attention merge launch");
