@@ -397,11 +397,16 @@ int qsa_gdn_conv_state(const void* qkvz, int64_t qkvz_stride, int tokens, void* 
 /* Gated delta rule over each sequence's tokens in order, the state [slots,
  * value_heads, 128, 128] fp32 updated in place: S <- e^g S,
  * u = beta (v - S^T k), S <- S + k u^T, o = S^T q; o [tokens, value_heads, 128]
- * bf16. Value head h reads key head h / (value_heads / key_heads). */
+ * bf16. Value head h reads key head h / (value_heads / key_heads).
+ * max_seq_tokens: the longest sequence's token count if the caller knows it,
+ * else -1. Below 16 (a decode batch) the chunked kernel for sequences of 16+
+ * tokens is not launched and the per-token kernel takes every sequence, so a
+ * bound that is too small still gives the same result, only slower. */
 int qsa_gdn_recurrence(const float* q, const float* k, const void* v, const float* g,
                        const float* beta, int tokens, float* state, int num_slots,
                        const int32_t* query_start_loc, const int64_t* slots, int num_seqs,
-                       int key_heads, int value_heads, int head_dim, void* o, void* stream);
+                       int key_heads, int value_heads, int head_dim, int max_seq_tokens, void* o,
+                       void* stream);
 
 /* Gated RMSNorm of the GDN output: y = bf16(rmsnorm(o) * weight * silu(z)) per
  * (token, value head), z read from the qkvz projection rows. */

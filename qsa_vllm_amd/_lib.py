@@ -18,7 +18,7 @@ _lib = None
 QSA_OK = 0
 QSA_ERR_WORKSPACE = -4
 SPARSE_ATTENTION_SCRATCH_BYTES = 32 << 20  # QSA_SPARSE_ATTENTION_SCRATCH_BYTES
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 c_i32 = ctypes.c_int
 c_i64 = ctypes.c_int64
@@ -155,7 +155,8 @@ SIGNATURES = {
     "qsa_gdn_conv_state": (c_i32, [c_ptr, c_i64, c_i32, c_ptr, c_i32, c_ptr, c_ptr, c_i32,
                                    c_i32, c_i32, c_i32, c_i32, c_ptr]),
     "qsa_gdn_recurrence": (c_i32, [c_ptr, c_ptr, c_ptr, c_ptr, c_ptr, c_i32, c_ptr, c_i32,
-                                   c_ptr, c_ptr, c_i32, c_i32, c_i32, c_i32, c_ptr, c_ptr]),
+                                   c_ptr, c_ptr, c_i32, c_i32, c_i32, c_i32, c_i32, c_ptr,
+                                   c_ptr]),
     "qsa_gdn_gated_norm": (c_i32, [c_ptr, c_ptr, c_i64, c_ptr, ctypes.c_float, c_i32, c_i32,
                                    c_i32, c_i32, c_ptr, c_ptr]),
 }

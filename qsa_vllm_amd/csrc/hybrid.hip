@@ -552,6 +552,7 @@ struct GdnRecurArgs {
   const int64_t* slots;
   int num_seqs, key_heads, value_heads, num_slots, tokens;
   uint16_t* o;  // [tokens, value_heads, 128]
+  int chunk_min;  // sequences this long go to gdn_chunk_kernel, shorter ones to the per-token kernel
 };
 
 __global__ __launch_bounds__(256) void gdn_recurrence_kernel(const GdnRecurArgs a) {
@@ -566,7 +567,7 @@ __global__ __launch_bounds__(256) void gdn_recurrence_kernel(const GdnRecurArgs 
   const int j = 32 * wave + (lane & 31);
   const int half = lane >> 5;
   const int start = a.seq_start[seq], len = a.seq_start[seq + 1] - start;
-  if (len <= 0 || len >= kChunkMin || start < 0 || start + len > a.tokens) return;
+  if (len <= 0 || len >= a.chunk_min || start < 0 || start + len > a.tokens) return;
   const int64_t slot = a.slots[seq];
   const bool slot_ok = slot >= 0 && slot < a.num_slots;
   float* sp = a.state + ((slot_ok ? slot : 0) * a.value_heads + h) * (int64_t)(kHeadDim * kHeadDim) +
@@ -705,7 +706,7 @@ __global__ __launch_bounds__(256) void gdn_chunk_kernel(const GdnRecurArgs a) {
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const int m = lane & 15, g = lane >> 4;
   const int start = a.seq_start[seq], len = a.seq_start[seq + 1] - start;
-  if (len < kChunkMin || start < 0 || start + len > a.tokens) return;
+  if (len < a.chunk_min || start < 0 || start + len > a.tokens) return;
   const int64_t slot = a.slots[seq];
   const bool slot_ok = slot >= 0 && slot < a.num_slots;
   float* state = a.state + ((slot_ok ? slot : 0) * a.value_heads + h) * (int64_t)(kHeadDim * kHeadDim);
@@ -1128,8 +1129,8 @@ extern "C" int qsa_gdn_conv_state(const void* qkvz, int64_t qkvz_stride, int tok
 extern "C" int qsa_gdn_recurrence(const float* q, const float* k, const void* v, const float* g,
                                   const float* beta, int tokens, float* state, int num_slots,
                                   const int* query_start_loc, const int64_t* slots, int num_seqs,
-                                  int key_heads, int value_heads, int head_dim, void* o,
-                                  void* stream) {
+                                  int key_heads, int value_heads, int head_dim,
+                                  int max_seq_tokens, void* o, void* stream) {
   GdnShape s;
   if (!gdn_shape(key_heads, value_heads, head_dim, 4, &s, "qsa_gdn_recurrence")) return QSA_ERR_UNSUPPORTED;
   if (num_seqs < 0 || tokens < 0) return fail(QSA_ERR_INVALID, "qsa_gdn_recurrence: negative size");
@@ -1140,13 +1141,20 @@ extern "C" int qsa_gdn_recurrence(const float* q, const float* k, const void* v,
     return fail(QSA_ERR_INVALID, "qsa_gdn_recurrence: tensors must be 16-byte aligned");
   if ((int64_t)num_seqs * value_heads > 0x7fffffffLL)
     return fail(QSA_ERR_UNSUPPORTED, "qsa_gdn_recurrence: too many (sequence, head) pairs");
+  // With no sequence of kChunkMin tokens (a decode batch, as the caller
+  // states), the chunked kernel is not launched and the per-token kernel
+  // takes every sequence, whatever its length: a wrong bound costs time only.
+  const bool chunks = max_seq_tokens < 0 || max_seq_tokens >= kChunkMin;
   GdnRecurArgs a{q, k, static_cast<const uint16_t*>(v), g, beta, state, query_start_loc, slots,
-                 num_seqs, key_heads, value_heads, num_slots, tokens, static_cast<uint16_t*>(o)};
-  // Long sequences (chunks) first on the stream: their workgroups are the long ones.
-  hipLaunchKernelGGL(gdn_chunk_kernel, dim3(num_seqs * value_heads), dim3(256), sizeof(ChunkLds),
-                     static_cast<hipStream_t>(stream), a);
-  const int st = check_launch("qsa_gdn_recurrence (chunks)");
-  if (st != QSA_OK) return st;
+                 num_seqs, key_heads, value_heads, num_slots, tokens, static_cast<uint16_t*>(o),
+                 chunks ? kChunkMin : 0x7fffffff};
+  if (chunks) {
+    // Long sequences (chunks) first on the stream: their workgroups are the long ones.
+    hipLaunchKernelGGL(gdn_chunk_kernel, dim3(num_seqs * value_heads), dim3(256), sizeof(ChunkLds),
+                       static_cast<hipStream_t>(stream), a);
+    const int st = check_launch("qsa_gdn_recurrence (chunks)");
+    if (st != QSA_OK) return st;
+  }
   hipLaunchKernelGGL(gdn_recurrence_kernel, dim3(num_seqs * value_heads), dim3(256), 0,
                      static_cast<hipStream_t>(stream), a);
   return check_launch("qsa_gdn_recurrence");

@@ -257,7 +257,8 @@ class GatedDeltaNet:
         gdn_conv_state(qkvz, self.conv_state, batch.query_start_loc, batch.state_slots, self.hk,
                        self.hv)
         o = gdn_recurrence(q, k, v, g, beta, self.ssm_state, batch.query_start_loc,
-                           batch.state_slots, self.hk, self.hv)
+                           batch.state_slots, self.hk, self.hv,
+                           max_query_len=batch.qsa.main.max_query_len)
         y = gdn_gated_norm(o, qkvz, self.norm_weight, self.eps, self.hk, self.hv)
         return F.linear(y.view(t, -1), self.out_proj)
 

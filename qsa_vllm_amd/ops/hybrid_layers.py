@@ -137,9 +137,12 @@ def gdn_conv_state(qkvz, conv_state, query_start_loc, slots, key_heads, value_he
                   query_start_loc.numel() - 1, key_heads, value_heads, HEAD_DIM, K, _stream(dev))
 
 
-def gdn_recurrence(q, k, v, g, beta, state, query_start_loc, slots, key_heads, value_heads):
+def gdn_recurrence(q, k, v, g, beta, state, query_start_loc, slots, key_heads, value_heads,
+                   max_query_len=None):
     """The gated delta rule over each sequence (state updated in place).
-    Returns o [T, Hv, 128] bf16."""
+    Returns o [T, Hv, 128] bf16. ``max_query_len``: the longest sequence's
+    token count when the caller knows it (a decode batch: 1); below 16 the
+    chunked kernel is not launched."""
     dev = _on_gpu(q, k, v, g, beta, state, query_start_loc, slots)
     tokens = q.size(0)
     for t, name in ((q, "q"), (k, "k")):
@@ -162,8 +165,8 @@ def gdn_recurrence(q, k, v, g, beta, state, query_start_loc, slots, key_heads, v
     with torch.cuda.device(dev):
         _lib.call("qsa_gdn_recurrence", _ptr(q), _ptr(k), _ptr(v), _ptr(g), _ptr(beta), tokens,
                   _ptr(state), state.size(0), _ptr(query_start_loc), _ptr(slots),
-                  query_start_loc.numel() - 1, key_heads, value_heads, HEAD_DIM, _ptr(o),
-                  _stream(dev))
+                  query_start_loc.numel() - 1, key_heads, value_heads, HEAD_DIM,
+                  -1 if max_query_len is None else int(max_query_len), _ptr(o), _stream(dev))
     return o
 
 

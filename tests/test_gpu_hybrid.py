@@ -370,6 +370,37 @@ def test_gdn_sequence_without_slot_has_no_state():
     _close(got.cpu(), want, "gdn without state")
 
 
+@pytest.mark.parametrize("bound", [None, 1])
+def test_gdn_recurrence_length_bound(bound):
+    """Sequences of 16+ tokens run on the chunked kernel, unless the caller
+    bounds every sequence below 16 tokens (a decode batch): then the per-token
+    kernel takes them all. Either way each sequence's output and state follow
+    the oracle's per-token rule, so a bound that is too small costs time only."""
+    gen = torch.Generator().manual_seed(41)
+    hk, hv, lens = 2, 4, [3, 40, 1, 17]
+    tokens = sum(lens)
+    q = torch.nn.functional.normalize(torch.randn(tokens, hk, 128, generator=gen), dim=-1) / 128 ** 0.5
+    k = torch.nn.functional.normalize(torch.randn(tokens, hk, 128, generator=gen), dim=-1)
+    v = torch.randn(tokens, hv, 128, generator=gen).to(torch.bfloat16)
+    g = -0.5 * torch.rand(tokens, hv, generator=gen)
+    beta = torch.rand(tokens, hv, generator=gen)
+    state0 = 0.05 * torch.randn(4, hv, 128, 128, generator=gen)
+    qsl = torch.tensor([0] + np.cumsum(lens).tolist(), dtype=torch.int32)
+    slots = torch.tensor([2, 0, 3, 1], dtype=torch.int64)
+    state = state0.to(DEV)
+    print(f"[hybrid] gdn recurrence, bound {bound}", flush=True)
+    o = L.gdn_recurrence(q.to(DEV), k.to(DEV), v.to(DEV), g.to(DEV), beta.to(DEV), state,
+                         qsl.to(DEV), slots.to(DEV), hk, hv, max_query_len=bound)
+    torch.cuda.synchronize()
+    kh = torch.arange(hv) // (hv // hk)  # value head h reads key head h / (hv / hk)
+    for i, n in enumerate(lens):
+        rows, slot = slice(int(qsl[i]), int(qsl[i]) + n), int(slots[i])
+        want_o, want_s = H.gated_delta_rule(q[rows][:, kh], k[rows][:, kh], v[rows].float(),
+                                            g[rows], beta[rows], state0[slot])
+        _close(o[rows].cpu(), want_o, f"gdn recurrence output, sequence of {n}")
+        _close(state[slot].cpu(), want_s, f"gdn recurrence state, sequence of {n}", 1e-2, 1e-3)
+
+
 def test_decode_graph_replay_equals_eager():
     """The whole model's uniform decode step from a HIP graph equals eager, for
     a batch other than the captured one (new tokens and positions)."""
