@@ -664,7 +664,7 @@ __global__ __launch_bounds__(256) void gdn_recurrence_kernel(const GdnRecurArgs 
 // same row order. Products run in bf16 with fp32 accumulation (the precision
 // of the reference's chunk kernels); the state, gates and the triangular
 // solve are fp32: 16-row blocks, each taking the earlier blocks' contribution
-// as fp32 MFMA work and solving its diagonal block per value column.
+// and the inverse of its diagonal block as fp32 MFMA work.
 // ---------------------------------------------------------------------------
 constexpr int kChunk = 64;
 
@@ -677,6 +677,7 @@ struct ChunkLds {
   uint16_t ut[kHeadDim][72];      // bf16 U^T
   float a[kChunk][68];            // fp32 A (strict lower)
   float r[kChunk][132];           // fp32 right-hand side of the solve
+  float tinv[4][16][17];          // fp32 inverses of the diagonal 16x16 blocks of I + A
   float G[kChunk], gam[kChunk], beta[kChunk];
 };
 
@@ -721,40 +722,56 @@ __global__ __launch_bounds__(256) void gdn_chunk_kernel(const GdnRecurArgs a) {
       for (int i = 0; i < 4; ++i)
         S[rt][nl][i] = slot_ok ? state[(16 * rt + 4 * g + i) * kHeadDim + 32 * w + 16 * nl + m] : 0.0f;
 
+  // Inputs of a chunk: this thread's slice of row tid / 4 (dims 32 (tid % 4)
+  // .. + 31) and the gates of row `lane`. The next chunk's are loaded as soon
+  // as the current ones are staged, so they arrive during this chunk's work.
+  // Loads are unconditional (rows past the sequence read its last token and
+  // are zeroed when staged), so every wait count is static.
+  const int row = tid >> 2, d0 = 32 * (tid & 3);
+  f32x4 pq[8], pk[8];
+  u32x4 pv[4];
+  float pg, pb;
+  auto load_chunk = [&](int c) {
+    const int64_t t = start + min(c + row, len - 1);
+    const float* qp = a.q + (t * a.key_heads + mk) * kHeadDim + d0;
+    const float* kp = a.k + (t * a.key_heads + mk) * kHeadDim + d0;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      pq[e] = *reinterpret_cast<const f32x4*>(qp + 4 * e);
+      pk[e] = *reinterpret_cast<const f32x4*>(kp + 4 * e);
+    }
+    const uint16_t* vp = a.v + (t * a.value_heads + h) * kHeadDim + d0;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) pv[e] = load_u32x4(vp + 8 * e);
+    const int64_t tg = start + min(c + lane, len - 1);
+    pg = a.g[tg * a.value_heads + h];
+    pb = a.beta[tg * a.value_heads + h];
+  };
+  load_chunk(0);
+
   for (int c0 = 0; c0 < len; c0 += kChunk) {
     const int nc = min(kChunk, len - c0);
-    // 1. Stage the chunk: thread -> (row tid / 4, dims 32 (tid % 4) .. + 31).
-    const int row = tid >> 2, d0 = 32 * (tid & 3);
+    // 1. Stage the chunk from the registers loaded one chunk earlier.
     const bool live = row < nc;
-    const int64_t t = start + c0 + row;
     float kf[32];
-    {
-      const float* qp = a.q + (t * a.key_heads + mk) * kHeadDim + d0;
-      const float* kp = a.k + (t * a.key_heads + mk) * kHeadDim + d0;
 #pragma unroll
-      for (int e = 0; e < 32; e += 4) {
-        f32x4 qv = {0.f, 0.f, 0.f, 0.f}, kv = {0.f, 0.f, 0.f, 0.f};
-        if (live) {
-          qv = *reinterpret_cast<const f32x4*>(qp + e);
-          kv = *reinterpret_cast<const f32x4*>(kp + e);
-        }
-        *reinterpret_cast<u32x2*>(&L.q[row][d0 + e]) = u32x2{pack_bf16x2(qv[0], qv[1]), pack_bf16x2(qv[2], qv[3])};
-        *reinterpret_cast<u32x2*>(&L.k[row][d0 + e]) = u32x2{pack_bf16x2(kv[0], kv[1]), pack_bf16x2(kv[2], kv[3])};
+    for (int e = 0; e < 8; ++e) {
+      const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
+      const f32x4 qv = live ? pq[e] : zero, kv = live ? pk[e] : zero;
+      *reinterpret_cast<u32x2*>(&L.q[row][d0 + 4 * e]) = u32x2{pack_bf16x2(qv[0], qv[1]), pack_bf16x2(qv[2], qv[3])};
+      *reinterpret_cast<u32x2*>(&L.k[row][d0 + 4 * e]) = u32x2{pack_bf16x2(kv[0], kv[1]), pack_bf16x2(kv[2], kv[3])};
 #pragma unroll
-        for (int j = 0; j < 4; ++j) kf[e + j] = rbf(kv[j]);
-      }
-      const uint16_t* vp = a.v + (t * a.value_heads + h) * kHeadDim + d0;
-#pragma unroll
-      for (int e = 0; e < 32; e += 8) {
-        u32x4 vv = {0, 0, 0, 0};
-        if (live) vv = load_u32x4(vp + e);
-        *reinterpret_cast<u32x4*>(&L.v[row][d0 + e]) = vv;
-      }
+      for (int j = 0; j < 4; ++j) kf[4 * e + j] = rbf(kv[j]);
     }
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const u32x4 zero = {0, 0, 0, 0};
+      *reinterpret_cast<u32x4*>(&L.v[row][d0 + 8 * e]) = live ? pv[e] : zero;
+    }
+    float gv = lane < nc ? pg : 0.0f;
+    const float bv = lane < nc ? pb : 0.0f;
+    load_chunk(c0 + kChunk);  // past the end: the last token again, never used
     if (w == 0) {  // gates of row `lane`, inclusive prefix sum of g
-      const bool ok = lane < nc;
-      float gv = ok ? a.g[(start + c0 + lane) * (int64_t)a.value_heads + h] : 0.0f;
-      const float bv = ok ? a.beta[(start + c0 + lane) * (int64_t)a.value_heads + h] : 0.0f;
 #pragma unroll
       for (int d = 1; d < 64; d <<= 1) {
         const float o = __shfl_up(gv, d, 64);
@@ -836,49 +853,74 @@ __global__ __launch_bounds__(256) void gdn_chunk_kernel(const GdnRecurArgs a) {
           L.r[tr][col] = L.beta[tr] * (vv - L.gam[tr] * KS[ct][nl][i]);
         }
     __syncthreads();
-    // 5. Forward substitution (I + A) U = R in 16-row blocks. Block b first
-    // takes the earlier blocks' contribution, A[b rows][0 : 16 b] U[0 : 16 b]
-    // (v_mfma_f32_16x16x4f32, fp32 products: lane (m, kk) holds A[m][kk] and
-    // B[kk][m] of each 4-deep slice), then solves its 16x16 diagonal block
-    // per value column in registers. U overwrites R (fp32) and goes to U^T
-    // (bf16) for the products below.
+    // 5. Solve (I + A) U = R in 16-row blocks. Wave b first inverts the unit
+    // lower-triangular diagonal block b of I + A (lane j < 16 solves for column
+    // j by forward substitution). Then each wave solves its own 32 value
+    // columns alone, with no barrier: block b takes the earlier blocks'
+    // contribution, R_b - A[b][0 : 16 b] U[0 : 16 b], and multiplies it by the
+    // inverse of its diagonal block, both as fp32 MFMA work
+    // (v_mfma_f32_16x16x4f32: lane (m, kk) holds A[m][kk] and B[kk][m] of each
+    // 4-deep slice). The wave reads back through LDS only what it wrote
+    // itself, in issue order. U overwrites R (fp32) and goes to U^T (bf16) for
+    // the products below, which read this wave's columns only.
+    if (lane < 16) {
+      const int j = lane;
+      float x[16];
 #pragma unroll
-    for (int blk = 0; blk < 4; ++blk) {
-      if (blk > 0) {
-        const int kk = lane >> 4;
-        f32x4 acc[2] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
+      for (int i = 0; i < 16; ++i) {
+        const float* arow = &L.a[16 * w + i][16 * w];
+        float p0 = i == j ? 1.0f : 0.0f, p1 = 0.0f;
+#pragma unroll
+        for (int s2 = 0; s2 < i; ++s2) {
+          if (s2 & 1) p1 -= arow[s2] * x[s2];
+          else p0 -= arow[s2] * x[s2];
+        }
+        x[i] = p0 + p1;
+        L.tinv[w][i][j] = x[i];
+      }
+    }
+    __syncthreads();
+    {
+      const int kk = lane >> 4;
+#pragma unroll
+      for (int blk = 0; blk < 4; ++blk) {
+        f32x4 acc[2];
+#pragma unroll
+        for (int nl = 0; nl < 2; ++nl)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) acc[nl][i] = L.r[16 * blk + 4 * g + i][32 * w + 16 * nl + m];
 #pragma unroll
         for (int ks = 0; ks < 4 * blk; ++ks) {
-          const float av = L.a[16 * blk + m][4 * ks + kk];
+          const float av = -L.a[16 * blk + m][4 * ks + kk];
 #pragma unroll
           for (int nl = 0; nl < 2; ++nl)
             acc[nl] = __builtin_amdgcn_mfma_f32_16x16x4f32(
                 av, L.r[4 * ks + kk][32 * w + 16 * nl + m], acc[nl], 0, 0, 0);
         }
+        if (blk > 0) {
+#pragma unroll
+          for (int nl = 0; nl < 2; ++nl)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) L.r[16 * blk + 4 * g + i][32 * w + 16 * nl + m] = acc[nl][i];
+        }
+        f32x4 u[2] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
+#pragma unroll
+        for (int ks = 0; ks < 4; ++ks) {
+          const float tv = L.tinv[blk][m][4 * ks + kk];
+#pragma unroll
+          for (int nl = 0; nl < 2; ++nl)
+            u[nl] = __builtin_amdgcn_mfma_f32_16x16x4f32(
+                tv, L.r[16 * blk + 4 * ks + kk][32 * w + 16 * nl + m], u[nl], 0, 0, 0);
+        }
 #pragma unroll
         for (int nl = 0; nl < 2; ++nl)
 #pragma unroll
-          for (int i = 0; i < 4; ++i) L.r[16 * blk + 4 * g + i][32 * w + 16 * nl + m] -= acc[nl][i];
-        __syncthreads();
-      }
-      if (tid < kHeadDim) {
-        const int j = tid;
-        float u[16];
-#pragma unroll
-        for (int i = 0; i < 16; ++i) {
-          const float* arow = &L.a[16 * blk + i][16 * blk];
-          float p0 = 0.0f, p1 = 0.0f;
-#pragma unroll
-          for (int s2 = 0; s2 < i; ++s2) {
-            if (s2 & 1) p1 += arow[s2] * u[s2];
-            else p0 += arow[s2] * u[s2];
+          for (int i = 0; i < 4; ++i) {
+            const int tr = 16 * blk + 4 * g + i, col = 32 * w + 16 * nl + m;
+            L.r[tr][col] = u[nl][i];
+            L.ut[col][tr] = bf16_bits(u[nl][i]);
           }
-          u[i] = L.r[16 * blk + i][j] - (p0 + p1);
-          L.r[16 * blk + i][j] = u[i];
-          L.ut[j][16 * blk + i] = bf16_bits(u[i]);
-        }
       }
-      __syncthreads();
     }
     // 6. O = gamma (Q S) + P U.
 #pragma unroll
