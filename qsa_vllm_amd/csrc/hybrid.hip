@@ -841,28 +841,9 @@ __global__ __launch_bounds__(256) void gdn_chunk_kernel(const GdnRecurArgs a) {
         L.p[tr][sc] = bf16_bits(e * qk[i]);
       }
     }
-    // 4. Right-hand side beta (V - gamma K S).
-#pragma unroll
-    for (int ct = 0; ct < 4; ++ct)
-#pragma unroll
-      for (int nl = 0; nl < 2; ++nl)
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const int tr = 16 * ct + 4 * g + i, col = 32 * w + 16 * nl + m;
-          const float vv = __builtin_bit_cast(float, (uint32_t)L.v[tr][col] << 16);
-          L.r[tr][col] = L.beta[tr] * (vv - L.gam[tr] * KS[ct][nl][i]);
-        }
-    __syncthreads();
-    // 5. Solve (I + A) U = R in 16-row blocks. Wave b first inverts the unit
-    // lower-triangular diagonal block b of I + A (lane j < 16 solves for column
-    // j by forward substitution). Then each wave solves its own 32 value
-    // columns alone, with no barrier: block b takes the earlier blocks'
-    // contribution, R_b - A[b][0 : 16 b] U[0 : 16 b], and multiplies it by the
-    // inverse of its diagonal block, both as fp32 MFMA work
-    // (v_mfma_f32_16x16x4f32: lane (m, kk) holds A[m][kk] and B[kk][m] of each
-    // 4-deep slice). The wave reads back through LDS only what it wrote
-    // itself, in issue order. U overwrites R (fp32) and goes to U^T (bf16) for
-    // the products below, which read this wave's columns only.
+    // 3b. Wave w wrote rows 16 w .. 16 w + 15 of A above, so it inverts the
+    // unit lower-triangular diagonal block w of I + A without a barrier: lane
+    // j < 16 solves for column j by forward substitution.
     if (lane < 16) {
       const int j = lane;
       float x[16];
@@ -879,7 +860,26 @@ __global__ __launch_bounds__(256) void gdn_chunk_kernel(const GdnRecurArgs a) {
         L.tinv[w][i][j] = x[i];
       }
     }
+    // 4. Right-hand side beta (V - gamma K S).
+#pragma unroll
+    for (int ct = 0; ct < 4; ++ct)
+#pragma unroll
+      for (int nl = 0; nl < 2; ++nl)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int tr = 16 * ct + 4 * g + i, col = 32 * w + 16 * nl + m;
+          const float vv = __builtin_bit_cast(float, (uint32_t)L.v[tr][col] << 16);
+          L.r[tr][col] = L.beta[tr] * (vv - L.gam[tr] * KS[ct][nl][i]);
+        }
     __syncthreads();
+    // 5. Solve (I + A) U = R in 16-row blocks, each wave its own 32 value
+    // columns alone, with no barrier: block b takes the earlier blocks'
+    // contribution, R_b - A[b][0 : 16 b] U[0 : 16 b], and multiplies it by the
+    // inverse of its diagonal block, both as fp32 MFMA work
+    // (v_mfma_f32_16x16x4f32: lane (m, kk) holds A[m][kk] and B[kk][m] of each
+    // 4-deep slice). The wave reads back through LDS only what it wrote
+    // itself, in issue order. U overwrites R (fp32) and goes to U^T (bf16) for
+    // the products below, which read this wave's columns only.
     {
       const int kk = lane >> 4;
 #pragma unroll
