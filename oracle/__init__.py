@@ -3,8 +3,8 @@
 TEST INFRASTRUCTURE ONLY. This package restates the reference algorithm in
 eager PyTorch on the CPU so the HIP kernels can be checked against it. Only
 ``tests/``, ``__graft_entry__.smoke()`` and the ``cpu_baseline`` leg of
-``bench.py`` may import it, and there only as the checker or the timed CPU
-baseline. The product path (``qsa_vllm_amd``) never imports it and fails
+``bench.py`` may import it, and there only as the reference the results are
+compared with or as the timed CPU baseline. The product path (``qsa_vllm_amd``) never imports it and fails
 loudly when its HIP library is missing.
 """
 
