@@ -1,7 +1,7 @@
 """CPU restatement of the hybrid decoder's layers around the QSA path.
 
-TEST INFRASTRUCTURE ONLY: the checker for ``qsa_vllm_amd.hybrid`` and its
-layer kernels (``qsa_vllm_amd.ops.hybrid_layers``). Nothing under
+TEST INFRASTRUCTURE ONLY: the reference that ``qsa_vllm_amd.hybrid`` and its
+layer kernels (``qsa_vllm_amd.ops.hybrid_layers``) are tested against. Nothing under
 ``qsa_vllm_amd`` imports it.
 
 Follows ``model.py:60-98`` (gated norm), ``:180-225`` (decoder layer),

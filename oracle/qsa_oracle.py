@@ -1,6 +1,6 @@
 """Eager-PyTorch CPU restatement of the YuLan QSA sparse-attention path.
 
-TEST INFRASTRUCTURE ONLY: this module is the checker for the HIP kernels and
+TEST INFRASTRUCTURE ONLY: this module is what the HIP kernels are tested against and
 the timed CPU baseline. Nothing under ``qsa_vllm_amd`` imports it.
 
 Every function cites the reference lines it restates (paths relative to the

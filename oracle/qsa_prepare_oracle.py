@@ -1,7 +1,7 @@
 """CPU restatement of the indexer preparation (the producers of the path).
 
-TEST INFRASTRUCTURE ONLY: the checker for ``qsa_indexer_prepare`` and
-``qsa_indexer_norm_rope``. Nothing under ``qsa_vllm_amd`` imports it.
+TEST INFRASTRUCTURE ONLY: what ``qsa_indexer_prepare`` and
+``qsa_indexer_norm_rope`` are tested against. Nothing under ``qsa_vllm_amd`` imports it.
 
 Follows ops/normalization.py:17-83 and ops/prepare.py:16-225 of the reference
 plugin. Arithmetic, step by step as the reference rounds it (it compiles with
