@@ -23,7 +23,7 @@ extern "C" {
 
 #define QSA_OK 0
 #define QSA_ERR_INVALID (-1)     /* bad shape, stride, pointer or size */
-#define QSA_ERR_UNSUPPORTED (-2) /* valid input this build has no kernel for */
+#define QSA_ERR_UNSUPPORTED (-2) /* valid input this library has no kernel for */
 #define QSA_ERR_HIP (-3)         /* a HIP runtime call failed */
 #define QSA_ERR_WORKSPACE (-4)   /* workspace missing or too small */
 

@@ -3,7 +3,7 @@
 // `topk` and `topk_expand` keep the reference plugin's schemas verbatim
 // (ops/csrc/topk.cu:548-557 registers them the same way: C++ definitions
 // with CUDA-key implementations); the indexer preparation, scoring, sparse
-// attention and helper ops are this build's, in the same namespace.
+// attention and helper ops are this library's, in the same namespace.
 // `select_decode` / `select_prefill` run a whole selection (scoring into a
 // logits buffer, then top-k + expansion, in row spans under a memory cap),
 // which is what the Python entry points of ops/indexer.py call.
@@ -710,7 +710,7 @@ TORCH_LIBRARY_FRAGMENT(yulan_qsa_kernels, m) {
       "topk_expand(Tensor scores, Tensor lengths, Tensor positions, Tensor sequence_lengths, "
       "Tensor token_to_req, Tensor table, Tensor(a!) output, Tensor(b!) counts, int ratio, "
       "int page_size, bool physical, bool store_counts) -> ()");
-  // This build's ops.
+  // This library's own ops.
   m.def(
       "indexer_prepare(Tensor index_qk, Tensor positions, Tensor q_norm_weight, "
       "Tensor k_norm_weight, Tensor cos_sin, float eps, Tensor(a!) index_q_out, "

@@ -2,7 +2,7 @@
 
 The ops are defined and implemented in C++ (``csrc/torch_ops.cpp``), as the
 reference registers its own (ops/csrc/topk.cu:548-557): ``topk`` and
-``topk_expand`` with the reference schemas verbatim, plus this build's
+``topk_expand`` with the reference schemas verbatim, plus this library's
 indexer preparation, scoring, whole-selection, sparse attention and helper ops
 in the same namespace. Each validates dtypes, devices and layouts (a
 RuntimeError, like the reference's ``TORCH_CHECK`` / ``data_ptr<T>()``
