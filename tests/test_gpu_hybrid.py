@@ -377,16 +377,16 @@ def test_gdn_recurrence_length_bound(bound):
     kernel takes them all. Either way each sequence's output and state follow
     the oracle's per-token rule, so a bound that is too small costs time only."""
     gen = torch.Generator().manual_seed(41)
-    hk, hv, lens = 2, 4, [3, 40, 1, 17]
+    hk, hv, lens = 2, 4, [3, 40, 1, 17, 200]  # 200: three full 64-token chunks and a partial one
     tokens = sum(lens)
     q = torch.nn.functional.normalize(torch.randn(tokens, hk, 128, generator=gen), dim=-1) / 128 ** 0.5
     k = torch.nn.functional.normalize(torch.randn(tokens, hk, 128, generator=gen), dim=-1)
     v = torch.randn(tokens, hv, 128, generator=gen).to(torch.bfloat16)
     g = -0.5 * torch.rand(tokens, hv, generator=gen)
     beta = torch.rand(tokens, hv, generator=gen)
-    state0 = 0.05 * torch.randn(4, hv, 128, 128, generator=gen)
+    state0 = 0.05 * torch.randn(5, hv, 128, 128, generator=gen)
     qsl = torch.tensor([0] + np.cumsum(lens).tolist(), dtype=torch.int32)
-    slots = torch.tensor([2, 0, 3, 1], dtype=torch.int64)
+    slots = torch.tensor([2, 0, 3, 1, 4], dtype=torch.int64)
     state = state0.to(DEV)
     print(f"[hybrid] gdn recurrence, bound {bound}", flush=True)
     o = L.gdn_recurrence(q.to(DEV), k.to(DEV), v.to(DEV), g.to(DEV), beta.to(DEV), state,
