@@ -409,7 +409,8 @@ int qsa_gdn_recurrence(const float* q, const float* k, const void* v, const floa
                        void* stream);
 
 /* Gated RMSNorm of the GDN output: y = bf16(rmsnorm(o) * weight * silu(z)) per
- * (token, value head), z read from the qkvz projection rows. */
+ * (token, value head), z read from the qkvz projection rows. Tensors 16-byte
+ * aligned, qkvz_stride a multiple of 8 elements. */
 int qsa_gdn_gated_norm(const void* o, const void* qkvz, int64_t qkvz_stride, const void* weight,
                        float eps, int tokens, int key_heads, int value_heads, int head_dim,
                        void* y, void* stream);

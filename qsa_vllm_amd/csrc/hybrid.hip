@@ -987,27 +987,36 @@ struct GdnNormArgs {
   int tokens;
 };
 
-// One wave per (token, value head); lane covers dims 2 lane, 2 lane + 1.
+// Sixteen lanes per (token, value head), lane l covering dims 8 l .. 8 l + 7
+// (one 16-byte load of o, z and the weight each), four rows per wave.
 __global__ __launch_bounds__(256) void gdn_norm_kernel(const GdnNormArgs a) {
-  const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
-  const int lane = threadIdx.x & 63;
+  const int64_t row = (int64_t)blockIdx.x * 16 + (threadIdx.x >> 4);
+  const int l = threadIdx.x & 15;
   const GdnShape& s = a.s;
   const bool ok = row < (int64_t)a.tokens * s.value_heads;
   const int64_t t = ok ? row / s.value_heads : 0;
   const int h = ok ? (int)(row - t * s.value_heads) : 0;
   const int m = h / s.r, hl = h - m * s.r;
-  uint32_t ov = 0, zv = 0;
+  u32x4 ov = {0, 0, 0, 0}, zv = {0, 0, 0, 0};
   if (ok) {
-    ov = *reinterpret_cast<const uint32_t*>(a.o + row * kHeadDim + 2 * lane);
-    zv = *reinterpret_cast<const uint32_t*>(a.qkvz + t * a.qkvz_stride + m * s.group +
-                                             2 * kHeadDim + s.r * kHeadDim + hl * kHeadDim + 2 * lane);
+    ov = load_u32x4(a.o + row * kHeadDim + 8 * l);
+    zv = load_u32x4(a.qkvz + t * a.qkvz_stride + m * s.group + 2 * kHeadDim + s.r * kHeadDim +
+                    hl * kHeadDim + 8 * l);
   }
-  const float o0 = bf16_lo(ov), o1 = bf16_hi(ov);
-  const float inv = rsqrtf(wave_sum(o0 * o0 + o1 * o1) * (1.0f / kHeadDim) + a.eps);
-  const uint32_t wv = *reinterpret_cast<const uint32_t*>(a.weight + 2 * lane);
-  const float y0 = o0 * inv * bf16_lo(wv) * silu_f(bf16_lo(zv));
-  const float y1 = o1 * inv * bf16_hi(wv) * silu_f(bf16_hi(zv));
-  if (ok) *reinterpret_cast<uint32_t*>(a.y + row * kHeadDim + 2 * lane) = pack_bf16x2(y0, y1);
+  float o[8], z[8], w[8];
+  unpack8(ov, o);
+  unpack8(zv, z);
+  unpack8(load_u32x4(a.weight + 8 * l), w);
+  float ss = 0.0f;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) ss += o[e] * o[e];
+#pragma unroll
+  for (int d = 1; d < 16; d <<= 1) ss += __shfl_xor(ss, d, 64);
+  const float inv = rsqrtf(ss * (1.0f / kHeadDim) + a.eps);
+  float y[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) y[e] = o[e] * inv * w[e] * silu_f(z[e]);
+  if (ok) *reinterpret_cast<u32x4*>(a.y + row * kHeadDim + 8 * l) = pack8(y);
 }
 
 bool gdn_shape(int key_heads, int value_heads, int head_dim, int kernel, GdnShape* s,
@@ -1210,13 +1219,15 @@ extern "C" int qsa_gdn_gated_norm(const void* o, const void* qkvz, int64_t qkvz_
   if (tokens < 0) return fail(QSA_ERR_INVALID, "qsa_gdn_gated_norm: negative size");
   if (tokens == 0) return QSA_OK;
   if (!o || !qkvz || !weight || !y) return fail(QSA_ERR_INVALID, "qsa_gdn_gated_norm: null tensor pointer");
-  if ((reinterpret_cast<uintptr_t>(o) | reinterpret_cast<uintptr_t>(qkvz) |
-       reinterpret_cast<uintptr_t>(weight) | reinterpret_cast<uintptr_t>(y)) & 3 || (qkvz_stride & 1))
-    return fail(QSA_ERR_INVALID, "qsa_gdn_gated_norm: tensors must be 4-byte aligned, even strides");
+  if (!aligned16(o) || !aligned16(qkvz) || !aligned16(weight) || !aligned16(y) || (qkvz_stride & 7))
+    return fail(QSA_ERR_INVALID,
+                "qsa_gdn_gated_norm: 16-byte aligned tensors, qkvz stride a multiple of 8 elements");
   GdnNormArgs a{static_cast<const uint16_t*>(o), static_cast<const uint16_t*>(qkvz), qkvz_stride,
                 static_cast<const uint16_t*>(weight), eps, static_cast<uint16_t*>(y), s, tokens};
   const int64_t rows = (int64_t)tokens * value_heads;
-  hipLaunchKernelGGL(gdn_norm_kernel, dim3((unsigned)((rows + 3) / 4)), dim3(256), 0,
+  if ((rows + 15) / 16 > 0x7fffffffLL)
+    return fail(QSA_ERR_UNSUPPORTED, "qsa_gdn_gated_norm: too many (token, head) rows");
+  hipLaunchKernelGGL(gdn_norm_kernel, dim3((unsigned)((rows + 15) / 16)), dim3(256), 0,
                      static_cast<hipStream_t>(stream), a);
   return check_launch("qsa_gdn_gated_norm");
 }
