@@ -401,7 +401,9 @@ int qsa_gdn_conv_state(const void* qkvz, int64_t qkvz_stride, int tokens, void* 
  * max_seq_tokens: the longest sequence's token count if the caller knows it,
  * else -1. Below 16 (a decode batch) the chunked kernel for sequences of 16+
  * tokens is not launched and the per-token kernel takes every sequence, so a
- * bound that is too small still gives the same result, only slower. */
+ * bound that is too small still gives a result within the same tolerance of
+ * the per-token rule (not bit-identical: the per-token kernel is fp32
+ * throughout, the chunked one multiplies in bf16), only slower. */
 int qsa_gdn_recurrence(const float* q, const float* k, const void* v, const float* g,
                        const float* beta, int tokens, float* state, int num_slots,
                        const int32_t* query_start_loc, const int64_t* slots, int num_seqs,

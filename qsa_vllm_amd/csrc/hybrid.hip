@@ -1071,7 +1071,10 @@ extern "C" int qsa_gated_norm(const void* x, int64_t x_stride, const void* resid
       (residual_in && !residual_out))
     return fail(QSA_ERR_INVALID, "qsa_gated_norm: null tensor pointer");
   if (rank != kRank) return fail(QSA_ERR_UNSUPPORTED, "qsa_gated_norm: gate rank must be 16");
-  if (hidden <= 0 || hidden % 512 || hidden > 4096)
+  // One supported set for both launch paths (one workgroup per token below
+  // kTokenNormRows rows, 16-token tiles above), so a hidden size that decodes
+  // also prefills.
+  if (hidden != 512 && hidden != 1024 && hidden != 2048 && hidden != 4096)
     return fail(QSA_ERR_UNSUPPORTED, "qsa_gated_norm: hidden size must be 512, 1024, 2048 or 4096");
   const void* ptrs[] = {x, weight, gate_down, gate_up, gate_up_bias, out, residual_in, residual_out};
   for (const void* p : ptrs)

@@ -12,8 +12,10 @@ All tensors live in persistent device buffers sized at construction, so a
 HIP graph captured over the path reads each new batch's metadata on replay;
 ``build`` refreshes them on the current stream and returns views of the
 batch's length. Requests are taken in the given order: the leading requests
-that schedule one token are the decode part (the plugin's decode-first row
-order), the rest are prefill.
+that schedule exactly ``decode_query_len`` tokens (1, or more for multi-token
+decode such as speculative verification) are the decode part (the plugin's
+decode-first row order, request i owning rows ``[i * dql, (i + 1) * dql)``,
+``ops/indexer.py:227-279``), the rest are prefill.
 
 Fields (per token t of request q at position p, ratio R):
 
@@ -84,7 +86,10 @@ class QSAMetadataBuilder:
         self.k_work = buf((self.k_work_capacity, 2), torch.int32)
 
     def build(self, num_computed_tokens, num_scheduled_tokens, main_block_table: torch.Tensor,
-              comp_block_table: torch.Tensor, ring_blocks) -> QSABatch:
+              comp_block_table: torch.Tensor, ring_blocks, *,
+              decode_query_len: int = 1) -> QSABatch:
+        if decode_query_len < 1:
+            raise ValueError(f"decode_query_len must be at least 1, got {decode_query_len}")
         computed = np.asarray(num_computed_tokens, dtype=np.int64)
         scheduled = np.asarray(num_scheduled_tokens, dtype=np.int64)
         nreq = int(scheduled.size)
@@ -153,7 +158,7 @@ class QSAMetadataBuilder:
             torch.full_like(p, -1)))
 
         decode_requests = 0
-        while decode_requests < nreq and scheduled[decode_requests] == 1:
+        while decode_requests < nreq and scheduled[decode_requests] == decode_query_len:
             decode_requests += 1
         max_query_len = int(scheduled.max())
         max_seq_len = int(seq.max())
@@ -169,7 +174,8 @@ class QSAMetadataBuilder:
             logical_positions=self.positions[:tokens], seq_lens=self.seq_lens[:nreq],
             query_start_loc=self.query_start_loc[:nreq + 1], max_query_len=max_query_len,
             max_seq_len=max_seq_len, num_decodes=decode_requests,
-            num_decode_tokens=decode_requests, decode_query_len=1,
+            num_decode_tokens=decode_requests * decode_query_len,
+            decode_query_len=decode_query_len,
             visible_blocks=self.visible[:tokens], slot_mapping=self.comp_slots[:tokens],
             k_work_metadata=self.k_work)
         return QSABatch(num_tokens=tokens, num_requests=nreq, positions=self.positions[:tokens],

@@ -10,10 +10,14 @@ kernel and the LSE merge run in ``libqsa_hip.so`` behind
 ``expand_block_indices``, ``store_cache_rows`` and ``compress_groups``.
 
 ``decode_config`` keeps the reference's ``(block_n, target_splits, warps)``
-tuple; only ``target_splits`` is meaningful here (the HIP kernel walks fixed
-32-token tiles and picks its own waves per workgroup), and it caps the split
-count exactly as the reference caps its own
-(``num_splits = min(pow2floor(tiles), target)``).
+tuple and, as there, applies to the decode kernel only (``use_decode_kernel``;
+``ops/qsa.py:620-622``). The split count follows the reference's rule from the
+caller's ``block_n`` and ``target_splits``:
+``num_splits = min(pow2floor(cdiv(W, block_n)), target_splits)``
+(``ops/qsa.py:643-645``), at least 1 and at most 1024 (the library's bound;
+the result does not depend on the split count beyond fp32 rounding). ``warps``
+has no effect: the HIP kernel walks fixed 32-token tiles whatever ``block_n``
+says and chooses its own waves per workgroup from the launch shape.
 """
 
 from __future__ import annotations
@@ -23,20 +27,31 @@ import torch
 from .. import _lib
 from .topk import _torch_ops  # noqa: F401  (registers torch.ops.yulan_qsa_kernels)
 
-_TILE = 32
+_MAX_SPLITS = 1024
 
 
 def _pow2floor(x: int) -> int:
     return 1 << (max(1, x).bit_length() - 1)
 
 
+def config_num_splits(width: int, decode_config) -> int:
+    """The reference's split count for a caller's ``(block_n, target_splits,
+    warps)`` (``ops/qsa.py:643-645``): ``min(pow2floor(cdiv(width, block_n)),
+    target_splits)``, clamped to [1, 1024]."""
+    block_n, target = int(decode_config[0]), int(decode_config[1])
+    if block_n <= 0:
+        raise ValueError(f"decode_config block_n must be positive, got {block_n}")
+    tiles = -(-int(width) // block_n)
+    return max(1, min(_pow2floor(tiles), target, _MAX_SPLITS))
+
+
 def choose_num_splits(q, k_cache, logical_indices, use_decode_kernel, decode_config=None):
-    """Split count for a call: the library heuristic, or the reference-style cap."""
+    """Split count for a call: the caller's ``decode_config`` on the decode
+    kernel, else the library's choice for the shape."""
     rows, hq, dim = q.shape
     width = logical_indices.shape[1]
-    if decode_config is not None:
-        target = int(decode_config[1])
-        return max(1, min(_pow2floor(-(-width // _TILE)), target))
+    if use_decode_kernel and decode_config is not None:
+        return config_num_splits(width, decode_config)
     return _lib.load().qsa_sparse_attention_splits(
         rows, hq, k_cache.shape[2], dim, width, int(bool(use_decode_kernel)))
 
@@ -61,7 +76,8 @@ def qsa_sparse_paged_attention(
         out = torch.empty_like(q)
     if not q.shape[0]:
         return out
-    if decode_config is None and bool(use_decode_kernel) == bool(indices_are_physical):
+    uses_config = bool(use_decode_kernel) and decode_config is not None
+    if not uses_config and bool(use_decode_kernel) == bool(indices_are_physical):
         num_splits = 0  # the library's choice for this shape, made inside the op
     else:
         num_splits = choose_num_splits(q, k_cache, logical_indices, use_decode_kernel,

@@ -11,8 +11,9 @@ reference plugin uses:
   page table (one key per ``compress_ratio`` tokens, complete blocks only);
 * block tables drawn from a seeded random permutation of the page pool,
   ``-1`` past each sequence's last page;
-* decode rows: position = seq_len - 1, visible = seq_len // compress_ratio;
-  chunked prefill rows: positions prefix .. prefix + chunk - 1.
+* decode rows: the last ``decode_query_len`` positions of each sequence (one
+  row at position seq_len - 1 by default), visible = min((pos + 1) // ratio,
+  seq_len // ratio); chunked prefill rows: positions prefix .. prefix + chunk - 1.
 
 Activations are N(0, 1) * ``act_scale`` rounded to bf16. Everything is
 generated on ``device`` from one ``torch.Generator`` seed.
@@ -50,7 +51,8 @@ class QSAShape:
     kv_layout: str = "token_major"
     chunk: int = 0                     # > 0: chunked prefill of `chunk` new tokens per sequence
     prefix: int = 0
-    decode_requests: int = 0           # with chunk > 0: the first requests decode one token
+    decode_requests: int = 0           # with chunk > 0: the first requests decode
+    decode_query_len: int = 1          # tokens per decode request (multi-token decode if > 1)
     table_tokens: int = 0              # > 0: page tables sized for this many tokens per request
     seed: int = 0
 
@@ -113,7 +115,7 @@ class QSAWorkload:
     gate: torch.Tensor | None = None
     max_seq_len: int = 0
     max_query_len: int = 1
-    num_decodes: int = 0              # leading decode requests (= their rows: one token each)
+    num_decodes: int = 0              # leading decode requests (decode_query_len rows each)
     extra: dict = field(default_factory=dict)
 
     @property
@@ -126,7 +128,7 @@ class QSAWorkload:
 
     @property
     def num_decode_tokens(self) -> int:
-        return self.num_decodes
+        return self.num_decodes * self.shape.decode_query_len
 
 
 def _seq_lens(shape: QSAShape, gen: torch.Generator) -> torch.Tensor:
@@ -182,23 +184,19 @@ def make_workload(shape: QSAShape | str, device="cpu", **overrides) -> QSAWorklo
 
     seq_lens = _seq_lens(shape, cpu_gen)
     b = shape.batch
-    if shape.chunk:
-        # Mixed batch: decode requests (one new token) first, then prefill chunks.
-        n_dec = min(shape.decode_requests, b)
-        q_lens = torch.tensor([1] * n_dec + [shape.chunk] * (b - n_dec), dtype=torch.int64)
-        positions = torch.cat([torch.arange(int(s) - int(n), int(s))
-                               for s, n in zip(seq_lens, q_lens)])
-        token_to_req = torch.arange(b, dtype=torch.int32).repeat_interleave(q_lens)
-        query_start_loc = torch.cat([torch.zeros(1, dtype=torch.int64),
-                                     q_lens.cumsum(0)]).to(torch.int32)
-        max_query_len = int(q_lens.max())
-        num_decodes = n_dec
-    else:
-        positions = seq_lens - 1
-        token_to_req = torch.arange(b, dtype=torch.int32)
-        query_start_loc = torch.arange(b + 1, dtype=torch.int32)
-        max_query_len = 1
-        num_decodes = b
+    dql = shape.decode_query_len
+    if dql < 1:
+        raise ValueError("decode_query_len must be at least 1")
+    # Decode requests (decode_query_len new tokens each) first, then prefill chunks.
+    n_dec = min(shape.decode_requests, b) if shape.chunk else b
+    q_lens = torch.tensor([dql] * n_dec + [shape.chunk] * (b - n_dec), dtype=torch.int64)
+    positions = torch.cat([torch.arange(int(s) - int(n), int(s))
+                           for s, n in zip(seq_lens, q_lens)])
+    token_to_req = torch.arange(b, dtype=torch.int32).repeat_interleave(q_lens)
+    query_start_loc = torch.cat([torch.zeros(1, dtype=torch.int64),
+                                 q_lens.cumsum(0)]).to(torch.int32)
+    max_query_len = int(q_lens.max())
+    num_decodes = n_dec
     rows = positions.numel()
     r = shape.compress_ratio
     visible = torch.minimum((positions + 1) // r, seq_lens[token_to_req.long()] // r).to(torch.int32)

@@ -64,7 +64,7 @@ def _compressed_meta(backend, wl):
         logical_positions=wl.positions, seq_lens=wl.seq_lens,
         query_start_loc=wl.query_start_loc, max_query_len=wl.max_query_len,
         max_seq_len=wl.max_seq_len, num_decodes=wl.num_decodes,
-        num_decode_tokens=wl.num_decode_tokens, decode_query_len=1,
+        num_decode_tokens=wl.num_decode_tokens, decode_query_len=wl.shape.decode_query_len,
         visible_blocks=wl.visible)
 
 
@@ -81,7 +81,8 @@ def _gpu_logits(wl):
         lg = torch.full((nd, cols), float("nan"), device=DEV)
         torch.ops.yulan_qsa_kernels.indexer_decode(wl.q_index[:nd], wl.index_cache,
                                                    wl.index_table[:wl.num_decodes],
-                                                   wl.visible[:nd], lg, 1)
+                                                   wl.visible[:nd], lg,
+                                                   wl.shape.decode_query_len)
         parts.append(lg.cpu())
     if nd < wl.rows:
         width = prefill_logits_width(wl.max_seq_len, s.compress_ratio, cap)
@@ -175,6 +176,70 @@ def test_run_qsa_prefill_and_mixed(decode_requests):
                                    want_idx, wl.block_table.cpu(), wl.token_to_req.cpu())
     _check_attn(output[:rows], want, "prefill/mixed")
     assert (output[rows:].float() == 0).all()
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("decode_requests", [0, 3])
+def test_run_qsa_multi_token_decode(decode_requests):
+    """decode_query_len = 2 (``attention.py:140``): request i owns decode rows
+    2i and 2i + 1, scored by the decode scorer (``ops/indexer.py:241-279``);
+    max_query_len = 2, so the plugin asks for logical ids and no counts
+    (``attention.py:202-213``, ``backend.py:62-66``). ``decode_requests`` 0:
+    a decode-only batch; 3: three decode requests, then ragged prefill chunks."""
+    if decode_requests:
+        wl = make_workload("prefill_8k_on_16k", device=DEV, batch=6, chunk=40, prefix=0,
+                           seq_len_min=700, seq_len_max=1500, seq_len_dist="uniform",
+                           token_topk=256, decode_requests=decode_requests, decode_query_len=2)
+    else:
+        wl = make_workload("cpu_decode_4k", device=DEV, batch=6, seq_len_min=3000,
+                           seq_len_max=4096, seq_len_dist="uniform", decode_query_len=2)
+    print(f"[backend] multi-token decode decode_requests={wl.num_decodes} rows={wl.rows} "
+          f"decode rows={wl.num_decode_tokens}", flush=True)
+    assert wl.max_query_len > 1 and wl.num_decode_tokens == 2 * wl.num_decodes
+    layer, output = _run_layer(wl)
+    want_idx, _ = _expected_selection(wl, physical=False)
+    rows = wl.rows
+    assert torch.equal(layer.topk_indices_buffer[:rows].cpu(), want_idx)
+    s = wl.shape
+    kv = wl.kv_cache.cpu()
+    want = oracle.sparse_attention(wl.q.cpu(), kv[..., :s.head_dim], kv[..., s.head_dim:],
+                                   want_idx, wl.block_table.cpu(), wl.token_to_req.cpu())
+    _check_attn(output[:rows], want, "multi-token decode")
+    assert (output[rows:].float() == 0).all()
+
+
+@pytest.mark.gpu
+def test_select_multi_token_decode_physical():
+    """``select_paged_tokens`` with decode_query_len = 2 and a main block table:
+    physical slots and valid counts for both rows of every request, bit-exact
+    against the oracle on the kernel's own logits; attention over them with the
+    decode kernel."""
+    from qsa_vllm_amd.ops import qsa_sparse_paged_attention, select_paged_tokens
+    wl = make_workload("cpu_decode_4k", device=DEV, batch=5, seq_len_min=2000, seq_len_max=4096,
+                       seq_len_dist="uniform", decode_query_len=2, seed=11)
+    s = wl.shape
+    rows = wl.rows
+    print(f"[backend] multi-token decode physical rows={rows}", flush=True)
+    idx = torch.full((rows, s.width), -7, dtype=torch.int32, device=DEV)
+    counts = torch.full((rows,), -7, dtype=torch.int32, device=DEV)
+    select_paged_tokens(wl.q_index, wl.index_cache, wl.index_table, wl.token_to_req,
+                        wl.positions, wl.seq_lens, s.token_topk, s.compress_ratio, idx,
+                        query_start_loc=wl.query_start_loc, max_query_len=2,
+                        max_seq_len=wl.max_seq_len, num_decodes=wl.num_decodes,
+                        num_decode_tokens=rows, decode_query_len=2,
+                        main_block_table=wl.block_table, main_page_size=s.page_size,
+                        valid_counts_out=counts)
+    want_idx, want_counts = _expected_selection(wl, physical=True)
+    assert torch.equal(idx.cpu(), want_idx)
+    assert torch.equal(counts.cpu(), want_counts)
+    out = qsa_sparse_paged_attention(wl.q, wl.k_cache, wl.v_cache, idx, wl.block_table,
+                                     wl.token_to_req, use_decode_kernel=True,
+                                     indices_are_physical=True, valid_counts=counts)
+    torch.cuda.synchronize()
+    want = oracle.sparse_attention(wl.q.cpu(), wl.k_cache.cpu(), wl.v_cache.cpu(), want_idx,
+                                   wl.block_table.cpu(), wl.token_to_req.cpu(),
+                                   indices_are_physical=True, valid_counts=want_counts)
+    _check_attn(out, want, "multi-token decode, physical")
 
 
 def _layer_step_case(prefix, chunk, seed):

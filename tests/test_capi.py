@@ -79,6 +79,19 @@ def test_topk_argument_errors_need_no_launch():
     assert lib.qsa_topk(*args) == -4                    # long rows need the partition workspace
 
 
+def test_gated_norm_hidden_sizes_checked_before_the_row_split():
+    """One supported hidden set for both launch paths (a workgroup per token
+    below 1024 rows, 16-token tiles above): 3072 is refused at any row count."""
+    lib = _lib.load()
+    p = [1 << 20, 4096, None, 0, None, 0, 1 << 21, 1 << 22, 1 << 23, 1 << 24, 1 << 25, 4096]
+    for rows in (16, 4096):
+        for hidden, want in ((3072, -2), (1536, -2), (8192, -2), (256, -2)):
+            args = p + [rows, hidden, 16, 1e-6, None, 0, None]
+            assert lib.qsa_gated_norm(*args) == want, (rows, hidden)
+            assert b"hidden size" in lib.qsa_last_error()
+    assert lib.qsa_gated_norm(*(p + [0, 3072, 16, 1e-6, None, 0, None])) == 0   # no rows
+
+
 def test_workspace_and_split_helpers():
     lib = _lib.load()
     assert lib.qsa_sparse_attention_workspace_bytes(64, 16, 128, 1) == 0

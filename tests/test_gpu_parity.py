@@ -323,12 +323,19 @@ def _physical_case(hq, hkv, dim, splits, layout, rows):
         assert (out[1::6].float() == 0).all(), "a row with no valid slot must be zero"
 
 
+# Logical (prefill) rows group up to four kv heads per workgroup (NKV = 4, 2
+# or 1 by head shape), and with D = 128 each NKV is its own K-into-LDS kernel
+# with its own wait counts, so every head shape that picks a different NKV runs
+# here: (16, 2) NKV 2, (8, 1) and (32, 2) NKV 1, (4, 4) and (16, 4) NKV 4,
+# (64, 2) NKV 1 with 16-head groups, and D = 64 with NKV 2 and 4.
+@pytest.mark.parametrize("hq,hkv,dim", [(16, 2, 128), (8, 1, 128), (4, 4, 128), (32, 2, 128),
+                                         (16, 4, 128), (64, 2, 128), (16, 2, 64), (8, 8, 64)])
 @pytest.mark.parametrize("splits", [1, 4])
 @pytest.mark.parametrize("reps", [1, 8])
-def test_attention_logical_parity(splits, reps):
-    _note(f"attention logical splits={splits} rows={9 * reps}")
-    g = torch.Generator().manual_seed(40 + splits + reps)
-    reqs, hq, hkv, dim, page, num_blocks = 3, 16, 2, 128, 16, 30
+def test_attention_logical_parity(hq, hkv, dim, splits, reps):
+    _note(f"attention logical hq={hq} hkv={hkv} dim={dim} splits={splits} rows={9 * reps}")
+    g = torch.Generator().manual_seed(40 + splits + reps + hq * 3 + hkv + dim)
+    reqs, page, num_blocks = 3, 16, 30
     k = torch.randn(num_blocks, page, hkv, dim, generator=g).to(torch.bfloat16)
     v = torch.randn(num_blocks, page, hkv, dim, generator=g).to(torch.bfloat16)
     table = torch.randperm(num_blocks, generator=g)[:reqs * 8].view(reqs, 8).to(torch.int32)
@@ -339,13 +346,23 @@ def test_attention_logical_parity(splits, reps):
     t2r = torch.tensor([0, 0, 1, 1, 2, 2, -1, 3, 0], dtype=torch.int32).repeat(reps)
     idx = torch.randint(-2, 8 * page + 10, (rows, width), generator=g, dtype=torch.int32)
     q = torch.randn(rows, hq, dim, generator=g).to(torch.bfloat16)
-    want = oracle.sparse_attention(q, k, v, idx, table, t2r)
+    gate = torch.randn(rows, hq, dim, generator=g).to(torch.bfloat16)
+    bad = ((t2r < 0) | (t2r >= reqs)).to(DEV)
+    for use_gate in (False, True):
+        want = oracle.sparse_attention(q, k, v, idx, table, t2r,
+                                       output_gate=gate if use_gate else None)
+        out = torch.full((rows, hq, dim), float("nan"), dtype=torch.bfloat16, device=DEV)
+        torch.ops.yulan_qsa_kernels.sparse_attention(
+            q.to(DEV), k.to(DEV), v.to(DEV), idx.to(DEV), table.to(DEV), t2r.to(DEV), out,
+            gate.to(DEV) if use_gate else None, None, False, splits)
+        torch.cuda.synchronize()
+        _attn_check(out, want, f"logical gate={use_gate}")
+        assert (out[bad].float() == 0).all()
+    # the plugin's call (the library picks the split count for the shape)
     out = qsa_sparse_paged_attention(q.to(DEV), k.to(DEV), v.to(DEV), idx.to(DEV), table.to(DEV),
-                                     t2r.to(DEV), decode_config=(32, splits, 4))
+                                     t2r.to(DEV))
     torch.cuda.synchronize()
-    _attn_check(out, want, "logical")
-    bad = (t2r < 0) | (t2r >= reqs)
-    assert (out[bad.to(DEV)].float() == 0).all()
+    _attn_check(out, oracle.sparse_attention(q, k, v, idx, table, t2r), "logical, library split")
 
 
 def test_decode_select_then_attend_small():

@@ -82,3 +82,40 @@ def test_gemm_tuning_file_is_well_formed(tmp_path):
     assert len({r[1] for r in records}) == len(records)  # one choice per shape
     assert all(r[1].startswith("tn_") and r[2] for r in records)
     assert enable_tuned_gemms(tmp_path / "missing.csv") is False
+
+
+@pytest.mark.parametrize("width,config,want", [
+    (2063, (64, 8, 4), 8),       # cdiv = 33 -> 32, capped by the target 8
+    (2063, (32, 64, 1), 64),     # cdiv = 65 -> 64
+    (2063, (64, 64, 1), 32),     # the same target with block_n 64 gives half the splits
+    (2063, (16, 1000, 4), 128),  # cdiv = 129 -> 128
+    (100, (32, 16, 4), 4),       # cdiv = 4
+    (1039, (32, 3, 4), 3),       # a target that is not a power of two is kept
+    (1, (64, 16, 4), 1),
+    (2063, (32, 0, 4), 1),       # never below one split
+    (100000, (1, 5000, 4), 1024),  # never above the library's bound
+])
+def test_decode_config_split_count(width, config, want):
+    """``ops/qsa.py:643-645``: num_splits = min(pow2floor(cdiv(W, block_n)),
+    target_splits), from the caller's block_n."""
+    from qsa_vllm_amd.ops.qsa import choose_num_splits, config_num_splits
+    assert config_num_splits(width, config) == want
+    q = torch.empty(4, 16, 128, dtype=torch.bfloat16)
+    k = torch.empty(8, 16, 2, 128, dtype=torch.bfloat16)
+    idx = torch.empty(4, width, dtype=torch.int32)
+    assert choose_num_splits(q, k, idx, True, config) == want
+
+
+def test_decode_config_ignored_for_prefill_rows():
+    """The reference reads ``decode_config`` only for the decode kernel
+    (``ops/qsa.py:620-622``); prefill rows take the library's choice."""
+    from qsa_vllm_amd import _lib
+    from qsa_vllm_amd.ops.qsa import choose_num_splits
+    q = torch.empty(64, 16, 128, dtype=torch.bfloat16)
+    k = torch.empty(8, 16, 2, 128, dtype=torch.bfloat16)
+    idx = torch.empty(64, 2063, dtype=torch.int32)
+    lib_choice = _lib.load().qsa_sparse_attention_splits(64, 16, 2, 128, 2063, 0)
+    assert choose_num_splits(q, k, idx, False, (16, 1000, 4)) == lib_choice
+    assert choose_num_splits(q, k, idx, False, None) == lib_choice
+    with pytest.raises(ValueError):
+        choose_num_splits(q, k, idx, True, (0, 4, 4))

@@ -2,12 +2,14 @@
 
 import random
 
+import pytest
 import torch
 
 from qsa_vllm_amd.metadata import QSAMetadataBuilder
 
 
-def _expected(computed, scheduled, main_table, comp_table, ring_blocks, R, page, cpage, ring):
+def _expected(computed, scheduled, main_table, comp_table, ring_blocks, R, page, cpage, ring,
+              dql=1):
     tokens = []
     for q, (c, n) in enumerate(zip(computed, scheduled)):
         for i in range(n):
@@ -32,7 +34,7 @@ def _expected(computed, scheduled, main_table, comp_table, ring_blocks, R, page,
         closed = sum(1 for p in range(c, c + n) if (p + 1) % R == 0)
         work += [[q, w] for w in range(max(closed, 1))]
     decodes = 0
-    while decodes < len(scheduled) and scheduled[decodes] == 1:
+    while decodes < len(scheduled) and scheduled[decodes] == dql:
         decodes += 1
     return tokens, seq, main, raw, comp, vis, work, decodes
 
@@ -44,8 +46,9 @@ def _table(rng, rows, width, pool):
     return t
 
 
-def test_builder_matches_plain_statement():
-    rng = random.Random(7)
+@pytest.mark.parametrize("dql", [1, 2, 3])
+def test_builder_matches_plain_statement(dql):
+    rng = random.Random(7 + dql)
     R, page, cpage, ring = 4, 4, 2, 4
     b = QSAMetadataBuilder(compress_ratio=R, main_page_size=page, comp_page_size=cpage,
                            ring_size=ring, max_num_requests=8, max_num_tokens=96,
@@ -53,15 +56,16 @@ def test_builder_matches_plain_statement():
     for trial in range(6):
         nreq = rng.randint(1, 8)
         ndec = rng.randint(0, nreq)
-        scheduled = [1] * ndec + [rng.randint(1, 15) for _ in range(nreq - ndec)]
+        scheduled = [dql] * ndec + [rng.randint(1, 15) for _ in range(nreq - ndec)]
         computed = [rng.randint(0, 30) for _ in range(nreq)]
         main_table = _table(rng, nreq, 12, 50)
         comp_table = _table(rng, nreq, 5, 20)
         ring_blocks = [rng.randint(-1, 9) for _ in range(nreq)]
         batch = b.build(computed, scheduled, torch.tensor(main_table, dtype=torch.int32),
-                        torch.tensor(comp_table, dtype=torch.int32), ring_blocks)
+                        torch.tensor(comp_table, dtype=torch.int32), ring_blocks,
+                        decode_query_len=dql)
         tokens, seq, main, raw, comp, vis, work, decodes = _expected(
-            computed, scheduled, main_table, comp_table, ring_blocks, R, page, cpage, ring)
+            computed, scheduled, main_table, comp_table, ring_blocks, R, page, cpage, ring, dql)
         assert batch.num_tokens == len(tokens)
         assert batch.positions.tolist() == [p for _, p in tokens]
         assert batch.token_to_req.tolist() == [q for q, _ in tokens]
@@ -73,7 +77,12 @@ def test_builder_matches_plain_statement():
         kw = batch.compressed.k_work_metadata.tolist()
         assert kw[:len(work)] == work
         assert all(item == [-1, 0] for item in kw[len(work):])
-        assert batch.compressed.num_decodes == decodes == batch.compressed.num_decode_tokens
+        assert batch.compressed.num_decodes == decodes
+        assert batch.compressed.num_decode_tokens == decodes * dql
+        assert batch.compressed.decode_query_len == dql
+        # decode rows come first: request i owns rows [i * dql, (i + 1) * dql)
+        assert batch.token_to_req.tolist()[:decodes * dql] == [
+            i for i in range(decodes) for _ in range(dql)]
         assert batch.main.max_query_len == max(scheduled)
         assert batch.raw.query_start_loc.tolist()[-1] == len(tokens)
 
