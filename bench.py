@@ -42,6 +42,10 @@ WORKLOADS = ("decode_32k", "decode_32k_serving_width", "decode_long_skew", "pref
              "hybrid_decoder_step")
 
 
+# CPU share of a one-GPU job on the benchmark hosts (worker pools are sized to it).
+CPU_SHARE_PER_GPU = 16
+
+
 def parse_args():
     p = argparse.ArgumentParser(description=__doc__.split("\n\n")[0])
     p.add_argument("--gpus", type=int, default=1)
@@ -52,7 +56,9 @@ def parse_args():
     p.add_argument("--sets", type=int, default=4, help="query sets rotated across steps")
     p.add_argument("--cpu-seconds", type=float, default=10.0,
                    help="CPU work budget for the oracle baseline (0 disables it)")
-    p.add_argument("--cpu-threads", type=int, default=0, help="0: min(16, cpu_count)")
+    p.add_argument("--cpu-threads", type=int, default=0,
+                   help="0: the job's CPU share (16 per GPU on the benchmark hosts), at most the "
+                        "CPUs this process may run on")
     p.add_argument("--no-extras", action="store_true",
                    help="headline workload only (no summaries of the other workloads)")
     p.add_argument("--no-hybrid", action="store_true",
@@ -1007,7 +1013,8 @@ def cpu_baseline(wl, args, seconds=None):
     import oracle
 
     seconds = args.cpu_seconds if seconds is None else seconds
-    threads = args.cpu_threads or min(16, os.cpu_count() or 1)
+    usable = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else os.cpu_count()
+    threads = args.cpu_threads or min(CPU_SHARE_PER_GPU, usable or 1)
     torch.set_num_threads(threads)
     cpu = {n: getattr(wl, n).cpu() for n in ("q", "q_index", "index_cache", "index_table",
                                              "block_table", "positions", "seq_lens")}
@@ -1028,6 +1035,10 @@ def cpu_baseline(wl, args, seconds=None):
         "value": round(steps * wl.rows / elapsed, 2),
         "unit": "tokens/s",
         "cores": threads,
+        "host_cpus": os.cpu_count(),
+        "threads_note": (f"{threads} threads: a one-GPU job on the benchmark hosts is granted "
+                         f"{CPU_SHARE_PER_GPU} CPUs; os.cpu_count() reports the whole host"
+                         if not args.cpu_threads else "threads set by --cpu-threads"),
         "kind": "port",
         "sample": f"{steps} full decode step(s) of the {wl.shape.name} batch ({wl.rows} rows) in "
                   f"{elapsed:.1f}s: oracle indexer -> top-k/expand -> fp32 sparse attention",

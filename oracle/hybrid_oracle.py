@@ -14,11 +14,20 @@ in float64, one sequence at a time. Values are rounded to bf16 where the
 model's tensors are bf16 (projection outputs, conv output, core output, norm
 outputs); the arithmetic between those points is float64.
 
-Pinning (``tests/test_hybrid_oracle.py``): the recurrence against an
-independent transition-matrix statement ``S_t = e^{g_t} (I - beta_t k_t k_t^T)
-S_{t-1} + beta_t k_t v_t^T``, closed forms (no writes: pure decay; orthonormal
-keys: exact key-value recall and overwrite), the convolution against
-``torch.nn.functional.conv1d``, the norms against closed forms.
+Pinning (``tests/test_hybrid_oracle.py``; ``tests/test_oracle_mutants.py``
+plants a mistake in each function and requires its pin to fail): the
+recurrence against an independent transition-matrix statement ``S_t = e^{g_t}
+(I - beta_t k_t k_t^T) S_{t-1} + beta_t k_t v_t^T`` and closed forms (no
+writes: pure decay; orthonormal keys: exact key-value recall and overwrite);
+the convolution against ``torch.nn.functional.conv1d``; ``rms_norm`` against
+closed forms (constant rows, power-of-two scaling, zero rows); ``gated_norm``
+with zero gate weights (``n * bf16(sigmoid(bias))``) and a rank-1 gate stated
+per element with scalar loops; ``swiglu`` by scalar loops (gate rows first)
+and a zero gate; ``gdn_mixer`` by closed forms (one token from zero states:
+``o = sigmoid(b) (k.q) v``; a second token with ``beta = 0``:
+``o = e^g sigmoid(b1) (k1.q2) v1`` with ``g = -exp(A_log) softplus(a +
+dt_bias)``) and the state hand-off (two calls equal one);
+``qsa_projection_split`` against an explicit element index map.
 
 Parity unpinned: vLLM's own GDN kernels (fla Triton, not vendored) - no golden
 vectors of theirs exist in the plugin.

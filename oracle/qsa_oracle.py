@@ -8,26 +8,40 @@ Every function cites the reference lines it restates (paths relative to the
 expansion, slot mapping, counts) are restated exactly; floating-point work is
 fp32 math on bf16 inputs, as the reference accumulates.
 
-Pinning (how each function is checked independently of its own formula, in
-``tests/test_oracle.py``):
+Pinning (how each function is checked independently of its own formula;
+``tests/test_oracle_mutants.py`` plants a mistake in each function's source
+and requires its pin to fail):
 
-* ``visible_blocks``      - closed form on hand-built rows.
-* ``indexer_scores_*``    - pure-Python brute-force loops; ReLU/positivity,
-                            positive homogeneity, unit-vector closed forms.
-* ``topk_ids``            - pure-Python rank counting over (uint32 key desc,
-                            id asc); hand-written known answers for ties,
+* ``visible_blocks``, ``*_logits_*`` - closed forms on hand-built rows.
+* ``indexer_scores_*``    - pure-Python brute-force loops (one and two rows per
+                            decode request); ReLU/positivity, positive
+                            homogeneity, unit-vector closed forms; prefill rows
+                            equal decode rows of the same request.
+* ``uint32_keys``, ``topk_ids`` - pure-Python rank counting over (uint32 key
+                            desc, id asc); hand-written known answers for ties,
                             -0.0, negatives, inf and NaN bit patterns.
-* ``topk_expand``         - a column-wise restatement of the second statement
-                            of the rule in the reference (the Triton expansion
-                            kernel, ``ops/qsa.py:18-106``) on the same blocks;
-                            hand-built physical mappings; prefix/dup/causal
-                            invariants.
+* ``topk_expand``, ``expand_blocks`` - a column-wise restatement of the second
+                            statement of the rule in the reference (the Triton
+                            expansion kernel, ``ops/qsa.py:18-106``) on the same
+                            blocks; hand-built physical mappings;
+                            prefix/dup/causal invariants.
+* ``store_cache_rows``, ``compress_groups`` - closed form; a walk over member
+                            positions.
+* ``select_paged_tokens`` - a mixed batch (two rows per decode request, ragged
+                            prefill chunks, padding rows) against each row's own
+                            selection by loops, rank counting and column-wise
+                            expansion, logical and physical.
 * ``sparse_attention``    - dense causal GQA through
                             ``torch.nn.functional.scaled_dot_product_attention``
                             when every token is selected; pure-Python softmax
                             loops; one-slot and empty-row closed forms;
                             permutation invariance; duplicate weighting.
-* ``merge_splits``        - LSE identity: split + merge equals one pass.
+* ``sparse_attention_partials``, ``merge_splits`` - LSE identity: split +
+                            merge equals one pass.
+* ``decode_step``         - slots and counts against each row's selection by
+                            loops, the output against softmax loops over the
+                            K/V rows at those slots, and against the same tokens
+                            given as logical ids through the block table.
 
 Parity unpinned: the un-vendored upstream metadata builder
 (``vllm.models.qwen4_exp.common.qsa_cache``, vllm 0.30.0) that produces
@@ -37,12 +51,9 @@ from their consumers' contracts here.
 
 from __future__ import annotations
 
-import math
-
 import torch
 
 __all__ = [
-    "c_trunc_div",
     "visible_blocks",
     "decode_logits_columns",
     "prefill_logits_width",
@@ -60,16 +71,6 @@ __all__ = [
     "merge_splits",
     "decode_step",
 ]
-
-
-def c_trunc_div(a: int, b: int) -> int:
-    """C integer division (truncation toward zero), as ``topk.cu`` computes it."""
-    q = abs(a) // abs(b)
-    return q if (a >= 0) == (b >= 0) else -q
-
-
-def _to_int32(x: int) -> int:
-    return ((int(x) + 2**31) % 2**32) - 2**31
 
 
 def visible_blocks(query_positions, sequence_lengths, token_to_req, compress_ratio):
@@ -483,8 +484,3 @@ def decode_step(q_idx, k_idx_cache, idx_page_table, q, k_cache, v_cache, block_t
                            output_gate=output_gate, indices_are_physical=True,
                            valid_counts=counts)
     return out, indices, counts
-
-
-def _selftest_math():  # pragma: no cover - used by tests as a sanity hook
-    assert c_trunc_div(-5, 4) == -1 and c_trunc_div(5, 4) == 1
-    assert math.isclose(128 ** -0.5, 0.08838834764831845)

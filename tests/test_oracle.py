@@ -22,12 +22,12 @@ def _bits(values):
 
 
 def test_visible_blocks_closed_form():
-    pos = torch.tensor([0, 14, 15, 16, 31, 100, 5], dtype=torch.int64)
+    pos = torch.tensor([0, 14, 15, 16, 31, 100, 5, 100], dtype=torch.int64)
     seq = torch.tensor([64, 20], dtype=torch.int32)
-    t2r = torch.tensor([0, 0, 0, 0, 1, 1, -1], dtype=torch.int32)
+    t2r = torch.tensor([0, 0, 0, 0, 1, 1, -1, -1], dtype=torch.int32)
     got = oracle.visible_blocks(pos, seq, t2r, 16).tolist()
     # min((pos+1)//16, seq[req]//16), 0 for padding rows
-    assert got == [0, 0, 1, 1, 1, 1, 0]
+    assert got == [0, 0, 1, 1, 1, 1, 0, 0]
 
 
 def test_logits_width_rules():
@@ -36,7 +36,9 @@ def test_logits_width_rules():
     assert oracle.decode_logits_columns(1000, 16, 2048) == 2048
     assert oracle.prefill_logits_width(24576, 16, 1536) == 1536
     assert oracle.prefill_logits_width(100, 16, 4096) == 64
+    assert oracle.prefill_logits_width(0, 16, 4096) == 64       # never below 64 columns
     assert oracle.prefill_logits_width(1100, 16, 4096) == 128
+    assert oracle.prefill_logits_width(1025 * 16, 16, 4096) == 1088   # 1025 keys -> 17 x 64
 
 
 # --------------------------------------------------------------------------- top-k
@@ -170,18 +172,20 @@ def test_topk_expand_invariants_logical():
 # --------------------------------------------------------------------------- indexer
 
 
-def test_indexer_scores_bruteforce():
+@pytest.mark.parametrize("dql", [1, 2])
+def test_indexer_scores_bruteforce(dql):
+    """Row r scores request r // dql's keys (``ops/indexer.py:241-279``)."""
     g = torch.Generator().manual_seed(5)
-    rows, heads, dim, page, blocks = 3, 3, 8, 4, 6
+    rows, heads, dim, page, blocks = 3 * dql, 3, 8, 4, 6
     q = (torch.randn(rows, heads, dim, generator=g)).to(torch.bfloat16)
     cache = torch.randn(blocks, page, 1, dim, generator=g).to(torch.bfloat16)
     table = torch.tensor([[4, 1, 3], [0, 2, -1], [5, 5, 5]], dtype=torch.int32)
-    visible = torch.tensor([9, 5, 0], dtype=torch.int32)
-    got = oracle.indexer_scores_decode(q, cache, table, visible, 1, 12)
+    visible = torch.tensor([9, 5, 0] if dql == 1 else [8, 9, 5, 4, 0, 2], dtype=torch.int32)
+    got = oracle.indexer_scores_decode(q, cache, table, visible, dql, 12)
     for r in range(rows):
         keys = []
         for c in range(int(visible[r])):
-            keys.append(cache[int(table[r, c // page]), c % page, 0].float().tolist())
+            keys.append(cache[int(table[r // dql, c // page]), c % page, 0].float().tolist())
         want = restate.relu_head_scores(q[r].float().tolist(), keys)
         assert got[r, :len(want)].tolist() == pytest.approx(want, rel=1e-5, abs=1e-5)
         assert torch.isnan(got[r, len(want):]).all()
@@ -325,13 +329,119 @@ def test_split_merge_identity():
         assert torch.allclose(merged, single, atol=1e-5)
 
 
-def test_decode_step_composition():
-    from qsa_vllm_amd.workloads import make_workload
-    wl = make_workload("cpu_decode_4k", device="cpu", batch=2)
-    out, idx, counts = oracle.decode_step(
-        wl.q_index, wl.index_cache, wl.index_table, wl.q, wl.k_cache, wl.v_cache,
-        wl.block_table, wl.positions, wl.seq_lens, wl.shape.token_topk, wl.shape.compress_ratio)
-    assert out.shape == wl.q.shape
-    # 4096 tokens, ratio 16, top-k 1024 tokens: 64 blocks, no tail
-    assert counts.tolist() == [1024, 1024]
-    assert (idx[:, 1024:] == -1).all()
+# --------------------------------------------------------------------------- selection by rows
+
+
+def _int_rows(g, shape, lo=-3, hi=3):
+    """Small integers (exact in bf16, so index scores are exact in fp32 and in
+    double: integer dot products times 16^-0.5 = 0.25)."""
+    return torch.randint(lo, hi + 1, shape, generator=g).to(torch.bfloat16)
+
+
+def _selection_by_rows(q, cache, table, t2r, pos, seq, ratio, k, width, physical=False,
+                       main_table=None, main_page=1):
+    """Per row, from its own request: visible blocks, every visible key's score
+    by explicit loops, rank-counted top-k, column-wise expansion. Written
+    without the oracle's decode/prefill split, so it pins that split."""
+    page = cache.shape[1]
+    rows_out, counts, visible = [], [], []
+    main = main_table.tolist() if main_table is not None else [[0]]
+    for r in range(q.shape[0]):
+        req = int(t2r[r])
+        vis = 0 if req < 0 else min((int(pos[r]) + 1) // ratio, int(seq[req]) // ratio)
+        keys = [cache[int(table[req, c // page]), c % page, 0].float().tolist() for c in range(vis)]
+        scores = restate.relu_head_scores(q[r].float().tolist(), keys)
+        ids = restate.topk_by_rank(restate.u32_keys(torch.tensor(scores, dtype=torch.float32)),
+                                   vis, k)
+        row, count = restate.expand_columns(ids, int(pos[r]), req, seq.tolist(), ratio, width,
+                                            physical, main, main_page)
+        rows_out.append(row)
+        counts.append(count)
+        visible.append(vis)
+    return rows_out, counts, visible
+
+
+def _mixed_batch(seed):
+    """Two decode requests of two rows each (decode_query_len 2), two ragged
+    prefill chunks (5 and 3 tokens), two padding rows (request -1)."""
+    g = torch.Generator().manual_seed(seed)
+    ratio, cpage, heads, dim = 4, 4, 2, 16
+    seq = torch.tensor([30, 21, 40, 9], dtype=torch.int32)
+    pos = torch.tensor([28, 29, 19, 20, 35, 36, 37, 38, 39, 6, 7, 8, 0, 3], dtype=torch.int64)
+    t2r = torch.tensor([0, 0, 1, 1, 2, 2, 2, 2, 2, 3, 3, 3, -1, -1], dtype=torch.int32)
+    qsl = torch.tensor([0, 2, 4, 9, 12], dtype=torch.int32)
+    table = torch.randperm(12, generator=g)[:12].view(4, 3).to(torch.int32)
+    cache = _int_rows(g, (12, cpage, 1, dim))
+    q = _int_rows(g, (pos.numel(), heads, dim))
+    main_page = 8
+    main_table = torch.randperm(40, generator=g)[:24].view(4, 6).to(torch.int32)
+    main_table[1, 2] = -1                       # an unmapped page: its slots are -1
+    return dict(q=q, cache=cache, table=table, t2r=t2r, pos=pos, seq=seq, qsl=qsl,
+                ratio=ratio, main_table=main_table, main_page=main_page)
+
+
+@pytest.mark.parametrize("physical", [False, True])
+def test_select_paged_tokens_mixed_batch_by_rows(physical):
+    """``ops/indexer.py:346-393``: decode rows (two per request) with
+    ``page_table[:num_decodes]``, then prefill rows with
+    ``page_table[num_decodes:]`` and ``query_start_loc[num_decodes:]``, and
+    padding rows, each equal to its own row's selection."""
+    b = _mixed_batch(21 + physical)
+    k, ratio = 3, b["ratio"]
+    width = k * ratio + ratio - 1
+    out, counts, visible = oracle.select_paged_tokens(
+        b["q"], b["cache"], b["table"], b["t2r"], b["pos"], b["seq"], k * ratio, ratio,
+        query_start_loc=b["qsl"], max_query_len=5, max_seq_len=int(b["seq"].max()),
+        num_decodes=2, num_decode_tokens=4, decode_query_len=2,
+        main_block_table=b["main_table"] if physical else None, main_page_size=b["main_page"])
+    want, want_counts, want_vis = _selection_by_rows(
+        b["q"], b["cache"], b["table"], b["t2r"], b["pos"], b["seq"], ratio, k, width,
+        physical, b["main_table"], b["main_page"])
+    assert visible.tolist() == want_vis
+    assert max(want_vis) > k                     # rows really select
+    for r in range(out.shape[0]):
+        assert out[r].tolist() == want[r], r
+    if physical:
+        assert counts.tolist() == want_counts
+
+
+def test_decode_step_against_loops():
+    """``attention.py:191-214`` -> ``backend.py:39-68`` in uniform decode:
+    physical slots and counts equal each row's own selection; the output
+    equals explicit softmax loops over the K/V rows at those slots, and
+    attention over the same tokens given as logical ids through the block
+    table."""
+    g = torch.Generator().manual_seed(31)
+    rows, ratio, cpage, hq, hkv, dim, page, k = 3, 4, 4, 4, 2, 16, 8, 3
+    seq = torch.tensor([37, 26, 44], dtype=torch.int32)
+    pos = seq.long() - 1
+    table = torch.randperm(12, generator=g)[:9].view(3, 3).to(torch.int32)
+    cache = _int_rows(g, (12, cpage, 1, 16))
+    q_idx = _int_rows(g, (rows, 2, 16))
+    main_table = torch.randperm(24, generator=g)[:18].view(3, 6).to(torch.int32)
+    kc = torch.randn(24, page, hkv, dim, generator=g).to(torch.bfloat16)
+    vc = torch.randn(24, page, hkv, dim, generator=g).to(torch.bfloat16)
+    q = torch.randn(rows, hq, dim, generator=g).to(torch.bfloat16)
+    out, idx, counts = oracle.decode_step(q_idx, cache, table, q, kc, vc, main_table, pos, seq,
+                                          k * ratio, ratio)
+    width = k * ratio + ratio - 1
+    t2r = torch.arange(rows, dtype=torch.int32)
+    want, want_counts, _ = _selection_by_rows(q_idx, cache, table, t2r, pos, seq, ratio, k,
+                                              width, True, main_table, page)
+    assert idx.tolist() == want and counts.tolist() == want_counts
+    group = hq // hkv
+    for r in range(rows):
+        slots = [s for s in idx[r, :int(counts[r])].tolist() if s >= 0]
+        assert len(slots) == int(counts[r])
+        for h in range(hq):
+            keys = [kc[s // page, s % page, h // group].float().tolist() for s in slots]
+            vals = [vc[s // page, s % page, h // group].float().tolist() for s in slots]
+            w = restate.softmax_attend(q[r, h].float().tolist(), keys, vals)
+            assert out[r, h].tolist() == pytest.approx(w, rel=1e-5, abs=1e-5)
+    # the same tokens as logical ids (inverse of the block table)
+    inverse = {int(main_table[r, i]) * page + o: i * page + o
+               for r in range(rows) for i in range(6) for o in range(page)}
+    logical = torch.tensor([[inverse[s] if s >= 0 else -1 for s in row] for row in idx.tolist()],
+                           dtype=torch.int32)
+    again = oracle.sparse_attention(q, kc, vc, logical, main_table, t2r)
+    assert torch.allclose(again, out, atol=1e-6)
