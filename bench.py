@@ -1036,15 +1036,22 @@ def cpu_baseline(wl, args, seconds=None):
         "unit": "tokens/s",
         "cores": threads,
         "host_cpus": os.cpu_count(),
-        "threads_note": (f"{threads} threads: a one-GPU job on the benchmark hosts is granted "
-                         f"{CPU_SHARE_PER_GPU} CPUs; os.cpu_count() reports the whole host"
-                         if not args.cpu_threads else "threads set by --cpu-threads"),
+        "threads_note": _threads_note(threads, usable, args.cpu_threads),
         "kind": "port",
         "sample": f"{steps} full decode step(s) of the {wl.shape.name} batch ({wl.rows} rows) in "
                   f"{elapsed:.1f}s: oracle indexer -> top-k/expand -> fp32 sparse attention",
         "cpu": _cpu_model(),
         "torch": torch.__version__,
     }
+
+
+def _threads_note(threads, usable, requested):
+    if requested:
+        return f"{threads} threads set by --cpu-threads"
+    if usable and usable > CPU_SHARE_PER_GPU:
+        return (f"{threads} of the {usable} CPUs this process may run on: the CPU share of a "
+                f"one-GPU job on the benchmark hosts")
+    return f"every CPU this process may run on ({threads})"
 
 
 def _cpu_model():
