@@ -54,9 +54,10 @@ __global__ __launch_bounds__(THREADS) void topk_direct_kernel(const TopkArgs a) 
   QSA_TOPK_LDS(THREADS, ITEMS, PAGES);
   const int row = blockIdx.x;
   const float* srow = a.scores + (int64_t)row * a.score_row_stride;
-  process_row<THREADS, ITEMS, EXPAND, PAGES>(DirectLoader{srow, 0}, a.cols, a.lengths[row], a.cols,
-                                             a.topk, a.meta, row,
-                                             a.out + (int64_t)row * a.out_row_stride, sh, st, sel);
+  process_row_whole<THREADS, ITEMS, EXPAND, PAGES>(DirectLoader{srow, 0}, a.cols, a.lengths[row],
+                                                   a.cols, a.topk, a.meta, row,
+                                                   a.out + (int64_t)row * a.out_row_stride, sh,
+                                                   st, sel);
 }
 
 // Pass 1 of long rows: rows short enough for one pass finish in partition 0.
@@ -134,6 +135,13 @@ __global__ __launch_bounds__(kAdaptiveThreads) void topk_adaptive_kernel(const T
     process_row<T, ITEMS, EXPAND, PAGES>(LOAD, LIMIT, LENGTH, CLAMP, topk, a.meta, row, out, sh, \
                                          st, reinterpret_cast<int*>(st.key));                   \
   }
+#define QSA_ADAPTIVE_WHOLE_ROW(ITEMS)                                                           \
+  {                                                                                             \
+    auto& st = *reinterpret_cast<TopkStage<T, ITEMS, PAGES>*>(stage_mem);                      \
+    static_assert(sizeof(TopkStage<T, ITEMS, PAGES>) <= sizeof(stage_mem), "stage too large");  \
+    process_row_whole<T, ITEMS, EXPAND, PAGES>(load, n, length, a.cols, topk, a.meta, row, out, \
+                                               sh, st, reinterpret_cast<int*>(st.key));         \
+  }
   if (n <= kAdaptiveHalf) {
     const DirectLoader load{srow, 0};
     // Keys, and room for the selection. Rows of up to 4096 keys take four
@@ -147,14 +155,14 @@ __global__ __launch_bounds__(kAdaptiveThreads) void topk_adaptive_kernel(const T
       // make each phase of a short row cheaper.
       if (threadIdx.x >= kAdaptiveNarrow) return;
       auto& st = *reinterpret_cast<TopkStage<kAdaptiveNarrow, 4, PAGES>*>(stage_mem);
-      process_row<kAdaptiveNarrow, 4, EXPAND, PAGES>(load, n, length, a.cols, topk, a.meta, row,
-                                                     out, shu.narrow, st,
-                                                     reinterpret_cast<int*>(st.key));
+      process_row_whole<kAdaptiveNarrow, 4, EXPAND, PAGES>(load, n, length, a.cols, topk, a.meta,
+                                                           row, out, shu.narrow, st,
+                                                           reinterpret_cast<int*>(st.key));
       return;
     }
-    if (need <= T * 4) QSA_ADAPTIVE_ROW(4, load, n, length, a.cols)
-    else if (need <= T * 8) QSA_ADAPTIVE_ROW(8, load, n, length, a.cols)
-    else QSA_ADAPTIVE_ROW(16, load, n, length, a.cols)
+    if (need <= T * 4) QSA_ADAPTIVE_WHOLE_ROW(4)
+    else if (need <= T * 8) QSA_ADAPTIVE_WHOLE_ROW(8)
+    else QSA_ADAPTIVE_WHOLE_ROW(16)
     return;
   }
   // Halves: [0, 16384) and [16384, n), winners (ascending ids) to LDS past the
@@ -180,6 +188,7 @@ __global__ __launch_bounds__(kAdaptiveThreads) void topk_adaptive_kernel(const T
   else if (need <= T * 8) QSA_ADAPTIVE_ROW(8, merged, count, count, count)
   else QSA_ADAPTIVE_ROW(16, merged, count, count, count)
 #undef QSA_ADAPTIVE_ROW
+#undef QSA_ADAPTIVE_WHOLE_ROW
 }
 
 template <int THREADS, int ITEMS>
@@ -355,24 +364,26 @@ extern "C" int qsa_topk(const float* scores, int64_t score_row_stride, int rows,
                             static_cast<hipStream_t>(stream));
 }
 
-extern "C" int qsa_topk_expand(const float* scores, int64_t score_row_stride, int rows, int cols,
-                               const int32_t* lengths, const int64_t* positions,
-                               const int32_t* sequence_lengths, int num_requests,
-                               const int32_t* token_to_req, const int32_t* table,
-                               int64_t table_row_stride, int table_width, int32_t* output,
-                               int64_t output_row_stride, int64_t output_col_stride,
-                               int output_width, int32_t* counts, int ratio, int page_size,
-                               int physical, int store_counts, void* workspace,
-                               size_t workspace_bytes, void* stream) {
-  if (ratio <= 0) return fail(QSA_ERR_INVALID, "qsa_topk_expand: ratio must be positive");
+namespace qsa {
+namespace {
+
+int topk_expand(const float* scores, int64_t score_row_stride, int rows, int cols,
+                const int32_t* lengths, const int64_t* positions, const int32_t* sequence_lengths,
+                int num_requests, const int32_t* token_to_req, const int32_t* table,
+                int64_t table_row_stride, int table_width, int32_t* output,
+                int64_t output_row_stride, int64_t output_col_stride, int output_width,
+                int32_t* counts, int ratio, int page_size, int physical, int store_counts,
+                void* workspace, size_t workspace_bytes, void* stream, const char* name) {
+  if (ratio <= 0) return fail(QSA_ERR_INVALID, std::string(name) + ": ratio must be positive");
   const int topk = output_width / ratio;
-  int st = check_common(scores, rows, cols, lengths, output, topk, "qsa_topk_expand");
+  int st = check_common(scores, rows, cols, lengths, output, topk, name);
   if (st != QSA_OK || rows == 0) return st;
   if (!positions || !sequence_lengths || !token_to_req)
-    return fail(QSA_ERR_INVALID, "qsa_topk_expand: null metadata pointer");
+    return fail(QSA_ERR_INVALID, std::string(name) + ": null metadata pointer");
   if (physical && (!table || page_size <= 0))
-    return fail(QSA_ERR_INVALID, "qsa_topk_expand: physical mapping needs a table and page_size");
-  if (store_counts && !counts) return fail(QSA_ERR_INVALID, "qsa_topk_expand: null counts");
+    return fail(QSA_ERR_INVALID,
+                std::string(name) + ": physical mapping needs a table and page_size");
+  if (store_counts && !counts) return fail(QSA_ERR_INVALID, std::string(name) + ": null counts");
   TopkArgs a = {};
   a.scores = scores;
   a.score_row_stride = score_row_stride;
@@ -399,6 +410,25 @@ extern "C" int qsa_topk_expand(const float* scores, int64_t score_row_stride, in
   a.meta.store_counts = store_counts ? 1 : 0;
   return launch_topk<true>(a, rows, cols, workspace, workspace_bytes,
                            static_cast<hipStream_t>(stream));
+}
+
+}  // namespace
+}  // namespace qsa
+
+extern "C" int qsa_topk_expand(const float* scores, int64_t score_row_stride, int rows, int cols,
+                               const int32_t* lengths, const int64_t* positions,
+                               const int32_t* sequence_lengths, int num_requests,
+                               const int32_t* token_to_req, const int32_t* table,
+                               int64_t table_row_stride, int table_width, int32_t* output,
+                               int64_t output_row_stride, int64_t output_col_stride,
+                               int output_width, int32_t* counts, int ratio, int page_size,
+                               int physical, int store_counts, void* workspace,
+                               size_t workspace_bytes, void* stream) {
+  return topk_expand(scores, score_row_stride, rows, cols, lengths, positions, sequence_lengths,
+                     num_requests, token_to_req, table, table_row_stride, table_width, output,
+                     output_row_stride, output_col_stride, output_width, counts, ratio, page_size,
+                     physical, store_counts, workspace, workspace_bytes, stream,
+                     "qsa_topk_expand");
 }
 
 extern "C" int qsa_expand_block_indices(const int32_t* block_indices, int64_t block_row_stride,

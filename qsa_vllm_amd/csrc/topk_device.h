@@ -9,10 +9,13 @@
 //    ExpandedWriter (topk.cu:97-180).
 //
 // Algorithm (own design for wave64 + LDS). One workgroup per row loads the
-// row coalesced into LDS and holds its keys in registers (blocked: thread t
-// owns ids [t*ITEMS, t*ITEMS+ITEMS)). Each full wave bounds the m-th largest
-// of its threads' maxima from below (m * full waves >= k); keys under the
-// smallest bound cannot be selected and are dropped. A radix select walks
+// row coalesced (thread t holds elements i * THREADS + t). Each full wave
+// bounds the m-th largest of its threads' maxima from below (m * full waves
+// >= k); keys under the smallest bound cannot be selected. A whole row
+// compacts the keys at or above the bound, in id order, straight from that
+// layout (process_row_whole); a row with too many of them, or a part of a
+// row, is staged through LDS so thread t owns ids [t*ITEMS, t*ITEMS+ITEMS)
+// and pruned the same way (process_row). A radix select walks
 // 8-bit digits downward from the highest bit in which the remaining keys
 // differ (one block min/max). Each pass builds an LDS histogram
 // (atomics with a wave-uniform fast path); after one barrier every wave reads
@@ -72,6 +75,7 @@ struct TopkShared {
   int wsel[THREADS / 64];
   int wtie[THREADS / 64];
   int tail_page[kTailSlots];
+  int ccount[16 * (THREADS / 64)];  // whole-row path: candidates per (item, wave)
 };
 
 // --- row metadata -------------------------------------------------------------
@@ -594,26 +598,25 @@ __device__ __forceinline__ void clear_histograms(TopkShared<THREADS>& sh) {
   for (int b = threadIdx.x; b < kHistBuffers * kBins; b += THREADS) (&sh.hist[0][0])[b] = 0u;
 }
 
-// Scores of elements [0, limit) of a contiguous row into the stage, then each
-// thread's ITEMS consecutive keys back into registers. Ends with the barrier
-// that also publishes the cleared histograms.
-template <int THREADS, int ITEMS, bool EXPAND, bool PAGES, typename Stage>
-__device__ __forceinline__ RowPrefetch stage_row(const DirectLoader& load, int limit,
-                                                 const ExpandMeta& m, int row, uint32_t (&key)[ITEMS],
-                                                 int (&id)[ITEMS], TopkShared<THREADS>& sh, Stage& st) {
+// The loads of a contiguous row's elements [0, limit): element i * THREADS +
+// tid's score (and, with PAGES, the physical page of its first token) in
+// thread tid's v[i] (pg[i]); the row metadata and causal-tail pages in the
+// returned prefetch.
+template <int THREADS, int ITEMS, bool EXPAND, bool PAGES>
+__device__ __forceinline__ RowPrefetch load_row(const DirectLoader& load, int limit,
+                                                const ExpandMeta& m, int row, uint32_t (&v)[ITEMS],
+                                                int (&pg)[ITEMS]) {
   const int tid = threadIdx.x;
   // Row metadata first: the tail and page loads depend on it, the scores do not.
   const int req = EXPAND ? m.token_to_req[row] : 0;
   const int pos = EXPAND ? (int)m.positions[row] : 0;
   const uint32_t* src = reinterpret_cast<const uint32_t*>(load.scores + load.start);
-  uint32_t v[ITEMS];
 #pragma unroll
   for (int i = 0; i < ITEMS; ++i) {
     const int e = i * THREADS + tid;
     v[i] = *(e < limit ? src + e : g_qsa_zero_rows);
   }
   const RowPrefetch f = prefetch_tail<EXPAND>(m, req, pos);
-  int pg[ITEMS];
   if (PAGES) {
 #pragma unroll
     for (int i = 0; i < ITEMS; ++i) {
@@ -621,6 +624,17 @@ __device__ __forceinline__ RowPrefetch stage_row(const DirectLoader& load, int l
       pg[i] = block_page(m, f.r, load.start + e, e < limit);
     }
   }
+  return f;
+}
+
+// The loaded scores (and pages) into the stage, then each thread's ITEMS
+// consecutive keys back into registers. Ends with the barrier that also
+// publishes the cleared histograms.
+template <int THREADS, int ITEMS, bool PAGES, typename Stage>
+__device__ __forceinline__ void stage_loaded(const DirectLoader& load, const uint32_t (&v)[ITEMS],
+                                             const int (&pg)[ITEMS], uint32_t (&key)[ITEMS],
+                                             int (&id)[ITEMS], TopkShared<THREADS>& sh, Stage& st) {
+  const int tid = threadIdx.x;
   clear_histograms(sh);
 #pragma unroll
   for (int i = 0; i < ITEMS; ++i) st.key[i * THREADS + tid] = v[i];
@@ -646,6 +660,18 @@ __device__ __forceinline__ RowPrefetch stage_row(const DirectLoader& load, int l
   }
 #pragma unroll
   for (int j = 0; j < ITEMS; ++j) id[j] = load.start + tid * ITEMS + j;
+}
+
+// Scores of elements [0, limit) of a contiguous row into the stage, then each
+// thread's ITEMS consecutive keys back into registers.
+template <int THREADS, int ITEMS, bool EXPAND, bool PAGES, typename Stage>
+__device__ __forceinline__ RowPrefetch stage_row(const DirectLoader& load, int limit,
+                                                 const ExpandMeta& m, int row, uint32_t (&key)[ITEMS],
+                                                 int (&id)[ITEMS], TopkShared<THREADS>& sh, Stage& st) {
+  uint32_t v[ITEMS];
+  int pg[ITEMS];
+  const RowPrefetch f = load_row<THREADS, ITEMS, EXPAND, PAGES>(load, limit, m, row, v, pg);
+  stage_loaded<THREADS, ITEMS, PAGES>(load, v, pg, key, id, sh, st);
   return f;
 }
 
@@ -675,6 +701,22 @@ __device__ __forceinline__ RowPrefetch stage_row(const IndirectLoader& load, int
   return f;
 }
 
+// Writes the selected row (sel[0..topk) ranked ids, sel[topk..) their first
+// slots) after the causal-tail pages are in LDS.
+template <int THREADS, bool EXPAND>
+__device__ __forceinline__ void write_row(const RowPrefetch& f, int topk, const ExpandMeta& m,
+                                          int row, int32_t* out, TopkShared<THREADS>& sh,
+                                          const int* sel) {
+  const int tid = threadIdx.x;
+  if (EXPAND && tid < kTailSlots && tid < m.ratio - 1) sh.tail_page[tid] = f.tail_ok ? f.tail_pp : -1;
+  lds_barrier();
+  if (EXPAND) {
+    write_expanded(m, f.r, row, topk, sel, sh.tail_page, out, THREADS);
+  } else {
+    for (int c = tid; c < topk; c += THREADS) out[c] = sel[c];
+  }
+}
+
 // Select and write one row from staged keys. `sel` (2 * topk ints) may alias
 // the key stage, which is dead once the keys are in registers.
 template <int THREADS, int ITEMS, bool EXPAND, bool PAGES, typename Loader, typename Stage>
@@ -702,13 +744,7 @@ __device__ __forceinline__ void finish_row(const Loader& load, const uint32_t (&
                           : -1;
     }
   }
-  if (EXPAND && tid < kTailSlots && tid < m.ratio - 1) sh.tail_page[tid] = f.tail_ok ? f.tail_pp : -1;
-  lds_barrier();
-  if (EXPAND) {
-    write_expanded(m, f.r, row, topk, sel, sh.tail_page, out, THREADS);
-  } else {
-    for (int c = tid; c < topk; c += THREADS) out[c] = sel[c];
-  }
+  write_row<THREADS, EXPAND>(f, topk, m, row, out, sh, sel);
 }
 
 // One row: stage the scores (and pages), select, write. PAGES stages the
@@ -727,6 +763,148 @@ __device__ __forceinline__ void process_row(const Loader& load, int limit, int l
   int id[ITEMS];
   const RowPrefetch f =
       stage_row<THREADS, ITEMS, EXPAND, PAGES>(load, limit, m, row, key, id, sh, st);
+  finish_row<THREADS, ITEMS, EXPAND, PAGES>(load, key, id, f, st, limit, length_raw, clamp, topk,
+                                            m, row, out, sh, sel);
+}
+
+// Radix select and ranking of `total` compacted candidates (keys, ids and
+// pages at index e of ckey / cid / cpage, in id order), C per thread.
+template <int THREADS, int C, bool PAGES>
+__device__ __forceinline__ void select_compacted(int total, int topk, uint32_t lo, uint32_t hi,
+                                                 const uint32_t* ckey, const int* cid,
+                                                 const int* cpage, const ExpandMeta& m,
+                                                 TopkShared<THREADS>& sh, int* sel) {
+  uint32_t ck[C];
+  int ci[C], cp[C];
+  uint32_t ccand = 0;
+#pragma unroll
+  for (int j = 0; j < C; ++j) {
+    const int e = C * (int)threadIdx.x + j;
+    const bool ok = e < total;
+    ck[j] = ok ? ckey[e] : 0u;
+    ci[j] = ok ? cid[e] : 0;
+    cp[j] = e;
+    ccand |= (uint32_t)ok << j;
+  }
+  radix_rank<THREADS, C, PAGES>(topk, lo, hi, ccand, ck, ci, cp, cpage, m, sh, sel);
+}
+
+// One whole contiguous row (load.start == 0), selected without staging its
+// keys. The workgroup bounds the loaded keys as select_long does (lo: the
+// smallest of the full waves' floors of the m-th largest of their threads'
+// maxima, at or below the k-th largest key; hi: the largest key), in the
+// layout the keys were loaded in, with one barrier. Each thread then tests
+// the elements it loaded (element i * THREADS + tid) against lo; the
+// candidates are compacted in id order (items, then waves, then lanes)
+// straight from the load layout, with their pages, after one barrier that
+// exchanges the per-(item, wave) counts, and the radix select and ranking run
+// on them. Against process_row this drops the staging round trip of every
+// key through LDS and one barrier. Rows with too many candidates to compact
+// take process_row's path with the scores already loaded.
+template <int THREADS, int ITEMS, bool EXPAND, bool PAGES, typename Stage>
+__device__ __forceinline__ void process_row_whole(const DirectLoader& load, int limit,
+                                                  int length_raw, int clamp, int topk,
+                                                  const ExpandMeta& m, int row, int32_t* out,
+                                                  TopkShared<THREADS>& sh, Stage& st, int* sel) {
+  constexpr int kWaves = THREADS / 64;
+  constexpr int kEntries = ITEMS * kWaves;  // (item, wave) counts, item-major
+  static_assert(ITEMS <= 16 && 64 % kWaves == 0, "count layout");
+  // Compacted keys and ids take the key stage, their pages the page stage.
+  constexpr int kCompact = ITEMS / 2 < 2 ? ITEMS / 2 : 2;
+  static_assert(kCompact >= 1 && 2 * kCompact <= ITEMS, "compaction must fit the stage");
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  uint32_t v[ITEMS];
+  int pg[ITEMS];
+  const RowPrefetch f = load_row<THREADS, ITEMS, EXPAND, PAGES>(load, limit, m, row, v, pg);
+  const int length = length_raw > topk ? min(length_raw, clamp) : length_raw;
+  constexpr uint32_t kNoBound = 0xffffffffu;
+  uint32_t lo = kNoBound, hi = 0u;
+  if (length > topk) {
+    clear_histograms(sh);
+    // Thread tid is active iff tid < length (element tid is its first); each
+    // thread's maximum is one of its own elements, so a full wave's floor of
+    // the m-th largest maximum is reached by m of its elements, and the full
+    // waves together by m * full >= topk.
+    uint32_t tmax = 0u;
+#pragma unroll
+    for (int i = 0; i < ITEMS; ++i)
+      if (i * THREADS + tid < length) tmax = max(tmax, v[i]);
+    const int full = min(THREADS, length) / 64;
+    const int mm = full > 0 ? (topk + full - 1) / full : 65;
+    const uint32_t wf = mm <= 64 && wave < full ? wave_floor_mth_largest(tmax, mm) : kNoBound;
+    const uint32_t wm = __ockl_wfred_max_u32(tid < length ? tmax : 0u);
+    if (lane == 0) {
+      sh.wfloor[wave] = wf;
+      sh.wmax[wave] = wm;
+    }
+    lds_barrier();
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) {
+      lo = min(lo, sh.wfloor[w]);
+      hi = max(hi, sh.wmax[w]);
+    }
+  }
+  if (length > topk && lo != kNoBound && lo <= hi) {
+    uint32_t cand = 0;
+    int below[ITEMS];  // candidates of item i in lower lanes of this wave
+#pragma unroll
+    for (int i = 0; i < ITEMS; ++i) {
+      const bool c = i * THREADS + tid < length && v[i] >= lo;
+      cand |= (uint32_t)c << i;
+      const uint64_t bal = __ballot(c);
+      below[i] = __builtin_amdgcn_mbcnt_hi((uint32_t)(bal >> 32),
+                                           __builtin_amdgcn_mbcnt_lo((uint32_t)bal, 0u));
+      if (lane == 0) sh.ccount[i * kWaves + wave] = __builtin_popcountll(bal);
+    }
+    lds_barrier();
+    // Exclusive prefix over the (item, wave) entries; entry x sits in lane
+    // x % 64 of group x / 64, and item i's entries stay within group
+    // i * kWaves / 64.
+    constexpr int kGroups = (kEntries + 63) / 64;
+    int pre[kGroups];
+    int total = 0;
+#pragma unroll
+    for (int g = 0; g < kGroups; ++g) {
+      const int x = g * 64 + lane;
+      const int c = x < kEntries ? sh.ccount[x] : 0;
+      const int ex = __ockl_wfscan_add_i32(c, false);
+      pre[g] = total + ex;
+      total += __builtin_amdgcn_readlane(ex + c, 63);
+    }
+    if (total <= kCompact * THREADS) {
+      // Up to THREADS candidates: one per thread (the usual case, and the
+      // cheapest radix passes); more: kCompact per thread.
+      uint32_t* ckey = st.key;
+      int* cid = reinterpret_cast<int*>(st.key + kCompact * THREADS);
+      int* cpage = st.page;
+#pragma unroll
+      for (int i = 0; i < ITEMS; ++i) {
+        const int x = i * kWaves + wave;
+        const int base = __builtin_amdgcn_readlane(pre[(i * kWaves) / 64], x % 64);
+        if ((cand >> i) & 1u) {
+          const int o = base + below[i];
+          ckey[o] = v[i];
+          cid[o] = load.start + i * THREADS + tid;
+          if (PAGES) cpage[o] = pg[i];
+        }
+      }
+      lds_barrier();
+      // sel shares the key stage's first 2 * topk words (topk <= total <=
+      // kCompact * THREADS); radix_rank writes it after its rank scan's
+      // barrier, when every candidate is in registers.
+      if (kCompact == 1 || total <= THREADS)
+        select_compacted<THREADS, 1, PAGES>(total, topk, lo, hi, ckey, cid, cpage, m, sh, sel);
+      else
+        select_compacted<THREADS, kCompact, PAGES>(total, topk, lo, hi, ckey, cid, cpage, m, sh,
+                                                  sel);
+      write_row<THREADS, EXPAND>(f, topk, m, row, out, sh, sel);
+      return;
+    }
+    lds_barrier();  // every wave has read the counts before they are reused
+  }
+  uint32_t key[ITEMS];
+  int id[ITEMS];
+  stage_loaded<THREADS, ITEMS, PAGES>(load, v, pg, key, id, sh, st);
   finish_row<THREADS, ITEMS, EXPAND, PAGES>(load, key, id, f, st, limit, length_raw, clamp, topk,
                                             m, row, out, sh, sel);
 }

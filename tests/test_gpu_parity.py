@@ -254,6 +254,43 @@ def _attn_check(got, want, what):
     assert err.max().item() <= MAX_ABS and err.mean().item() <= MEAN_ABS, what
 
 
+# A whole row is compacted to the keys at or above its bound: one per thread
+# up to THREADS of them, two per thread up to 2 x THREADS, staged through LDS
+# beyond. Rows whose top keys are `ones` tied maxima scattered over the row put
+# the candidate count below, between and above those limits for the 512 x 2
+# (1000 columns), 512 x 4 (2048) and 1024 x 8 (8192) launch shapes.
+@pytest.mark.parametrize("cols,ones", [(1000, 100), (1000, 600), (2048, 300), (2048, 700),
+                                       (2048, 1100), (8192, 900), (8192, 1500), (8192, 2500)])
+def test_topk_whole_row_candidate_counts(cols, ones):
+    _note(f"topk whole-row candidates cols={cols} ones={ones}")
+    g = torch.Generator().manual_seed(cols + ones)
+    rows, k, ratio, page = 6, 128, 16, 16
+    scores = torch.rand(rows, cols, generator=g) * 0.5
+    for r in range(rows):
+        hot = torch.randperm(cols, generator=g)[:ones]
+        scores[r, hot] = 1.0 + (r % 2) * torch.randint(0, 3, (ones,), generator=g).float()
+    lengths = torch.full((rows,), cols, dtype=torch.int32)
+    lengths[5] = cols // 2
+    width = k * ratio + ratio - 1
+    seq = lengths.long() * ratio + 7
+    pos = seq - 1
+    t2r = torch.arange(rows, dtype=torch.int32)
+    table = torch.randperm(rows * (cols + 1), generator=g).view(rows, cols + 1).to(torch.int32)
+    for physical in (False, True):
+        idx = torch.full((rows, width), -9, dtype=torch.int32, device=DEV)
+        cnt = torch.full((rows,), -9, dtype=torch.int32, device=DEV)
+        topk_expand(scores.to(DEV), lengths.to(DEV), pos.to(DEV), seq.to(torch.int32).to(DEV),
+                    t2r.to(DEV), idx, ratio,
+                    main_block_table=table.to(DEV) if physical else None, main_page_size=page,
+                    valid_counts_out=cnt)
+        torch.cuda.synchronize()
+        want, want_cnt = oracle.topk_expand(scores, lengths, pos, seq.to(torch.int32), t2r,
+                                            table if physical else None, width, ratio, page,
+                                            physical)
+        assert torch.equal(idx.cpu(), want), f"physical={physical}"
+        assert torch.equal(cnt.cpu(), want_cnt)
+
+
 def _random_physical_indices(g, rows, width, num_blocks, page, counts):
     idx = torch.randint(0, num_blocks * page, (rows, width), generator=g, dtype=torch.int32)
     idx[torch.rand(rows, width, generator=g) < 0.05] = -1
