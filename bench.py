@@ -152,6 +152,7 @@ def main():
             "graph": "HIP graph per block of steps",
         },
         "roofline": dict(m["roofline"], traffic=traffic),
+        "step_roofline": m["step_roofline"],
         "breakdown_us": m["breakdown_us"],
         "eager": m["eager"],
         "indexer_gbps": m["indexer_gbps"],
@@ -239,7 +240,7 @@ def measure_decode(wl, steps, warmup, n_sets, eager=False):
 
     from qsa_vllm_amd.graph_dispatch import decode_logits_columns
     from qsa_vllm_amd.ops import qsa_sparse_paged_attention, select_paged_tokens, topk_expand
-    from qsa_vllm_amd.workloads import attention_bytes, indexer_bytes
+    from qsa_vllm_amd.workloads import attention_bytes, decode_step_bytes, indexer_bytes
 
     s = wl.shape
     rows = wl.rows
@@ -365,6 +366,8 @@ def measure_decode(wl, steps, warmup, n_sets, eager=False):
 
     attn_bytes = sum(attention_bytes(wl, counts[i]) for i in range(n_sets)) / n_sets
     attn_gbps = attn_bytes / (attn_us * 1e-6) / 1e9
+    step_bytes = sum(decode_step_bytes(wl, counts[i]) for i in range(n_sets)) / n_sets
+    step_gbps = step_bytes / (us_step * 1e-6) / 1e9
     out.update({
         "query_sets": n_sets,
         "us_per_step": us_step,
@@ -378,6 +381,18 @@ def measure_decode(wl, steps, warmup, n_sets, eager=False):
             "frac": round(attn_gbps / HBM_PEAK_GBPS, 4),
             "algorithmic_bytes_per_launch": int(attn_bytes),
             "us_per_launch": round(attn_us, 3),
+        },
+        # The whole step (indexer + top-k + attention + merge, graph-replayed)
+        # against the HBM time of its algorithmic bytes.
+        "step_roofline": {
+            "bound": "hbm",
+            "achieved": round(step_gbps, 1),
+            "peak": HBM_PEAK_GBPS,
+            "unit": "GB/s",
+            "frac": round(step_gbps / HBM_PEAK_GBPS, 4),
+            "algorithmic_bytes_per_step": int(step_bytes),
+            "floor_us": round(step_bytes / (HBM_PEAK_GBPS * 1e3), 3),
+            "us_per_step": round(us_step, 3),
         },
         "breakdown_us": {
             "indexer_decode": round(index_us, 3),
@@ -403,7 +418,8 @@ def workload_summary(name, dev, steps=40, warmup=8):
         out = {"workload": describe(wl.shape), "rows": wl.rows,
                "tokens_per_s": m["tokens_per_s"], "us_per_step": round(m["us_per_step"], 3),
                "breakdown_us": m["breakdown_us"], "logits_columns": m["logits_columns"],
-               "roofline": m["roofline"], "indexer_gbps": m["indexer_gbps"]}
+               "roofline": m["roofline"], "step_roofline": m["step_roofline"],
+               "indexer_gbps": m["indexer_gbps"]}
     else:
         m = measure_prefill(wl, steps=5, warmup=2)
         out = {"workload": describe(wl.shape), "rows": wl.rows,

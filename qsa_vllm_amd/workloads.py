@@ -272,6 +272,23 @@ def indexer_bytes(wl: QSAWorkload) -> int:
     return vis * s.index_dim * 2 + wl.rows * s.index_heads * s.index_dim * 2 + vis * 4
 
 
+def topk_bytes(wl: QSAWorkload) -> int:
+    """Algorithmic bytes of the decode top-k + expansion to physical slots: the
+    visible logits read, the W index columns and the count written, the
+    page-table entry of every selected block and the row's position, sequence
+    length and request id."""
+    s = wl.shape
+    vis = wl.visible.to(torch.int64)
+    k = s.token_topk // s.compress_ratio
+    selected = int(vis.clamp(max=k).sum())
+    return int(vis.sum()) * 4 + wl.rows * ((s.width + 1) * 4 + 12) + selected * 4
+
+
+def decode_step_bytes(wl: QSAWorkload, counts: torch.Tensor) -> int:
+    """Algorithmic HBM bytes of one decode step: indexer + top-k + attention."""
+    return indexer_bytes(wl) + topk_bytes(wl) + attention_bytes(wl, counts)
+
+
 def indexer_flops(wl: QSAWorkload) -> int:
     s = wl.shape
     return 2 * s.index_heads * s.index_dim * int(wl.visible.to(torch.int64).sum())

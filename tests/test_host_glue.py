@@ -119,3 +119,23 @@ def test_decode_config_ignored_for_prefill_rows():
     assert choose_num_splits(q, k, idx, False, None) == lib_choice
     with pytest.raises(ValueError):
         choose_num_splits(q, k, idx, True, (0, 4, 4))
+
+
+def test_decode_step_bytes_adds_the_three_launches():
+    """The bench's whole-step roofline counts the indexer, the top-k (one
+    page-table entry per selected block, at most k per row) and the attention."""
+    from qsa_vllm_amd.workloads import (QSAShape, attention_bytes, decode_step_bytes,
+                                        indexer_bytes, make_workload, topk_bytes)
+
+    shape = QSAShape("tiny_decode", batch=4, num_q_heads=4, num_kv_heads=1, head_dim=64,
+                     page_size=16, compress_ratio=16, index_heads=4, index_dim=64,
+                     token_topk=256, seq_len_min=40, seq_len_max=600, seed=0)
+    wl = make_workload(shape)
+    k = shape.token_topk // shape.compress_ratio
+    vis = [int(v) for v in wl.visible]
+    assert min(vis) < k < max(vis)  # rows on both sides of k
+    want_topk = sum(v * 4 + (shape.width + 1) * 4 + 12 + min(v, k) * 4 for v in vis)
+    assert topk_bytes(wl) == want_topk
+    counts = shape.token_topk + wl.seq_lens % shape.compress_ratio
+    assert decode_step_bytes(wl, counts) == (indexer_bytes(wl) + want_topk
+                                             + attention_bytes(wl, counts))
