@@ -123,11 +123,35 @@ __global__ __launch_bounds__(kAdaptiveThreads) void topk_adaptive_kernel(const T
   auto& sh = shu.full;
   __shared__ __attribute__((aligned(16))) uint32_t stage_mem[T * 16 * 2];
   const int row = blockIdx.x;
-  const int length = a.lengths[row];
-  const int n = min(max(length, 0), a.cols);
   const float* srow = a.scores + (int64_t)row * a.score_row_stride;
   int32_t* out = a.out + (int64_t)row * a.out_row_stride;
   const int topk = a.topk;
+  // Rows of up to kNarrowCols keys (the usual decode batch in a wide class)
+  // run on the lower waves in the 512 x 4 shape. Their loads go out before
+  // the row's length is known: every row of this kernel has more columns than
+  // that, so they stay inside the row, and a short row waits for one round
+  // trip instead of the length's and then its scores'.
+  constexpr int kNarrowCols = kAdaptiveNarrow * 4;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // uniform branches
+  if (wave < kAdaptiveNarrow / 64 && 2 * topk <= kNarrowCols) {
+    const DirectLoader load{srow, 0};
+    uint32_t v[4];
+    int pg[4];
+    const RowPrefetch f =
+        load_row<kAdaptiveNarrow, 4, EXPAND, PAGES>(load, kNarrowCols, a.meta, row, v, pg);
+    // Nothing below may wait for the length before the loads above are out.
+    __builtin_amdgcn_sched_barrier(0);
+    const int length = a.lengths[row];
+    if (length <= kNarrowCols) {  // n <= kNarrowCols (every row here has more columns)
+      auto& st = *reinterpret_cast<TopkStage<kAdaptiveNarrow, 4, PAGES>*>(stage_mem);
+      process_loaded_whole<kAdaptiveNarrow, 4, EXPAND, PAGES>(
+          load, kNarrowCols, v, pg, f, length, a.cols, topk, a.meta, row, out, shu.narrow, st,
+          reinterpret_cast<int*>(st.key));
+      return;
+    }
+  }
+  const int length = a.lengths[row];
+  const int n = min(max(length, 0), a.cols);
 #define QSA_ADAPTIVE_ROW(ITEMS, LOAD, LIMIT, LENGTH, CLAMP)                                     \
   {                                                                                             \
     auto& st = *reinterpret_cast<TopkStage<T, ITEMS, PAGES>*>(stage_mem);                      \
@@ -148,18 +172,12 @@ __global__ __launch_bounds__(kAdaptiveThreads) void topk_adaptive_kernel(const T
     // per thread, so the candidates the bound leaves are compacted to one per
     // thread.
     const int need = max(n, 2 * topk);
-    if (need <= kAdaptiveNarrow * 4) {
-      // The upper waves end here. A barrier waits only for the waves of the
-      // workgroup that have not ended, so the lower half runs the 512-thread
-      // row with its own barriers; fewer waves per barrier and per block scan
-      // make each phase of a short row cheaper.
-      if (threadIdx.x >= kAdaptiveNarrow) return;
-      auto& st = *reinterpret_cast<TopkStage<kAdaptiveNarrow, 4, PAGES>*>(stage_mem);
-      process_row_whole<kAdaptiveNarrow, 4, EXPAND, PAGES>(load, n, length, a.cols, topk, a.meta,
-                                                           row, out, shu.narrow, st,
-                                                           reinterpret_cast<int*>(st.key));
-      return;
-    }
+    // A short row was selected above by the lower waves; the upper waves end
+    // here. A barrier waits only for the waves of the workgroup that have not
+    // ended, so the lower half runs the 512-thread row with its own barriers;
+    // fewer waves per barrier and per block scan make each phase of a short
+    // row cheaper.
+    if (need <= kNarrowCols) return;
     if (need <= T * 4) QSA_ADAPTIVE_WHOLE_ROW(4)
     else if (need <= T * 8) QSA_ADAPTIVE_WHOLE_ROW(8)
     else QSA_ADAPTIVE_WHOLE_ROW(16)

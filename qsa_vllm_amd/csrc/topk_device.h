@@ -801,11 +801,17 @@ __device__ __forceinline__ void select_compacted(int total, int topk, uint32_t l
 // on them. Against process_row this drops the staging round trip of every
 // key through LDS and one barrier. Rows with too many candidates to compact
 // take process_row's path with the scores already loaded.
+//
+// process_loaded_whole is the same row after load_row: a caller may issue the
+// loads before it knows the row's length (any limit >= the clamped length
+// gives the same result; elements past the length are never selected).
 template <int THREADS, int ITEMS, bool EXPAND, bool PAGES, typename Stage>
-__device__ __forceinline__ void process_row_whole(const DirectLoader& load, int limit,
-                                                  int length_raw, int clamp, int topk,
-                                                  const ExpandMeta& m, int row, int32_t* out,
-                                                  TopkShared<THREADS>& sh, Stage& st, int* sel) {
+__device__ __forceinline__ void process_loaded_whole(const DirectLoader& load, int limit,
+                                                     const uint32_t (&v)[ITEMS],
+                                                     const int (&pg)[ITEMS], const RowPrefetch& f,
+                                                     int length_raw, int clamp, int topk,
+                                                     const ExpandMeta& m, int row, int32_t* out,
+                                                     TopkShared<THREADS>& sh, Stage& st, int* sel) {
   constexpr int kWaves = THREADS / 64;
   constexpr int kEntries = ITEMS * kWaves;  // (item, wave) counts, item-major
   static_assert(ITEMS <= 16 && 64 % kWaves == 0, "count layout");
@@ -813,9 +819,6 @@ __device__ __forceinline__ void process_row_whole(const DirectLoader& load, int 
   constexpr int kCompact = ITEMS / 2 < 2 ? ITEMS / 2 : 2;
   static_assert(kCompact >= 1 && 2 * kCompact <= ITEMS, "compaction must fit the stage");
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  uint32_t v[ITEMS];
-  int pg[ITEMS];
-  const RowPrefetch f = load_row<THREADS, ITEMS, EXPAND, PAGES>(load, limit, m, row, v, pg);
   const int length = length_raw > topk ? min(length_raw, clamp) : length_raw;
   constexpr uint32_t kNoBound = 0xffffffffu;
   uint32_t lo = kNoBound, hi = 0u;
@@ -907,6 +910,18 @@ __device__ __forceinline__ void process_row_whole(const DirectLoader& load, int 
   stage_loaded<THREADS, ITEMS, PAGES>(load, v, pg, key, id, sh, st);
   finish_row<THREADS, ITEMS, EXPAND, PAGES>(load, key, id, f, st, limit, length_raw, clamp, topk,
                                             m, row, out, sh, sel);
+}
+
+template <int THREADS, int ITEMS, bool EXPAND, bool PAGES, typename Stage>
+__device__ __forceinline__ void process_row_whole(const DirectLoader& load, int limit,
+                                                  int length_raw, int clamp, int topk,
+                                                  const ExpandMeta& m, int row, int32_t* out,
+                                                  TopkShared<THREADS>& sh, Stage& st, int* sel) {
+  uint32_t v[ITEMS];
+  int pg[ITEMS];
+  const RowPrefetch f = load_row<THREADS, ITEMS, EXPAND, PAGES>(load, limit, m, row, v, pg);
+  process_loaded_whole<THREADS, ITEMS, EXPAND, PAGES>(load, limit, v, pg, f, length_raw, clamp,
+                                                      topk, m, row, out, sh, st, sel);
 }
 
 }  // namespace
