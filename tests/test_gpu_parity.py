@@ -248,6 +248,41 @@ def test_indexer_prefill_many_requests(dim, heads):
         assert torch.allclose(got[written], want[written], rtol=2e-5, atol=2e-4), (offset, n)
 
 
+@pytest.mark.parametrize("dim,heads", [(128, 32), (64, 20)])
+def test_indexer_prefill_balanced_launch(dim, heads):
+    """Launches of more than 128 row tiles score each row tile's whole key
+    range in one workgroup (no key chunks). Causal chunks of three requests
+    give row tiles of 1 to 8 key tiles; 151 row tiles (the last partial), a
+    span starting inside a request, and random visibility."""
+    _note(f"indexer_prefill balanced launch dim={dim} heads={heads}")
+    g = torch.Generator().manual_seed(29)
+    cpage, width = 16, 40
+    lens = [1500, 1310, 2000]
+    prefix = [0, 3000, 6000]
+    nreq = len(lens)
+    qsl = torch.tensor([0] + list(torch.cumsum(torch.tensor(lens), 0)), dtype=torch.int32)
+    rows = sum(lens)
+    q = torch.randn(rows, heads, dim, generator=g).to(torch.bfloat16)
+    blocks = nreq * width
+    cache = torch.randn(blocks, cpage, 1, dim, generator=g).to(torch.bfloat16)
+    table = torch.randperm(blocks, generator=g).view(nreq, width).to(torch.int32)
+    lw = width * cpage
+    causal = torch.cat([(torch.arange(n) + prefix[r] + 1) // 16 for r, n in enumerate(lens)])
+    cases = [(causal.clamp_max(lw).to(torch.int32), 0, rows),
+             (causal.clamp_max(lw).to(torch.int32), 600, 4200),
+             (torch.randint(0, lw + 1, (rows,), generator=g, dtype=torch.int32), 0, rows)]
+    for vis, offset, n in cases:
+        want = oracle.indexer_scores_prefill(q, cache, table, qsl, vis, offset, n, lw)
+        logits = torch.full((n, lw), float("nan"), device=DEV)
+        torch.ops.yulan_qsa_kernels.indexer_prefill(q.to(DEV), cache.to(DEV), table.to(DEV),
+                                                    qsl.to(DEV), vis.to(DEV), logits, offset, n,
+                                                    max(lens))
+        got = logits.cpu()
+        written = ~torch.isnan(want)
+        assert torch.equal(written, ~torch.isnan(got)), (offset, n)
+        assert torch.allclose(got[written], want[written], rtol=2e-5, atol=2e-4), (offset, n)
+
+
 def _attn_check(got, want, what):
     err = (got.float().cpu() - want).abs()
     _note(f"{what}: max_abs={err.max().item():.3e} mean_abs={err.mean().item():.3e}")
