@@ -128,24 +128,26 @@ __global__ __launch_bounds__(kAdaptiveThreads) void topk_adaptive_kernel(const T
   const int topk = a.topk;
   // Rows of up to kNarrowCols keys (the usual decode batch in a wide class)
   // run on the lower waves in the 512 x 4 shape. Their loads go out before
-  // the row's length is known: every row of this kernel has more columns than
-  // that, so they stay inside the row, and a short row waits for one round
-  // trip instead of the length's and then its scores'.
+  // the row's length is known (the first min(kNarrowCols, cols) columns, all
+  // inside the row; the launch gives this kernel rows of more than
+  // kNarrowCols columns), so a short row waits for one round trip instead of
+  // the length's and then its scores'.
   constexpr int kNarrowCols = kAdaptiveNarrow * 4;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // uniform branches
   if (wave < kAdaptiveNarrow / 64 && 2 * topk <= kNarrowCols) {
     const DirectLoader load{srow, 0};
+    const int limit = min(kNarrowCols, a.cols);
     uint32_t v[4];
     int pg[4];
     const RowPrefetch f =
-        load_row<kAdaptiveNarrow, 4, EXPAND, PAGES>(load, kNarrowCols, a.meta, row, v, pg);
+        load_row<kAdaptiveNarrow, 4, EXPAND, PAGES>(load, limit, a.meta, row, v, pg);
     // Nothing below may wait for the length before the loads above are out.
     __builtin_amdgcn_sched_barrier(0);
     const int length = a.lengths[row];
-    if (length <= kNarrowCols) {  // n <= kNarrowCols (every row here has more columns)
+    if (min(length, a.cols) <= kNarrowCols) {  // n <= kNarrowCols
       auto& st = *reinterpret_cast<TopkStage<kAdaptiveNarrow, 4, PAGES>*>(stage_mem);
       process_loaded_whole<kAdaptiveNarrow, 4, EXPAND, PAGES>(
-          load, kNarrowCols, v, pg, f, length, a.cols, topk, a.meta, row, out, shu.narrow, st,
+          load, limit, v, pg, f, length, a.cols, topk, a.meta, row, out, shu.narrow, st,
           reinterpret_cast<int*>(st.key));
       return;
     }
