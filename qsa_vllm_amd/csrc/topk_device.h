@@ -892,6 +892,24 @@ __device__ __forceinline__ void process_loaded_whole(const DirectLoader& load, i
         }
       }
       lds_barrier();
+      // A 1024-thread row hands up to 1024 candidates to its lower 512
+      // threads and the upper waves end: a barrier waits only for the waves
+      // that have not ended, so every radix pass, block scan and barrier of
+      // the selection and the row writer spans half the waves (the
+      // histogram sits at the start of the shared block in both layouts,
+      // already cleared).
+      if constexpr (THREADS == 1024) {
+        if (total <= 1024) {
+          if (__builtin_amdgcn_readfirstlane(wave) >= 8) return;  // a uniform branch: the wave ends
+          auto& sh2 = *reinterpret_cast<TopkShared<512>*>(&sh);
+          if (total <= 512)
+            select_compacted<512, 1, PAGES>(total, topk, lo, hi, ckey, cid, cpage, m, sh2, sel);
+          else
+            select_compacted<512, 2, PAGES>(total, topk, lo, hi, ckey, cid, cpage, m, sh2, sel);
+          write_row<512, EXPAND>(f, topk, m, row, out, sh2, sel);
+          return;
+        }
+      }
       // sel shares the key stage's first 2 * topk words (topk <= total <=
       // kCompact * THREADS); radix_rank writes it after its rank scan's
       // barrier, when every candidate is in registers.

@@ -59,6 +59,7 @@ def test_topk_bit_exact(cols, k, mode):
     lengths[0], lengths[1], lengths[2] = cols, k, min(cols, k + 1)
     if rows > 5:  # lengths at the per-thread size boundaries of the row-sized shape
         lengths[3], lengths[4], lengths[5] = min(cols, 2048), min(cols, 2049), min(cols, 16385)
+    lengths[-1] = -5  # a negative length selects nothing (ids -1), like a length of 0
     want = oracle.topk_ids(scores, lengths, k)
     out = torch.full((rows, k), -7, dtype=torch.int32, device=DEV)
     topk(scores.to(DEV), lengths.to(DEV), out)
@@ -291,11 +292,13 @@ def _attn_check(got, want, what):
 
 # A whole row is compacted to the keys at or above its bound: one per thread
 # up to THREADS of them, two per thread up to 2 x THREADS, staged through LDS
-# beyond. Rows whose top keys are `ones` tied maxima scattered over the row put
+# beyond; a 1024-thread row hands up to 1024 candidates to its lower 512
+# threads. Rows whose top keys are `ones` tied maxima scattered over the row put
 # the candidate count below, between and above those limits for the 512 x 2
-# (1000 columns), 512 x 4 (2048) and 1024 x 8 (8192) launch shapes.
+# (1000 columns), 512 x 4 (2048), 1024 x 4 (4096) and 1024 x 8 (8192) shapes.
 @pytest.mark.parametrize("cols,ones", [(1000, 100), (1000, 600), (2048, 300), (2048, 700),
-                                       (2048, 1100), (8192, 900), (8192, 1500), (8192, 2500)])
+                                       (2048, 1100), (4096, 300), (4096, 700), (8192, 300),
+                                       (8192, 900), (8192, 1500), (8192, 2500)])
 def test_topk_whole_row_candidate_counts(cols, ones):
     _note(f"topk whole-row candidates cols={cols} ones={ones}")
     g = torch.Generator().manual_seed(cols + ones)
