@@ -99,18 +99,30 @@ __device__ __forceinline__ RopeLane rope_lane(const NormRope& nr, int64_t pos, i
   return r;
 }
 
-// RMSNorm + partial RoPE of one row held by a 16-lane group; lane j holds
-// dims 8 j .. 8 j + 7 in x (zeros past the row). Every lane of the group
-// must call it (it shuffles within the group).
-__device__ __forceinline__ u32x4 norm_rope_apply(const NormRope& nr, const RopeLane& rl, u32x4 x) {
+// This lane's exact partial sum of squares of x (each bf16 square is exact in
+// fp32, and the sums of 128 of them are exact in double).
+__device__ __forceinline__ double lane_sumsq(u32x4 x) {
   float f[8];
   unpack8(x, f);
   double ss = 0.0;
 #pragma unroll
-  for (int i = 0; i < 8; ++i) ss += (double)(f[i] * f[i]);  // each square is exact
-  ss = group_sum(ss);
+  for (int i = 0; i < 8; ++i) ss += (double)(f[i] * f[i]);
+  return ss;
+}
+
+// 1 / sqrt(fp32(sum) / dim + eps), evaluated in double and rounded to fp32.
+__device__ __forceinline__ float inv_rms(const NormRope& nr, double ss) {
   const float mean = __fdiv_rn((float)ss, (float)nr.dim);
-  const float inv = (float)__ddiv_rn(1.0, __dsqrt_rn((double)__fadd_rn(mean, nr.eps)));
+  return (float)__ddiv_rn(1.0, __dsqrt_rn((double)__fadd_rn(mean, nr.eps)));
+}
+
+// RMSNorm (with the row's inverse RMS `inv`) + partial RoPE of one row held
+// by a 16-lane group; lane j holds dims 8 j .. 8 j + 7 in x (zeros past the
+// row). Every lane of the group must call it (it shuffles within the group).
+__device__ __forceinline__ u32x4 norm_rope_scaled(const NormRope& nr, const RopeLane& rl, u32x4 x,
+                                                  float inv) {
+  float f[8];
+  unpack8(x, f);
   float gamma[8];
   unpack8(rl.gamma, gamma);
   float scaled[8];
@@ -133,6 +145,11 @@ __device__ __forceinline__ u32x4 norm_rope_apply(const NormRope& nr, const RopeL
     out[i] = a + b;  // rounded to bf16 by pack8
   }
   return pack8(out);
+}
+
+// The same for a row whose inverse RMS is not known yet.
+__device__ __forceinline__ u32x4 norm_rope_apply(const NormRope& nr, const RopeLane& rl, u32x4 x) {
+  return norm_rope_scaled(nr, rl, x, inv_rms(nr, group_sum(lane_sumsq(x))));
 }
 
 // Row load (zeros for lanes past the row or when !ok).
@@ -194,8 +211,13 @@ struct PrepareArgs {
 };
 
 // Rows a lane loads before it uses any: loads in a loop whose trip count is
-// only known at run time would otherwise each wait out a round trip.
-constexpr int kBatch = 16;
+// only known at run time would otherwise each wait out a round trip. The
+// preparation launch loads 8 at a time: its register footprint then allows 5
+// waves per SIMD instead of 3 (64 decode tokens: 8.5 against 9.2 us; the
+// prefill launch the same within noise). The stand-alone compression kernel
+// loads 16.
+constexpr int kBatch = 8;
+constexpr int kCompressBatch = 16;
 // Query heads of one token per row group: they share the position's rotary
 // slices, and eight rows per group keep enough bytes in flight.
 constexpr int kQHeads = 8;
@@ -284,7 +306,11 @@ __device__ void prepare_group(const PrepareArgs& a, int q, int w, int j) {
 }
 
 // kQHeads query heads of one token: every row load is issued before the
-// first row is normalised.
+// first row is normalised. The eight rows' sums of squares are reduce-scattered
+// over the group (lanes 2 r and 2 r + 1 end with row r's exact sum), so one
+// double-precision inverse-RMS evaluation per lane serves all eight rows, and
+// row r's value is read from lane 2 r.
+static_assert(kQHeads == 8 && kGroupLanes == 16, "the reduce-scatter pairs 8 rows with 16 lanes");
 __device__ __forceinline__ void norm_rope_heads(const NormRope& nr, const uint16_t* token_row,
                                                 int64_t head_stride, int h0, int heads,
                                                 int64_t pos, bool ok, uint16_t* out_row, int j) {
@@ -293,9 +319,34 @@ __device__ __forceinline__ void norm_rope_heads(const NormRope& nr, const uint16
   for (int i = 0; i < kQHeads; ++i)
     x[i] = load_row(token_row + (int64_t)(h0 + i) * head_stride, j, nr.dim, ok && h0 + i < heads);
   const RopeLane rl = rope_lane(nr, pos, j);
+  double ps[kQHeads];
+#pragma unroll
+  for (int i = 0; i < kQHeads; ++i) ps[i] = lane_sumsq(x[i]);
+  // Each level keeps half of the rows (by one bit of j) and adds the
+  // partner lane's partial sums of the same rows; the sums are exact, so the
+  // order of the additions does not matter.
+  const bool b3 = (j & 8) != 0, b2 = (j & 4) != 0, b1 = (j & 2) != 0;
+  double s4[4];
+#pragma unroll
+  for (int t = 0; t < 4; ++t) {
+    const double keep = b3 ? ps[4 + t] : ps[t];
+    const double give = b3 ? ps[t] : ps[4 + t];
+    s4[t] = keep + __shfl_xor(give, 8, kGroupLanes);
+  }
+  double s2[2];
+#pragma unroll
+  for (int t = 0; t < 2; ++t) {
+    const double keep = b2 ? s4[2 + t] : s4[t];
+    const double give = b2 ? s4[t] : s4[2 + t];
+    s2[t] = keep + __shfl_xor(give, 4, kGroupLanes);
+  }
+  double s1 = (b1 ? s2[1] : s2[0]) + __shfl_xor(b1 ? s2[0] : s2[1], 2, kGroupLanes);
+  s1 += __shfl_xor(s1, 1, kGroupLanes);  // row (j >> 1), summed over all 16 lanes
+  const float inv_lane = inv_rms(nr, s1);
 #pragma unroll
   for (int i = 0; i < kQHeads; ++i) {
-    const u32x4 out = norm_rope_apply(nr, rl, x[i]);
+    const float inv = __shfl(inv_lane, 2 * i, kGroupLanes);
+    const u32x4 out = norm_rope_scaled(nr, rl, x[i], inv);
     if (ok && h0 + i < heads) store_row(out_row + (int64_t)(h0 + i) * nr.dim, j, nr.dim, out);
   }
 }
@@ -436,10 +487,10 @@ __global__ __launch_bounds__(kPrepThreads) void compress_groups_kernel(const Com
   const bool ring_ok = sblock >= 0 && sblock < a.num_state_blocks;
   const uint16_t* ring = a.state + (int64_t)(ring_ok ? sblock : 0) * a.state_block_stride;
   float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-  for (int m0 = 0; m0 < R; m0 += kBatch) {
-    u32x4 v[kBatch];
+  for (int m0 = 0; m0 < R; m0 += kCompressBatch) {
+    u32x4 v[kCompressBatch];
 #pragma unroll
-    for (int i = 0; i < kBatch; ++i) {
+    for (int i = 0; i < kCompressBatch; ++i) {
       const int64_t position = end_pos - (R - 1) + m0 + i;
       const bool use_raw = position >= chunk_start;
       const int64_t raw_row = qs + position - chunk_start;
@@ -450,7 +501,7 @@ __global__ __launch_bounds__(kPrepThreads) void compress_groups_kernel(const Com
       v[i] = load_row(src, j, a.dim, valid && m0 + i < R && (use_raw ? raw_ok : ring_ok));
     }
 #pragma unroll
-    for (int i = 0; i < kBatch; ++i) {
+    for (int i = 0; i < kCompressBatch; ++i) {
       float f[8];
       unpack8(v[i], f);
       const bool member = m0 + i < R;
