@@ -125,10 +125,17 @@ __device__ __forceinline__ u32x4 norm_rope_scaled(const NormRope& nr, const Rope
   unpack8(x, f);
   float gamma[8];
   unpack8(rl.gamma, gamma);
+  // Two dims per conversion: each half of a pack rounds to nearest even on
+  // its own, so pairing the roundings changes no bit.
   float scaled[8];
+  u32x4 sc;
 #pragma unroll
-  for (int i = 0; i < 8; ++i) scaled[i] = round_bf16(round_bf16(f[i] * inv) * gamma[i]);
-  const u32x4 sc = pack8(scaled);
+  for (int i = 0; i < 4; ++i) {
+    const uint32_t r = pack_bf16x2(f[2 * i] * inv, f[2 * i + 1] * inv);
+    sc[i] = pack_bf16x2(bf16_lo(r) * gamma[2 * i], bf16_hi(r) * gamma[2 * i + 1]);
+    scaled[2 * i] = bf16_lo(sc[i]);
+    scaled[2 * i + 1] = bf16_hi(sc[i]);
+  }
   u32x4 pr;
 #pragma unroll
   for (int i = 0; i < 4; ++i) pr[i] = __builtin_amdgcn_ds_bpermute(4 * rl.src, sc[i]);
@@ -140,9 +147,8 @@ __device__ __forceinline__ u32x4 norm_rope_scaled(const NormRope& nr, const Rope
 #pragma unroll
   for (int i = 0; i < 8; ++i) {
     const float rotated = rl.first_half ? -partner[i] : partner[i];
-    const float a = round_bf16(scaled[i] * cosv[i]);
-    const float b = round_bf16(rotated * sinv[i]);
-    out[i] = a + b;  // rounded to bf16 by pack8
+    const uint32_t ab = pack_bf16x2(scaled[i] * cosv[i], rotated * sinv[i]);
+    out[i] = bf16_lo(ab) + bf16_hi(ab);  // rounded to bf16 by pack8
   }
   return pack8(out);
 }
