@@ -38,7 +38,11 @@
 // per thread by the row's own length, up to 16384 keys at once; a row of up
 // to 32768 keys takes its halves in turn and then the halves' winners, in one
 // workgroup. Longer rows use two launches: exact top-k per 8192-column
-// partition, then exact top-k over the partition winners.
+// partition, then exact top-k over the partition winners. Fewer waves make
+// each barrier-separated phase cheaper: a short row of a 1024-thread launch
+// runs on its lower 512 threads from the start, and a 1024-thread row whose
+// compacted candidates fit 1024 selects and writes on its lower 512 threads
+// (the upper waves end; a barrier waits only for waves that have not ended).
 #pragma once
 
 #include "qsa_common.h"

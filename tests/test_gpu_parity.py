@@ -364,6 +364,36 @@ def test_attention_physical_parity_grouped_heads(hq, hkv, dim, splits):
     _physical_case(hq, hkv, dim, splits, "token_major", rows=264)
 
 
+@pytest.mark.parametrize("config,splits", [((64, 1, 4), 1), ((32, 2, 4), 2), ((32, 8, 1), 4),
+                                           ((16, 64, 4), 8)])
+def test_attention_decode_config_through_plugin_call(config, splits):
+    """``qsa_sparse_paged_attention(..., decode_config=...)`` on decode rows:
+    the caller's (block_n, target_splits, warps) sets the split count as the
+    reference does (ops/qsa.py:643-645) and every count matches the oracle."""
+    from qsa_vllm_amd.ops import qsa_sparse_paged_attention
+    from qsa_vllm_amd.ops.qsa import choose_num_splits
+    _note(f"attention decode_config={config}")
+    g = torch.Generator().manual_seed(sum(config))
+    hq, hkv, dim, rows, page, num_blocks, width = 16, 2, 128, 12, 16, 40, 200
+    kv = torch.randn(num_blocks, page, hkv, 2 * dim, generator=g).to(torch.bfloat16)
+    k, v = kv[..., :dim], kv[..., dim:]
+    q = torch.randn(rows, hq, dim, generator=g).to(torch.bfloat16)
+    counts = torch.tensor([width, 0, 1, 33, 150, 199], dtype=torch.int32).repeat(rows // 6)
+    idx = _random_physical_indices(g, rows, width, num_blocks, page, counts)
+    table = torch.zeros(1, 1, dtype=torch.int32)
+    t2r = torch.zeros(rows, dtype=torch.int32)
+    kvd = kv.to(DEV)
+    assert choose_num_splits(q, kvd[..., :dim], idx, True, config) == splits
+    want = oracle.sparse_attention(q, k, v, idx, table, t2r, indices_are_physical=True,
+                                   valid_counts=counts)
+    out = qsa_sparse_paged_attention(q.to(DEV), kvd[..., :dim], kvd[..., dim:], idx.to(DEV),
+                                     table.to(DEV), t2r.to(DEV), use_decode_kernel=True,
+                                     indices_are_physical=True, valid_counts=counts.to(DEV),
+                                     decode_config=config)
+    torch.cuda.synchronize()
+    _attn_check(out, want, f"decode_config={config}")
+
+
 def _physical_case(hq, hkv, dim, splits, layout, rows):
     _note(f"attention physical hq={hq} hkv={hkv} dim={dim} splits={splits} layout={layout} "
           f"rows={rows}")
