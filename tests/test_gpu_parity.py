@@ -67,6 +67,50 @@ def test_topk_bit_exact(cols, k, mode):
     assert torch.equal(out.cpu(), want)
 
 
+# Seeded random launches over every top-k path: row counts on both sides of
+# the throughput switch, widths at the launch-shape boundaries (2048 / 4096 /
+# 8192 / 16384 / 32768 and one past each), k from 1 to 512, lengths from -3 to
+# the width, every score mode; plain selection and physical expansion.
+_SWEEP_COLS = [5, 100, 1000, 2048, 2049, 3000, 4096, 4097, 8192, 9000, 16384, 16385, 32768,
+               40000]
+
+
+@pytest.mark.parametrize("seed", range(48))
+def test_topk_random_launches(seed):
+    g = torch.Generator().manual_seed(1000 + seed)
+    pick = lambda seq: seq[int(torch.randint(0, len(seq), (1,), generator=g))]  # noqa: E731
+    cols = pick(_SWEEP_COLS)
+    k = pick([1, 16, 64, 128, 512])
+    mode = pick(["random", "ties", "relu", "specials"])
+    rows = pick([1, 3, 17, 64, 200, 1100])
+    rows = max(1, min(rows, 3_000_000 // cols))
+    _note(f"topk sweep seed={seed} rows={rows} cols={cols} k={k} mode={mode}")
+    scores = _special_scores(rows, cols, g, mode)
+    lengths = torch.randint(-3, cols + 1, (rows,), generator=g, dtype=torch.int32)
+    lengths[0] = cols
+    want = oracle.topk_ids(scores, lengths, k)
+    out = torch.full((rows, k), -7, dtype=torch.int32, device=DEV)
+    topk(scores.to(DEV), lengths.to(DEV), out)
+    torch.cuda.synchronize()
+    assert torch.equal(out.cpu(), want)
+    # The same rows expanded to physical slots (ratio 16, page 16), with counts.
+    ratio, page = 16, 16
+    width = k * ratio + ratio - 1
+    vis = lengths.clamp_min(0)
+    seq = (vis.long() * ratio + torch.randint(0, ratio, (rows,), generator=g)).to(torch.int32)
+    pos = seq.long() - 1
+    t2r = torch.arange(rows, dtype=torch.int32)
+    table = torch.randint(0, 1 << 20, (rows, cols + 2), generator=g, dtype=torch.int32)
+    want_e, want_c = oracle.topk_expand(scores, vis, pos, seq, t2r, table, width, ratio, page, True)
+    got_e = torch.full((rows, width), -9, dtype=torch.int32, device=DEV)
+    got_c = torch.full((rows,), -9, dtype=torch.int32, device=DEV)
+    topk_expand(scores.to(DEV), vis.to(DEV), pos.to(DEV), seq.to(DEV), t2r.to(DEV), got_e, ratio,
+                main_block_table=table.to(DEV), main_page_size=page, valid_counts_out=got_c)
+    torch.cuda.synchronize()
+    assert torch.equal(got_e.cpu(), want_e)
+    assert torch.equal(got_c.cpu(), want_c)
+
+
 # 1024+ rows switch top-k to its throughput launch shapes and row writer.
 @pytest.mark.parametrize("cols,ratio,page,physical", [(1000, 16, 16, True), (2048, 16, 16, False),
                                                       (3000, 4, 6, True), (2048, 4, 8, True)])
