@@ -514,6 +514,56 @@ def test_attention_logical_parity(hq, hkv, dim, splits, reps):
     _attn_check(out, oracle.sparse_attention(q, k, v, idx, table, t2r), "logical, library split")
 
 
+# Seeded random attention launches: head groupings, head dims, batch sizes on
+# both sides of the launch-plan switches, widths, split counts, physical and
+# logical indices (with padding rows and invalid entries), both cache layouts
+# and the output gate.
+_SWEEP_HEADS = [(16, 2, 128), (8, 1, 128), (4, 4, 128), (32, 2, 128), (16, 4, 128), (64, 2, 128),
+                (16, 2, 64), (8, 8, 64)]
+
+
+@pytest.mark.parametrize("seed", range(24))
+def test_attention_random_launches(seed):
+    g = torch.Generator().manual_seed(2000 + seed)
+    pick = lambda seq: seq[int(torch.randint(0, len(seq), (1,), generator=g))]  # noqa: E731
+    hq, hkv, dim = pick(_SWEEP_HEADS)
+    rows, width = pick([1, 5, 37, 70, 300]), pick([1, 31, 100, 257, 600])
+    splits, physical, use_gate = pick([1, 2, 3, 5, 8]), pick([True, False]), pick([True, False])
+    layout = pick(["token_major", "head_major"]) if physical else "token_major"
+    _note(f"attention sweep seed={seed} hq={hq} hkv={hkv} dim={dim} rows={rows} width={width} "
+          f"splits={splits} physical={physical} gate={use_gate} layout={layout}")
+    page, num_blocks, reqs = 16, 48, 4
+    if layout == "token_major":
+        kv = torch.randn(num_blocks, page, hkv, 2 * dim, generator=g).to(torch.bfloat16)
+    else:
+        kv = torch.randn(num_blocks, hkv, page, 2 * dim, generator=g).to(torch.bfloat16)
+    split_kv = lambda t: ((t[..., :dim], t[..., dim:]) if layout == "token_major"  # noqa: E731
+                          else t.transpose(1, 2).split(dim, dim=-1))
+    k, v = split_kv(kv)
+    q = torch.randn(rows, hq, dim, generator=g).to(torch.bfloat16)
+    gate = torch.randn(rows, hq, dim, generator=g).to(torch.bfloat16) if use_gate else None
+    if physical:
+        counts = torch.randint(0, width + 1, (rows,), generator=g, dtype=torch.int32)
+        idx = _random_physical_indices(g, rows, width, num_blocks, page, counts)
+        table = torch.zeros(1, 1, dtype=torch.int32)
+        t2r = torch.zeros(rows, dtype=torch.int32)
+    else:
+        counts = None
+        table = torch.randperm(num_blocks, generator=g)[:reqs * 10].view(reqs, 10).to(torch.int32)
+        table[1, 6:] = -1
+        t2r = torch.randint(-1, reqs + 1, (rows,), generator=g, dtype=torch.int32)
+        idx = torch.randint(-2, 10 * page + 8, (rows, width), generator=g, dtype=torch.int32)
+    want = oracle.sparse_attention(q, k, v, idx, table, t2r, indices_are_physical=physical,
+                                   valid_counts=counts, output_gate=gate)
+    kd, vd = split_kv(kv.to(DEV))
+    out = torch.full((rows, hq, dim), float("nan"), dtype=torch.bfloat16, device=DEV)
+    torch.ops.yulan_qsa_kernels.sparse_attention(
+        q.to(DEV), kd, vd, idx.to(DEV), table.to(DEV), t2r.to(DEV), out,
+        gate.to(DEV) if use_gate else None, counts.to(DEV) if physical else None, physical, splits)
+    torch.cuda.synchronize()
+    _attn_check(out, want, f"seed={seed}")
+
+
 def test_decode_select_then_attend_small():
     _note("end-to-end small decode (cpu_decode_4k shape)")
     wl = make_workload("cpu_decode_4k", device="cpu")
