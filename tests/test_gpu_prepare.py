@@ -62,6 +62,25 @@ def test_prepare_parity(prefix, chunk, kw):
     _check(case)
 
 
+@pytest.mark.parametrize("seed", range(16))
+def test_prepare_random_cases(seed):
+    """Seeded random batches: request counts, prefixes (mid-group and past the
+    ring), chunk lengths, index-head counts that leave partial 8-row groups,
+    64/128 dims, ratios, rotary widths, ring sizes, kv heads, unmapped slots."""
+    g = torch.Generator().manual_seed(3000 + seed)
+    pick = lambda seq: seq[int(torch.randint(0, len(seq), (1,), generator=g))]  # noqa: E731
+    nreq = pick([1, 2, 4, 6])
+    prefix = torch.randint(0, 300, (nreq,), generator=g).tolist()
+    chunk = torch.randint(1, 80, (nreq,), generator=g).tolist()
+    dim = pick([64, 128])
+    ratio = pick([4, 8, 16])
+    kw = dict(num_index_heads=pick([1, 3, 8, 16, 32]), index_head_dim=dim, compress_ratio=ratio,
+              rotary_dim=pick([0, 32, 64, dim]), state_size=pick([None, 2 * ratio]),
+              main_kv_heads=pick([1, 2, 4]), main_head_dim=dim, drop_slot_every=pick([0, 5]))
+    case = make_prepare_case(prefix, chunk, device=DEV, seed=seed, **kw)
+    _check(case)
+
+
 def test_prepare_parity_prefill_8k_on_16k():
     # The benchmark's chunked prefill: 4 requests x 8192 tokens on a 16384 prefix.
     case = make_prepare_case([16384] * 4, [8192] * 4, device=DEV, seed=1)
