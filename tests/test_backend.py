@@ -209,6 +209,48 @@ def test_run_qsa_multi_token_decode(decode_requests):
 
 
 @pytest.mark.gpu
+@pytest.mark.parametrize("seed", range(12))
+def test_select_random_batches(seed):
+    """``select_paged_tokens`` on seeded random batches: decode-only (physical
+    slots and counts) or decode requests of 1-3 rows followed by ragged prefill
+    chunks (logical ids), top-k 256 or 512 tokens; bit-exact against the oracle
+    on the kernels' own logits."""
+    from qsa_vllm_amd.ops import select_paged_tokens
+    g = torch.Generator().manual_seed(4000 + seed)
+    pick = lambda seq: seq[int(torch.randint(0, len(seq), (1,), generator=g))]  # noqa: E731
+    batch, dql, topk_tokens = pick([1, 2, 5, 8]), pick([1, 2, 3]), pick([256, 512])
+    decode_requests = pick([0, batch // 2, batch])
+    physical = decode_requests == batch
+    if physical:
+        wl = make_workload("cpu_decode_4k", device=DEV, batch=batch, seq_len_min=1500,
+                           seq_len_max=6000, seq_len_dist="uniform", decode_query_len=dql,
+                           token_topk=topk_tokens, seed=seed)
+    else:
+        wl = make_workload("prefill_8k_on_16k", device=DEV, batch=batch, chunk=pick([7, 33, 60]),
+                           prefix=0, seq_len_min=600, seq_len_max=2500, seq_len_dist="uniform",
+                           token_topk=topk_tokens, decode_requests=decode_requests,
+                           decode_query_len=dql, seed=seed)
+    s = wl.shape
+    rows = wl.rows
+    print(f"[backend] random select seed={seed} batch={batch} decodes={wl.num_decodes} dql={dql} "
+          f"rows={rows} physical={physical}", flush=True)
+    idx = torch.full((rows, s.width), -7, dtype=torch.int32, device=DEV)
+    counts = torch.full((rows,), -7, dtype=torch.int32, device=DEV)
+    select_paged_tokens(wl.q_index, wl.index_cache, wl.index_table, wl.token_to_req,
+                        wl.positions, wl.seq_lens, s.token_topk, s.compress_ratio, idx,
+                        query_start_loc=wl.query_start_loc, max_query_len=wl.max_query_len,
+                        max_seq_len=wl.max_seq_len, num_decodes=wl.num_decodes,
+                        num_decode_tokens=wl.num_decode_tokens, decode_query_len=dql,
+                        main_block_table=wl.block_table if physical else None,
+                        main_page_size=s.page_size,
+                        valid_counts_out=counts if physical else None)
+    want_idx, want_counts = _expected_selection(wl, physical=physical)
+    assert torch.equal(idx.cpu(), want_idx)
+    if physical:
+        assert torch.equal(counts.cpu(), want_counts)
+
+
+@pytest.mark.gpu
 def test_select_multi_token_decode_physical():
     """``select_paged_tokens`` with decode_query_len = 2 and a main block table:
     physical slots and valid counts for both rows of every request, bit-exact
