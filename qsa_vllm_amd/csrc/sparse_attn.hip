@@ -922,10 +922,14 @@ struct HeadPlan {
 // merge; batch 16: 8 splits 12.0 us against 16.2 us). A split pays for its
 // merge below ~160 workgroups (batch 64: 2 splits 27.5 us, none 29.4 us;
 // batch 96: none 38.0 us, 2 splits 43.8 us). So physical rows group kv heads
-// only while a full round remains, and split smaller batches up to a round,
-// but not below 8 tiles (256 tokens) per split: shorter splits add partials to
-// merge faster than they shorten the launch (batch 8 of 2055 tokens: 4 splits
-// 11.9 us, 8 splits 10.3, 16 splits 10.9, 32 splits 12.7, merge included).
+// only while a full round remains, and split smaller batches up to a round but
+// never past it: a second, partial round of workgroups costs about as much as
+// the first (batch 48: 2 splits 22.9 us, 4 splits 24.6; batch 36: 2 splits
+// 18.7, 4 splits 22.7; batch 24: 4 splits 14.2, 8 splits 15.0; contexts
+// U[8192, 32768], four query sets with their own selections). Nor below 8
+// tiles (256 tokens) per split: shorter splits add partials to merge faster
+// than they shorten the launch (batch 8 of 2055 tokens: 4 splits 11.9 us, 8
+// splits 10.3, 16 splits 10.9, 32 splits 12.7, merge included).
 constexpr int kDecodeRoundWorkgroups = 256;
 constexpr int kDecodeNoSplitWorkgroups = 160;
 constexpr int kDecodeMinSplitTiles = 8;
@@ -1048,7 +1052,7 @@ extern "C" int qsa_sparse_attention_splits(int rows, int num_q_heads, int num_kv
   int splits = 1;
   if (physical) {
     if (base < kDecodeNoSplitWorkgroups)
-      while (splits * base < kDecodeRoundWorkgroups &&
+      while (splits * 2 * base <= kDecodeRoundWorkgroups &&
              splits * 2 <= std::max(1, tiles / kDecodeMinSplitTiles) && splits < 64)
         splits *= 2;
   } else {

@@ -100,8 +100,13 @@ def test_workspace_and_split_helpers():
     assert s >= 1 and s & (s - 1) == 0
     assert lib.qsa_sparse_attention_splits(32768, 16, 2, 128, 2063, 0) == 1
     # Decode rows: 64 rows x 2 kv heads take 2 splits (a full round); small
-    # batches split up to a round but keep at least 8 tiles (256 tokens) each.
+    # batches split up to a round, never past it (36 and 48 rows: 2, not 4;
+    # 24 rows: 4, not 8), and keep at least 8 tiles (256 tokens) each.
     assert lib.qsa_sparse_attention_splits(64, 16, 2, 128, 2063, 1) == 2
+    assert lib.qsa_sparse_attention_splits(48, 16, 2, 128, 2063, 1) == 2
+    assert lib.qsa_sparse_attention_splits(36, 16, 2, 128, 2063, 1) == 2
+    assert lib.qsa_sparse_attention_splits(32, 16, 2, 128, 2063, 1) == 4
+    assert lib.qsa_sparse_attention_splits(24, 16, 2, 128, 2063, 1) == 4
     assert lib.qsa_sparse_attention_splits(16, 16, 2, 128, 2063, 1) == 8
     assert lib.qsa_sparse_attention_splits(8, 16, 2, 128, 2063, 1) == 8
     assert lib.qsa_sparse_attention_splits(1, 16, 2, 128, 2063, 1) == 8
