@@ -64,11 +64,15 @@ def parse_args():
     p.add_argument("--no-hybrid", action="store_true",
                    help="decode_32k: skip the hybrid decoder step figures added to the line")
     p.add_argument("--traffic", default=os.path.join(os.path.dirname(os.path.abspath(__file__)),
-                                                     "profiles", "sparse_attn_decode_32k_traffic.txt"),
-                   help="committed rocprofv3 PMC summary giving HBM bytes per attention launch")
-    p.add_argument("--traffic-run", action="store_true",
-                   help="no timing: eager attention launches of the workload plus a calibration "
-                        "copy, for rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE passes")
+                                                     "profiles", "select_attend_decode_32k_traffic.txt"),
+                   help="committed rocprofv3 PMC summary giving HBM bytes per top-k + attention "
+                        "launch")
+    p.add_argument("--traffic-run", nargs="?", const="select_attend", default=None,
+                   choices=("select_attend", "attention"),
+                   help="no timing: eager launches of the workload's combined top-k + attention "
+                        "op (or, with 'attention', of the sparse attention op alone over the "
+                        "same selections) plus a calibration copy, for rocprofv3 --pmc "
+                        "FETCH_SIZE / WRITE_SIZE passes")
     p.add_argument("--pmc-run", action="store_true",
                    help="no timing: three eager steps of the workload, for rocprofv3 --pmc runs")
     p.add_argument("--pmc-summary", metavar="DIR",
@@ -84,7 +88,7 @@ def log(msg):
 
 
 def read_traffic(path):
-    """HBM bytes per attention launch from the committed PMC summary, if present."""
+    """HBM bytes per top-k + attention launch from the committed PMC summary, if present."""
     try:
         with open(path) as fh:
             for line in fh:
@@ -152,6 +156,8 @@ def main():
             "graph": "HIP graph per block of steps",
         },
         "roofline": dict(m["roofline"], traffic=traffic),
+        "sparse_attention_roofline": m["sparse_attention_roofline"],
+        "select_attend_fused": m["select_attend_fused"],
         "step_roofline": m["step_roofline"],
         "breakdown_us": m["breakdown_us"],
         "eager": m["eager"],
@@ -196,51 +202,72 @@ def decode_queries(wl, n_sets):
 
 
 def decode_counter_run(args, wl):
-    """Eager decode steps for a rocprofv3 counter pass (no timing)."""
+    """Eager decode steps for a rocprofv3 counter pass (no timing): scoring
+    into logits, then the combined top-k + attention launch."""
     import torch
 
-    from qsa_vllm_amd.ops import qsa_sparse_paged_attention, select_paged_tokens
+    from qsa_vllm_amd.graph_dispatch import decode_logits_columns
+    from qsa_vllm_amd.ops import topk  # noqa: F401  (registers torch.ops.yulan_qsa_kernels)
 
     s, rows, dev = wl.shape, wl.rows, wl.device
     sets = decode_queries(wl, args.sets)
     idx = [torch.empty(rows, s.width, dtype=torch.int32, device=dev) for _ in sets]
     counts = [torch.empty(rows, dtype=torch.int32, device=dev) for _ in sets]
     out = torch.zeros_like(wl.q)
+    cols = decode_logits_columns(wl.max_seq_len, s.compress_ratio,
+                                 wl.index_table.shape[1] * wl.index_cache.shape[1])
+    logits = [torch.empty(rows, cols, dtype=torch.float32, device=dev) for _ in sets]
 
-    def select(i):
-        select_paged_tokens(sets[i][1], wl.index_cache, wl.index_table, wl.token_to_req,
-                            wl.positions, wl.seq_lens, s.token_topk, s.compress_ratio, idx[i],
-                            query_start_loc=wl.query_start_loc, max_query_len=1,
-                            max_seq_len=wl.max_seq_len, num_decodes=rows, num_decode_tokens=rows,
-                            visible_blocks=wl.visible, main_block_table=wl.block_table,
-                            main_page_size=s.page_size, valid_counts_out=counts[i])
+    def score(i):
+        torch.ops.yulan_qsa_kernels.indexer_decode(sets[i][1], wl.index_cache, wl.index_table,
+                                                   wl.visible, logits[i], 1)
+
+    def select_attend(i):
+        torch.ops.yulan_qsa_kernels.decode_select_attend(
+            logits[i], wl.visible, wl.positions, wl.seq_lens, wl.token_to_req, wl.block_table,
+            idx[i], counts[i], s.compress_ratio, sets[i][0], wl.k_cache, wl.v_cache, out, None,
+            0)
 
     def attend(i):
-        qsa_sparse_paged_attention(sets[i][0], wl.k_cache, wl.v_cache, idx[i], wl.block_table,
-                                   wl.token_to_req, out, use_decode_kernel=True,
-                                   indices_are_physical=True, valid_counts=counts[i])
+        torch.ops.yulan_qsa_kernels.sparse_attention(sets[i][0], wl.k_cache, wl.v_cache, idx[i],
+                                                     wl.block_table, wl.token_to_req, out, None,
+                                                     counts[i], True, 0)
 
-    if args.traffic_run:
+    if args.traffic_run == "attention":
+        # Selections by the top-k op (not in the summary's kernels), then the
+        # attention alone.
+        def select(i):
+            score(i)
+            torch.ops.yulan_qsa_kernels.topk_expand(logits[i], wl.visible, wl.positions,
+                                                    wl.seq_lens, wl.token_to_req, wl.block_table,
+                                                    idx[i], counts[i], s.compress_ratio,
+                                                    s.page_size, True, True)
+
         return traffic_run(select, attend, len(sets))
+    if args.traffic_run:
+        return traffic_run(score, select_attend, len(sets))
     for _ in range(3):
         for i in range(len(sets)):
-            select(i)
-            attend(i)
+            score(i)
+            select_attend(i)
     torch.cuda.synchronize()
     log(f"pmc run: {3 * len(sets)} eager decode steps")
     return 0
 
 
 def measure_decode(wl, steps, warmup, n_sets, eager=False):
-    """Decode steps of `wl` (indexer -> top-k/expand -> sparse attention +
-    merge) from HIP graphs over n_sets rotating query sets, then the same
-    kernels alone for the breakdown and the attention roofline. Returns the
+    """Decode steps of `wl` (indexer scoring -> top-k/expand + sparse attention,
+    one op: decode_select_attend) from HIP graphs over n_sets rotating query
+    sets, then each launch alone for the breakdown and the rooflines (the
+    combined launch, and the standalone top-k and attention ops). Returns the
     figures as a dict (times in us)."""
     import torch
 
+    from qsa_vllm_amd import _lib
     from qsa_vllm_amd.graph_dispatch import decode_logits_columns
-    from qsa_vllm_amd.ops import qsa_sparse_paged_attention, select_paged_tokens, topk_expand
-    from qsa_vllm_amd.workloads import attention_bytes, decode_step_bytes, indexer_bytes
+    from qsa_vllm_amd.ops import decode_select_attend, qsa_sparse_paged_attention, topk_expand
+    from qsa_vllm_amd.workloads import (attention_bytes, decode_step_bytes, indexer_bytes,
+                                        topk_bytes)
 
     s = wl.shape
     rows = wl.rows
@@ -253,38 +280,43 @@ def measure_decode(wl, steps, warmup, n_sets, eager=False):
     cols = decode_logits_columns(wl.max_seq_len, s.compress_ratio,
                                  wl.index_table.shape[1] * wl.index_cache.shape[1])
     logits = [torch.empty(rows, cols, dtype=torch.float32, device=dev) for _ in sets]
+    fused = bool(_lib.load().qsa_decode_select_attention_fuses(
+        rows, cols, s.width, s.compress_ratio, s.num_q_heads, s.num_kv_heads, s.head_dim)) and \
+        s.kv_layout == "token_major"
 
-    def select(i):
-        select_paged_tokens(sets[i][1], wl.index_cache, wl.index_table, wl.token_to_req,
-                            wl.positions, wl.seq_lens, s.token_topk, s.compress_ratio, idx[i],
-                            query_start_loc=wl.query_start_loc, max_query_len=1,
-                            max_seq_len=wl.max_seq_len, num_decodes=rows, num_decode_tokens=rows,
-                            visible_blocks=wl.visible, main_block_table=wl.block_table,
-                            main_page_size=s.page_size, valid_counts_out=counts[i])
-
-    def attend(i):
-        qsa_sparse_paged_attention(sets[i][0], wl.k_cache, wl.v_cache, idx[i], wl.block_table,
-                                   wl.token_to_req, outs[i], use_decode_kernel=True,
-                                   indices_are_physical=True, valid_counts=counts[i])
+    def step(i):
+        decode_select_attend(sets[i][1], wl.index_cache, wl.index_table, wl.visible, sets[i][0],
+                             wl.k_cache, wl.v_cache, wl.block_table, wl.token_to_req,
+                             wl.positions, wl.seq_lens, s.token_topk, s.compress_ratio,
+                             wl.max_seq_len, idx[i], counts[i], outs[i])
 
     def index_only(i):
         torch.ops.yulan_qsa_kernels.indexer_decode(sets[i][1], wl.index_cache, wl.index_table,
                                                    wl.visible, logits[i], 1)
+
+    def select_attend_only(i):
+        torch.ops.yulan_qsa_kernels.decode_select_attend(
+            logits[i], wl.visible, wl.positions, wl.seq_lens, wl.token_to_req, wl.block_table,
+            idx[i], counts[i], s.compress_ratio, sets[i][0], wl.k_cache, wl.v_cache, outs[i],
+            None, 0)
 
     def topk_only(i):
         topk_expand(logits[i], wl.visible, wl.positions, wl.seq_lens, wl.token_to_req, idx[i],
                     s.compress_ratio, main_block_table=wl.block_table,
                     main_page_size=s.page_size, valid_counts_out=counts[i])
 
-    def step(i):
-        select(i)
-        attend(i)
+    def attend_only(i):
+        qsa_sparse_paged_attention(sets[i][0], wl.k_cache, wl.v_cache, idx[i], wl.block_table,
+                                   wl.token_to_req, outs[i], use_decode_kernel=True,
+                                   indices_are_physical=True, valid_counts=counts[i])
 
     # Eager pass (also initialises allocator pools), then capture.
     for i in range(n_sets):
-        step(i)
         index_only(i)
         topk_only(i)
+        attend_only(i)
+        select_attend_only(i)
+        step(i)
     torch.cuda.synchronize()
 
     def capture(fn, indices):
@@ -304,7 +336,8 @@ def measure_decode(wl, steps, warmup, n_sets, eager=False):
     block_graph = capture(step, list(range(n_sets)))
     single = [capture(step, [i]) for i in range(n_sets)]
     reps = 8
-    attn_graph = capture(attend, list(range(n_sets)) * reps)
+    fused_graph = capture(select_attend_only, list(range(n_sets)) * reps)
+    attn_graph = capture(attend_only, list(range(n_sets)) * reps)
     index_graph = capture(index_only, list(range(n_sets)) * reps)
     topk_graph = capture(topk_only, list(range(n_sets)) * reps)
 
@@ -337,6 +370,7 @@ def measure_decode(wl, steps, warmup, n_sets, eager=False):
         return a.elapsed_time(b) * 1e3 / (launches * rounds)  # us per launch
 
     rounds = max(2, steps // (n_sets * reps))
+    fused_us = time_graph(fused_graph, n_sets * reps, rounds)
     attn_us = time_graph(attn_graph, n_sets * reps, rounds)
     index_us = time_graph(index_graph, n_sets * reps, rounds)
     topk_us = time_graph(topk_graph, n_sets * reps, rounds)
@@ -366,13 +400,33 @@ def measure_decode(wl, steps, warmup, n_sets, eager=False):
 
     attn_bytes = sum(attention_bytes(wl, counts[i]) for i in range(n_sets)) / n_sets
     attn_gbps = attn_bytes / (attn_us * 1e-6) / 1e9
+    fused_bytes = attn_bytes + topk_bytes(wl)
+    fused_gbps = fused_bytes / (fused_us * 1e-6) / 1e9
     step_bytes = sum(decode_step_bytes(wl, counts[i]) for i in range(n_sets)) / n_sets
     step_gbps = step_bytes / (us_step * 1e-6) / 1e9
     out.update({
         "query_sets": n_sets,
         "us_per_step": us_step,
         "tokens_per_s": round(rows / (us_step * 1e-6), 1),
+        "select_attend_fused": fused,
+        # The step's dominant launch: the row selection and the sparse
+        # attention in one kernel (select_attend_kernel) plus the split merge,
+        # or, for shapes the library does not fuse, the top-k and attention
+        # launches it runs instead.
         "roofline": {
+            "kernel": ("select_attend_kernel (top-k + sparse attention, + split merge)" if fused
+                       else "topk + sparse_attn_kernel (+ split merge)"),
+            "bound": "hbm",
+            "achieved": round(fused_gbps, 1),
+            "peak": HBM_PEAK_GBPS,
+            "unit": "GB/s",
+            "frac": round(fused_gbps / HBM_PEAK_GBPS, 4),
+            "algorithmic_bytes_per_launch": int(fused_bytes),
+            "us_per_launch": round(fused_us, 3),
+        },
+        # The sparse attention op alone (qsa_sparse_paged_attention over the
+        # same selections: the prefill rows' and unfused shapes' kernel).
+        "sparse_attention_roofline": {
             "kernel": "sparse_attn_kernel (+ split merge)",
             "bound": "hbm",
             "achieved": round(attn_gbps, 1),
@@ -396,8 +450,9 @@ def measure_decode(wl, steps, warmup, n_sets, eager=False):
         },
         "breakdown_us": {
             "indexer_decode": round(index_us, 3),
-            "topk_expand": round(topk_us, 3),
-            "sparse_attention": round(attn_us, 3),
+            "select_attend": round(fused_us, 3),
+            "topk_expand_alone": round(topk_us, 3),
+            "sparse_attention_alone": round(attn_us, 3),
             "step": round(us_step, 3),
         },
         "indexer_gbps": round(indexer_bytes(wl) / (index_us * 1e-6) / 1e9, 1),
@@ -418,8 +473,10 @@ def workload_summary(name, dev, steps=40, warmup=8):
         out = {"workload": describe(wl.shape), "rows": wl.rows,
                "tokens_per_s": m["tokens_per_s"], "us_per_step": round(m["us_per_step"], 3),
                "breakdown_us": m["breakdown_us"], "logits_columns": m["logits_columns"],
-               "roofline": m["roofline"], "step_roofline": m["step_roofline"],
-               "indexer_gbps": m["indexer_gbps"]}
+               "roofline": m["roofline"],
+               "sparse_attention_roofline": m["sparse_attention_roofline"],
+               "select_attend_fused": m["select_attend_fused"],
+               "step_roofline": m["step_roofline"], "indexer_gbps": m["indexer_gbps"]}
     else:
         m = measure_prefill(wl, steps=5, warmup=2)
         out = {"workload": describe(wl.shape), "rows": wl.rows,
@@ -915,24 +972,28 @@ def run_hybrid(args, dev):
 # CAL_BYTES once each), recognised in the counter CSV by its kernel name.
 CAL_BYTES = 256 << 20
 CAL_KERNEL = "neg_kernel"
-ATTN_KERNELS = ("sparse_attn_kernel", "merge_kernel")
+# The decode step's dominant launch (the combined top-k + attention kernel) or
+# the sparse attention kernel alone, and the split merge.
+ATTN_KERNELS = ("select_attend_kernel", "sparse_attn_kernel", "merge_kernel")
 
 
-def traffic_run(select, attend, n_sets, rounds=3):
+def traffic_run(prepare, launch, n_sets, rounds=3):
+    """prepare(i) for every set, then `rounds` passes of launch(i), whose
+    kernels the counter summary reads."""
     import torch
 
     for i in range(n_sets):
-        select(i)
+        prepare(i)
     torch.cuda.synchronize()
     for _ in range(rounds):
         for i in range(n_sets):
-            attend(i)
+            launch(i)
     src = torch.ones(CAL_BYTES // 4, dtype=torch.float32, device="cuda")
     dst = torch.empty_like(src)
     for _ in range(rounds):
         torch.neg(src, out=dst)
     torch.cuda.synchronize()
-    log(f"traffic run: {rounds * n_sets} attention launches, {rounds} calibration copies "
+    log(f"traffic run: {rounds * n_sets} top-k + attention launches, {rounds} calibration copies "
         f"of {CAL_BYTES} B")
     return 0
 
@@ -965,7 +1026,7 @@ def _counter_means(root, counter):
     return {g: (sums[g] / counts[g], counts[g]) for g in sums}
 
 
-QSA_KERNELS = ("sparse_attn_kernel", "merge_kernel", "topk_direct_kernel",
+QSA_KERNELS = ("select_attend_kernel", "sparse_attn_kernel", "merge_kernel", "topk_direct_kernel",
                "topk_adaptive_kernel", "topk_partition_kernel", "topk_merge_kernel",
                "indexer_decode_kernel", "indexer_prefill_kernel")
 
@@ -996,12 +1057,14 @@ def pmc_summary(root):
 
 
 def traffic_summary(fetch_dir, write_dir):
-    """HBM bytes per attention launch (attention kernel + split merge), each
+    """HBM bytes per combined launch (top-k + attention kernel + split merge), each
     counter scaled by what it reads for the calibration copy of CAL_BYTES."""
     fetch = _counter_means(fetch_dir, "FETCH_SIZE")
     write = _counter_means(write_dir, "WRITE_SIZE")
     for table, name in ((fetch, "FETCH_SIZE"), (write, "WRITE_SIZE")):
-        missing = [k for k in ATTN_KERNELS[:1] + (CAL_KERNEL,) if k not in table]
+        missing = [k for k in (CAL_KERNEL,) if k not in table]
+        if not any(k in table for k in ATTN_KERNELS[:2]):
+            missing.append(" or ".join(ATTN_KERNELS[:2]))
         if missing:
             raise SystemExit(f"{name} pass lacks dispatches of {missing}")
     f_scale = CAL_BYTES / (fetch[CAL_KERNEL][0] * 1024.0)

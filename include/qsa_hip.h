@@ -288,6 +288,58 @@ int qsa_sparse_attention(const void* q, int64_t q_row_stride, int64_t q_head_str
                          int indices_are_physical, int num_splits,
                          void* workspace, size_t workspace_bytes, void* stream);
 
+/* Whether qsa_decode_select_attention runs this decode batch shape as one
+ * launch (plus the split merge) over token-major K/V views spanning under
+ * 4 GB per kv head; 0: it runs the top-k and the attention as two calls. */
+int qsa_decode_select_attention_fuses(int rows, int cols, int width, int ratio,
+                                      int num_q_heads, int num_kv_heads, int head_dim);
+
+/* Bytes of workspace qsa_decode_select_attention needs: the larger of the
+ * top-k's (qsa_topk_workspace_bytes of topk = width / ratio) and the split
+ * partials' (qsa_sparse_attention_workspace_bytes). */
+size_t qsa_decode_select_attention_workspace_bytes(int rows, int cols, int width, int ratio,
+                                                   int num_q_heads, int head_dim,
+                                                   int num_splits);
+
+/*
+ * The decode half of a QSA layer after scoring: replaces the top-k +
+ * expansion that qsa_select_paged_decode runs on the logits
+ * (ops/indexer.py:241-279, attention.py:128-145) followed by the backend's
+ * sparse attention over the selection (backend.py:49-68 with
+ * indices_are_physical and valid_counts), for a batch of decode rows.
+ *
+ * Results equal qsa_topk_expand(scores, ..., output = indices,
+ * output_col_stride = 1, output_width = width, counts, ratio, page_size,
+ * physical = 1, store_counts = 1) followed by qsa_sparse_attention(q, ...,
+ * indices, width, block_table, ..., valid_counts = counts,
+ * indices_are_physical = 1, num_splits): the selection (indices, counts) and
+ * the attention output. Batches of fewer than 1024 rows of at most 2048
+ * logits columns whose attention runs 8-wave workgroups over buffer-addressed
+ * caches with at most 2 kv heads per workgroup run both in one launch (plus
+ * the split merge), each workgroup selecting its row into LDS; other shapes
+ * run the two calls. num_splits <= 0 takes qsa_sparse_attention_splits'
+ * choice. The workspace is qsa_decode_select_attention_workspace_bytes().
+ */
+int qsa_decode_select_attention(const float* scores, int64_t score_row_stride, int rows,
+                                int cols, const int32_t* lengths, const int64_t* positions,
+                                const int32_t* sequence_lengths, int num_requests,
+                                const int32_t* token_to_req, const int32_t* block_table,
+                                int64_t table_row_stride, int table_width, int ratio,
+                                int32_t* indices, int64_t indices_row_stride, int width,
+                                int32_t* counts,
+                                const void* q, int64_t q_row_stride, int64_t q_head_stride,
+                                int num_q_heads, int head_dim,
+                                const void* k_cache, int64_t k_block_stride,
+                                int64_t k_token_stride, int64_t k_head_stride,
+                                const void* v_cache, int64_t v_block_stride,
+                                int64_t v_token_stride, int64_t v_head_stride,
+                                int num_blocks, int page_size, int num_kv_heads,
+                                void* out, int64_t out_row_stride, int64_t out_head_stride,
+                                const void* gate, int64_t gate_row_stride,
+                                int64_t gate_head_stride, int64_t gate_dim_stride,
+                                int num_splits, void* workspace, size_t workspace_bytes,
+                                void* stream);
+
 /* Bytes of device scratch qsa_sparse_attention_noalloc holds per GPU. */
 #define QSA_SPARSE_ATTENTION_SCRATCH_BYTES ((size_t)32 << 20)
 

@@ -18,7 +18,7 @@ _lib = None
 QSA_OK = 0
 QSA_ERR_WORKSPACE = -4
 SPARSE_ATTENTION_SCRATCH_BYTES = 32 << 20  # QSA_SPARSE_ATTENTION_SCRATCH_BYTES
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 c_i32 = ctypes.c_int
 c_i64 = ctypes.c_int64
@@ -129,6 +129,20 @@ SIGNATURES = {
                                      c_ptr, c_i64, c_i64, c_i64,
                                      c_i32, c_i32,
                                      c_ptr, c_size, c_ptr]),
+    "qsa_decode_select_attention_fuses": (c_i32, [c_i32, c_i32, c_i32, c_i32, c_i32, c_i32,
+                                                  c_i32]),
+    "qsa_decode_select_attention_workspace_bytes": (c_size, [c_i32, c_i32, c_i32, c_i32, c_i32,
+                                                             c_i32, c_i32]),
+    "qsa_decode_select_attention": (c_i32, [c_ptr, c_i64, c_i32, c_i32, c_ptr, c_ptr,
+                                            c_ptr, c_i32, c_ptr, c_ptr, c_i64, c_i32, c_i32,
+                                            c_ptr, c_i64, c_i32, c_ptr,
+                                            c_ptr, c_i64, c_i64, c_i32, c_i32,
+                                            c_ptr, c_i64, c_i64, c_i64,
+                                            c_ptr, c_i64, c_i64, c_i64,
+                                            c_i32, c_i32, c_i32,
+                                            c_ptr, c_i64, c_i64,
+                                            c_ptr, c_i64, c_i64, c_i64,
+                                            c_i32, c_ptr, c_size, c_ptr]),
     "qsa_sparse_attention_noalloc": (c_i32, [c_ptr, c_i64, c_i64, c_i32, c_i32, c_i32,
                                              c_ptr, c_i64, c_i64, c_i64,
                                              c_ptr, c_i64, c_i64, c_i64,

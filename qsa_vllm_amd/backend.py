@@ -31,6 +31,7 @@ from dataclasses import dataclass
 
 import torch
 
+from .ops.indexer import _visible_blocks, decode_select_attend
 from .ops.indexer import select_paged_tokens as qsa_select_paged_tokens  # attention.py:21
 from .ops.normalization import IndexerRMSNorm, rotary_cache
 from .ops.prepare import qsa_prepare
@@ -101,16 +102,23 @@ class YuLanQSAIndexer:
     def output_width(self):
         return self.token_topk + self.compress_ratio - 1
 
-    def forward(self, projected, positions, raw_metadata, compressed_metadata, out,
-                main_key, main_value, main_key_cache, main_value_cache, main_slots,
-                *, main_block_table=None, valid_counts_out=None):
-        query = qsa_prepare(
+    def prepare(self, projected, positions, raw_metadata, compressed_metadata, main_key,
+                main_value, main_key_cache, main_value_cache, main_slots):
+        """The preparation half of ``forward`` (``attention.py:118-126``): returns
+        the normed, rotated index query after the cache writes."""
+        return qsa_prepare(
             projected, positions, self.q_layernorm.weight, self.k_layernorm.weight,
             self.cos_sin_cache, self.q_layernorm.variance_epsilon, raw_metadata,
             compressed_metadata, self.raw_key_cache, self.compressed_key_cache, main_key,
             main_value, main_key_cache, main_value_cache, main_slots,
             num_index_heads=self.num_heads, index_head_dim=self.head_dim,
             rotary_dim=self.rotary_dim, compress_ratio=self.compress_ratio)
+
+    def forward(self, projected, positions, raw_metadata, compressed_metadata, out,
+                main_key, main_value, main_key_cache, main_value_cache, main_slots,
+                *, main_block_table=None, valid_counts_out=None):
+        query = self.prepare(projected, positions, raw_metadata, compressed_metadata, main_key,
+                             main_value, main_key_cache, main_value_cache, main_slots)
         return select_for_layer(query, self.compressed_key_cache, compressed_metadata, out,
                                 self.token_topk, self.compress_ratio, main_key_cache,
                                 main_block_table=main_block_table,
@@ -222,7 +230,25 @@ def run_qsa(layer: QSALayerState, impl: YuLanQSAImpl, index_query: torch.Tensor,
         return output
     count = main.num_actual_tokens
     is_decode = main.max_query_len == 1
-    key_cache, _ = layer.main_kv_views()
+    key_cache, value_cache = layer.main_kv_views()
+    if is_decode and compressed.decode_query_len == 1:
+        # One token per request: scoring, then the top-k + expansion and the
+        # attention as one op (the same selection into the layer's buffers and
+        # the same output as the two calls below).
+        t2r = compressed.token_to_req[:count]
+        pos = compressed.logical_positions[:count]
+        visible = compressed.visible_blocks
+        visible = (visible[:count] if visible is not None
+                   else _visible_blocks(pos, compressed.seq_lens, t2r, compress_ratio))
+        output[count:].zero_()
+        decode_select_attend(
+            index_query[:count], compressed_key_cache, compressed.block_table, visible,
+            query[:count], key_cache, value_cache, main.block_table, t2r, pos,
+            compressed.seq_lens, token_topk,
+            compress_ratio, compressed.max_seq_len, layer.topk_indices_buffer[:count],
+            layer.topk_counts_buffer[:count], output[:count],
+            output_gate=gate[:count] if gate is not None else None)
+        return output
     select_for_layer(
         index_query[:count], compressed_key_cache, compressed,
         layer.topk_indices_buffer[:count], token_topk, compress_ratio, key_cache,

@@ -24,4 +24,4 @@ int check_launch(const char* what) {
 
 extern "C" const char* qsa_last_error(void) { return qsa::t_last_error.c_str(); }
 
-extern "C" int qsa_abi_version(void) { return 2; }
+extern "C" int qsa_abi_version(void) { return 3; }

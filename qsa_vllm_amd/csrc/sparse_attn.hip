@@ -49,6 +49,7 @@
 // fences write back the XCD's L2, and write-through partial stores cost more
 // than the second launch.
 #include "qsa_common.h"
+#include "topk_device.h"
 #include "../../include/qsa_hip.h"
 
 #include <algorithm>
@@ -219,6 +220,9 @@ struct TileIdx {
   uint32_t ok;  // bit u: k[u]
   __device__ __forceinline__ int key(int u) const { return (ok >> u) & 1u ? k[u] : -1; }
 };
+// LDS: irow is a row of entries in LDS (the fused selection's), read at
+// column 0 where an entry is not valid.
+template <bool LDS>
 __device__ __forceinline__ void load_tile_idx(const int32_t* irow, int tile, int t_end,
                                               int n_valid, int n, TileIdx& r) {
   const int32_t* zero = reinterpret_cast<const int32_t*>(g_qsa_zero_rows);
@@ -228,7 +232,8 @@ __device__ __forceinline__ void load_tile_idx(const int32_t* irow, int tile, int
   for (int u = 0; u < 2; ++u) {
     const int col = k_col(tile, u, n);
     const bool ok = live && col < n_valid;
-    r.k[u] = *(ok ? irow + col : zero);
+    if constexpr (LDS) r.k[u] = irow[ok ? col : 0];
+    else r.k[u] = *(ok ? irow + col : zero);
     r.ok |= (uint32_t)ok << u;
   }
 }
@@ -533,34 +538,39 @@ __device__ __forceinline__ void pv_mfma(const TileV<D, NKV>& V, u32x4 praw, int 
   }
 }
 
-// Two waves per SIMD wherever the registers allow it without spilling.
-template <int D, int NKV, int WAVES, bool PHYSICAL, bool BUF>
-__global__ __launch_bounds__(64 * WAVES)
-__attribute__((amdgpu_waves_per_eu(D == 128 && NKV == 4 ? 1 : 2)))
-void sparse_attn_kernel(const AttnParams p) {
+// LDS of one attention workgroup: each wave's K staging region (physical
+// rows, or the direct loads of logical rows with D = 128), which the waves'
+// partial outputs reuse for the combine after the tile loop, and the waves'
+// running maxima and sums.
+template <int D, int NKV, int WAVES, bool PHYSICAL>
+struct AttnLds {
+  static constexpr bool kDmaK = !PHYSICAL && D == 128;
+  static constexpr int kStageUnits = (PHYSICAL || kDmaK) ? NKV * kTile * (D / 8) : 0;
+  static constexpr int kStageBytes = WAVES * kStageUnits * 16;
+  static constexpr int kCombineBytes = WAVES * 16 * (D + 4) * 4;
+  static constexpr int kBufBytes = kStageBytes > kCombineBytes ? kStageBytes : kCombineBytes;
+};
+
+// One workgroup's share of the attention: row `row`, split `split` of
+// p.num_splits, head group `hg`. Index entries come from global memory
+// (p.indices, p.valid_counts) or, with LDS_IDX, from a row of n_valid_lds
+// entries in LDS at irow_lds.
+template <int D, int NKV, int WAVES, bool PHYSICAL, bool BUF, bool LDS_IDX>
+__device__ __forceinline__ void attend(const AttnParams& p, int row, int split, int hg,
+                                       const int32_t* irow_lds, int n_valid_lds, char* s_lds,
+                                       float (*s_m)[16], float (*s_l)[16]) {
   constexpr int DPL = D / 16;  // V dims per lane = P.V MFMAs per kv slot
   constexpr int KS = D / 32;   // K steps of the Q.K MFMA
 
   // Logical rows with D = 128 load K rows into LDS directly (dma_k).
-  constexpr bool DMA_K = !PHYSICAL && D == 128;
-  // Each wave's K staging region (physical rows, or the direct loads), then
-  // (after the tile loop) the waves' partial outputs for the combine.
-  constexpr int kStageUnits = (PHYSICAL || DMA_K) ? NKV * kTile * (D / 8) : 0;
-  constexpr int kStageBytes = WAVES * kStageUnits * 16;
-  constexpr int kCombineBytes = WAVES * 16 * (D + 4) * 4;
-  __shared__ __attribute__((aligned(16))) char s_lds[kStageBytes > kCombineBytes ? kStageBytes
-                                                                                  : kCombineBytes];
-  __shared__ float s_m[WAVES][16];
-  __shared__ float s_l[WAVES][16];
+  constexpr bool DMA_K = AttnLds<D, NKV, WAVES, PHYSICAL>::kDmaK;
+  constexpr int kStageUnits = AttnLds<D, NKV, WAVES, PHYSICAL>::kStageUnits;
   float(*s_o)[16][D + 4] = reinterpret_cast<float(*)[16][D + 4]>(s_lds);
 
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const int g = lane >> 4;
   const int n = lane & 15;
-  const int row = blockIdx.x;
-  const int split = blockIdx.y;
-  const int hg = blockIdx.z;
 
   const int head0 = hg * p.heads_per_wave;
   const int kv0 = head0 / p.group;
@@ -580,11 +590,12 @@ void sparse_attn_kernel(const AttnParams p) {
   }
 
   int n_valid = p.width;
-  if (p.valid_counts) n_valid = max(0, min(p.valid_counts[row], p.width));
+  if constexpr (LDS_IDX) n_valid = max(0, min(n_valid_lds, p.width));
+  else if (p.valid_counts) n_valid = max(0, min(p.valid_counts[row], p.width));
   const int req = p.token_to_req[row];
   const bool req_ok = req >= 0 && req < p.num_requests;
   const int32_t* trow = p.table + (int64_t)(req_ok ? req : 0) * p.table_row;
-  const int32_t* irow = p.indices + (int64_t)row * p.idx_row;
+  const int32_t* irow = LDS_IDX ? irow_lds : p.indices + (int64_t)row * p.idx_row;
   const int tiles = (n_valid + kTile - 1) / kTile;
   const int t_begin = (int)((int64_t)split * tiles / p.num_splits);
   const int t_end = (int)((int64_t)(split + 1) * tiles / p.num_splits);
@@ -634,20 +645,20 @@ void sparse_attn_kernel(const AttnParams p) {
     int ks[2], vs[8];
     TileK<D, NKV> K;
     TileV<D, NKV> V;
-    load_tile_idx(irow, t, t_end, n_valid, n, ia);
+    load_tile_idx<LDS_IDX>(irow, t, t_end, n_valid, n, ia);
 #pragma unroll
     for (int u = 0; u < 2; ++u) pa[u] = table_page(p, trow, req_ok, ia.key(u));
 #pragma unroll
     for (int u = 0; u < 2; ++u) ks[u] = logical_slot(p, req_ok, ia.key(u), pa[u]);
     v_slots_from_k(ks, g, vs);
-    load_tile_idx(irow, t + WAVES, t_end, n_valid, n, ia);
+    load_tile_idx<LDS_IDX>(irow, t + WAVES, t_end, n_valid, n, ia);
     QSA_SCHED_FENCE();
     dma_k<D, NKV>(p, vs, khead, n, g, kregion);
     QSA_SCHED_FENCE();
 #pragma unroll
     for (int u = 0; u < 2; ++u) pa[u] = table_page(p, trow, req_ok, ia.key(u));
     QSA_SCHED_FENCE();
-    load_tile_idx(irow, t + 2 * WAVES, t_end, n_valid, n, ib);
+    load_tile_idx<LDS_IDX>(irow, t + 2 * WAVES, t_end, n_valid, n, ib);
     QSA_SCHED_FENCE();
     load_v(vs, V);
     QSA_SCHED_FENCE();
@@ -671,7 +682,7 @@ void sparse_attn_kernel(const AttnParams p) {
       for (int u = 0; u < 2; ++u) pa[u] = table_page(p, trow, req_ok, ib.key(u));
       ia = ib;
       QSA_SCHED_FENCE();
-      load_tile_idx(irow, t + 3 * WAVES, t_end, n_valid, n, ib);
+      load_tile_idx<LDS_IDX>(irow, t + 3 * WAVES, t_end, n_valid, n, ib);
       QSA_SCHED_FENCE();
       load_v(vs, V);
       QSA_SCHED_FENCE();
@@ -690,20 +701,20 @@ void sparse_attn_kernel(const AttnParams p) {
     int ks[2], vs[8];
     TileK<D, NKV> K;
     TileV<D, NKV> V;
-    load_tile_idx(irow, t, t_end, n_valid, n, ia);
+    load_tile_idx<LDS_IDX>(irow, t, t_end, n_valid, n, ia);
 #pragma unroll
     for (int u = 0; u < 2; ++u) pa[u] = table_page(p, trow, req_ok, ia.key(u));
 #pragma unroll
     for (int u = 0; u < 2; ++u) ks[u] = logical_slot(p, req_ok, ia.key(u), pa[u]);
     v_slots_from_k(ks, g, vs);
-    load_tile_idx(irow, t + WAVES, t_end, n_valid, n, ia);
+    load_tile_idx<LDS_IDX>(irow, t + WAVES, t_end, n_valid, n, ia);
     QSA_SCHED_FENCE();
     load_k_direct(ks, K);
     QSA_SCHED_FENCE();
 #pragma unroll
     for (int u = 0; u < 2; ++u) pa[u] = table_page(p, trow, req_ok, ia.key(u));
     QSA_SCHED_FENCE();
-    load_tile_idx(irow, t + 2 * WAVES, t_end, n_valid, n, ib);
+    load_tile_idx<LDS_IDX>(irow, t + 2 * WAVES, t_end, n_valid, n, ib);
     QSA_SCHED_FENCE();
     load_v(vs, V);
     QSA_SCHED_FENCE();
@@ -720,7 +731,7 @@ void sparse_attn_kernel(const AttnParams p) {
       for (int u = 0; u < 2; ++u) pa[u] = table_page(p, trow, req_ok, ib.key(u));
       ia = ib;  // arrived: its table entries were just addressed from it
       QSA_SCHED_FENCE();
-      load_tile_idx(irow, t + 3 * WAVES, t_end, n_valid, n, ib);
+      load_tile_idx<LDS_IDX>(irow, t + 3 * WAVES, t_end, n_valid, n, ib);
       QSA_SCHED_FENCE();
       v_slots_from_k(ks, g, vs);
       load_v(vs, V);
@@ -735,13 +746,13 @@ void sparse_attn_kernel(const AttnParams p) {
     TileKRows<D, NKV> KR;
     TileV<D, NKV> V;
     // Prologue, in issue order: K(t), index entries of t+W, V(t).
-    load_tile_idx(irow, t, t_end, n_valid, n, idx);
+    load_tile_idx<LDS_IDX>(irow, t, t_end, n_valid, n, idx);
 #pragma unroll
     for (int u = 0; u < 2; ++u) ks[u] = phys(idx.key(u));
     v_slots_from_k(ks, g, vs);
     load_k(vs, KR);
     QSA_SCHED_FENCE();
-    load_tile_idx(irow, t + WAVES, t_end, n_valid, n, idx);
+    load_tile_idx<LDS_IDX>(irow, t + WAVES, t_end, n_valid, n, idx);
     QSA_SCHED_FENCE();
     load_v(vs, V);
     QSA_SCHED_FENCE();
@@ -760,7 +771,7 @@ void sparse_attn_kernel(const AttnParams p) {
       QSA_SCHED_FENCE();
       pv_mfma<D, NKV>(V, praw, vslot, oacc);
       QSA_SCHED_FENCE();
-      load_tile_idx(irow, t + 2 * WAVES, t_end, n_valid, n, idx);
+      load_tile_idx<LDS_IDX>(irow, t + 2 * WAVES, t_end, n_valid, n, idx);
       QSA_SCHED_FENCE();
       load_v(vs, V);
       QSA_SCHED_FENCE();
@@ -836,6 +847,78 @@ void sparse_attn_kernel(const AttnParams p) {
       b = bf16_hi(ob) * sigmoidf_(gb);
     }
     *reinterpret_cast<uint32_t*>(optr + d) = pack_bf16x2(a, b);
+  }
+}
+
+// Two waves per SIMD wherever the registers allow it without spilling.
+template <int D, int NKV, int WAVES, bool PHYSICAL, bool BUF>
+__global__ __launch_bounds__(64 * WAVES)
+__attribute__((amdgpu_waves_per_eu(D == 128 && NKV == 4 ? 1 : 2)))
+void sparse_attn_kernel(const AttnParams p) {
+  __shared__ __attribute__((aligned(16))) char s_lds[AttnLds<D, NKV, WAVES, PHYSICAL>::kBufBytes];
+  __shared__ float s_m[WAVES][16];
+  __shared__ float s_l[WAVES][16];
+  attend<D, NKV, WAVES, PHYSICAL, BUF, false>(p, blockIdx.x, blockIdx.y, blockIdx.z, nullptr, 0,
+                                              s_lds, s_m, s_l);
+}
+
+// Decode selection fused with the attention (physical slots, 8-wave
+// workgroups). Every workgroup of a row first selects the row itself, with the
+// top-k kernel's 512-thread whole-row code (topk_device.h), and writes the
+// expanded row into LDS instead of global memory; its attention then reads
+// its index entries from LDS. The row's selection is computed once per
+// workgroup of the row (splits x head groups copies of a 2048-column row, a
+// few KB each), which removes the top-k launch, its boundary with the
+// attention, and the attention's first index round trip. Workgroup (row, 0, 0)
+// also writes the expanded row and its count for the caller, after its
+// attention, so no store sits ahead of its K/V loads in the wave's in-order
+// memory counter.
+constexpr int kFusedThreads = 512;
+constexpr int kFusedMaxWidth = 4160;  // LDS-resident expanded row (4096 + a causal tail)
+
+struct FusedSelect {
+  const float* scores;
+  int64_t score_row_stride;
+  const int32_t* lengths;
+  int cols;
+  int topk;
+  ExpandMeta meta;  // physical expansion into LDS: out_col_stride 1, no counts
+  int32_t* indices;  // the caller's copy of the expanded rows
+  int64_t indices_row_stride;
+  int32_t* counts;
+};
+
+template <int ITEMS>
+struct FusedTopkLds {
+  TopkShared<kFusedThreads> sh;
+  alignas(16) TopkStage<kFusedThreads, ITEMS, true> st;
+};
+
+template <int D, int NKV, int ITEMS>
+__global__ __launch_bounds__(kFusedThreads) __attribute__((amdgpu_waves_per_eu(2)))
+void select_attend_kernel(const FusedSelect a, const AttnParams p) {
+  using Lds = AttnLds<D, NKV, 8, true>;
+  constexpr int kBytes = Lds::kBufBytes > (int)sizeof(FusedTopkLds<ITEMS>)
+                             ? Lds::kBufBytes
+                             : (int)sizeof(FusedTopkLds<ITEMS>);
+  __shared__ __attribute__((aligned(16))) char s_lds[kBytes];
+  __shared__ float s_m[8][16];
+  __shared__ float s_l[8][16];
+  __shared__ int s_idx[kFusedMaxWidth];
+  auto& tk = *reinterpret_cast<FusedTopkLds<ITEMS>*>(s_lds);
+  const int row = blockIdx.x;
+  const float* srow = a.scores + (int64_t)row * a.score_row_stride;
+  const RowMeta r = process_row_whole<kFusedThreads, ITEMS, true, true>(
+      DirectLoader{srow, 0}, a.cols, a.lengths[row], a.cols, a.topk, a.meta, row, s_idx, tk.sh,
+      tk.st, reinterpret_cast<int*>(tk.st.key));
+  const int count = expanded_span(a.meta, r, a.topk).count(r);
+  __syncthreads();  // the row is in s_idx; the top-k's LDS is free for the attention
+  attend<D, NKV, 8, true, true, true>(p, row, blockIdx.y, blockIdx.z, s_idx, count, s_lds, s_m,
+                                      s_l);
+  if (blockIdx.y == 0 && blockIdx.z == 0) {
+    int32_t* irow = a.indices + (int64_t)row * a.indices_row_stride;
+    for (int c = threadIdx.x; c < a.meta.out_width; c += kFusedThreads) irow[c] = s_idx[c];
+    if (threadIdx.x == 0) a.counts[row] = count;
   }
 }
 
@@ -1070,7 +1153,22 @@ extern "C" size_t qsa_sparse_attention_workspace_bytes(int rows, int num_q_heads
   return n * head_dim * sizeof(float) + n * sizeof(float);
 }
 
-extern "C" int qsa_sparse_attention(
+namespace qsa {
+namespace {
+
+// A validated attention call: its parameters and launch plan.
+struct AttnLaunch {
+  AttnParams p;
+  HeadPlan plan;
+  dim3 grid;
+  int waves;
+  bool buf;
+  int head_dim;
+  int64_t out_row, out_head, g_row, g_head, g_dim;
+};
+
+// Checks qsa_sparse_attention's arguments (rows > 0) and fills the launch.
+int prepare_attention(
     const void* q, int64_t q_row_stride, int64_t q_head_stride, int rows, int num_q_heads,
     int head_dim, const void* k_cache, int64_t k_block_stride, int64_t k_token_stride,
     int64_t k_head_stride, const void* v_cache, int64_t v_block_stride, int64_t v_token_stride,
@@ -1080,9 +1178,7 @@ extern "C" int qsa_sparse_attention(
     const int32_t* valid_counts, void* out, int64_t out_row_stride, int64_t out_head_stride,
     const void* gate, int64_t gate_row_stride, int64_t gate_head_stride, int64_t gate_dim_stride,
     int indices_are_physical, int num_splits, void* workspace, size_t workspace_bytes,
-    void* stream) {
-  if (rows < 0) return fail(QSA_ERR_INVALID, "qsa_sparse_attention: rows < 0");
-  if (rows == 0) return QSA_OK;
+    AttnLaunch* L) {
   if (head_dim != 64 && head_dim != 128)
     return fail(QSA_ERR_UNSUPPORTED, "qsa_sparse_attention: head_dim must be 64 or 128");
   HeadPlan plan;
@@ -1158,32 +1254,191 @@ extern "C" int qsa_sparse_attention(
 
   if (plan.groups > 65535 || num_splits > 65535)
     return fail(QSA_ERR_UNSUPPORTED, "qsa_sparse_attention: grid too large");
-  const dim3 grid(rows, num_splits, plan.groups);
-  const int waves = waves_for(rows, plan, head_dim, indices_are_physical != 0);
   p.num_slots = num_blocks * page_size;
   p.k_bytes = p.v_bytes = 0;
-  const bool buf = buffer_addressable(p.kb, p.kt, p.kh, p.vb, p.vt, p.vh, page_size, p.num_slots,
-                                      num_kv_heads, head_dim, &p.k_bytes, &p.v_bytes);
-  p.kt32 = buf ? (uint32_t)p.kt : 0;
-  p.vt32 = buf ? (uint32_t)p.vt : 0;
-  hipStream_t s = static_cast<hipStream_t>(stream);
+  L->buf = buffer_addressable(p.kb, p.kt, p.kh, p.vb, p.vt, p.vh, page_size, p.num_slots,
+                              num_kv_heads, head_dim, &p.k_bytes, &p.v_bytes);
+  p.kt32 = L->buf ? (uint32_t)p.kt : 0;
+  p.vt32 = L->buf ? (uint32_t)p.vt : 0;
+  L->p = p;
+  L->plan = plan;
+  L->grid = dim3(rows, num_splits, plan.groups);
+  L->waves = waves_for(rows, plan, head_dim, indices_are_physical != 0);
+  L->head_dim = head_dim;
+  L->out_row = out_row_stride;
+  L->out_head = out_head_stride;
+  L->g_row = gate_row_stride;
+  L->g_head = gate_head_stride;
+  L->g_dim = gate_dim_stride;
+  return QSA_OK;
+}
+
+// The merge of a launch's split partials (none with one split).
+int merge_splits(const AttnLaunch& L, hipStream_t s) {
+  const AttnParams& p = L.p;
+  if (p.num_splits <= 1) return QSA_OK;
+  return launch_merge(p.part_out, p.part_lse, p.num_splits, p.rows, p.num_q_heads, L.head_dim,
+                      p.out, L.out_row, L.out_head, p.gate, L.g_row, L.g_head, L.g_dim, s);
+}
+
+int launch_attention(const AttnLaunch& L, hipStream_t s) {
+  const AttnParams& p = L.p;
   hipError_t err = hipSuccess;
-  if (head_dim == 128) {
-    if (plan.nkv == 1) err = launch_attn<128, 1>(p, grid, waves, buf, s);
-    else if (plan.nkv == 2) err = launch_attn<128, 2>(p, grid, waves, buf, s);
-    else err = launch_attn<128, 4>(p, grid, waves, buf, s);
+  if (L.head_dim == 128) {
+    if (L.plan.nkv == 1) err = launch_attn<128, 1>(p, L.grid, L.waves, L.buf, s);
+    else if (L.plan.nkv == 2) err = launch_attn<128, 2>(p, L.grid, L.waves, L.buf, s);
+    else err = launch_attn<128, 4>(p, L.grid, L.waves, L.buf, s);
   } else {
-    if (plan.nkv == 1) err = launch_attn<64, 1>(p, grid, waves, buf, s);
-    else if (plan.nkv == 2) err = launch_attn<64, 2>(p, grid, waves, buf, s);
-    else err = launch_attn<64, 4>(p, grid, waves, buf, s);
+    if (L.plan.nkv == 1) err = launch_attn<64, 1>(p, L.grid, L.waves, L.buf, s);
+    else if (L.plan.nkv == 2) err = launch_attn<64, 2>(p, L.grid, L.waves, L.buf, s);
+    else err = launch_attn<64, 4>(p, L.grid, L.waves, L.buf, s);
   }
   if (err != hipSuccess)
     return fail(QSA_ERR_HIP, std::string("qsa_sparse_attention launch: ") + hipGetErrorString(err));
-  if (num_splits > 1)
-    return launch_merge(p.part_out, p.part_lse, num_splits, rows, num_q_heads, head_dim, p.out,
-                        out_row_stride, out_head_stride, p.gate, gate_row_stride,
-                        gate_head_stride, gate_dim_stride, s);
-  return QSA_OK;
+  return merge_splits(L, s);
+}
+
+}  // namespace
+}  // namespace qsa
+
+extern "C" int qsa_sparse_attention(
+    const void* q, int64_t q_row_stride, int64_t q_head_stride, int rows, int num_q_heads,
+    int head_dim, const void* k_cache, int64_t k_block_stride, int64_t k_token_stride,
+    int64_t k_head_stride, const void* v_cache, int64_t v_block_stride, int64_t v_token_stride,
+    int64_t v_head_stride, int num_blocks, int page_size, int num_kv_heads,
+    const int32_t* indices, int64_t indices_row_stride, int width, const int32_t* block_table,
+    int64_t table_row_stride, int table_width, int num_requests, const int32_t* token_to_req,
+    const int32_t* valid_counts, void* out, int64_t out_row_stride, int64_t out_head_stride,
+    const void* gate, int64_t gate_row_stride, int64_t gate_head_stride, int64_t gate_dim_stride,
+    int indices_are_physical, int num_splits, void* workspace, size_t workspace_bytes,
+    void* stream) {
+  if (rows < 0) return fail(QSA_ERR_INVALID, "qsa_sparse_attention: rows < 0");
+  if (rows == 0) return QSA_OK;
+  AttnLaunch L;
+  const int st = prepare_attention(
+      q, q_row_stride, q_head_stride, rows, num_q_heads, head_dim, k_cache, k_block_stride,
+      k_token_stride, k_head_stride, v_cache, v_block_stride, v_token_stride, v_head_stride,
+      num_blocks, page_size, num_kv_heads, indices, indices_row_stride, width, block_table,
+      table_row_stride, table_width, num_requests, token_to_req, valid_counts, out,
+      out_row_stride, out_head_stride, gate, gate_row_stride, gate_head_stride, gate_dim_stride,
+      indices_are_physical, num_splits, workspace, workspace_bytes, &L);
+  if (st != QSA_OK) return st;
+  return launch_attention(L, static_cast<hipStream_t>(stream));
+}
+
+namespace qsa {
+namespace {
+
+// Rows below which the top-k runs one 512-thread workgroup per row for rows
+// of up to 2048 columns (its latency-bound launch shapes), the shapes the
+// fused kernel reuses.
+constexpr int kFusedMaxRows = 1024;
+constexpr int kFusedMaxColumns = 2048;
+
+// Whether a decode batch's selection and attention run as one launch:
+// the top-k's 512-thread shapes (rows < 1024, at most 2048 columns, the
+// selected ids within the key stage), an expanded row that fits LDS, and the
+// attention's 8-wave, buffer-addressed plan with at most 2 kv heads per
+// workgroup.
+bool fuses(int rows, int cols, int width, int ratio, int waves, bool buf, int nkv) {
+  const int items = cols <= 1024 ? 2 : 4;
+  const int topk = ratio > 0 ? width / ratio : 0;
+  return rows > 0 && rows < kFusedMaxRows && cols <= kFusedMaxColumns && topk > 0 &&
+         2 * topk <= kFusedThreads * items && width <= kFusedMaxWidth && waves == 8 && buf &&
+         nkv <= 2;
+}
+
+template <int D, int NKV>
+hipError_t launch_fused(const FusedSelect& a, const AttnLaunch& L, hipStream_t s) {
+  if (a.cols <= 1024)
+    hipLaunchKernelGGL((select_attend_kernel<D, NKV, 2>), L.grid, dim3(kFusedThreads), 0, s, a, L.p);
+  else
+    hipLaunchKernelGGL((select_attend_kernel<D, NKV, 4>), L.grid, dim3(kFusedThreads), 0, s, a, L.p);
+  return hipGetLastError();
+}
+
+}  // namespace
+}  // namespace qsa
+
+extern "C" int qsa_decode_select_attention_fuses(int rows, int cols, int width, int ratio,
+                                                 int num_q_heads, int num_kv_heads,
+                                                 int head_dim) {
+  HeadPlan plan;
+  if ((head_dim != 64 && head_dim != 128) || !plan_heads(num_q_heads, num_kv_heads, rows, true, &plan))
+    return 0;
+  return fuses(rows, cols, width, ratio, waves_for(rows, plan, head_dim, true), true, plan.nkv);
+}
+
+extern "C" size_t qsa_decode_select_attention_workspace_bytes(int rows, int cols, int width,
+                                                              int ratio, int num_q_heads,
+                                                              int head_dim, int num_splits) {
+  if (rows <= 0 || ratio <= 0) return 0;
+  const size_t sel = qsa_topk_workspace_bytes(rows, cols, width / ratio);
+  const size_t att = qsa_sparse_attention_workspace_bytes(rows, num_q_heads, head_dim, num_splits);
+  return std::max(sel, att);
+}
+
+extern "C" int qsa_decode_select_attention(
+    const float* scores, int64_t score_row_stride, int rows, int cols, const int32_t* lengths,
+    const int64_t* positions, const int32_t* sequence_lengths, int num_requests,
+    const int32_t* token_to_req, const int32_t* block_table, int64_t table_row_stride,
+    int table_width, int ratio, int32_t* indices, int64_t indices_row_stride, int width,
+    int32_t* counts, const void* q, int64_t q_row_stride, int64_t q_head_stride, int num_q_heads,
+    int head_dim, const void* k_cache, int64_t k_block_stride, int64_t k_token_stride,
+    int64_t k_head_stride, const void* v_cache, int64_t v_block_stride, int64_t v_token_stride,
+    int64_t v_head_stride, int num_blocks, int page_size, int num_kv_heads, void* out,
+    int64_t out_row_stride, int64_t out_head_stride, const void* gate, int64_t gate_row_stride,
+    int64_t gate_head_stride, int64_t gate_dim_stride, int num_splits, void* workspace,
+    size_t workspace_bytes, void* stream) {
+  const char* name = "qsa_decode_select_attention";
+  if (rows < 0 || cols < 0) return fail(QSA_ERR_INVALID, std::string(name) + ": negative shape");
+  if (rows == 0) return QSA_OK;
+  if (ratio <= 0) return fail(QSA_ERR_INVALID, std::string(name) + ": ratio must be positive");
+  const int topk = width / ratio;
+  if (topk <= 0) return fail(QSA_ERR_INVALID, std::string(name) + ": topk must be positive");
+  if (!scores || !lengths || !indices || !counts || !positions || !sequence_lengths ||
+      !token_to_req || !block_table)
+    return fail(QSA_ERR_INVALID, std::string(name) + ": null selection pointer");
+  if (num_splits <= 0)
+    num_splits = qsa_sparse_attention_splits(rows, num_q_heads, num_kv_heads, head_dim, width, 1);
+  AttnLaunch L;
+  int st = prepare_attention(
+      q, q_row_stride, q_head_stride, rows, num_q_heads, head_dim, k_cache, k_block_stride,
+      k_token_stride, k_head_stride, v_cache, v_block_stride, v_token_stride, v_head_stride,
+      num_blocks, page_size, num_kv_heads, indices, indices_row_stride, width, block_table,
+      table_row_stride, table_width, num_requests, token_to_req, counts, out, out_row_stride,
+      out_head_stride, gate, gate_row_stride, gate_head_stride, gate_dim_stride, 1, num_splits,
+      workspace, workspace_bytes, &L);
+  if (st != QSA_OK) return st;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (!fuses(rows, cols, width, ratio, L.waves, L.buf, L.plan.nkv)) {
+    st = qsa_topk_expand(scores, score_row_stride, rows, cols, lengths, positions,
+                         sequence_lengths, num_requests, token_to_req, block_table,
+                         table_row_stride, table_width, indices, indices_row_stride, 1, width,
+                         counts, ratio, page_size, 1, 1, workspace, workspace_bytes, stream);
+    if (st != QSA_OK) return st;
+    return launch_attention(L, s);
+  }
+  FusedSelect a = {};
+  a.scores = scores;
+  a.score_row_stride = score_row_stride;
+  a.lengths = lengths;
+  a.cols = cols;
+  a.topk = topk;
+  a.meta = make_expand_meta(positions, sequence_lengths, num_requests, token_to_req, block_table,
+                            table_row_stride, table_width, nullptr, 1, width, ratio, page_size,
+                            1, 0);
+  a.indices = indices;
+  a.indices_row_stride = indices_row_stride;
+  a.counts = counts;
+  hipError_t err;
+  if (head_dim == 128)
+    err = L.plan.nkv == 1 ? launch_fused<128, 1>(a, L, s) : launch_fused<128, 2>(a, L, s);
+  else
+    err = L.plan.nkv == 1 ? launch_fused<64, 1>(a, L, s) : launch_fused<64, 2>(a, L, s);
+  if (err != hipSuccess)
+    return fail(QSA_ERR_HIP, std::string(name) + " launch: " + hipGetErrorString(err));
+  return merge_splits(L, s);
 }
 
 extern "C" int qsa_sparse_attention_merge(const float* partial_out, const float* partial_lse,

@@ -412,22 +412,9 @@ int topk_expand(const float* scores, int64_t score_row_stride, int rows, int col
   a.out_row_stride = output_row_stride;
   a.topk = topk;
   a.cols = cols;
-  a.meta.positions = positions;
-  a.meta.sequence_lengths = sequence_lengths;
-  a.meta.token_to_req = token_to_req;
-  a.meta.table = physical ? table : nullptr;
-  a.meta.counts = counts;
-  a.meta.table_row_stride = table_row_stride;
-  a.meta.out_col_stride = output_col_stride;
-  a.meta.num_requests = num_requests;
-  a.meta.table_width = physical ? table_width : 0;
-  a.meta.page_size = page_size > 0 ? page_size : 1;
-  a.meta.page_div = FastDiv::make(page_size > 0 ? page_size : 1);
-  a.meta.ratio = ratio;
-  a.meta.ratio_div = FastDiv::make(ratio);
-  a.meta.out_width = output_width;
-  a.meta.physical = physical ? 1 : 0;
-  a.meta.store_counts = store_counts ? 1 : 0;
+  a.meta = make_expand_meta(positions, sequence_lengths, num_requests, token_to_req, table,
+                            table_row_stride, table_width, counts, output_col_stride,
+                            output_width, ratio, page_size, physical, store_counts);
   return launch_topk<true>(a, rows, cols, workspace, workspace_bytes,
                            static_cast<hipStream_t>(stream));
 }

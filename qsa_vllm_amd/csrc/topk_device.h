@@ -103,6 +103,33 @@ struct ExpandMeta {
   int store_counts;
 };
 
+// Expansion parameters of qsa_topk_expand's arguments (host side).
+inline ExpandMeta make_expand_meta(const int64_t* positions, const int32_t* sequence_lengths,
+                                   int num_requests, const int32_t* token_to_req,
+                                   const int32_t* table, int64_t table_row_stride,
+                                   int table_width, int32_t* counts, int64_t out_col_stride,
+                                   int out_width, int ratio, int page_size, int physical,
+                                   int store_counts) {
+  ExpandMeta m = {};
+  m.positions = positions;
+  m.sequence_lengths = sequence_lengths;
+  m.token_to_req = token_to_req;
+  m.table = physical ? table : nullptr;
+  m.counts = counts;
+  m.table_row_stride = table_row_stride;
+  m.out_col_stride = out_col_stride;
+  m.num_requests = num_requests;
+  m.table_width = physical ? table_width : 0;
+  m.page_size = page_size > 0 ? page_size : 1;
+  m.page_div = FastDiv::make(page_size > 0 ? page_size : 1);
+  m.ratio = ratio;
+  m.ratio_div = FastDiv::make(ratio);
+  m.out_width = out_width;
+  m.physical = physical ? 1 : 0;
+  m.store_counts = store_counts ? 1 : 0;
+  return m;
+}
+
 // Raw per-row inputs of the expansion (topk.cu:166-180); everything derived
 // from them is computed when the row is written.
 struct RowMeta {
@@ -502,14 +529,31 @@ __device__ __forceinline__ void select_long(int length, int topk, const uint32_t
 // no global load: on gfx9 stores count in the same in-order counter as loads,
 // and the compiler cannot tell a skipped load from a pending one, so a load
 // anywhere in the loop would make every iteration wait for all earlier stores.
-__device__ __forceinline__ void write_expanded(const ExpandMeta& m, const RowMeta& r, int row,
-                                               int topk, const int* sel, const int* tail_page,
-                                               int32_t* out, int threads) {
+// Tokens of an expanded row: the complete selected blocks (at most topk) and
+// the causal tail, together at most the sequence length (the row's count).
+struct ExpandedSpan {
+  int expanded;    // complete blocks x ratio
+  int tail_start;  // first token of the causal tail
+  int tail_count;
+  __device__ __forceinline__ int count(const RowMeta& r) const {
+    return min(expanded + tail_count, r.seq_len);
+  }
+};
+__device__ __forceinline__ ExpandedSpan expanded_span(const ExpandMeta& m, const RowMeta& r,
+                                                      int topk) {
   const int p1 = r.pos + 1;
   const int complete = max(0, min(min(div_ratio(m, p1), div_ratio(m, r.seq_len)), topk));
   const int tail_start = tail_start_of(m, r.pos);
-  const int tail_count = p1 - tail_start;
-  const int expanded = complete * m.ratio;
+  return ExpandedSpan{complete * m.ratio, tail_start, p1 - tail_start};
+}
+
+__device__ __forceinline__ void write_expanded(const ExpandMeta& m, const RowMeta& r, int row,
+                                               int topk, const int* sel, const int* tail_page,
+                                               int32_t* out, int threads) {
+  const ExpandedSpan span = expanded_span(m, r, topk);
+  const int tail_start = span.tail_start;
+  const int tail_count = span.tail_count;
+  const int expanded = span.expanded;
   const bool block_in_page = m.physical && (m.page_size % m.ratio == 0);
   const bool from_lds = !m.physical || (block_in_page && m.ratio - 1 <= kTailSlots);
   const int64_t cs = m.out_col_stride;
@@ -563,7 +607,7 @@ __device__ __forceinline__ void write_expanded(const ExpandMeta& m, const RowMet
       out[(int64_t)c * cs] = v;
     }
   }
-  if (m.store_counts && threadIdx.x == 0) m.counts[row] = min(expanded + tail_count, r.seq_len);
+  if (m.store_counts && threadIdx.x == 0) m.counts[row] = span.count(r);
 }
 
 // Row metadata and causal-tail pages of the expansion, loaded while the
@@ -934,16 +978,19 @@ __device__ __forceinline__ void process_loaded_whole(const DirectLoader& load, i
                                             m, row, out, sh, sel);
 }
 
+// Returns the row's expansion inputs (sequence length and position).
 template <int THREADS, int ITEMS, bool EXPAND, bool PAGES, typename Stage>
-__device__ __forceinline__ void process_row_whole(const DirectLoader& load, int limit,
-                                                  int length_raw, int clamp, int topk,
-                                                  const ExpandMeta& m, int row, int32_t* out,
-                                                  TopkShared<THREADS>& sh, Stage& st, int* sel) {
+__device__ __forceinline__ RowMeta process_row_whole(const DirectLoader& load, int limit,
+                                                     int length_raw, int clamp, int topk,
+                                                     const ExpandMeta& m, int row, int32_t* out,
+                                                     TopkShared<THREADS>& sh, Stage& st,
+                                                     int* sel) {
   uint32_t v[ITEMS];
   int pg[ITEMS];
   const RowPrefetch f = load_row<THREADS, ITEMS, EXPAND, PAGES>(load, limit, m, row, v, pg);
   process_loaded_whole<THREADS, ITEMS, EXPAND, PAGES>(load, limit, v, pg, f, length_raw, clamp,
                                                       topk, m, row, out, sh, st, sel);
+  return f.r;
 }
 
 }  // namespace

@@ -450,6 +450,63 @@ void sparse_attention_impl(const Tensor& q, const Tensor& k_cache, const Tensor&
         "qsa_sparse_attention");
 }
 
+// Decode rows: top-k + physical expansion of `scores` into indices/counts,
+// then the sparse attention over them (qsa_decode_select_attention: one
+// launch for the shapes it fuses). The expansion's page size is the main
+// cache's.
+void decode_select_attend_impl(const Tensor& scores, const Tensor& lengths, const Tensor& pos,
+                               const Tensor& sequence_lengths, const Tensor& token_to_req,
+                               const Tensor& table, const Tensor& indices, const Tensor& counts,
+                               int64_t ratio, const Tensor& q, const Tensor& k_cache,
+                               const Tensor& v_cache, const Tensor& out,
+                               const OptTensor& output_gate, int64_t num_splits) {
+  const auto dev = on_gpu({&scores, &lengths, &pos, &sequence_lengths, &token_to_req, &table,
+                           &indices, &counts, &q, &k_cache, &v_cache, &out, opt(output_gate)});
+  scores2d(scores, "scores");
+  const int64_t rows = scores.size(0);
+  vec(lengths, at::kInt, "lengths", rows);
+  QSA_REQUIRE(k_cache.dim() == 4, "k_cache must be [blocks, page, kv_heads, dim]");
+  const ExpandArgs e{&table, &counts, ratio, k_cache.size(1)};
+  check_expand(pos, sequence_lengths, token_to_req, indices, rows, e);
+  QSA_REQUIRE(indices.size(0) == rows && indices.stride(1) == 1,
+              "indices must be [rows, width] with unit column stride");
+  dtype(q, at::kBFloat16, "q");
+  dtype(k_cache, at::kBFloat16, "k_cache");
+  dtype(v_cache, at::kBFloat16, "v_cache");
+  QSA_REQUIRE(q.dim() == 3 && q.stride(2) == 1 && q.size(0) == rows,
+              "q must be [rows, heads, dim] with unit dim stride");
+  const int64_t hq = q.size(1), dim = q.size(2);
+  QSA_REQUIRE(v_cache.dim() == 4 && k_cache.sizes() == v_cache.sizes(),
+              "k_cache/v_cache must be [blocks, page, kv_heads, dim] of one shape");
+  QSA_REQUIRE(k_cache.stride(3) == 1 && v_cache.stride(3) == 1, "k/v caches need a unit dim stride");
+  QSA_REQUIRE(k_cache.size(3) == dim, "cache head dim must match q");
+  check_out(out, rows, hq, dim);
+  const GateStrides g = gate_strides(output_gate, rows, hq, dim);
+  if (rows == 0) return;
+  c10::hip::HIPGuard guard(dev.index());
+  const int cols = (int)scores.size(1), width = (int)indices.size(1);
+  int splits = (int)num_splits;
+  if (splits <= 0)
+    splits = qsa_sparse_attention_splits((int)rows, (int)hq, (int)k_cache.size(2), (int)dim,
+                                         width, 1);
+  const size_t ws_bytes = qsa_decode_select_attention_workspace_bytes(
+      (int)rows, cols, width, (int)ratio, (int)hq, (int)dim, splits);
+  Tensor ws = ws_bytes ? workspace(ws_bytes, dev) : Tensor();
+  check(qsa_decode_select_attention(
+            at_elem<float>(scores), scores.stride(0), (int)rows, cols, at_elem<int32_t>(lengths),
+            at_elem<int64_t>(pos), at_elem<int32_t>(sequence_lengths),
+            (int)sequence_lengths.numel(), at_elem<int32_t>(token_to_req), at_elem<int32_t>(table),
+            table.stride(0), (int)table.size(1), (int)ratio, at_elem<int32_t>(indices),
+            indices.stride(0), width, at_elem<int32_t>(counts), q.data_ptr(), sdim(q, 0),
+            sdim(q, 1), (int)hq, (int)dim, k_cache.data_ptr(), sdim(k_cache, 0),
+            sdim(k_cache, 1), sdim(k_cache, 2), v_cache.data_ptr(), sdim(v_cache, 0),
+            sdim(v_cache, 1), sdim(v_cache, 2), (int)k_cache.size(0), (int)k_cache.size(1),
+            (int)k_cache.size(2), out.data_ptr(), sdim(out, 0), sdim(out, 1),
+            ptr_or_null(opt(output_gate)), g.row, g.head, g.dim, splits,
+            ws_bytes ? ws.data_ptr() : nullptr, ws_bytes, stream_of(dev)),
+        "qsa_decode_select_attention");
+}
+
 void sparse_attention_merge_impl(const Tensor& partial_out, const Tensor& partial_lse,
                                  const Tensor& out, const OptTensor& output_gate) {
   const auto dev = on_gpu({&partial_out, &partial_lse, &out, opt(output_gate)});
@@ -756,6 +813,11 @@ TORCH_LIBRARY_FRAGMENT(yulan_qsa_kernels, m) {
   m.def(
       "sparse_attention_merge(Tensor partial_out, Tensor partial_lse, Tensor(a!) out, "
       "Tensor? output_gate) -> ()");
+  m.def(
+      "decode_select_attend(Tensor scores, Tensor lengths, Tensor positions, "
+      "Tensor sequence_lengths, Tensor token_to_req, Tensor table, Tensor(a!) indices, "
+      "Tensor(b!) counts, int ratio, Tensor q, Tensor k_cache, Tensor v_cache, Tensor(c!) out, "
+      "Tensor? output_gate, int num_splits) -> ()");
 }
 
 TORCH_LIBRARY_IMPL(yulan_qsa_kernels, CUDA, m) {
@@ -772,6 +834,7 @@ TORCH_LIBRARY_IMPL(yulan_qsa_kernels, CUDA, m) {
   m.impl("select_prefill", &select_prefill_impl);
   m.impl("sparse_attention", &sparse_attention_impl);
   m.impl("sparse_attention_merge", &sparse_attention_merge_impl);
+  m.impl("decode_select_attend", &decode_select_attend_impl);
 }
 
 // Shape-only tracing (fake / meta tensors): the ops mutate their outputs in
@@ -798,6 +861,10 @@ TORCH_LIBRARY_IMPL(yulan_qsa_kernels, Meta, m) {
                                 const OptTensor&, bool, int64_t) {});
   m.impl("sparse_attention_merge",
          [](const Tensor&, const Tensor&, const Tensor&, const OptTensor&) {});
+  m.impl("decode_select_attend",
+         [](const Tensor&, const Tensor&, const Tensor&, const Tensor&, const Tensor&,
+            const Tensor&, const Tensor&, const Tensor&, int64_t, const Tensor&, const Tensor&,
+            const Tensor&, const Tensor&, const OptTensor&, int64_t) {});
   m.impl("indexer_prepare",
          [](const Tensor&, const Tensor&, const Tensor&, const Tensor&, const Tensor&, double,
             const Tensor&, const Tensor&, const Tensor&, const Tensor&, const Tensor&,

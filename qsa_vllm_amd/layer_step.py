@@ -17,29 +17,29 @@ from __future__ import annotations
 
 import torch
 
+from .backend import run_qsa
 from .graph_dispatch import capture_column_scope, check_decode_graph_batch
 
 
 def qsa_layer_step(indexer, impl, layer, batch, index_qk, main_key, main_value, query, output,
                    gate=None):
-    """Prepare + select into the layer's top-k buffers (physical slots and
-    counts in uniform decode, logical ids otherwise), then sparse attention
-    into ``output``. Returns ``output``. A step without metadata (``batch`` is
-    None: vLLM's memory-profiling forward, ``attention.py:193-198``) zeroes
-    ``output`` and writes nothing else."""
+    """Prepare, then ``run_qsa``: select into the layer's top-k buffers
+    (physical slots and counts in uniform decode, logical ids otherwise) and
+    sparse attention into ``output`` (one op for single-token decode). Returns
+    ``output``. A step without metadata (``batch`` is None: vLLM's
+    memory-profiling forward, ``attention.py:193-198``) zeroes ``output`` and
+    writes nothing else."""
     if batch is None:
         output.zero_()
         return output
     n = batch.num_tokens
-    decode = batch.main.max_query_len == 1
     key_cache, value_cache = layer.main_kv_views()
-    indexer.forward(index_qk[:n], batch.positions, batch.raw, batch.compressed,
-                    layer.topk_indices_buffer[:n], main_key[:n], main_value[:n], key_cache,
-                    value_cache, batch.main.slot_mapping,
-                    main_block_table=batch.main.block_table if decode else None,
-                    valid_counts_out=layer.topk_counts_buffer[:n] if decode else None)
-    return impl.forward(layer, query, batch.main, output, token_to_req=batch.token_to_req,
-                        output_gate=gate)
+    index_query = indexer.prepare(index_qk[:n], batch.positions, batch.raw, batch.compressed,
+                                  main_key[:n], main_value[:n], key_cache, value_cache,
+                                  batch.main.slot_mapping)
+    return run_qsa(layer, impl, index_query, indexer.compressed_key_cache, query, gate, output,
+                   batch.main, batch.compressed, indexer.token_topk, indexer.compress_ratio,
+                   batch.token_to_req)
 
 
 class QSALayerStepGraph:

@@ -50,6 +50,64 @@ def qsa_select_paged_decode(
         main_page_size, _LOGITS_CAP_BYTES)
 
 
+def decode_select_attend(
+    index_q: torch.Tensor,
+    index_cache: torch.Tensor,
+    index_table: torch.Tensor,
+    visible_blocks: torch.Tensor,
+    q: torch.Tensor,
+    k_cache: torch.Tensor,
+    v_cache: torch.Tensor,
+    main_block_table: torch.Tensor,
+    token_to_req: torch.Tensor,
+    query_positions: torch.Tensor,
+    sequence_lengths: torch.Tensor,
+    token_topk: int,
+    compress_ratio: int,
+    max_seq_len: int,
+    indices_out: torch.Tensor,
+    counts_out: torch.Tensor,
+    out: torch.Tensor,
+    *,
+    output_gate: torch.Tensor | None = None,
+    num_splits: int = 0,
+) -> torch.Tensor:
+    """A decode batch (one row per request) from index queries to attention
+    output: the selection of :func:`qsa_select_paged_decode` with physical
+    slots (``indices_out``, ``counts_out``) and the backend's sparse attention
+    over it (``qsa_sparse_paged_attention`` with ``indices_are_physical`` and
+    ``valid_counts``; ``backend.py:49-68``), same results. The scores go to a
+    logits buffer of the decode width class; the top-k, expansion and
+    attention then run as one op, which launches them as one kernel (plus the
+    split merge) for the batch shapes the library fuses. ``num_splits`` 0 is
+    the library's split choice. Batches whose logits exceed the workspace cap
+    run the two calls."""
+    rows = index_q.shape[0]
+    if rows == 0:
+        return out
+    columns = decode_logits_columns(max_seq_len, compress_ratio,
+                                    index_table.shape[1] * index_cache.shape[1])
+    if rows * columns * 4 > _LOGITS_CAP_BYTES:
+        qsa_select_paged_decode(index_q, index_cache, index_table, visible_blocks, token_topk,
+                                compress_ratio, 1, indices_out, max_seq_len,
+                                query_positions=query_positions,
+                                sequence_lengths=sequence_lengths, token_to_req=token_to_req,
+                                main_block_table=main_block_table,
+                                main_page_size=k_cache.shape[1], valid_counts_out=counts_out)
+        torch.ops.yulan_qsa_kernels.sparse_attention(
+            q, k_cache, v_cache, indices_out, main_block_table, token_to_req, out, output_gate,
+            counts_out, True, int(num_splits))
+        return out
+    logits = torch.empty(rows, columns, dtype=torch.float32, device=index_q.device)
+    torch.ops.yulan_qsa_kernels.indexer_decode(index_q, index_cache, index_table, visible_blocks,
+                                               logits, 1)
+    torch.ops.yulan_qsa_kernels.decode_select_attend(
+        logits, visible_blocks, query_positions, sequence_lengths, token_to_req, main_block_table,
+        indices_out, counts_out, compress_ratio, q, k_cache, v_cache, out, output_gate,
+        int(num_splits))
+    return out
+
+
 def qsa_select_paged_prefill(
     q: torch.Tensor,
     k_cache: torch.Tensor,

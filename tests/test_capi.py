@@ -209,3 +209,24 @@ def test_torch_ops_meta_kernels_trace_shapes():
         torch.empty(4, 64, dtype=torch.int32, **m), torch.empty(1, 1, dtype=torch.int32, **m),
         torch.empty(4, dtype=torch.int32, **m), torch.empty(4, 16, 128, dtype=torch.bfloat16, **m),
         None, None, True, 0)
+
+
+def test_decode_select_attention_fusion_rule():
+    """Which decode batch shapes the combined selection + attention runs as one
+    launch: the top-k's 512-thread shapes (fewer than 1024 rows, at most 2048
+    logits columns), an 8-wave attention plan, at most 2 kv heads per
+    workgroup."""
+    fuses = _lib.load().qsa_decode_select_attention_fuses
+    # decode_32k: 64 rows x 2048 columns, 16 q / 2 kv heads x 128, width 2063.
+    assert fuses(64, 2048, 2063, 16, 16, 2, 128) == 1
+    assert fuses(64, 1024, 2063, 16, 16, 2, 128) == 1
+    assert fuses(256, 2048, 2063, 16, 16, 2, 128) == 1  # 2 kv heads per workgroup
+    assert fuses(64, 2048, 2063, 16, 8, 1, 64) == 1
+    assert fuses(1023, 2048, 2063, 16, 16, 2, 128) == 1
+    assert fuses(1024, 2048, 2063, 16, 16, 2, 128) == 0  # throughput-shaped top-k
+    assert fuses(64, 4096, 2063, 16, 16, 2, 128) == 0    # wider than 2048 columns
+    assert fuses(16, 2048, 2063, 16, 16, 2, 128) == 0    # 4-wave attention workgroups
+    assert fuses(512, 2048, 2063, 16, 16, 4, 128) == 0   # 4 kv heads per workgroup
+    assert fuses(64, 1024, 16399, 16, 16, 2, 128) == 0   # 1024 blocks need more than the stage
+    assert fuses(64, 2048, 2063, 16, 16, 2, 96) == 0
+    assert fuses(0, 2048, 2063, 16, 16, 2, 128) == 0
