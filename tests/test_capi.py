@@ -230,3 +230,32 @@ def test_decode_select_attention_fusion_rule():
     assert fuses(64, 1024, 16399, 16, 16, 2, 128) == 0   # 1024 blocks need more than the stage
     assert fuses(64, 2048, 2063, 16, 16, 2, 96) == 0
     assert fuses(0, 2048, 2063, 16, 16, 2, 128) == 0
+
+
+def _select_attend_args(**over):
+    a = dict(scores=1 << 20, srs=2048, rows=4, cols=2048, lengths=1 << 21, pos=1 << 22,
+             seq=1 << 23, nreq=4, t2r=1 << 24, table=1 << 25, tabr=2048, tabw=2048, ratio=16,
+             idx=1 << 26, idxr=2063, width=2063, counts=1 << 27, q=1 << 28, qr=2048, qh=128,
+             hq=16, d=128, k=1 << 29, kb=8192, kt=512, kh=128, v=(1 << 29) + 256, vb=8192,
+             vt=512, vh=128, nblk=64, page=16, hkv=2, out=1 << 30, outr=2048, outh=128,
+             gate=None, gr=0, gh=0, gd=0, splits=1, ws=None, wsb=0, stream=None)
+    a.update(over)
+    return list(a.values())
+
+
+def test_decode_select_attention_argument_errors_need_no_launch():
+    lib = _lib.load()
+    f = lib.qsa_decode_select_attention
+    assert f(*_select_attend_args(rows=0)) == 0
+    assert f(*_select_attend_args(ratio=0)) == -1
+    assert b"ratio" in lib.qsa_last_error()
+    assert f(*_select_attend_args(width=8)) == -1                 # topk = 8 / 16 = 0
+    assert f(*_select_attend_args(counts=None)) == -1
+    assert f(*_select_attend_args(table=None)) == -1
+    assert f(*_select_attend_args(d=96)) == -2                    # the attention's checks
+    assert f(*_select_attend_args(splits=4)) == -4                # partials need a workspace
+    assert lib.qsa_decode_select_attention_workspace_bytes(64, 2048, 2063, 16, 16, 128, 2) == \
+        lib.qsa_sparse_attention_workspace_bytes(64, 16, 128, 2)
+    # Long rows: the top-k's partition winners may be the larger workspace.
+    assert lib.qsa_decode_select_attention_workspace_bytes(2048, 65536, 2063, 16, 16, 128, 1) == \
+        lib.qsa_topk_workspace_bytes(2048, 65536, 128)
