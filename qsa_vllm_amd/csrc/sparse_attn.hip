@@ -864,16 +864,15 @@ void sparse_attn_kernel(const AttnParams p) {
 
 // Decode selection fused with the attention (physical slots, 8-wave
 // workgroups). Every workgroup of a row first selects the row itself, with the
-// top-k kernel's 512-thread whole-row code (topk_device.h), and writes the
-// expanded row into LDS instead of global memory; its attention then reads
-// its index entries from LDS. The row's selection is computed once per
-// workgroup of the row (splits x head groups copies of a 2048-column row, a
-// few KB each), which removes the top-k launch, its boundary with the
-// attention, and the attention's first index round trip. Workgroup (row, 0, 0)
-// also writes the expanded row and its count for the caller, after its
-// attention, so no store sits ahead of its K/V loads in the wave's in-order
-// memory counter.
-constexpr int kFusedThreads = 512;
+// top-k kernel's whole-row code (topk_device.h) on all of the workgroup's
+// threads, and writes the expanded row into LDS instead of global memory; its
+// attention then reads its index entries from LDS. The row's selection is
+// computed once per workgroup of the row (splits x head groups copies of a
+// row of at most 2048 columns, a few KB each), which removes the top-k launch,
+// its boundary with the attention, and the attention's first index round
+// trip. Workgroup (row, 0, 0) also writes the expanded row and its count for
+// the caller, after its attention, so no store sits ahead of its K/V loads in
+// the wave's in-order memory counter.
 constexpr int kFusedMaxWidth = 4160;  // LDS-resident expanded row (4096 + a causal tail)
 
 struct FusedSelect {
@@ -888,36 +887,36 @@ struct FusedSelect {
   int32_t* counts;
 };
 
-template <int ITEMS>
+template <int THREADS, int ITEMS>
 struct FusedTopkLds {
-  TopkShared<kFusedThreads> sh;
-  alignas(16) TopkStage<kFusedThreads, ITEMS, true> st;
+  TopkShared<THREADS> sh;
+  alignas(16) TopkStage<THREADS, ITEMS, true> st;
 };
 
-template <int D, int NKV, int ITEMS>
-__global__ __launch_bounds__(kFusedThreads) __attribute__((amdgpu_waves_per_eu(2)))
+template <int D, int NKV, int WAVES, int ITEMS>
+__global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(2)))
 void select_attend_kernel(const FusedSelect a, const AttnParams p) {
-  using Lds = AttnLds<D, NKV, 8, true>;
-  constexpr int kBytes = Lds::kBufBytes > (int)sizeof(FusedTopkLds<ITEMS>)
-                             ? Lds::kBufBytes
-                             : (int)sizeof(FusedTopkLds<ITEMS>);
+  constexpr int kThreads = 64 * WAVES;
+  using Lds = AttnLds<D, NKV, WAVES, true>;
+  using Topk = FusedTopkLds<kThreads, ITEMS>;
+  constexpr int kBytes = Lds::kBufBytes > (int)sizeof(Topk) ? Lds::kBufBytes : (int)sizeof(Topk);
   __shared__ __attribute__((aligned(16))) char s_lds[kBytes];
-  __shared__ float s_m[8][16];
-  __shared__ float s_l[8][16];
+  __shared__ float s_m[WAVES][16];
+  __shared__ float s_l[WAVES][16];
   __shared__ int s_idx[kFusedMaxWidth];
-  auto& tk = *reinterpret_cast<FusedTopkLds<ITEMS>*>(s_lds);
+  auto& tk = *reinterpret_cast<Topk*>(s_lds);
   const int row = blockIdx.x;
   const float* srow = a.scores + (int64_t)row * a.score_row_stride;
-  const RowMeta r = process_row_whole<kFusedThreads, ITEMS, true, true>(
+  const RowMeta r = process_row_whole<kThreads, ITEMS, true, true>(
       DirectLoader{srow, 0}, a.cols, a.lengths[row], a.cols, a.topk, a.meta, row, s_idx, tk.sh,
       tk.st, reinterpret_cast<int*>(tk.st.key));
   const int count = expanded_span(a.meta, r, a.topk).count(r);
   __syncthreads();  // the row is in s_idx; the top-k's LDS is free for the attention
-  attend<D, NKV, 8, true, true, true>(p, row, blockIdx.y, blockIdx.z, s_idx, count, s_lds, s_m,
-                                      s_l);
+  attend<D, NKV, WAVES, true, true, true>(p, row, blockIdx.y, blockIdx.z, s_idx, count, s_lds,
+                                          s_m, s_l);
   if (blockIdx.y == 0 && blockIdx.z == 0) {
     int32_t* irow = a.indices + (int64_t)row * a.indices_row_stride;
-    for (int c = threadIdx.x; c < a.meta.out_width; c += kFusedThreads) irow[c] = s_idx[c];
+    for (int c = threadIdx.x; c < a.meta.out_width; c += kThreads) irow[c] = s_idx[c];
     if (threadIdx.x == 0) a.counts[row] = count;
   }
 }
@@ -1329,31 +1328,38 @@ extern "C" int qsa_sparse_attention(
 namespace qsa {
 namespace {
 
-// Rows below which the top-k runs one 512-thread workgroup per row for rows
-// of up to 2048 columns (its latency-bound launch shapes), the shapes the
-// fused kernel reuses.
+// Rows below which the top-k runs one workgroup per row for rows of up to
+// 2048 columns (its latency-bound launch shapes), the shapes the fused kernel
+// reuses.
 constexpr int kFusedMaxRows = 1024;
 constexpr int kFusedMaxColumns = 2048;
 
-// Whether a decode batch's selection and attention run as one launch:
-// the top-k's 512-thread shapes (rows < 1024, at most 2048 columns, the
-// selected ids within the key stage), an expanded row that fits LDS, and the
+// Keys per thread of the fused selection (512 threads): every row of up to
+// `cols` keys in the workgroup's registers.
+int fused_items(int cols) { return cols <= 1024 ? 2 : 4; }
+
+// Whether a decode batch's selection and attention run as one launch: the
+// top-k's 512-thread shapes (rows < 1024, at most 2048 columns, the selected
+// ids within the key stage), an expanded row that fits LDS, and the
 // attention's 8-wave, buffer-addressed plan with at most 2 kv heads per
-// workgroup.
+// workgroup. Smaller batches (4-wave attention workgroups) keep two launches:
+// a 256-thread selection (256 x 4 and 256 x 8) inside their workgroups cost
+// as much as the launch it removed (batch 1, 4, 8, 16, 24, 31 of decode_32k's
+// shapes: 17.93 / 18.76 / 19.66 / 22.57 / 26.09 / 28.44 us as two launches,
+// 17.96 / 19.19 / 19.94 / 22.67 / 26.04 / 28.52 combined).
 bool fuses(int rows, int cols, int width, int ratio, int waves, bool buf, int nkv) {
-  const int items = cols <= 1024 ? 2 : 4;
   const int topk = ratio > 0 ? width / ratio : 0;
   return rows > 0 && rows < kFusedMaxRows && cols <= kFusedMaxColumns && topk > 0 &&
-         2 * topk <= kFusedThreads * items && width <= kFusedMaxWidth && waves == 8 && buf &&
+         2 * topk <= 512 * fused_items(cols) && width <= kFusedMaxWidth && waves == 8 && buf &&
          nkv <= 2;
 }
 
 template <int D, int NKV>
 hipError_t launch_fused(const FusedSelect& a, const AttnLaunch& L, hipStream_t s) {
-  if (a.cols <= 1024)
-    hipLaunchKernelGGL((select_attend_kernel<D, NKV, 2>), L.grid, dim3(kFusedThreads), 0, s, a, L.p);
+  if (fused_items(a.cols) == 2)
+    hipLaunchKernelGGL((select_attend_kernel<D, NKV, 8, 2>), L.grid, dim3(512), 0, s, a, L.p);
   else
-    hipLaunchKernelGGL((select_attend_kernel<D, NKV, 4>), L.grid, dim3(kFusedThreads), 0, s, a, L.p);
+    hipLaunchKernelGGL((select_attend_kernel<D, NKV, 8, 4>), L.grid, dim3(512), 0, s, a, L.p);
   return hipGetLastError();
 }
 

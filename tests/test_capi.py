@@ -226,6 +226,7 @@ def test_decode_select_attention_fusion_rule():
     assert fuses(1024, 2048, 2063, 16, 16, 2, 128) == 0  # throughput-shaped top-k
     assert fuses(64, 4096, 2063, 16, 16, 2, 128) == 0    # wider than 2048 columns
     assert fuses(16, 2048, 2063, 16, 16, 2, 128) == 0    # 4-wave attention workgroups
+    assert fuses(1, 1024, 2063, 16, 16, 2, 128) == 0
     assert fuses(512, 2048, 2063, 16, 16, 4, 128) == 0   # 4 kv heads per workgroup
     assert fuses(64, 1024, 16399, 16, 16, 2, 128) == 0   # 1024 blocks need more than the stage
     assert fuses(64, 2048, 2063, 16, 16, 2, 96) == 0

@@ -27,6 +27,9 @@ CASES = [
     ("dim64_batch256", {"batch": 256, "head_dim": 64, "seq_len_min": 1024,
                         "seq_len_max": 32768, "seed": 15}, True),
     ("batch_16_four_waves", {"batch": 16, "seed": 16}, False),
+    ("batch_1_four_waves_1024_columns", {"batch": 1, "seq_len_min": 4096,
+                                         "seq_len_max": 16384, "seed": 19}, False),
+    ("batch_8_four_waves_dim64", {"batch": 8, "head_dim": 64, "gate": True, "seed": 20}, False),
     ("long_rows_8192_columns", {"batch": 8, "seq_len_min": 65536, "seq_len_max": 131072,
                                 "seed": 17}, False),
     ("head_major_cache", {"kv_layout": "head_major", "seed": 18}, False),
