@@ -16,6 +16,7 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef int32_t i32x4 __attribute__((ext_vector_type(4)));
 
 // ---------------------------------------------------------------------------
 // Host-side error reporting shared by every entry point (qsa_errors.hip).
@@ -95,3 +96,7 @@ __device__ __forceinline__ u32x2 load_u32x2(const void* p) {
 // A block of zeros in device memory (one copy per translation unit). Gathers of
 // invalid slots are redirected here so masked K/V rows read as exact zeros.
 static __device__ __attribute__((aligned(256))) uint32_t g_qsa_zero_rows[256];
+// A -1 page-table entry: loads of entries that do not exist read it, so the
+// loaded value needs no select afterwards (a select right after a load makes
+// the compiler wait for that load, and with it every older one, at once).
+static __device__ int32_t g_qsa_no_page[1] = {-1};  // never written

@@ -903,11 +903,11 @@ void select_attend_kernel(const FusedSelect a, const AttnParams p) {
   __shared__ __attribute__((aligned(16))) char s_lds[kBytes];
   __shared__ float s_m[WAVES][16];
   __shared__ float s_l[WAVES][16];
-  __shared__ int s_idx[kFusedMaxWidth];
+  __shared__ __attribute__((aligned(16))) int s_idx[kFusedMaxWidth];
   auto& tk = *reinterpret_cast<Topk*>(s_lds);
   const int row = blockIdx.x;
   const float* srow = a.scores + (int64_t)row * a.score_row_stride;
-  const RowMeta r = process_row_whole<kThreads, ITEMS, true, true>(
+  const RowMeta r = process_row_whole<kThreads, ITEMS, true, true, decltype(tk.st), true>(
       DirectLoader{srow, 0}, a.cols, a.lengths[row], a.cols, a.topk, a.meta, row, s_idx, tk.sh,
       tk.st, reinterpret_cast<int*>(tk.st.key));
   const int count = expanded_span(a.meta, r, a.topk).count(r);

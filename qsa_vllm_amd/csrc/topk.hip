@@ -146,9 +146,9 @@ __global__ __launch_bounds__(kAdaptiveThreads) void topk_adaptive_kernel(const T
     const int length = a.lengths[row];
     if (min(length, a.cols) <= kNarrowCols) {  // n <= kNarrowCols
       auto& st = *reinterpret_cast<TopkStage<kAdaptiveNarrow, 4, PAGES>*>(stage_mem);
-      process_loaded_whole<kAdaptiveNarrow, 4, EXPAND, PAGES>(
-          load, limit, v, pg, f, length, a.cols, topk, a.meta, row, out, shu.narrow, st,
-          reinterpret_cast<int*>(st.key));
+      process_loaded_whole<kAdaptiveNarrow, 4, EXPAND, PAGES, false>(
+          load, limit, v, pg, [&] { return f; }, length, a.cols, topk, a.meta, row, out,
+          shu.narrow, st, reinterpret_cast<int*>(st.key));
       return;
     }
   }

@@ -133,10 +133,21 @@ inline ExpandMeta make_expand_meta(const int64_t* positions, const int32_t* sequ
 // Raw per-row inputs of the expansion (topk.cu:166-180); everything derived
 // from them is computed when the row is written.
 struct RowMeta {
-  int seq_len;
+  int seq_len;  // loaded per lane (see load_request); seq() is the row's value
   int pos;
   const int32_t* table_row;  // null unless physical
+  __device__ __forceinline__ int seq() const { return __builtin_amdgcn_readfirstlane(seq_len); }
 };
+
+// Zero that the compiler cannot prove uniform. A load of a per-row value
+// indexed with it is a vector load: it completes in order with the wave's
+// other vector loads, whereas a scalar load shares its counter with LDS
+// operations, so the first LDS wait after it would stall until it returned.
+__device__ __forceinline__ int vector_zero() {
+  int z = 0;
+  asm volatile("" : "+v"(z));
+  return z;
+}
 
 // x / ratio with C semantics: one multiply-high for x >= 0 (the integer
 // division sequence runs only for a negative x).
@@ -157,7 +168,7 @@ __device__ __forceinline__ int token_page(const ExpandMeta& m, int t) {
 
 // Physical slot of token t given its prefetched physical page (topk.cu:116-125).
 __device__ __forceinline__ int slot_of(const ExpandMeta& m, const RowMeta& r, int t, int pp) {
-  if (t < 0 || t >= r.seq_len) return -1;
+  if (t < 0 || t >= r.seq()) return -1;
   if (!m.physical) return t;
   if (pp < 0) return -1;
   return pp * m.page_size + (t - m.page_div.div(t) * m.page_size);
@@ -297,11 +308,14 @@ __device__ __forceinline__ void block_scan2(int& a, int& b, TopkShared<THREADS>&
 // and, with PAGES, the physical slot of each one's first token (from
 // page[pos[j]], the staged page of the element) to sel[topk..2 topk).
 // Candidates are in id order across threads (thread t's before thread t+1's).
-template <int THREADS, int ITEMS, bool PAGES>
-__device__ __forceinline__ void radix_rank(int topk, uint32_t lo, uint32_t hi, uint32_t cand,
-                                           const uint32_t (&key)[ITEMS], const int (&id)[ITEMS],
-                                           const int (&pos)[ITEMS], const int* page,
-                                           const ExpandMeta& m, TopkShared<THREADS>& sh, int* sel) {
+//
+// radix_rank_emit hands each selected candidate to emit(rank, id, pos)
+// instead (rank: its place in ascending-id order).
+template <int THREADS, int ITEMS, typename Emit>
+__device__ __forceinline__ void radix_rank_emit(int topk, uint32_t lo, uint32_t hi, uint32_t cand,
+                                                const uint32_t (&key)[ITEMS],
+                                                const int (&id)[ITEMS], const int (&pos)[ITEMS],
+                                                TopkShared<THREADS>& sh, Emit&& emit) {
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const uint32_t cand0 = cand;
@@ -416,11 +430,20 @@ __device__ __forceinline__ void radix_rank(int topk, uint32_t lo, uint32_t hi, u
       if (n_tie < remaining) rank = n_sel + n_tie;
       ++n_tie;
     }
-    if (rank >= 0) {
-      sel[rank] = id[j];
-      sel[topk + rank] = PAGES ? first_slot(m, page[pos[j]], id[j]) : -1;
-    }
+    if (rank >= 0) emit(rank, id[j], pos[j]);
   }
+}
+
+template <int THREADS, int ITEMS, bool PAGES>
+__device__ __forceinline__ void radix_rank(int topk, uint32_t lo, uint32_t hi, uint32_t cand,
+                                           const uint32_t (&key)[ITEMS], const int (&id)[ITEMS],
+                                           const int (&pos)[ITEMS], const int* page,
+                                           const ExpandMeta& m, TopkShared<THREADS>& sh, int* sel) {
+  radix_rank_emit<THREADS, ITEMS>(topk, lo, hi, cand, key, id, pos, sh,
+                                  [&](int rank, int i, int p) {
+                                    sel[rank] = i;
+                                    sel[topk + rank] = PAGES ? first_slot(m, page[p], i) : -1;
+                                  });
 }
 
 // Exact top-k of `length` (> topk) keys in registers (thread t holds
@@ -536,13 +559,13 @@ struct ExpandedSpan {
   int tail_start;  // first token of the causal tail
   int tail_count;
   __device__ __forceinline__ int count(const RowMeta& r) const {
-    return min(expanded + tail_count, r.seq_len);
+    return min(expanded + tail_count, r.seq());
   }
 };
 __device__ __forceinline__ ExpandedSpan expanded_span(const ExpandMeta& m, const RowMeta& r,
                                                       int topk) {
   const int p1 = r.pos + 1;
-  const int complete = max(0, min(min(div_ratio(m, p1), div_ratio(m, r.seq_len)), topk));
+  const int complete = max(0, min(min(div_ratio(m, p1), div_ratio(m, r.seq())), topk));
   const int tail_start = tail_start_of(m, r.pos);
   return ExpandedSpan{complete * m.ratio, tail_start, p1 - tail_start};
 }
@@ -565,7 +588,7 @@ __device__ __forceinline__ void write_expanded(const ExpandMeta& m, const RowMet
         const int o = c - rank * m.ratio;
         const int block = sel[rank];
         const int t = block * m.ratio + o;
-        if (block >= 0 && t < r.seq_len) {
+        if (block >= 0 && t < r.seq()) {
           if (!m.physical) {
             v = t;
           } else {  // the block lies inside one page (topk.cu:134-146)
@@ -588,7 +611,7 @@ __device__ __forceinline__ void write_expanded(const ExpandMeta& m, const RowMet
         const int o = c - rank * m.ratio;
         const int block = sel[rank];
         const int t = block * m.ratio + o;
-        if (block >= 0 && t < r.seq_len) {
+        if (block >= 0 && t < r.seq()) {
           if (block_in_page) {
             const int s0 = sel[topk + rank];
             v = s0 >= 0 ? s0 + o : -1;
@@ -618,12 +641,14 @@ struct RowPrefetch {
   bool tail_ok;
 };
 
-template <bool EXPAND>
+// VSEQ loads the sequence length per lane (vector_zero), for callers that
+// must not wait for it at their next LDS wait.
+template <bool EXPAND, bool VSEQ = false>
 __device__ __forceinline__ RowPrefetch prefetch_tail(const ExpandMeta& m, int req, int pos) {
   RowPrefetch f{RowMeta{0, pos, nullptr}, -1, false};
   if (!EXPAND) return f;
   const bool mapped = req >= 0 && req < m.num_requests;
-  f.r.seq_len = mapped ? m.sequence_lengths[req] : 0;
+  f.r.seq_len = mapped ? m.sequence_lengths[req + (VSEQ ? vector_zero() : 0)] : 0;
   f.r.table_row = m.physical ? m.table + (int64_t)(mapped ? req : 0) * m.table_row_stride : nullptr;
   const int tid = threadIdx.x;
   const int lp = (tid < kTailSlots && tid < m.ratio - 1) ? token_page(m, tail_start_of(m, pos) + tid)
@@ -637,8 +662,7 @@ __device__ __forceinline__ RowPrefetch prefetch_tail(const ExpandMeta& m, int re
 __device__ __forceinline__ int block_page(const ExpandMeta& m, const RowMeta& r, int id, bool in) {
   const int lp = in ? token_page(m, id * m.ratio) : -1;
   const bool ok = r.table_row && lp >= 0;
-  const int v = *(ok ? r.table_row + lp : reinterpret_cast<const int32_t*>(g_qsa_zero_rows));
-  return ok ? v : -1;
+  return *(ok ? r.table_row + lp : g_qsa_no_page);
 }
 
 template <int THREADS>
@@ -646,32 +670,99 @@ __device__ __forceinline__ void clear_histograms(TopkShared<THREADS>& sh) {
   for (int b = threadIdx.x; b < kHistBuffers * kBins; b += THREADS) (&sh.hist[0][0])[b] = 0u;
 }
 
-// The loads of a contiguous row's elements [0, limit): element i * THREADS +
-// tid's score (and, with PAGES, the physical page of its first token) in
-// thread tid's v[i] (pg[i]); the row metadata and causal-tail pages in the
-// returned prefetch.
-template <int THREADS, int ITEMS, bool EXPAND, bool PAGES>
-__device__ __forceinline__ RowPrefetch load_row(const DirectLoader& load, int limit,
-                                                const ExpandMeta& m, int row, uint32_t (&v)[ITEMS],
-                                                int (&pg)[ITEMS]) {
+// Scores of a contiguous row's elements [0, limit): element i * THREADS +
+// tid's score in thread tid's v[i].
+template <int THREADS, int ITEMS>
+__device__ __forceinline__ void load_scores(const DirectLoader& load, int limit,
+                                            uint32_t (&v)[ITEMS]) {
   const int tid = threadIdx.x;
-  // Row metadata first: the tail and page loads depend on it, the scores do not.
-  const int req = EXPAND ? m.token_to_req[row] : 0;
-  const int pos = EXPAND ? (int)m.positions[row] : 0;
   const uint32_t* src = reinterpret_cast<const uint32_t*>(load.scores + load.start);
 #pragma unroll
   for (int i = 0; i < ITEMS; ++i) {
     const int e = i * THREADS + tid;
     v[i] = *(e < limit ? src + e : g_qsa_zero_rows);
   }
-  const RowPrefetch f = prefetch_tail<EXPAND>(m, req, pos);
-  if (PAGES) {
+}
+
+// Physical page of the first token of every element [0, limit) of a
+// contiguous row (element i * THREADS + tid in pg[i], as load_scores), read
+// from page-table row `table_row` (null: -1 everywhere).
+template <int THREADS, int ITEMS>
+__device__ __forceinline__ void load_element_pages(const DirectLoader& load, int limit,
+                                                   const ExpandMeta& m,
+                                                   const int32_t* table_row, int (&pg)[ITEMS]) {
+  const RowMeta r{0, 0, table_row};
 #pragma unroll
-    for (int i = 0; i < ITEMS; ++i) {
-      const int e = i * THREADS + tid;
-      pg[i] = block_page(m, f.r, load.start + e, e < limit);
-    }
+  for (int i = 0; i < ITEMS; ++i) {
+    const int e = i * THREADS + threadIdx.x;
+    pg[i] = block_page(m, r, load.start + e, e < limit);
   }
+}
+
+// The row's request and position, loaded per lane after the scores: a wave's
+// vector loads complete in order, so the scores can be used while these are
+// in flight, and no LDS wait stalls on them (vector_zero). The position is
+// used as an int (its low word, little-endian): loading only that word keeps
+// the load's whole destination live until it is used, so the compiler does
+// not drain every load in flight to reuse a dead high half.
+//
+// With PAGES, the element pages are loaded at the same time from the table
+// row of request `row` (clamped to the requests), the row's request in a
+// decode batch of one-token requests, instead of after the request arrives;
+// load_pages loads them again from the right row when the request differs.
+struct RowRequest {
+  int req;
+  int pos;
+  const int32_t* guess_row;  // table row of the pages in flight (null: none)
+};
+template <int THREADS, int ITEMS, bool EXPAND, bool PAGES>
+__device__ __forceinline__ RowRequest load_request(const DirectLoader& load, int limit,
+                                                   const ExpandMeta& m, int row,
+                                                   int (&pg)[ITEMS]) {
+  RowRequest q{0, 0, nullptr};
+  if (!EXPAND) return q;
+  // Unconditional (a null row reads -1 entries): loads issued under a branch
+  // would leave the compiler unsure how many are in flight after it, and it
+  // would then wait for these pages too before using the scores.
+  if (PAGES) {
+    if (m.table && m.num_requests > 0)
+      q.guess_row = m.table + (int64_t)min(row, m.num_requests - 1) * m.table_row_stride;
+    load_element_pages<THREADS, ITEMS>(load, limit, m, q.guess_row, pg);
+  }
+  const int z = vector_zero();
+  const int32_t* pos_words = reinterpret_cast<const int32_t*>(m.positions);
+  q.req = m.token_to_req[row + z];
+  q.pos = pos_words[2 * (row + z)];
+  return q;
+}
+
+// The expansion's row metadata and causal-tail pages, after the request
+// arrives; with PAGES, the element pages again when the ones in flight came
+// from another request's table row.
+template <int THREADS, int ITEMS, bool EXPAND, bool PAGES>
+__device__ __forceinline__ RowPrefetch load_pages(const DirectLoader& load, int limit,
+                                                  const ExpandMeta& m, const RowRequest& q,
+                                                  int (&pg)[ITEMS]) {
+  const int req = __builtin_amdgcn_readfirstlane(q.req);
+  const int pos = __builtin_amdgcn_readfirstlane(q.pos);
+  const RowPrefetch f = prefetch_tail<EXPAND, true>(m, req, pos);
+  if (PAGES && f.r.table_row != q.guess_row)  // uniform
+    load_element_pages<THREADS, ITEMS>(load, limit, m, f.r.table_row, pg);
+  return f;
+}
+
+// All the loads of a contiguous row: the row's request and position first
+// (the tail and page loads depend on them, the scores do not), the scores,
+// then the metadata and pages of the request.
+template <int THREADS, int ITEMS, bool EXPAND, bool PAGES>
+__device__ __forceinline__ RowPrefetch load_row(const DirectLoader& load, int limit,
+                                                const ExpandMeta& m, int row, uint32_t (&v)[ITEMS],
+                                                int (&pg)[ITEMS]) {
+  const int req = EXPAND ? m.token_to_req[row] : 0;
+  const int pos = EXPAND ? (int)m.positions[row] : 0;
+  load_scores<THREADS, ITEMS>(load, limit, v);
+  const RowPrefetch f = prefetch_tail<EXPAND>(m, req, pos);
+  if (PAGES) load_element_pages<THREADS, ITEMS>(load, limit, m, f.r.table_row, pg);
   return f;
 }
 
@@ -817,11 +908,10 @@ __device__ __forceinline__ void process_row(const Loader& load, int limit, int l
 
 // Radix select and ranking of `total` compacted candidates (keys, ids and
 // pages at index e of ckey / cid / cpage, in id order), C per thread.
-template <int THREADS, int C, bool PAGES>
-__device__ __forceinline__ void select_compacted(int total, int topk, uint32_t lo, uint32_t hi,
-                                                 const uint32_t* ckey, const int* cid,
-                                                 const int* cpage, const ExpandMeta& m,
-                                                 TopkShared<THREADS>& sh, int* sel) {
+template <int THREADS, int C, typename Emit>
+__device__ __forceinline__ void select_compacted_emit(int total, int topk, uint32_t lo, uint32_t hi,
+                                                      const uint32_t* ckey, const int* cid,
+                                                      TopkShared<THREADS>& sh, Emit&& emit) {
   uint32_t ck[C];
   int ci[C], cp[C];
   uint32_t ccand = 0;
@@ -834,7 +924,103 @@ __device__ __forceinline__ void select_compacted(int total, int topk, uint32_t l
     cp[j] = e;
     ccand |= (uint32_t)ok << j;
   }
-  radix_rank<THREADS, C, PAGES>(topk, lo, hi, ccand, ck, ci, cp, cpage, m, sh, sel);
+  radix_rank_emit<THREADS, C>(topk, lo, hi, ccand, ck, ci, cp, sh, emit);
+}
+
+template <int THREADS, int C, bool PAGES>
+__device__ __forceinline__ void select_compacted(int total, int topk, uint32_t lo, uint32_t hi,
+                                                 const uint32_t* ckey, const int* cid,
+                                                 const int* cpage, const ExpandMeta& m,
+                                                 TopkShared<THREADS>& sh, int* sel) {
+  select_compacted_emit<THREADS, C>(total, topk, lo, hi, ckey, cid, sh,
+                                    [&](int rank, int i, int p) {
+                                      sel[rank] = i;
+                                      sel[topk + rank] = PAGES ? first_slot(m, cpage[p], i) : -1;
+                                    });
+}
+
+// --- expansion written by the selecting threads -----------------------------
+//
+// When a block's tokens map to consecutive slots from its first (logical
+// token ids, or physical pages that hold whole blocks) and the causal tail's
+// pages were prefetched one per thread (write_expanded's from-LDS case), the
+// thread that ranks a selected block writes the block's `ratio` columns
+// itself, and the columns after the selected blocks (the causal tail, then
+// -1) go to the thread that prefetched the tail token's page. The row needs
+// no ranked list in LDS, no barrier before it is written, and no pass over
+// every column reading that list; the columns and their values are those of
+// write_expanded.
+__device__ __forceinline__ bool direct_expansion(const ExpandMeta& m) {
+  const bool block_in_page = m.physical && (m.page_size % m.ratio == 0);
+  return (!m.physical || block_in_page) && m.ratio - 1 <= kTailSlots;
+}
+
+// Columns [rank * ratio, rank * ratio + ratio) of selected block `id` (pp: the
+// physical page of its first token), those below out_width; nothing for a
+// rank past the span's complete blocks.
+// `quads`: the row is contiguous and 16-byte aligned, ratio is a multiple of
+// 4 and every complete block lies below out_width (uniform), so the block's
+// columns go out as 16-byte stores.
+__device__ __forceinline__ void write_block(const ExpandMeta& m, int seq, int expanded, bool quads,
+                                            int rank, int id, int pp, int32_t* out) {
+  const int c0 = rank * m.ratio;
+  if (c0 >= expanded) return;
+  const int first = id * m.ratio;
+  const int s0 = m.physical ? first_slot(m, pp, id) : first;
+  if (quads) {
+    i32x4* dst = reinterpret_cast<i32x4*>(out + c0);
+    for (int q = 0; q < m.ratio / 4; ++q) {
+      i32x4 v;
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        const int o = 4 * q + k;
+        v[k] = (first + o < seq && s0 >= 0) ? s0 + o : -1;
+      }
+      dst[q] = v;
+    }
+    return;
+  }
+  const int n = min(m.ratio, m.out_width - c0);
+  const int64_t cs = m.out_col_stride;
+  for (int o = 0; o < n; ++o)
+    out[(int64_t)(c0 + o) * cs] = (first + o < seq && s0 >= 0) ? s0 + o : -1;
+}
+
+// Columns [expanded, out_width): thread tid writes tail token tid with the
+// page it prefetched (prefetch_tail), every other column is -1; then the
+// row's count.
+template <int THREADS>
+__device__ __forceinline__ void write_tail(const ExpandMeta& m, const RowPrefetch& f,
+                                           const ExpandedSpan& span, int row, int32_t* out) {
+  static_assert(kTailSlots <= THREADS, "one tail token per thread");
+  const int64_t cs = m.out_col_stride;
+  const int tail = min(span.tail_count, m.ratio - 1);
+  for (int c = span.expanded + (int)threadIdx.x; c < m.out_width; c += THREADS) {
+    const int off = c - span.expanded;
+    const int pp = m.physical ? (f.tail_ok ? f.tail_pp : -1) : 0;
+    out[(int64_t)c * cs] = off < tail ? slot_of(m, f.r, span.tail_start + off, pp) : -1;
+  }
+  if (m.store_counts && threadIdx.x == 0) m.counts[row] = span.count(f.r);
+}
+
+// Selection of `total` compacted candidates (keys, ids and pages at index e
+// of ckey / cid / cpage) with the expansion written by the selecting threads
+// (direct_expansion).
+template <int THREADS, int C, bool PAGES>
+__device__ __forceinline__ void select_compacted_direct(int total, int topk, uint32_t lo,
+                                                        uint32_t hi, const uint32_t* ckey,
+                                                        const int* cid, const int* cpage,
+                                                        const ExpandMeta& m, const RowPrefetch& f,
+                                                        int row, int32_t* out,
+                                                        TopkShared<THREADS>& sh) {
+  const ExpandedSpan span = expanded_span(m, f.r, topk);
+  const int seq = f.r.seq();
+  const bool quads = m.out_col_stride == 1 && m.ratio % 4 == 0 && span.expanded <= m.out_width &&
+                     (reinterpret_cast<uintptr_t>(out) & 15) == 0;
+  select_compacted_emit<THREADS, C>(total, topk, lo, hi, ckey, cid, sh, [&](int rank, int i, int p) {
+    write_block(m, seq, span.expanded, quads, rank, i, PAGES ? cpage[p] : -1, out);
+  });
+  write_tail<THREADS>(m, f, span, row, out);
 }
 
 // One whole contiguous row (load.start == 0), selected without staging its
@@ -850,16 +1036,24 @@ __device__ __forceinline__ void select_compacted(int total, int topk, uint32_t l
 // key through LDS and one barrier. Rows with too many candidates to compact
 // take process_row's path with the scores already loaded.
 //
-// process_loaded_whole is the same row after load_row: a caller may issue the
-// loads before it knows the row's length (any limit >= the clamped length
-// gives the same result; elements past the length are never selected).
-template <int THREADS, int ITEMS, bool EXPAND, bool PAGES, typename Stage>
-__device__ __forceinline__ void process_loaded_whole(const DirectLoader& load, int limit,
-                                                     const uint32_t (&v)[ITEMS],
-                                                     const int (&pg)[ITEMS], const RowPrefetch& f,
-                                                     int length_raw, int clamp, int topk,
-                                                     const ExpandMeta& m, int row, int32_t* out,
-                                                     TopkShared<THREADS>& sh, Stage& st, int* sel) {
+// process_loaded_whole is the same row after its scores were loaded: a caller
+// may issue the loads before it knows the row's length (any limit >= the
+// clamped length gives the same result; elements past the length are never
+// selected). `meta()` returns the row's expansion inputs and leaves the
+// element pages in pg; it is called after the bound, which needs the scores
+// alone, so loads it waits for can still be in flight while the bound is
+// computed. DIRECT writes the expansion from the selecting threads
+// (direct_expansion) when the row allows it. Returns the row's expansion
+// inputs (sequence length and position).
+template <int THREADS, int ITEMS, bool EXPAND, bool PAGES, bool DIRECT, typename Stage,
+          typename Meta>
+__device__ __forceinline__ RowMeta process_loaded_whole(const DirectLoader& load, int limit,
+                                                        const uint32_t (&v)[ITEMS],
+                                                        const int (&pg)[ITEMS], Meta&& meta,
+                                                        int length_raw, int clamp, int topk,
+                                                        const ExpandMeta& m, int row,
+                                                        int32_t* out, TopkShared<THREADS>& sh,
+                                                        Stage& st, int* sel) {
   constexpr int kWaves = THREADS / 64;
   constexpr int kEntries = ITEMS * kWaves;  // (item, wave) counts, item-major
   static_assert(ITEMS <= 16 && 64 % kWaves == 0, "count layout");
@@ -895,6 +1089,10 @@ __device__ __forceinline__ void process_loaded_whole(const DirectLoader& load, i
       hi = max(hi, sh.wmax[w]);
     }
   }
+  const RowPrefetch f = meta();
+  // The expansion written by the selecting threads (uniform).
+  static_assert(!DIRECT || THREADS <= 512, "the direct writer runs on all of the row's threads");
+  const bool direct = DIRECT && EXPAND && (PAGES || !m.physical) && direct_expansion(m);
   if (length > topk && lo != kNoBound && lo <= hi) {
     uint32_t cand = 0;
     int below[ITEMS];  // candidates of item i in lower lanes of this wave
@@ -940,6 +1138,15 @@ __device__ __forceinline__ void process_loaded_whole(const DirectLoader& load, i
         }
       }
       lds_barrier();
+      if (direct) {
+        if (kCompact == 1 || total <= THREADS)
+          select_compacted_direct<THREADS, 1, PAGES>(total, topk, lo, hi, ckey, cid, cpage, m, f,
+                                                     row, out, sh);
+        else
+          select_compacted_direct<THREADS, kCompact, PAGES>(total, topk, lo, hi, ckey, cid, cpage,
+                                                            m, f, row, out, sh);
+        return f.r;
+      }
       // A 1024-thread row hands up to 1024 candidates to its lower 512
       // threads and the upper waves end: a barrier waits only for the waves
       // that have not ended, so every radix pass, block scan and barrier of
@@ -948,14 +1155,14 @@ __device__ __forceinline__ void process_loaded_whole(const DirectLoader& load, i
       // already cleared).
       if constexpr (THREADS == 1024) {
         if (total <= 1024) {
-          if (__builtin_amdgcn_readfirstlane(wave) >= 8) return;  // a uniform branch: the wave ends
+          if (__builtin_amdgcn_readfirstlane(wave) >= 8) return f.r;  // a uniform branch: the wave ends
           auto& sh2 = *reinterpret_cast<TopkShared<512>*>(&sh);
           if (total <= 512)
             select_compacted<512, 1, PAGES>(total, topk, lo, hi, ckey, cid, cpage, m, sh2, sel);
           else
             select_compacted<512, 2, PAGES>(total, topk, lo, hi, ckey, cid, cpage, m, sh2, sel);
           write_row<512, EXPAND>(f, topk, m, row, out, sh2, sel);
-          return;
+          return f.r;
         }
       }
       // sel shares the key stage's first 2 * topk words (topk <= total <=
@@ -967,7 +1174,7 @@ __device__ __forceinline__ void process_loaded_whole(const DirectLoader& load, i
         select_compacted<THREADS, kCompact, PAGES>(total, topk, lo, hi, ckey, cid, cpage, m, sh,
                                                   sel);
       write_row<THREADS, EXPAND>(f, topk, m, row, out, sh, sel);
-      return;
+      return f.r;
     }
     lds_barrier();  // every wave has read the counts before they are reused
   }
@@ -976,10 +1183,21 @@ __device__ __forceinline__ void process_loaded_whole(const DirectLoader& load, i
   stage_loaded<THREADS, ITEMS, PAGES>(load, v, pg, key, id, sh, st);
   finish_row<THREADS, ITEMS, EXPAND, PAGES>(load, key, id, f, st, limit, length_raw, clamp, topk,
                                             m, row, out, sh, sel);
+  return f.r;
 }
 
 // Returns the row's expansion inputs (sequence length and position).
-template <int THREADS, int ITEMS, bool EXPAND, bool PAGES, typename Stage>
+//
+// FUSED (the decode selection inside the attention's workgroups, writing the
+// expanded row into LDS): the scores go out first, then the element pages
+// from the guessed table row and the request (load_request), so the bound is
+// computed while those are in flight, and the selecting threads write the
+// expansion. Measured on decode_32k's rows it shortens the selection phase of
+// each workgroup, while for rows written to global memory (the top-k kernels)
+// both changes were slower: the per-block 16-byte stores to scattered
+// columns cost more than the column-coalesced writer, and the later page
+// loads more than the earlier bound.
+template <int THREADS, int ITEMS, bool EXPAND, bool PAGES, typename Stage, bool FUSED = false>
 __device__ __forceinline__ RowMeta process_row_whole(const DirectLoader& load, int limit,
                                                      int length_raw, int clamp, int topk,
                                                      const ExpandMeta& m, int row, int32_t* out,
@@ -987,10 +1205,17 @@ __device__ __forceinline__ RowMeta process_row_whole(const DirectLoader& load, i
                                                      int* sel) {
   uint32_t v[ITEMS];
   int pg[ITEMS];
-  const RowPrefetch f = load_row<THREADS, ITEMS, EXPAND, PAGES>(load, limit, m, row, v, pg);
-  process_loaded_whole<THREADS, ITEMS, EXPAND, PAGES>(load, limit, v, pg, f, length_raw, clamp,
-                                                      topk, m, row, out, sh, st, sel);
-  return f.r;
+  if constexpr (FUSED) {
+    load_scores<THREADS, ITEMS>(load, limit, v);
+    const RowRequest q = load_request<THREADS, ITEMS, EXPAND, PAGES>(load, limit, m, row, pg);
+    return process_loaded_whole<THREADS, ITEMS, EXPAND, PAGES, true>(
+        load, limit, v, pg, [&] { return load_pages<THREADS, ITEMS, EXPAND, PAGES>(load, limit, m, q, pg); },
+        length_raw, clamp, topk, m, row, out, sh, st, sel);
+  } else {
+    const RowPrefetch f = load_row<THREADS, ITEMS, EXPAND, PAGES>(load, limit, m, row, v, pg);
+    return process_loaded_whole<THREADS, ITEMS, EXPAND, PAGES, false>(
+        load, limit, v, pg, [&] { return f; }, length_raw, clamp, topk, m, row, out, sh, st, sel);
+  }
 }
 
 }  // namespace
