@@ -172,5 +172,108 @@ __device__ __forceinline__ void score_tiles(const IndexerParams& p, const int32_
   }
 }
 
+// s_waitcnt immediate that waits for the vector-memory counter alone (gfx9
+// encoding: vmcnt in bits 3:0 and 15:14, expcnt and lgkmcnt at their maxima).
+constexpr int ix_vmcnt_only(int n) { return (n & 15) | (7 << 4) | (15 << 8) | ((n >> 4) << 14); }
+
+// Waits until at most n (a multiple of 4 below 32, constant once the caller's
+// loop is unrolled) vector-memory operations are in flight.
+__device__ __forceinline__ void wait_vmcnt_quads(int n) {
+  switch (n) {
+    case 0: __builtin_amdgcn_s_waitcnt(ix_vmcnt_only(0)); break;
+    case 4: __builtin_amdgcn_s_waitcnt(ix_vmcnt_only(4)); break;
+    case 8: __builtin_amdgcn_s_waitcnt(ix_vmcnt_only(8)); break;
+    case 12: __builtin_amdgcn_s_waitcnt(ix_vmcnt_only(12)); break;
+    case 16: __builtin_amdgcn_s_waitcnt(ix_vmcnt_only(16)); break;
+    case 20: __builtin_amdgcn_s_waitcnt(ix_vmcnt_only(20)); break;
+    case 24: __builtin_amdgcn_s_waitcnt(ix_vmcnt_only(24)); break;
+    default: __builtin_amdgcn_s_waitcnt(ix_vmcnt_only(28)); break;
+  }
+}
+
+// score_tiles with the keys moved straight into LDS (D = 128, a cache page of
+// a multiple of 16 keys, so a tile's keys share one page-table entry).
+// global_load_lds_dwordx4 writes lane l's 16 bytes at the destination + 16 l,
+// so instruction i of a tile moves keys 4 i .. 4 i + 3 as whole 256 B rows
+// (lane (n, g) loads unit n ^ (4 i + g) of key 4 i + g): four full rows per
+// instruction instead of the B operand's 16 keys x 64 bytes, which a CU's
+// texture path streams at about half the rate. Unit c of key m then sits at
+// position c ^ m of its row, so the B-operand reads (lane (n, g): unit 4 s +
+// g of key n) are conflict-free. The data never passes through VGPRs; each
+// tile's reads wait (vmcnt) only for that tile's four loads. `region`: the
+// wave's TPW x 4 KB of LDS.
+template <int HB, int TPW, typename Sink>
+__device__ __forceinline__ void score_tiles_dma(const IndexerParams& p, const int32_t* trow,
+                                                int tile0, int vis, const bf16x8 (&qa)[HB][4],
+                                                char* region, Sink sink) {
+  static_assert(TPW <= 8, "at most 28 loads behind a tile");
+  constexpr int kTileBytes = kKeysPerTile * 256;
+  const int n = threadIdx.x & 15;
+  const int g = (threadIdx.x >> 4) & 3;
+  const char* zero = reinterpret_cast<const char*>(g_qsa_zero_rows);
+  const int32_t* zero_i = reinterpret_cast<const int32_t*>(g_qsa_zero_rows);
+  // Every read of the region from a previous call has completed before the
+  // new rows overwrite it.
+  __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0)
+  __builtin_amdgcn_sched_barrier(0);
+  // Lane t < TPW loads tile t's page-table entry (one load, one wait); the
+  // tiles' pages are then read from those lanes.
+  const int tl = (int)(threadIdx.x % TPW);
+  const int cl = (tile0 + tl) * kKeysPerTile;
+  const int page_l = *(cl < vis ? trow + p.page_div.div(cl) : zero_i);
+  int page[TPW];
+#pragma unroll
+  for (int t = 0; t < TPW; ++t) page[t] = __builtin_amdgcn_readlane(page_l, t);
+  // This lane's byte offsets within a tile's first key, the same for every
+  // tile: instruction i, key 4 i + g, unit n ^ key.
+  int64_t loff[4];
+  int zoff[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int key = 4 * i + g;
+    zoff[i] = 16 * (n ^ key);
+    loff[i] = (int64_t)key * p.kt + zoff[i];
+  }
+#pragma unroll
+  for (int t = 0; t < TPW; ++t) {
+    const int c0 = (tile0 + t) * kKeysPerTile;
+    const int off0 = c0 - p.page_div.div(c0) * p.cache_page;
+    const bool page_ok = page[t] >= 0 && page[t] < p.num_blocks;
+    const char* base = p.k + (int64_t)page[t] * p.kb + (int64_t)off0 * p.kt;  // uniform
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const bool ok = page_ok && c0 + 4 * i + g < vis;
+      const char* src = ok ? base + loff[i] : zero + zoff[i];
+      __builtin_amdgcn_global_load_lds(
+          (const __attribute__((address_space(1))) void*)src,
+          (__attribute__((address_space(3))) void*)(region + t * kTileBytes + i * 1024), 16, 0,
+          0);
+    }
+  }
+  __builtin_amdgcn_sched_barrier(0);
+  // The logits are stored after the last tile: a store counts as a vector
+  // memory operation too, and one issued between the tiles would make each
+  // later tile's wait cover it as well.
+  float val[TPW];
+#pragma unroll
+  for (int t = 0; t < TPW; ++t) {
+    // Tile t has landed once at most the later tiles' loads are in flight.
+    wait_vmcnt_quads(4 * (TPW - 1 - t));
+    __builtin_amdgcn_sched_barrier(0);
+    bf16x8 kb[4];
+    const char* krow = region + t * kTileBytes + n * 256;
+#pragma unroll
+    for (int s2 = 0; s2 < 4; ++s2)
+      kb[s2] = __builtin_bit_cast(
+          bf16x8, *reinterpret_cast<const u32x4*>(krow + 16 * ((4 * s2 + g) ^ n)));
+    val[t] = tile_logit<128, HB>(p, qa, kb);
+  }
+#pragma unroll
+  for (int t = 0; t < TPW; ++t) {
+    const int c = (tile0 + t) * kKeysPerTile + n;
+    if (threadIdx.x < 16 && c < vis) sink(c, val[t]);
+  }
+}
+
 }  // namespace
 }  // namespace qsa

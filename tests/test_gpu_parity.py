@@ -193,13 +193,17 @@ def _score_tol(q, keys, dim):
     return 2e-5 * mag + 1e-6
 
 
-# The last two cases launch at least one wave per CU, which takes the
-# eight-tiles-per-wave split; the others take four.
-# The last case's longest rows need two passes of their waves (rows stride
-# over their keys: the grid follows the batch, not the logits width).
+# The last three cases launch at least one wave per CU, which takes the
+# eight-tiles-per-wave split; the others take four. Head dim 128 moves the keys
+# into LDS (the index cache page is 16 keys), head dim 64 loads them straight
+# into the MFMA operand.
+# The 64 x 400 case's longest rows need two passes of their waves (rows stride
+# over their keys, reusing the wave's LDS region: the grid follows the batch,
+# not the logits width). The 520-row case's first 512 rows, launched alone (a
+# different program count), must match bit for bit.
 @pytest.mark.parametrize("heads,dim,dql,reqs,width", [
     (32, 128, 1, 9, 13), (8, 64, 1, 9, 13), (4, 128, 2, 9, 13), (48, 128, 1, 9, 13),
-    (32, 128, 1, 36, 64), (16, 64, 2, 20, 64), (32, 128, 1, 64, 400)])
+    (32, 128, 1, 36, 64), (16, 64, 2, 20, 64), (32, 128, 1, 64, 400), (8, 64, 1, 520, 4)])
 def test_indexer_decode_parity(heads, dim, dql, reqs, width):
     _note(f"indexer_decode heads={heads} dim={dim} dql={dql} reqs={reqs} width={width}")
     g = torch.Generator().manual_seed(heads + dim + dql + reqs)
@@ -232,6 +236,11 @@ def test_indexer_decode_parity(heads, dim, dql, reqs, width):
         torch.ops.yulan_qsa_kernels.indexer_decode(q[:sub].to(DEV), cache.to(DEV), table[:2].to(DEV),
                                                    vis[:sub].to(DEV), small, dql)
         assert torch.equal(small.cpu().nan_to_num(-7.0), got[:sub].nan_to_num(-7.0))
+    if rows > 512:
+        part = torch.full((512, cols), float("nan"), device=DEV)
+        torch.ops.yulan_qsa_kernels.indexer_decode(q[:512].to(DEV), cache.to(DEV), table.to(DEV),
+                                                   vis[:512].to(DEV), part, dql)
+        assert torch.equal(part.cpu().nan_to_num(-7.0), got[:512].nan_to_num(-7.0))
 
 
 def test_indexer_prefill_parity():
