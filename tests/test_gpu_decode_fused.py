@@ -46,14 +46,19 @@ def _logits(wl):
     return logits
 
 
-def _two_calls(wl, logits, num_splits, pad_row):
+def _requests(wl, pad_row, t2r):
+    t2r = wl.token_to_req.clone() if t2r is None else t2r.clone()
+    if pad_row:
+        t2r[-1] = -1
+    return t2r
+
+
+def _two_calls(wl, logits, num_splits, pad_row, t2r=None):
     s = wl.shape
     idx = torch.full((wl.rows, s.width), -7, dtype=torch.int32, device=wl.device)
     counts = torch.full((wl.rows,), -7, dtype=torch.int32, device=wl.device)
     out = torch.zeros_like(wl.q)
-    t2r = wl.token_to_req.clone()
-    if pad_row:
-        t2r[-1] = -1
+    t2r = _requests(wl, pad_row, t2r)
     torch.ops.yulan_qsa_kernels.topk_expand(logits, wl.visible, wl.positions, wl.seq_lens, t2r,
                                             wl.block_table, idx, counts, s.compress_ratio,
                                             s.page_size, True, True)
@@ -63,23 +68,21 @@ def _two_calls(wl, logits, num_splits, pad_row):
     return idx, counts, out
 
 
-def _one_op(wl, logits, num_splits, pad_row):
+def _one_op(wl, logits, num_splits, pad_row, t2r=None):
     s = wl.shape
     idx = torch.full((wl.rows, s.width), -9, dtype=torch.int32, device=wl.device)
     counts = torch.full((wl.rows,), -9, dtype=torch.int32, device=wl.device)
     out = torch.full_like(wl.q, 3.0)
-    t2r = wl.token_to_req.clone()
-    if pad_row:
-        t2r[-1] = -1
+    t2r = _requests(wl, pad_row, t2r)
     torch.ops.yulan_qsa_kernels.decode_select_attend(
         logits, wl.visible, wl.positions, wl.seq_lens, t2r, wl.block_table, idx, counts,
         s.compress_ratio, wl.q, wl.k_cache, wl.v_cache, out, wl.gate, num_splits)
     return idx, counts, out
 
 
-def _check(wl, logits, num_splits, pad_row=False):
-    want = _two_calls(wl, logits, num_splits, pad_row)
-    got = _one_op(wl, logits, num_splits, pad_row)
+def _check(wl, logits, num_splits, pad_row=False, t2r=None):
+    want = _two_calls(wl, logits, num_splits, pad_row, t2r)
+    got = _one_op(wl, logits, num_splits, pad_row, t2r)
     torch.cuda.synchronize()
     assert torch.equal(got[0], want[0]), "selection differs"
     assert torch.equal(got[1], want[1]), "counts differ"
@@ -118,6 +121,21 @@ def test_decode_select_attend_padding_row():
     idx, counts, out = _check(wl, _logits(wl), 0, pad_row=True)
     assert int(counts[-1]) == 0 and bool((idx[-1] == -1).all())
     assert not bool(out[-1].any())
+
+
+@pytest.mark.parametrize("mapping", ["reversed", "pairs"])
+def test_decode_select_attend_request_mapping(mapping):
+    """Rows whose request is not their own index: the combined kernel loads
+    the page-table entries of row r's table row ahead of the request and must
+    load them again from the right row. Reversed requests, and two rows per
+    request (token_to_req[r] = r // 2), against the two calls."""
+    print(f"[case] decode_select_attend request mapping {mapping}", flush=True)
+    wl = make_workload("decode_32k", device="cuda", seed=23)
+    rows = wl.rows
+    r = torch.arange(rows, dtype=torch.int32, device=wl.device)
+    t2r = (rows - 1 - r) if mapping == "reversed" else r // 2
+    idx, counts, out = _check(wl, _logits(wl), 0, t2r=t2r)
+    assert int(counts.min()) >= 0 and bool(out.abs().amax() > 0)
 
 
 def test_decode_select_attend_plugin_entry():
