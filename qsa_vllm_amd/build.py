@@ -24,7 +24,8 @@ LIB_NAME = "libqsa_hip.so"
 LIB_PATH = PACKAGE_DIR / LIB_NAME
 OBJ_DIR = PACKAGE_DIR / "_build"
 
-SOURCES = ["qsa_errors.hip", "prepare.hip", "topk.hip", "indexer.hip", "sparse_attn.hip", "hybrid.hip"]
+SOURCES = ["qsa_errors.hip", "prepare.hip", "topk.hip", "indexer.hip", "sparse_attn.hip",
+           "sparse_attn_wide.hip", "hybrid.hip"]
 
 # Packed fp32 VALU ops are disabled: the kernels get no benefit from them and
 # some of their forms are not trusted on this hardware.

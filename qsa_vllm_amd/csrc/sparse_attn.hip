@@ -53,7 +53,19 @@
 #include "../../include/qsa_hip.h"
 
 #include <algorithm>
+#include <cstring>
 #include <mutex>
+
+// The combined decode kernel for wide logits buffers lives in its own code
+// object (sparse_attn_wide.hip compiles this file with QSA_ATTN_WIDE_UNIT):
+// its long-row selection is over a megabyte of code, and with it in this
+// file's code object the 2048-column kernel - the same instructions -
+// made decode_32k's step 0.4-0.6 us slower (measured: the step returned to
+// its earlier time once the wide kernels moved to a separate code object).
+// Arguments pass as the bytes of this file's FusedSelect and AttnParams.
+extern "C" __attribute__((visibility("hidden"))) int qsa_attn_launch_fused_wide(
+    const void* select, size_t select_bytes, const void* params, size_t params_bytes,
+    unsigned grid_x, unsigned grid_y, unsigned grid_z, int head_dim, int nkv, hipStream_t stream);
 
 namespace qsa {
 namespace {
@@ -893,13 +905,29 @@ struct FusedTopkLds {
   alignas(16) TopkStage<THREADS, ITEMS, true> st;
 };
 
-template <int D, int NKV, int WAVES, int ITEMS>
+// Selection LDS of a wide buffer's long rows (select_wide_row).
+struct FusedWideLds {
+  TopkShared<kWideThreads> sh;
+  alignas(16) uint32_t stage[kWideThreads * 32 * 2];
+};
+
+// WIDE: a logits buffer wider than 2048 columns (a decode batch in a wide
+// width class, whose rows are usually much shorter than the buffer). As
+// topk_adaptive_kernel does, every workgroup issues the loads of the row's
+// first 2048 columns in the 512 x 4 shape before the row's length arrives;
+// a row of at most 2048 keys is then selected from them, a longer one by
+// select_wide_row (up to 32768 keys, slower than the top-k launch's 1024
+// threads, but a row that long is rare in such a class).
+template <int D, int NKV, int WAVES, int ITEMS, bool WIDE>
 __global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(2)))
 void select_attend_kernel(const FusedSelect a, const AttnParams p) {
   constexpr int kThreads = 64 * WAVES;
   using Lds = AttnLds<D, NKV, WAVES, true>;
   using Topk = FusedTopkLds<kThreads, ITEMS>;
-  constexpr int kBytes = Lds::kBufBytes > (int)sizeof(Topk) ? Lds::kBufBytes : (int)sizeof(Topk);
+  constexpr int kSelBytes =
+      WIDE && (int)sizeof(FusedWideLds) > (int)sizeof(Topk) ? (int)sizeof(FusedWideLds)
+                                                             : (int)sizeof(Topk);
+  constexpr int kBytes = Lds::kBufBytes > kSelBytes ? Lds::kBufBytes : kSelBytes;
   __shared__ __attribute__((aligned(16))) char s_lds[kBytes];
   __shared__ float s_m[WAVES][16];
   __shared__ float s_l[WAVES][16];
@@ -907,9 +935,34 @@ void select_attend_kernel(const FusedSelect a, const AttnParams p) {
   auto& tk = *reinterpret_cast<Topk*>(s_lds);
   const int row = blockIdx.x;
   const float* srow = a.scores + (int64_t)row * a.score_row_stride;
-  const RowMeta r = process_row_whole<kThreads, ITEMS, true, true, decltype(tk.st), true>(
-      DirectLoader{srow, 0}, a.cols, a.lengths[row], a.cols, a.topk, a.meta, row, s_idx, tk.sh,
-      tk.st, reinterpret_cast<int*>(tk.st.key));
+  RowMeta r;
+  if constexpr (WIDE) {
+    static_assert(kThreads == kWideThreads && ITEMS == 4, "the 512 x 4 shape of 2048 columns");
+    constexpr int kNarrowCols = kThreads * ITEMS;
+    const DirectLoader load{srow, 0};
+    uint32_t v[ITEMS];
+    int pg[ITEMS];
+    load_scores<kThreads, ITEMS>(load, kNarrowCols, v);
+    const RowRequest q =
+        load_request<kThreads, ITEMS, true, true>(load, kNarrowCols, a.meta, row, pg);
+    // Nothing below may wait for the length before the loads above are out.
+    __builtin_amdgcn_sched_barrier(0);
+    const int length = a.lengths[row];
+    if (min(length, a.cols) <= kNarrowCols) {  // uniform
+      r = process_loaded_whole<kThreads, ITEMS, true, true, true>(
+          load, kNarrowCols, v, pg,
+          [&] { return load_pages<kThreads, ITEMS, true, true>(load, kNarrowCols, a.meta, q, pg); },
+          length, a.cols, a.topk, a.meta, row, s_idx, tk.sh, tk.st,
+          reinterpret_cast<int*>(tk.st.key));
+    } else {
+      auto& wide = *reinterpret_cast<FusedWideLds*>(s_lds);
+      r = select_wide_row(srow, a.cols, length, a.topk, a.meta, row, s_idx, wide.sh, wide.stage);
+    }
+  } else {
+    r = process_row_whole<kThreads, ITEMS, true, true, decltype(tk.st), true>(
+        DirectLoader{srow, 0}, a.cols, a.lengths[row], a.cols, a.topk, a.meta, row, s_idx, tk.sh,
+        tk.st, reinterpret_cast<int*>(tk.st.key));
+  }
   const int count = expanded_span(a.meta, r, a.topk).count(r);
   __syncthreads();  // the row is in s_idx; the top-k's LDS is free for the attention
   attend<D, NKV, WAVES, true, true, true>(p, row, blockIdx.y, blockIdx.z, s_idx, count, s_lds,
@@ -1116,6 +1169,32 @@ int launch_merge(const float* part_out, const float* part_lse, int num_splits, i
 
 }  // namespace
 }  // namespace qsa
+
+#ifdef QSA_ATTN_WIDE_UNIT
+
+extern "C" __attribute__((visibility("hidden"))) int qsa_attn_launch_fused_wide(
+    const void* select, size_t select_bytes, const void* params, size_t params_bytes,
+    unsigned grid_x, unsigned grid_y, unsigned grid_z, int head_dim, int nkv, hipStream_t stream) {
+  using namespace qsa;
+  if (select_bytes != sizeof(FusedSelect) || params_bytes != sizeof(AttnParams))
+    return (int)hipErrorInvalidValue;
+  FusedSelect a;
+  AttnParams p;
+  std::memcpy(&a, select, sizeof a);
+  std::memcpy(&p, params, sizeof p);
+  const dim3 grid(grid_x, grid_y, grid_z);
+  if (head_dim == 128 && nkv == 1)
+    hipLaunchKernelGGL((select_attend_kernel<128, 1, 8, 4, true>), grid, dim3(512), 0, stream, a, p);
+  else if (head_dim == 128)
+    hipLaunchKernelGGL((select_attend_kernel<128, 2, 8, 4, true>), grid, dim3(512), 0, stream, a, p);
+  else if (nkv == 1)
+    hipLaunchKernelGGL((select_attend_kernel<64, 1, 8, 4, true>), grid, dim3(512), 0, stream, a, p);
+  else
+    hipLaunchKernelGGL((select_attend_kernel<64, 2, 8, 4, true>), grid, dim3(512), 0, stream, a, p);
+  return (int)hipGetLastError();
+}
+
+#else  // the library's entry points
 
 using namespace qsa;
 
@@ -1335,7 +1414,8 @@ constexpr int kFusedMaxRows = 1024;
 constexpr int kFusedMaxColumns = 2048;
 
 // Keys per thread of the fused selection (512 threads): every row of up to
-// `cols` keys in the workgroup's registers.
+// `cols` keys in the workgroup's registers; a wider buffer starts with its
+// rows' first 2048 columns (the WIDE kernel).
 int fused_items(int cols) { return cols <= 1024 ? 2 : 4; }
 
 // Whether a decode batch's selection and attention run as one launch: the
@@ -1349,17 +1429,22 @@ int fused_items(int cols) { return cols <= 1024 ? 2 : 4; }
 // 17.96 / 19.19 / 19.94 / 22.67 / 26.04 / 28.52 combined).
 bool fuses(int rows, int cols, int width, int ratio, int waves, bool buf, int nkv) {
   const int topk = ratio > 0 ? width / ratio : 0;
-  return rows > 0 && rows < kFusedMaxRows && cols <= kFusedMaxColumns && topk > 0 &&
+  return rows > 0 && rows < kFusedMaxRows && cols <= kWideMaxColumns && topk > 0 &&
          2 * topk <= 512 * fused_items(cols) && width <= kFusedMaxWidth && waves == 8 && buf &&
          nkv <= 2;
 }
 
 template <int D, int NKV>
 hipError_t launch_fused(const FusedSelect& a, const AttnLaunch& L, hipStream_t s) {
+  if (a.cols > kFusedMaxColumns)
+    return (hipError_t)qsa_attn_launch_fused_wide(&a, sizeof a, &L.p, sizeof L.p, L.grid.x,
+                                                  L.grid.y, L.grid.z, D, NKV, s);
   if (fused_items(a.cols) == 2)
-    hipLaunchKernelGGL((select_attend_kernel<D, NKV, 8, 2>), L.grid, dim3(512), 0, s, a, L.p);
+    hipLaunchKernelGGL((select_attend_kernel<D, NKV, 8, 2, false>), L.grid, dim3(512), 0, s, a,
+                       L.p);
   else
-    hipLaunchKernelGGL((select_attend_kernel<D, NKV, 8, 4>), L.grid, dim3(512), 0, s, a, L.p);
+    hipLaunchKernelGGL((select_attend_kernel<D, NKV, 8, 4, false>), L.grid, dim3(512), 0, s, a,
+                       L.p);
   return hipGetLastError();
 }
 
@@ -1554,3 +1639,4 @@ extern "C" int qsa_sparse_attention_noalloc(
       stream);
 }
 
+#endif  // QSA_ATTN_WIDE_UNIT

@@ -1218,5 +1218,89 @@ __device__ __forceinline__ RowMeta process_row_whole(const DirectLoader& load, i
   }
 }
 
+// The expansion inputs of a row (its request's sequence length, its position
+// and the request's page-table row), loaded directly.
+__device__ __forceinline__ RowMeta load_row_meta(const ExpandMeta& m, int row) {
+  const int req = m.token_to_req[row];
+  const bool mapped = req >= 0 && req < m.num_requests;
+  RowMeta r;
+  r.seq_len = mapped ? m.sequence_lengths[req] : 0;
+  r.pos = (int)m.positions[row];
+  r.table_row = m.physical ? m.table + (int64_t)(mapped ? req : 0) * m.table_row_stride : nullptr;
+  return r;
+}
+
+// A row of a wide logits buffer selected by one 512-thread workgroup into an
+// expanded row `out` (the decode selection inside the attention's
+// workgroups, for rows longer than the 2048 keys its usual shape holds).
+// As topk_adaptive_kernel with half the threads: up to 8192 keys as a whole
+// row (8 or 16 keys per thread by the row's length, the selecting threads
+// writing the expansion); up to 16384 staged through LDS, 32 keys per thread;
+// 16385..32768 keys as exact top-k of the two halves in turn (winners kept
+// in LDS), then exact top-k over the halves' winners in id order. `stage` is
+// 512 x 32 keys and as many pages or winners (128 KB). Needs 2 topk <= 8192
+// (the combined decode kernel allows 2 topk <= 2048).
+constexpr int kWideThreads = 512;
+constexpr int kWideHalf = kWideThreads * 32;
+constexpr int kWideMaxColumns = 2 * kWideHalf;
+
+__device__ __forceinline__ RowMeta select_wide_row(const float* srow, int cols, int length,
+                                                   int topk, const ExpandMeta& m, int row,
+                                                   int32_t* out, TopkShared<kWideThreads>& sh,
+                                                   uint32_t* stage) {
+  constexpr int T = kWideThreads;
+  const int n = min(max(length, 0), cols);
+  const int whole = max(n, 2 * topk);
+  if (whole <= T * 16) {
+    const DirectLoader load{srow, 0};
+#define QSA_WIDE_WHOLE_ROW(ITEMS)                                                              \
+  {                                                                                            \
+    using Stage = TopkStage<T, ITEMS, true>;                                                   \
+    auto& st = *reinterpret_cast<Stage*>(stage);                                               \
+    return process_row_whole<T, ITEMS, true, true, Stage, true>(                               \
+        load, n, length, cols, topk, m, row, out, sh, st, reinterpret_cast<int*>(st.key));     \
+  }
+    if (whole <= T * 8) QSA_WIDE_WHOLE_ROW(8)
+    else QSA_WIDE_WHOLE_ROW(16)
+#undef QSA_WIDE_WHOLE_ROW
+  }
+  if (n <= kWideHalf) {
+    auto& st = *reinterpret_cast<TopkStage<T, 32, true>*>(stage);
+    process_row<T, 32, true, true>(DirectLoader{srow, 0}, n, length, cols, topk, m, row, out, sh,
+                                   st, reinterpret_cast<int*>(st.key));
+    return load_row_meta(m, row);
+  }
+  // Halves [0, kWideHalf) and [kWideHalf, n); the winners (ascending ids) go
+  // past the halves' key stage, the second half's after the first's, so the
+  // merged list is in id order (ties go to the lower id, as in one pass).
+  int* winners = reinterpret_cast<int*>(stage + T * 32);
+  auto& hst = *reinterpret_cast<TopkStage<T, 32, false>*>(stage);
+  int* hsel = reinterpret_cast<int*>(hst.key);
+  process_row<T, 32, false, false>(DirectLoader{srow, 0}, kWideHalf, kWideHalf, kWideHalf, topk, m,
+                                   row, winners, sh, hst, hsel);
+  __syncthreads();
+  const int rest = n - kWideHalf;
+  process_row<T, 32, false, false>(DirectLoader{srow, kWideHalf}, rest, rest, rest, topk, m, row,
+                                   winners + topk, sh, hst, hsel);
+  __syncthreads();
+  const int count = topk + min(rest, topk);
+  const IndirectLoader merged{srow, winners};
+  // Each thread reads its candidates' ids before it overwrites the same LDS
+  // words with their pages (the page half of a 32-key stage is the winners).
+  const int need = max(count, 2 * topk);
+#define QSA_WIDE_MERGED(ITEMS)                                                                 \
+  {                                                                                            \
+    auto& st = *reinterpret_cast<TopkStage<T, ITEMS, true>*>(stage);                           \
+    process_row<T, ITEMS, true, true>(merged, count, count, count, topk, m, row, out, sh, st,  \
+                                      reinterpret_cast<int*>(st.key));                         \
+  }
+  if (need <= T * 2) QSA_WIDE_MERGED(2)
+  else if (need <= T * 4) QSA_WIDE_MERGED(4)
+  else if (need <= T * 8) QSA_WIDE_MERGED(8)
+  else QSA_WIDE_MERGED(16)
+#undef QSA_WIDE_MERGED
+  return load_row_meta(m, row);
+}
+
 }  // namespace
 }  // namespace qsa

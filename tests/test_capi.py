@@ -224,7 +224,12 @@ def test_decode_select_attention_fusion_rule():
     assert fuses(64, 2048, 2063, 16, 8, 1, 64) == 1
     assert fuses(1023, 2048, 2063, 16, 16, 2, 128) == 1
     assert fuses(1024, 2048, 2063, 16, 16, 2, 128) == 0  # throughput-shaped top-k
-    assert fuses(64, 4096, 2063, 16, 16, 2, 128) == 0    # wider than 2048 columns
+    # A wide class: the first 2048 columns in the 512 x 4 shape, longer rows
+    # selected inside the workgroup, up to 32768 columns.
+    assert fuses(64, 4096, 2063, 16, 16, 2, 128) == 1
+    assert fuses(64, 32768, 2063, 16, 16, 2, 128) == 1
+    assert fuses(64, 32769, 2063, 16, 16, 2, 128) == 0
+    assert fuses(64, 65536, 2063, 16, 16, 2, 128) == 0
     assert fuses(16, 2048, 2063, 16, 16, 2, 128) == 0    # 4-wave attention workgroups
     assert fuses(1, 1024, 2063, 16, 16, 2, 128) == 0
     assert fuses(512, 2048, 2063, 16, 16, 4, 128) == 0   # 4 kv heads per workgroup

@@ -33,6 +33,17 @@ CASES = [
     ("long_rows_8192_columns", {"batch": 8, "seq_len_min": 65536, "seq_len_max": 131072,
                                 "seed": 17}, False),
     ("head_major_cache", {"kv_layout": "head_major", "seed": 18}, False),
+    # The plugin's 32768-column class (max-model-len 524288): rows of at most
+    # 2048 keys selected from their first 2048 columns...
+    ("serving_width_32768_columns", {"table_tokens": 524288, "seed": 24}, True),
+    # ...and rows of 256 to 32768 keys in that class: whole rows of up to 2048
+    # and 8192 keys, rows of up to 16384 staged through LDS, longer rows from
+    # their two halves, all inside the attention's workgroups.
+    # (45 / 10 / 6 / 3 rows, 3.2 M tokens: the K/V views stay under the 4 GB
+    # that buffer addressing covers.)
+    ("wide_class_long_rows", {"table_tokens": 524288, "seq_len_dist": "lognormal",
+                              "lognormal_median": 24576.0, "lognormal_sigma": 1.5,
+                              "seq_len_min": 4096, "seq_len_max": 524288, "seed": 38}, True),
 ]
 
 
