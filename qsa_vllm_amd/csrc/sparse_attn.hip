@@ -1094,20 +1094,21 @@ bool plan_heads(int num_q_heads, int num_kv_heads, int rows, bool physical, Head
   return true;
 }
 
-// Waves per workgroup. Physical (decode) rows: 8 once (row, head group)
-// pairs alone reach 64, so a few splits give every CU one 8-wave workgroup; 4
-// below that, where more and smaller workgroups spread a small batch wider. On
-// the 64-row, 16-head decode shape 8 waves x 4 splits measured faster than 4
-// waves x 8 splits. Logical (prefill) rows always take 4 waves: at 256
+// Waves per workgroup. Physical (decode) rows take 8 at every batch: on the
+// 64-row, 16-head decode shape 8 waves x 4 splits measured faster than 4 waves
+// x 8 splits, and small batches (1 to 31 rows, four rotating query sets) ran
+// the attention alone 0.0-0.4 us faster with 8 waves than with 4 and, through
+// the combined selection + attention launch that 8 waves make possible,
+// 1.5-2 us faster than as two launches. Logical (prefill) rows always take 4 waves: at 256
 // registers a lane two such workgroups share a CU, so one row's start (index ->
 // table -> K round trips) overlaps the other's streaming; measured 5.11 ms
 // against 5.58 ms with 8 waves on the 32768-row chunked prefill. D = 128 with
 // 4 kv heads per group needs more than the 256 registers a lane gets at two
 // waves per SIMD, so it always runs 4 waves (one per SIMD).
 bool fits_8_waves(int head_dim, int nkv) { return !(head_dim == 128 && nkv == 4); }
-int waves_for(int rows, const HeadPlan& plan, int head_dim, bool physical) {
+int waves_for(const HeadPlan& plan, int head_dim, bool physical) {
   if (!physical) return 4;
-  return (int64_t)rows * plan.groups >= 64 && fits_8_waves(head_dim, plan.nkv) ? 8 : 4;
+  return fits_8_waves(head_dim, plan.nkv) ? 8 : 4;
 }
 
 template <int D, int NKV, bool PHYSICAL, bool BUF>
@@ -1341,7 +1342,7 @@ int prepare_attention(
   L->p = p;
   L->plan = plan;
   L->grid = dim3(rows, num_splits, plan.groups);
-  L->waves = waves_for(rows, plan, head_dim, indices_are_physical != 0);
+  L->waves = waves_for(plan, head_dim, indices_are_physical != 0);
   L->head_dim = head_dim;
   L->out_row = out_row_stride;
   L->out_head = out_head_stride;
@@ -1419,14 +1420,14 @@ constexpr int kFusedMaxColumns = 2048;
 int fused_items(int cols) { return cols <= 1024 ? 2 : 4; }
 
 // Whether a decode batch's selection and attention run as one launch: the
-// top-k's 512-thread shapes (rows < 1024, at most 2048 columns, the selected
-// ids within the key stage), an expanded row that fits LDS, and the
+// top-k's 512-thread shapes (rows < 1024, at most kWideMaxColumns columns, the
+// selected ids within the key stage), an expanded row that fits LDS, and the
 // attention's 8-wave, buffer-addressed plan with at most 2 kv heads per
-// workgroup. Smaller batches (4-wave attention workgroups) keep two launches:
-// a 256-thread selection (256 x 4 and 256 x 8) inside their workgroups cost
-// as much as the launch it removed (batch 1, 4, 8, 16, 24, 31 of decode_32k's
-// shapes: 17.93 / 18.76 / 19.66 / 22.57 / 26.09 / 28.44 us as two launches,
-// 17.96 / 19.19 / 19.94 / 22.67 / 26.04 / 28.52 combined).
+// workgroup. 4-wave workgroups (D = 128 with 4 kv heads per group) keep two
+// launches: a 256-thread selection inside them cost as much as the launch it
+// removed (batch 1, 4, 8, 16, 24, 31 of decode_32k's shapes when those batches
+// ran 4 waves: 17.93 / 18.76 / 19.66 / 22.57 / 26.09 / 28.44 us as two
+// launches, 17.96 / 19.19 / 19.94 / 22.67 / 26.04 / 28.52 combined).
 bool fuses(int rows, int cols, int width, int ratio, int waves, bool buf, int nkv) {
   const int topk = ratio > 0 ? width / ratio : 0;
   return rows > 0 && rows < kFusedMaxRows && cols <= kWideMaxColumns && topk > 0 &&
@@ -1457,7 +1458,7 @@ extern "C" int qsa_decode_select_attention_fuses(int rows, int cols, int width, 
   HeadPlan plan;
   if ((head_dim != 64 && head_dim != 128) || !plan_heads(num_q_heads, num_kv_heads, rows, true, &plan))
     return 0;
-  return fuses(rows, cols, width, ratio, waves_for(rows, plan, head_dim, true), true, plan.nkv);
+  return fuses(rows, cols, width, ratio, waves_for(plan, head_dim, true), true, plan.nkv);
 }
 
 extern "C" size_t qsa_decode_select_attention_workspace_bytes(int rows, int cols, int width,

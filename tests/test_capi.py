@@ -230,8 +230,10 @@ def test_decode_select_attention_fusion_rule():
     assert fuses(64, 32768, 2063, 16, 16, 2, 128) == 1
     assert fuses(64, 32769, 2063, 16, 16, 2, 128) == 0
     assert fuses(64, 65536, 2063, 16, 16, 2, 128) == 0
-    assert fuses(16, 2048, 2063, 16, 16, 2, 128) == 0    # 4-wave attention workgroups
-    assert fuses(1, 1024, 2063, 16, 16, 2, 128) == 0
+    # Small batches run 8-wave attention workgroups too, so they fuse.
+    assert fuses(16, 2048, 2063, 16, 16, 2, 128) == 1
+    assert fuses(1, 1024, 2063, 16, 16, 2, 128) == 1
+    assert fuses(8, 8192, 2063, 16, 16, 2, 128) == 1
     assert fuses(512, 2048, 2063, 16, 16, 4, 128) == 0   # 4 kv heads per workgroup
     assert fuses(64, 1024, 16399, 16, 16, 2, 128) == 0   # 1024 blocks need more than the stage
     assert fuses(64, 2048, 2063, 16, 16, 2, 96) == 0

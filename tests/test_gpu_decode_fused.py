@@ -26,12 +26,17 @@ CASES = [
     ("dim64_group8", {"num_q_heads": 8, "num_kv_heads": 1, "head_dim": 64, "seed": 14}, True),
     ("dim64_batch256", {"batch": 256, "head_dim": 64, "seq_len_min": 1024,
                         "seq_len_max": 32768, "seed": 15}, True),
-    ("batch_16_four_waves", {"batch": 16, "seed": 16}, False),
-    ("batch_1_four_waves_1024_columns", {"batch": 1, "seq_len_min": 4096,
-                                         "seq_len_max": 16384, "seed": 19}, False),
-    ("batch_8_four_waves_dim64", {"batch": 8, "head_dim": 64, "gate": True, "seed": 20}, False),
+    ("batch_16", {"batch": 16, "seed": 16}, True),
+    ("batch_1_1024_columns", {"batch": 1, "seq_len_min": 4096, "seq_len_max": 16384,
+                              "seed": 19}, True),
+    ("batch_8_dim64", {"batch": 8, "head_dim": 64, "gate": True, "seed": 20}, True),
+    # Rows of 4096 to 8192 keys (decode_long_skew's lengths) from an
+    # 8192-column buffer, selected inside the attention's workgroups.
     ("long_rows_8192_columns", {"batch": 8, "seq_len_min": 65536, "seq_len_max": 131072,
-                                "seed": 17}, False),
+                                "seed": 17}, True),
+    # Past the widest class the combined kernel takes (32768 columns): two calls.
+    ("rows_past_32768_columns", {"batch": 1, "seq_len_min": 655360, "seq_len_max": 655360,
+                                 "seed": 25}, False),
     ("head_major_cache", {"kv_layout": "head_major", "seed": 18}, False),
     # The plugin's 32768-column class (max-model-len 524288): rows of at most
     # 2048 keys selected from their first 2048 columns...
