@@ -948,7 +948,12 @@ void select_attend_kernel(const FusedSelect a, const AttnParams p) {
     // Nothing below may wait for the length before the loads above are out.
     __builtin_amdgcn_sched_barrier(0);
     const int length = a.lengths[row];
-    if (min(length, a.cols) <= kNarrowCols) {  // uniform
+    // Rows longer than 2048 keys are rare in a wide class: the hint keeps
+    // the long-row selection's code out of the way of the common path, which
+    // with it runs straight into the attention (measured: the serving width's
+    // step 42.4 -> 41.2 us and decode_long_skew's 25.4 -> 24.4 us, with the
+    // same instructions otherwise).
+    if (__builtin_expect(min(length, a.cols) <= kNarrowCols, 1)) {  // uniform
       r = process_loaded_whole<kThreads, ITEMS, true, true, true>(
           load, kNarrowCols, v, pg,
           [&] { return load_pages<kThreads, ITEMS, true, true>(load, kNarrowCols, a.meta, q, pg); },

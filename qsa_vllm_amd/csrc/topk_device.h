@@ -1120,7 +1120,10 @@ __device__ __forceinline__ RowMeta process_loaded_whole(const DirectLoader& load
       pre[g] = total + ex;
       total += __builtin_amdgcn_readlane(ex + c, 63);
     }
-    if (total <= kCompact * THREADS) {
+    // The hints here place the rare paths (too many candidates, a row the
+    // direct writer cannot take) after the common one in the code, so the
+    // common path's instructions are contiguous.
+    if (__builtin_expect(total <= kCompact * THREADS, 1)) {
       // Up to THREADS candidates: one per thread (the usual case, and the
       // cheapest radix passes); more: kCompact per thread.
       uint32_t* ckey = st.key;
@@ -1138,8 +1141,8 @@ __device__ __forceinline__ RowMeta process_loaded_whole(const DirectLoader& load
         }
       }
       lds_barrier();
-      if (direct) {
-        if (kCompact == 1 || total <= THREADS)
+      if (__builtin_expect(direct, 1)) {
+        if (__builtin_expect(kCompact == 1 || total <= THREADS, 1))
           select_compacted_direct<THREADS, 1, PAGES>(total, topk, lo, hi, ckey, cid, cpage, m, f,
                                                      row, out, sh);
         else
