@@ -911,14 +911,32 @@ struct FusedWideLds {
   alignas(16) uint32_t stage[kWideThreads * 32 * 2];
 };
 
-// WIDE: a logits buffer wider than 2048 columns (a decode batch in a wide
+// WIDE 1: a logits buffer wider than 8192 columns (a decode batch in a wide
 // width class, whose rows are usually much shorter than the buffer). As
 // topk_adaptive_kernel does, every workgroup issues the loads of the row's
 // first 2048 columns in the 512 x 4 shape before the row's length arrives;
 // a row of at most 2048 keys is then selected from them, a longer one by
 // select_wide_row (up to 32768 keys, slower than the top-k launch's 1024
 // threads, but a row that long is rare in such a class).
-template <int D, int NKV, int WAVES, int ITEMS, bool WIDE>
+// WIDE 2: a buffer of 2049 to 8192 columns, whose rows are often longer than
+// 2048 keys: the loads of every column go out before the length arrives (16
+// per thread; element i * 512 + tid in v[i], so the first 4 and 8 items are
+// the 512 x 4 and 512 x 8 layouts of the row's first 2048 and 4096 keys),
+// and the row is selected whole from registers in the smallest of those
+// shapes that holds it, without a second round trip for its scores.
+constexpr int kMidMaxColumns = 8192;
+
+template <int K, int N>
+__device__ __forceinline__ void take_items(const uint32_t (&v)[N], const int (&pg)[N],
+                                           uint32_t (&vk)[K], int (&pk)[K]) {
+#pragma unroll
+  for (int i = 0; i < K; ++i) {
+    vk[i] = v[i];
+    pk[i] = pg[i];
+  }
+}
+
+template <int D, int NKV, int WAVES, int ITEMS, int WIDE>
 __global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(2)))
 void select_attend_kernel(const FusedSelect a, const AttnParams p) {
   constexpr int kThreads = 64 * WAVES;
@@ -936,7 +954,37 @@ void select_attend_kernel(const FusedSelect a, const AttnParams p) {
   const int row = blockIdx.x;
   const float* srow = a.scores + (int64_t)row * a.score_row_stride;
   RowMeta r;
-  if constexpr (WIDE) {
+  if constexpr (WIDE == 2) {
+    static_assert(kThreads == kWideThreads && ITEMS == 4, "the 512 x 4 shape of 2048 columns");
+    constexpr int kMidItems = kMidMaxColumns / kThreads;
+    const DirectLoader load{srow, 0};
+    uint32_t v[kMidItems];
+    int pg[kMidItems];
+    load_scores<kThreads, kMidItems>(load, a.cols, v);
+    const RowRequest q =
+        load_request<kThreads, kMidItems, true, true>(load, a.cols, a.meta, row, pg);
+    // Nothing below may wait for the length before the loads above are out.
+    __builtin_amdgcn_sched_barrier(0);
+    const int length = a.lengths[row];
+    const int whole = max(min(max(length, 0), a.cols), 2 * a.topk);
+    auto& wide = *reinterpret_cast<FusedWideLds*>(s_lds);
+#define QSA_MID_ROW(K, LIMIT)                                                                  \
+  {                                                                                            \
+    using Stage = TopkStage<kThreads, K, true>;                                                \
+    auto& st = *reinterpret_cast<Stage*>(wide.stage);                                          \
+    uint32_t vk[K];                                                                            \
+    int pk[K];                                                                                 \
+    take_items<K>(v, pg, vk, pk);                                                              \
+    r = process_loaded_whole<kThreads, K, true, true, true>(                                   \
+        load, LIMIT, vk, pk,                                                                   \
+        [&] { return load_pages<kThreads, K, true, true>(load, LIMIT, a.meta, q, pk); },       \
+        length, a.cols, a.topk, a.meta, row, s_idx, wide.sh, st, reinterpret_cast<int*>(st.key)); \
+  }
+    if (whole <= kThreads * 4) QSA_MID_ROW(4, kThreads * 4)
+    else if (whole <= kThreads * 8) QSA_MID_ROW(8, kThreads * 8)
+    else QSA_MID_ROW(kMidItems, a.cols)
+#undef QSA_MID_ROW
+  } else if constexpr (WIDE == 1) {
     static_assert(kThreads == kWideThreads && ITEMS == 4, "the 512 x 4 shape of 2048 columns");
     constexpr int kNarrowCols = kThreads * ITEMS;
     const DirectLoader load{srow, 0};
@@ -1178,6 +1226,19 @@ int launch_merge(const float* part_out, const float* part_lse, int num_splits, i
 
 #ifdef QSA_ATTN_WIDE_UNIT
 
+namespace qsa {
+namespace {
+template <int D, int NKV>
+void launch_wide(bool mid, dim3 grid, const FusedSelect& a, const AttnParams& p,
+                 hipStream_t stream) {
+  if (mid)
+    hipLaunchKernelGGL((select_attend_kernel<D, NKV, 8, 4, 2>), grid, dim3(512), 0, stream, a, p);
+  else
+    hipLaunchKernelGGL((select_attend_kernel<D, NKV, 8, 4, 1>), grid, dim3(512), 0, stream, a, p);
+}
+}  // namespace
+}  // namespace qsa
+
 extern "C" __attribute__((visibility("hidden"))) int qsa_attn_launch_fused_wide(
     const void* select, size_t select_bytes, const void* params, size_t params_bytes,
     unsigned grid_x, unsigned grid_y, unsigned grid_z, int head_dim, int nkv, hipStream_t stream) {
@@ -1189,14 +1250,15 @@ extern "C" __attribute__((visibility("hidden"))) int qsa_attn_launch_fused_wide(
   std::memcpy(&a, select, sizeof a);
   std::memcpy(&p, params, sizeof p);
   const dim3 grid(grid_x, grid_y, grid_z);
+  const bool mid = a.cols <= kMidMaxColumns;
   if (head_dim == 128 && nkv == 1)
-    hipLaunchKernelGGL((select_attend_kernel<128, 1, 8, 4, true>), grid, dim3(512), 0, stream, a, p);
+    launch_wide<128, 1>(mid, grid, a, p, stream);
   else if (head_dim == 128)
-    hipLaunchKernelGGL((select_attend_kernel<128, 2, 8, 4, true>), grid, dim3(512), 0, stream, a, p);
+    launch_wide<128, 2>(mid, grid, a, p, stream);
   else if (nkv == 1)
-    hipLaunchKernelGGL((select_attend_kernel<64, 1, 8, 4, true>), grid, dim3(512), 0, stream, a, p);
+    launch_wide<64, 1>(mid, grid, a, p, stream);
   else
-    hipLaunchKernelGGL((select_attend_kernel<64, 2, 8, 4, true>), grid, dim3(512), 0, stream, a, p);
+    launch_wide<64, 2>(mid, grid, a, p, stream);
   return (int)hipGetLastError();
 }
 
@@ -1446,10 +1508,10 @@ hipError_t launch_fused(const FusedSelect& a, const AttnLaunch& L, hipStream_t s
     return (hipError_t)qsa_attn_launch_fused_wide(&a, sizeof a, &L.p, sizeof L.p, L.grid.x,
                                                   L.grid.y, L.grid.z, D, NKV, s);
   if (fused_items(a.cols) == 2)
-    hipLaunchKernelGGL((select_attend_kernel<D, NKV, 8, 2, false>), L.grid, dim3(512), 0, s, a,
+    hipLaunchKernelGGL((select_attend_kernel<D, NKV, 8, 2, 0>), L.grid, dim3(512), 0, s, a,
                        L.p);
   else
-    hipLaunchKernelGGL((select_attend_kernel<D, NKV, 8, 4, false>), L.grid, dim3(512), 0, s, a,
+    hipLaunchKernelGGL((select_attend_kernel<D, NKV, 8, 4, 0>), L.grid, dim3(512), 0, s, a,
                        L.p);
   return hipGetLastError();
 }

@@ -34,6 +34,11 @@ CASES = [
     # 8192-column buffer, selected inside the attention's workgroups.
     ("long_rows_8192_columns", {"batch": 8, "seq_len_min": 65536, "seq_len_max": 131072,
                                 "seed": 17}, True),
+    # An 8192-column buffer with rows of 32 to 8192 keys: every column's load
+    # goes out before the row's length, and rows are selected in the 512 x 4,
+    # 512 x 8 and 512 x 16 shapes by length.
+    ("mid_class_mixed_rows", {"table_tokens": 131072, "seq_len_min": 512,
+                              "seq_len_max": 131072, "seed": 26}, True),
     # Past the widest class the combined kernel takes (32768 columns): two calls.
     ("rows_past_32768_columns", {"batch": 1, "seq_len_min": 655360, "seq_len_max": 655360,
                                  "seed": 25}, False),
