@@ -144,14 +144,21 @@ def test_decode_select_attend_padding_row():
     assert not bool(out[-1].any())
 
 
+@pytest.mark.parametrize("table_tokens", [None, 131072, 524288],
+                         ids=["2048_columns", "8192_columns", "32768_columns"])
 @pytest.mark.parametrize("mapping", ["reversed", "pairs"])
-def test_decode_select_attend_request_mapping(mapping):
+def test_decode_select_attend_request_mapping(mapping, table_tokens):
     """Rows whose request is not their own index: the combined kernel loads
     the page-table entries of row r's table row ahead of the request and must
     load them again from the right row. Reversed requests, and two rows per
-    request (token_to_req[r] = r // 2), against the two calls."""
-    print(f"[case] decode_select_attend request mapping {mapping}", flush=True)
-    wl = make_workload("decode_32k", device="cuda", seed=23)
+    request (token_to_req[r] = r // 2), against the two calls, in each of the
+    combined kernel's buffer classes (2048, 8192 and 32768 columns; the
+    8192-column one with rows of 512 to 8192 keys)."""
+    print(f"[case] decode_select_attend request mapping {mapping} {table_tokens}", flush=True)
+    over = {} if table_tokens is None else {"table_tokens": table_tokens}
+    if table_tokens == 131072:
+        over.update(seq_len_min=8192, seq_len_max=131072)
+    wl = make_workload("decode_32k", device="cuda", seed=23, **over)
     rows = wl.rows
     r = torch.arange(rows, dtype=torch.int32, device=wl.device)
     t2r = (rows - 1 - r) if mapping == "reversed" else r // 2
